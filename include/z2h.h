@@ -1,0 +1,134 @@
+/* z2h.h — C ABI of libzonos2_hip.so, the MI355X (gfx950) ragged continuous-batching decode step of
+ * the ZONOS2 MoE backbone.
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, and returns an int status
+ * (Z2H_OK == 0). The per-context message of the last failure is available from z2h_last_error().
+ * No C++ exception crosses this boundary. A context is not reentrant: one thread drives it, as in
+ * the reference (src/server.cpp:905-911, docs/INTERNALS.md:200).
+ *
+ * Reference interfaces replaced (file:line in Zyphra/zonos2.cpp):
+ *   z2h_create            zonos2_batch_init            src/zonos2-graph.cpp:639-690 (KV alloc, S rounding)
+ *   z2h_upload_tensor     zonos2_model_load tensor set src/zonos2.cpp:100-119, name map 137-183
+ *   z2h_finalize          zonos2_model_load field map  src/zonos2.cpp:126-185
+ *   z2h_step              zonos2_batch_step            src/zonos2-graph.cpp:762-837 (+ slot_logits 839-841)
+ *   z2h_prefill           zonos2_batch_slot_prefill    src/zonos2-graph.cpp:703-760
+ *   z2h_moe_forward       build_moe                    src/zonos2-graph.cpp:191-239 (one MoE layer)
+ *   z2h_set_expert_mask   zonos2_set_expert_mask       src/zonos2.cpp:203-239
+ *   z2h_destroy           zonos2_batch_free            src/zonos2-graph.cpp:692-701
+ */
+#ifndef Z2H_H
+#define Z2H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    Z2H_OK = 0,
+    Z2H_EINVAL = 1,     /* bad argument (shape, range, missing tensor) */
+    Z2H_ENOMEM = 2,     /* device or host allocation failed */
+    Z2H_EDEVICE = 3,    /* HIP runtime error */
+    Z2H_ESTATE = 4,     /* call not valid in the context's current state */
+    Z2H_ENOTSUP = 5     /* unsupported tensor type / layout */
+};
+
+/* GGUF tensor type ids accepted by z2h_upload_tensor */
+enum { Z2H_F32 = 0, Z2H_F16 = 1, Z2H_Q8_0 = 8, Z2H_Q4_K = 12, Z2H_Q6_K = 14 };
+
+/* Mirrors zonos2_hparams (src/zonos2.h:14-50); router_dim = router_down.ne1 (src/zonos2.cpp:241-246). */
+typedef struct z2h_hparams {
+    int32_t n_layer, n_embd, head_dim, n_head, n_head_kv, n_ff, n_expert, n_ctx_train;
+    float   rope_freq_base, rms_eps, qk_norm_eps, logit_softcap;
+    int32_t n_codebooks, codebook_size, audio_vocab, eoa_id, audio_pad_id, text_vocab;
+    int32_t spk_dim, spk_lda_dim;
+    int32_t router_dim;
+    const int32_t * expert_used;   /* [n_layer]: 0 = dense FFN, else MoE top-k */
+} z2h_hparams;
+
+typedef struct z2h_ctx z2h_ctx;
+
+/* Create a context on HIP device `device` with n_slots decode slots of slot_cap_frames rows each
+ * (rounded up to a multiple of 256, as the reference does). The KV cache is zero-filled. */
+int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int device, z2h_ctx ** out);
+
+/* Hand over one GGUF tensor: name as in the reference GGUF, ggml ne order (ne0 fastest, unused = 1),
+ * host bytes in GGUF block layout. The bytes are copied (repacked for the device) before return. */
+int z2h_upload_tensor(z2h_ctx * ctx, const char * name, int type, const int64_t ne[4],
+                      const void * data, size_t nbytes);
+
+/* After all uploads: checks that every tensor the forward pass needs is present. */
+int z2h_finalize(z2h_ctx * ctx);
+
+/* Slot rows per slot after rounding (the reference's slot_cap). */
+int z2h_slot_cap(const z2h_ctx * ctx);
+
+/* Write / read KV rows [row0, row0+n_rows) of `slot` in layer `layer`. Host layout
+ * [n_rows][n_head_kv][head_dim] of f16 bits; either pointer may be NULL. */
+int z2h_kv_write(z2h_ctx * ctx, int layer, int slot, int row0, int n_rows, const uint16_t * k, const uint16_t * v);
+int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n_rows, uint16_t * k, uint16_t * v);
+
+/* One batched decode step over n_active columns. slot_idx[i] selects the KV band, n_past[i] is the
+ * row the new K/V are written at (the row count already in the cache), ids is [n_active][n_codebooks+1]
+ * (audio codes then the text id), or NULL when emb ([n_active][n_embd] fp32, injected in place of the
+ * summed embedding before emb_norm) is given. out_logits receives [n_active][n_codebooks][audio_vocab]
+ * post-softcap logits. Unlike the reference, idle slots are simply not listed (no padded columns). */
+int z2h_step(z2h_ctx * ctx, int n_active, const int32_t * slot_idx, const int32_t * n_past,
+             const int32_t * ids, const float * emb, float * out_logits);
+
+/* Same step with device-resident inputs/outputs, enqueued on `stream` (a hipStream_t, NULL = the
+ * context's stream) without synchronizing. d_slot_idx/d_n_past: [n_active] int32; d_ids or d_emb as
+ * above; d_logits [n_active][n_codebooks*audio_vocab]. h_n_past must hold the same n_past values on
+ * the host (grid sizing for the ragged attention). */
+int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, const int32_t * d_n_past,
+                    const int32_t * h_n_past, const int32_t * d_ids, const float * d_emb,
+                    float * d_logits, void * stream);
+
+/* Prefill n0 prompt rows into `slot` (rows [0, n0)), causal within the prompt as in the reference's
+ * per-slot prefill; ids [n0][n_codebooks+1]. spk (optional, [spk_dim]) replaces row spk_pos's
+ * embedding by spk_proj(spk_lda(spk)) (+ delta [n_embd] if non-NULL). last_logits receives the final
+ * row's [n_codebooks][audio_vocab] logits. */
+int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
+                const float * delta, float * last_logits);
+
+/* One MoE layer (build_moe) on n_tokens host rows x [n_tokens][n_embd] (the layer's ffn_in); state_in
+ * ([n_tokens][router_dim], may be NULL) is the previous MoE layer's router state. out [n_tokens][n_embd]. */
+int z2h_moe_forward(z2h_ctx * ctx, int layer, int n_tokens, const float * x, const float * state_in, float * out);
+/* Device-pointer variant, enqueued on `stream` without synchronizing. */
+int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int n_tokens, const float * d_x, const float * d_state_in,
+                           float * d_out, void * stream);
+
+/* Runtime expert mask for one MoE layer: keep[e] != 0 keeps expert e routable (logits and selection
+ * scores of the others get -inf); keep == NULL clears the layer's mask. */
+int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep);
+
+/* Additive pre-softmax router-logit bias for one MoE layer ([n_expert] fp32, NULL clears). Not a
+ * reference input: a benchmark hook to impose a skewed expert popularity. */
+int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias);
+
+/* Debug capture of per-layer intermediates of the following steps (off by default). */
+enum {
+    Z2H_CAP_RES_IN = 0, Z2H_CAP_ATTN_IN, Z2H_CAP_Q, Z2H_CAP_K, Z2H_CAP_V, Z2H_CAP_GATE, Z2H_CAP_ATTN_O,
+    Z2H_CAP_ATTN_OUT, Z2H_CAP_FFN_IN, Z2H_CAP_ROUTER_STATE, Z2H_CAP_ROUTER_LOGITS, Z2H_CAP_PROBS,
+    Z2H_CAP_SEL, Z2H_CAP_WEIGHTS, Z2H_CAP_FFN_OUT, Z2H_CAP_OUT_NORM, Z2H_CAP_COUNTS, Z2H_CAP_OFFSETS,
+    Z2H_CAP_PERM, Z2H_CAP_EXPERT_OUT, Z2H_CAP_COUNT_
+};
+int z2h_set_capture(z2h_ctx * ctx, int enable);
+/* Copy capture `what` of `layer` (ignored for OUT_NORM) from the last step / moe_forward into host.
+ * Sizes: see z2h_capture_bytes. */
+int64_t z2h_capture_bytes(z2h_ctx * ctx, int what, int n_tokens);
+int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nbytes);
+
+/* Device memory held by weights, KV cache and scratch (bytes). */
+int64_t z2h_device_bytes(const z2h_ctx * ctx, int what /* 0 weights, 1 kv, 2 scratch */);
+
+/* Message of the context's last failure. */
+const char * z2h_last_error(const z2h_ctx * ctx);
+void z2h_destroy(z2h_ctx * ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Z2H_H */

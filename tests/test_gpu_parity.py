@@ -1,0 +1,123 @@
+"""Device decode step vs the CPU oracle (C ABI via ctypes), on the tiny config and one MoE layer.
+
+Bars: routing (router state, logits, probabilities, top-k ids, weights) and the grouping (counts,
+offsets, permutation) bit-exact on identical router inputs; hidden states and logits cos >= 0.9999
+and max-abs <= 1e-2 per layer.
+"""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from helpers import COS_MIN, MAXABS, assert_close, fill_kv, oracle_pair, min_topk_margin
+from zonos2_amd import configs, synth
+from zonos2_amd.z2h import Context
+
+pytestmark = pytest.mark.gpu
+
+
+def _build(cfg, wl, seed=42):
+    model = synth.generate_model(cfg, seed)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    om, okv = oracle_pair(cfg, model, wl)
+    fill_kv(cfg, wl, [ctx.kv_write, okv.write])
+    return model, ctx, om, okv
+
+
+def _check_routing(cfg, ctx, om, T):
+    """Teacher-forced: the oracle router on the device's router input must match bit for bit."""
+    prev = None
+    E, rd = cfg.n_expert, cfg.router_dim
+    for L in range(cfg.n_layer):
+        k = cfg.expert_used[L]
+        if k == 0:
+            continue
+        x = ctx.read_capture(L, "ffn_in", T).reshape(T, cfg.n_embd)
+        ref = O.router(om, L, x, prev)
+        rh = ctx.read_capture(L, "router_state", T).reshape(T, rd)
+        lg = ctx.read_capture(L, "router_logits", T).reshape(T, E)
+        pr = ctx.read_capture(L, "probs", T).reshape(T, E)
+        sel = ctx.read_capture(L, "sel", T).reshape(T, ctx.kmax)[:, :k]
+        w = ctx.read_capture(L, "weights", T).reshape(T, ctx.kmax)[:, :k]
+        for name, a, b in (("rh", rh, ref["rh"]), ("logits", lg, ref["logits"]), ("probs", pr, ref["probs"]),
+                           ("w", w, ref["w"])):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"layer {L} {name} not bit-exact"
+        assert np.array_equal(sel, ref["sel"]), f"layer {L} top-k ids differ"
+        counts, offsets, perm = O.group(sel, E)
+        assert np.array_equal(ctx.read_capture(L, "counts", T), counts)
+        assert np.array_equal(ctx.read_capture(L, "offsets", T), offsets)
+        assert np.array_equal(ctx.read_capture(L, "perm", T)[:T * k], perm)
+        # experts on the same routing: weighted per-route outputs and the k-sum
+        eo, out = O.experts(om, L, x, sel, w)
+        geo = ctx.read_capture(L, "expert_out", T).reshape(-1, cfg.n_embd)[:T * k]
+        assert_close(f"layer {L} expert_out", geo, eo)
+        print(f"layer {L}: routing bit-exact, min top-k margin {min_topk_margin(ref['probs'], np.zeros(E), k):.3e}")
+        prev = rh
+
+
+def test_c1_step_vs_oracle():
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl)
+    inp = synth.step_inputs(cfg, wl)
+    T = len(wl.kv_lens)
+    ctx.set_capture(True)
+    got = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    want, cap = O.step(om, okv, inp.slot_idx, inp.n_past, emb=inp.emb, capture=True)
+    for L in range(cfg.n_layer):
+        for name in ("res_in", "attn_in", "q", "k", "v", "attn_o", "attn_out", "ffn_in", "ffn_out"):
+            g = ctx.read_capture(L, name, T).reshape(cap[name][L].shape)
+            assert_close(f"layer {L} {name}", g, cap[name][L])
+    assert_close("out_norm", ctx.read_capture(0, "out_norm", T).reshape(T, -1), cap["out_norm"])
+    assert_close("logits", got, want)
+    _check_routing(cfg, ctx, om, T)
+    # the new K/V rows written by the step
+    for L in range(cfg.n_layer):
+        for s, n in enumerate(wl.kv_lens):
+            gk, gv = ctx.kv_read(L, s, n, 1)
+            ok, ov = okv.read(L, s, n, 1)
+            assert_close(f"kv {L}/{s}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32))
+            assert_close(f"kv {L}/{s}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32))
+
+
+def test_c1_step_with_token_ids():
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl, seed=43)
+    inp = synth.step_inputs(cfg, wl)
+    got = ctx.step(inp.slot_idx, inp.n_past, ids=inp.ids)
+    want = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)
+    assert_close("logits(ids)", got, want)
+
+
+def test_c1_batch_invariance():
+    """A column's result does not depend on the other columns (reference --batch-test F.1/F.2)."""
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl, seed=44)
+    inp = synth.step_inputs(cfg, wl)
+    full = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    for t in range(len(wl.kv_lens)):
+        one = ctx.step(inp.slot_idx[t:t + 1], inp.n_past[t:t + 1], emb=inp.emb[t:t + 1])
+        assert np.array_equal(one[0], full[t]), f"column {t} differs when stepped alone"
+
+
+def test_c2_moe_layer_vs_oracle():
+    cfg, wl = configs.C2()
+    model = synth.generate_model(cfg, 42)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    om = O.OracleModel(cfg.hparams(), model)
+    T = wl.n_slots
+    x = synth.gen_normal_f32((T, cfg.n_embd), wl.seed, "inputs.moe")
+    ctx.set_capture(True)
+    got = ctx.moe_forward(0, x)
+    ref = O.router(om, 0, x, None)
+    sel = ctx.read_capture(0, "sel", T).reshape(T, ctx.kmax)[:, :cfg.top_k]
+    assert np.array_equal(sel, ref["sel"])
+    for name in ("router_state", "router_logits", "probs"):
+        key = {"router_state": "rh", "router_logits": "logits", "probs": "probs"}[name]
+        assert np.array_equal(ctx.read_capture(0, name, T).reshape(ref[key].shape).view(np.uint32), ref[key].view(np.uint32)), name
+    counts, offsets, perm = O.group(ref["sel"], cfg.n_expert)
+    assert np.array_equal(ctx.read_capture(0, "counts", T), counts)
+    assert np.array_equal(ctx.read_capture(0, "offsets", T), offsets)
+    assert np.array_equal(ctx.read_capture(0, "perm", T), perm)
+    eo, out = O.experts(om, 0, x, ref["sel"], ref["w"])
+    assert_close("moe out", got, out)

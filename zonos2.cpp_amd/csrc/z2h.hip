@@ -1,0 +1,857 @@
+// z2h.hip — context, weight repack/upload and step orchestration behind include/z2h.h.
+//
+// One HIP stream per context; every device buffer is allocated at create / finalize time, so a
+// step performs no allocation. A step is a fixed sequence of kernels per layer (see z2h_kernels.h):
+//   k_resnorm -> k_gemv(QKV+gate) -> k_qkv_post -> k_attn_partial -> k_attn_combine -> k_gemv(W_o)
+//   -> k_resnorm(+attn, ffn_norm) -> [MoE] k_router_down -> k_router_tail -> k_gemv(gate/up, grouped)
+//   -> k_gemv(down, grouped, SwiGLU staging) | [dense] k_gemv(up/gate) -> k_gemv(down)
+// and after the last layer k_resnorm(output_norm) -> k_gemv(head, softcap).
+#include "z2h.h"
+#include "z2h_kernels.h"
+#include "z2_formats.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+using namespace z2d;
+
+namespace {
+
+struct DevMat {
+    int type = -1;
+    int rows = 0, K = 0, nsb = 0, tiles = 0, n_mats = 1;
+    uint8_t * w = nullptr;            // tiled bytes
+    uint16_t * dpl = nullptr;         // Q6_K d plane
+    int64_t mat_bytes = 0, dpl_elems = 0;
+    bool ok() const { return w != nullptr; }
+};
+
+struct HostTensor { int type; int64_t ne[4]; std::vector<uint8_t> bytes; };
+
+struct Layer {
+    DevMat qkvg, wo, gate_exps, up_exps, down_exps, ffn_up, ffn_gate, ffn_down;
+    float * attn_norm = nullptr, * ffn_norm = nullptr, * attn_temp = nullptr;
+    bool moe = false;
+    int k = 0, E = 0;
+    float * r_down = nullptr, * r_down_b = nullptr, * r_m0t = nullptr, * r_m0_b = nullptr, * r_m2t = nullptr,
+          * r_m2_b = nullptr, * r_m4t = nullptr, * r_norm = nullptr, * r_bias = nullptr, * r_eda = nullptr;
+    float * logit_bias = nullptr, * mask = nullptr, * bias_buf = nullptr, * mask_buf = nullptr;
+    std::map<std::string, HostTensor> stash;   // attn q/k/v/gate until all four are present
+};
+
+int act_of(int wtype) {
+    switch (wtype) { case Z2H_Q4_K: case Z2H_Q6_K: return ACT_Q8_K; case Z2H_Q8_0: return ACT_Q8_0; case Z2H_F16: return ACT_F16; }
+    return ACT_NONE;
+}
+int chunks_of(int wtype) {
+    switch (wtype) { case Z2H_Q4_K: return 9; case Z2H_Q6_K: return 13; case Z2H_Q8_0: return 17; case Z2H_F16: return 32; }
+    return 0;
+}
+
+} // namespace
+
+struct z2h_ctx {
+    z2h_hparams hp{};
+    std::vector<int32_t> expert_used;
+    int device = 0, n_slots = 0, S = 0, W = 0, kmax = 1, rd = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    bool finalized = false;
+    int64_t bytes_w = 0, bytes_kv = 0, bytes_scratch = 0;
+    std::vector<void *> allocs;
+
+    // weights
+    std::vector<uint8_t *> tab; std::vector<int> tab_type; std::vector<int64_t> tab_rows;
+    DevMat head;
+    float * output_norm = nullptr;
+    DevMat spk_lda, spk_proj;
+    float * spk_lda_b = nullptr, * spk_proj_b = nullptr;
+    std::vector<Layer> layers;
+    std::map<std::string, bool> seen;
+
+    // KV cache [L][2][slot][kvh][S][hd]
+    uint16_t * kv = nullptr;
+
+    // scratch (sized for n_slots tokens)
+    int Tmax = 0, Kmax = 0, items_max = 0;
+    int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
+    float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * gate = nullptr, * wo_out = nullptr;
+    uint16_t * q16 = nullptr;
+    float * part_o = nullptr, * part_ml = nullptr;
+    ActBuf act{};
+    float * state = nullptr;          // [L][T][rd]
+    float * state_ext = nullptr;      // [T][rd] external state for moe_forward
+    int32_t * sel = nullptr; float * wsel = nullptr;
+    float * gu_g = nullptr, * gu_u = nullptr, * eo = nullptr, * logits = nullptr, * tmp_x = nullptr;
+    int * d_err = nullptr;
+    int32_t * h_pin = nullptr;        // pinned staging for step inputs
+    size_t h_pin_bytes = 0;
+
+    // capture
+    bool capture = false;
+    std::vector<uint8_t *> cap;       // per `what`: [L][Tmax][width]
+    int cap_T = 0;
+};
+
+namespace {
+
+int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; return code; }
+
+#define HIPX(expr) do { hipError_t e_ = (expr); if (e_ != hipSuccess) \
+    return seterr(ctx, Z2H_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); } while (0)
+
+template <class T>
+int dalloc(z2h_ctx * ctx, T ** p, size_t bytes, int64_t & counter) {
+    void * v = nullptr;
+    if (bytes == 0) bytes = 16;
+    if (hipMalloc(&v, bytes) != hipSuccess) return seterr(ctx, Z2H_ENOMEM, "hipMalloc failed (" + std::to_string(bytes) + " B)");
+    ctx->allocs.push_back(v);
+    counter += (int64_t) bytes;
+    *p = (T *) v;
+    return Z2H_OK;
+}
+
+int upload_f32(z2h_ctx * ctx, const HostTensor & t, float ** out, int64_t n_expect) {
+    const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    if (n_expect >= 0 && n != n_expect) return seterr(ctx, Z2H_EINVAL, "unexpected vector length");
+    std::vector<float> f((size_t) n);
+    const int64_t rows = n / t.ne[0];
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t * src = t.bytes.data() + r * z2::row_bytes(t.type, t.ne[0]);
+        float * y = f.data() + r * t.ne[0];
+        switch (t.type) {
+            case Z2H_F32: std::memcpy(y, src, t.ne[0] * 4); break;
+            case Z2H_F16: for (int64_t i = 0; i < t.ne[0]; ++i) { uint16_t h; std::memcpy(&h, src + 2 * i, 2); y[i] = z2::f16_to_f32(h); } break;
+            case Z2H_Q8_0:
+                for (int64_t b = 0; b < t.ne[0] / 32; ++b) {
+                    uint16_t h; std::memcpy(&h, src + 34 * b, 2);
+                    const float d = z2::f16_to_f32(h);
+                    for (int j = 0; j < 32; ++j) y[32 * b + j] = (float) (int8_t) src[34 * b + 2 + j] * d;
+                }
+                break;
+            default: return seterr(ctx, Z2H_ENOTSUP, "router/vector tensors must be F32, F16 or Q8_0");
+        }
+    }
+    if (int rc = dalloc(ctx, out, f.size() * 4, ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(*out, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+    return Z2H_OK;
+}
+
+int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
+    const int64_t in = t.ne[0], outn = t.ne[1];
+    std::vector<float> full((size_t) (in * outn)), tr((size_t) (in * outn));
+    for (int64_t r = 0; r < outn; ++r) {
+        const uint8_t * src = t.bytes.data() + r * z2::row_bytes(t.type, in);
+        for (int64_t i = 0; i < in; ++i) {
+            float v = 0.0f;
+            if (t.type == Z2H_F32) std::memcpy(&v, src + 4 * i, 4);
+            else if (t.type == Z2H_F16) { uint16_t h; std::memcpy(&h, src + 2 * i, 2); v = z2::f16_to_f32(h); }
+            else if (t.type == Z2H_Q8_0) { uint16_t h; std::memcpy(&h, src + 34 * (i / 32), 2); v = (float) (int8_t) src[34 * (i / 32) + 2 + i % 32] * z2::f16_to_f32(h); }
+            else return seterr(ctx, Z2H_ENOTSUP, "router matrices must be F32, F16 or Q8_0");
+            full[r * in + i] = v;
+        }
+    }
+    for (int64_t r = 0; r < outn; ++r) for (int64_t i = 0; i < in; ++i) tr[i * outn + r] = full[r * in + i];
+    if (int rc = dalloc(ctx, out, tr.size() * 4, ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(*out, tr.data(), tr.size() * 4, hipMemcpyHostToDevice));
+    return Z2H_OK;
+}
+
+// Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the row-tiled layout.
+int upload_mat(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+    const int C = chunks_of(type);
+    if (!C) return seterr(ctx, Z2H_ENOTSUP, "matrix type not supported on the device (F16, Q8_0, Q4_K, Q6_K)");
+    if ((type == Z2H_Q4_K || type == Z2H_Q6_K) && K % 256) return seterr(ctx, Z2H_EINVAL, "K-quant row not a multiple of 256");
+    if (type == Z2H_Q8_0 && K % 32) return seterr(ctx, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
+    dm.type = type; dm.rows = (int) rows; dm.K = (int) K; dm.nsb = (int) ((K + 255) / 256);
+    dm.tiles = (int) ((rows + TILE - 1) / TILE); dm.n_mats = n_mats;
+    dm.mat_bytes = (int64_t) dm.tiles * dm.nsb * C * TILE * 16;
+    dm.dpl_elems = type == Z2H_Q6_K ? (int64_t) dm.tiles * dm.nsb * TILE : 0;
+    const int64_t rb = z2::row_bytes(type, K);
+    std::vector<uint8_t> tiled((size_t) dm.mat_bytes * n_mats, 0);
+    std::vector<uint16_t> dpl((size_t) dm.dpl_elems * n_mats, 0);
+    for (int e = 0; e < n_mats; ++e) {
+        uint8_t * dst = tiled.data() + (size_t) e * dm.mat_bytes;
+        for (int64_t r = 0; r < rows; ++r) {
+            const uint8_t * row = src + ((int64_t) e * rows + r) * rb;
+            const int64_t tile = r / TILE, lane = r % TILE;
+            for (int sb = 0; sb < dm.nsb; ++sb) {
+                uint8_t unit[512];
+                std::memset(unit, 0, sizeof(unit));
+                switch (type) {
+                    case Z2H_Q4_K: std::memcpy(unit, row + 144 * sb, 144); break;
+                    case Z2H_Q6_K:
+                        std::memcpy(unit, row + 210 * sb, 208);
+                        std::memcpy(&dpl[(size_t) e * dm.dpl_elems + ((size_t) tile * dm.nsb + sb) * TILE + lane], row + 210 * sb + 208, 2);
+                        break;
+                    case Z2H_Q8_0:
+                        for (int b = 0; b < 8; ++b) {
+                            const int64_t blk = (int64_t) sb * 8 + b;
+                            if (blk * 32 >= K) break;
+                            std::memcpy(unit + 32 * b, row + 34 * blk + 2, 32);
+                            std::memcpy(unit + 256 + 2 * b, row + 34 * blk, 2);
+                        }
+                        break;
+                    case Z2H_F16: {
+                        const int64_t n = std::min<int64_t>(256, K - (int64_t) sb * 256);
+                        std::memcpy(unit, row + (int64_t) sb * 512, (size_t) n * 2);
+                        break;
+                    }
+                }
+                for (int c = 0; c < C; ++c)
+                    std::memcpy(dst + ((((size_t) tile * dm.nsb + sb) * C + c) * TILE + lane) * 16, unit + 16 * c, 16);
+            }
+        }
+    }
+    if (int rc = dalloc(ctx, &dm.w, tiled.size(), ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(dm.w, tiled.data(), tiled.size(), hipMemcpyHostToDevice));
+    if (type == Z2H_Q6_K) {
+        if (int rc = dalloc(ctx, &dm.dpl, dpl.size() * 2, ctx->bytes_w)) return rc;
+        HIPX(hipMemcpy(dm.dpl, dpl.data(), dpl.size() * 2, hipMemcpyHostToDevice));
+    }
+    return Z2H_OK;
+}
+
+bool parse_layer(const std::string & name, int & L, std::string & rest) {
+    if (name.rfind("blk.", 0) != 0) return false;
+    const size_t dot = name.find('.', 4);
+    if (dot == std::string::npos) return false;
+    L = std::atoi(name.substr(4, dot - 4).c_str());
+    rest = name.substr(dot + 1);
+    return true;
+}
+
+int fuse_qkvg(z2h_ctx * ctx, Layer & ly) {
+    static const char * parts[4] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_gate.weight"};
+    for (auto * p : parts) if (!ly.stash.count(p)) return Z2H_OK;   // not complete yet
+    const int type = ly.stash["attn_q.weight"].type;
+    const int64_t K = ly.stash["attn_q.weight"].ne[0];
+    int64_t rows = 0;
+    for (auto * p : parts) {
+        const HostTensor & t = ly.stash[p];
+        if (t.type != type || t.ne[0] != K) return seterr(ctx, Z2H_ENOTSUP, "attention projections must share type and input size");
+        rows += t.ne[1];
+    }
+    std::vector<uint8_t> cat;
+    for (auto * p : parts) cat.insert(cat.end(), ly.stash[p].bytes.begin(), ly.stash[p].bytes.end());
+    ly.stash.clear();
+    return upload_mat(ctx, type, K, rows, 1, cat.data(), ly.qkvg);
+}
+
+int alloc_scratch(z2h_ctx * ctx) {
+    const auto & hp = ctx->hp;
+    const int T = ctx->n_slots, d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
+    const int ff = hp.n_ff, K = ctx->kmax, E = std::max(1, hp.n_expert), rd = std::max(1, ctx->rd);
+    ctx->Tmax = T;
+    ctx->Kmax = std::max({kpad(d), kpad(nh * hd), kpad(ff), kpad(std::max(1, hp.spk_dim)), kpad(std::max(1, hp.spk_lda_dim))});
+    const int R = (nh + 2 * nkv) * hd + nh;
+    const int grp = nh / nkv;
+    ctx->items_max = T * ((ctx->S + ATT_CH - 1) / ATT_CH) * nkv;
+    int64_t & b = ctx->bytes_scratch;
+    int rc = 0;
+    const int KM = ctx->Kmax;
+    const int W = ctx->W;
+    if ((rc = dalloc(ctx, &ctx->d_slot, T * 4, b)) || (rc = dalloc(ctx, &ctx->d_npast, T * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->d_ids, (size_t) T * W * 4, b)) || (rc = dalloc(ctx, &ctx->d_emb, (size_t) T * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->res, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->cur, (size_t) T * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->tmp_x, (size_t) T * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->qkvg, (size_t) T * R * 4, b)) || (rc = dalloc(ctx, &ctx->gate, (size_t) T * nh * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->wo_out, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->q16, (size_t) T * nh * hd * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->part_o, (size_t) ctx->items_max * grp * hd * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->part_ml, (size_t) ctx->items_max * grp * 2 * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act.q, (size_t) T * KM, b)) || (rc = dalloc(ctx, &ctx->act.d32, (size_t) T * (KM / 32) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act.d256, (size_t) T * (KM / 256) * 4, b)) || (rc = dalloc(ctx, &ctx->act.bs, (size_t) T * (KM / 16) * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->act.h, (size_t) T * KM * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->state, (size_t) hp.n_layer * T * rd * 4, b)) || (rc = dalloc(ctx, &ctx->state_ext, (size_t) T * rd * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->sel, (size_t) T * K * 4, b)) || (rc = dalloc(ctx, &ctx->wsel, (size_t) T * K * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->gu_g, (size_t) T * K * std::max(ff, 1) * 4, b)) || (rc = dalloc(ctx, &ctx->gu_u, (size_t) T * K * std::max(ff, 1) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->eo, (size_t) T * K * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->logits, (size_t) T * hp.n_codebooks * hp.audio_vocab * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->d_err, 16, b)))
+        return rc;
+    (void) E;
+    ctx->h_pin_bytes = (size_t) T * (2 + W) * 4;
+    if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
+        return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
+    return Z2H_OK;
+}
+
+// capture widths (elements per token, or per layer for grouping ids)
+int64_t cap_width(const z2h_ctx * c, int what, int T) {
+    const auto & hp = c->hp;
+    const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
+    switch (what) {
+        case Z2H_CAP_RES_IN: case Z2H_CAP_ATTN_IN: case Z2H_CAP_ATTN_OUT: case Z2H_CAP_FFN_IN:
+        case Z2H_CAP_FFN_OUT: case Z2H_CAP_OUT_NORM: return (int64_t) T * d;
+        case Z2H_CAP_Q: case Z2H_CAP_ATTN_O: return (int64_t) T * nh * hd;
+        case Z2H_CAP_K: case Z2H_CAP_V: return (int64_t) T * nkv * hd;
+        case Z2H_CAP_GATE: return (int64_t) T * nh;
+        case Z2H_CAP_ROUTER_STATE: return (int64_t) T * std::max(1, c->rd);
+        case Z2H_CAP_ROUTER_LOGITS: case Z2H_CAP_PROBS: return (int64_t) T * std::max(1, hp.n_expert);
+        case Z2H_CAP_SEL: case Z2H_CAP_WEIGHTS: return (int64_t) T * c->kmax;
+        case Z2H_CAP_COUNTS: return std::max(1, hp.n_expert);
+        case Z2H_CAP_OFFSETS: return std::max(1, hp.n_expert) + 1;
+        case Z2H_CAP_PERM: return (int64_t) T * c->kmax;
+        case Z2H_CAP_EXPERT_OUT: return (int64_t) T * c->kmax * d;
+    }
+    return 0;
+}
+
+uint8_t * capp(z2h_ctx * c, int what, int L) {
+    if (!c->capture) return nullptr;
+    return c->cap[what] + (size_t) L * cap_width(c, what, c->Tmax) * 4;
+}
+
+int cap_copy(z2h_ctx * ctx, int what, int L, const void * src, int T) {
+    if (!ctx->capture) return Z2H_OK;
+    HIPX(hipMemcpyAsync(capp(ctx, what, L), src, (size_t) cap_width(ctx, what, T) * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    return Z2H_OK;
+}
+
+// ---------------------------------------------------------------- launch helpers
+int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & base, int stage, int grid_y) {
+    GemvArgs a = base;
+    a.w[0] = m0.w; a.w[1] = m1 ? m1->w : m0.w;
+    a.dpl[0] = m0.dpl; a.dpl[1] = m1 ? m1->dpl : m0.dpl;
+    a.mat_bytes = m0.mat_bytes; a.dpl_elems = m0.dpl_elems;
+    a.nsb = m0.nsb; a.tiles = m0.tiles; a.rows = m0.rows; a.K = m0.K;
+    const int af = act_of(m0.type);
+    const size_t lds = gemv_lds_bytes(af, m0.nsb * 256, stage);
+    dim3 grid(m0.tiles, grid_y, m1 ? 2 : 1), block(256);
+#define GEMV_CASE(WF_) \
+    if (stage == ST_ACT) hipLaunchKernelGGL((k_gemv<WF_, ST_ACT>), grid, block, lds, ctx->stream, a); \
+    else hipLaunchKernelGGL((k_gemv<WF_, ST_SWIGLU>), grid, block, lds, ctx->stream, a);
+    switch (m0.type) {
+        case Z2H_Q4_K: GEMV_CASE(WF_Q4_K); break;
+        case Z2H_Q6_K: GEMV_CASE(WF_Q6_K); break;
+        case Z2H_Q8_0: GEMV_CASE(WF_Q8_0); break;
+        case Z2H_F16:  GEMV_CASE(WF_F16); break;
+        default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
+    }
+#undef GEMV_CASE
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+GemvArgs gemv_dense(z2h_ctx * ctx, int T, float * out, int out_ld, int epi) {
+    GemvArgs a{};
+    a.grouped = 0; a.n_tok = T; a.act = ctx->act;
+    a.out[0] = out; a.out[1] = out; a.out_ld = out_ld; a.epi = epi; a.cap = ctx->hp.logit_softcap;
+    return a;
+}
+
+int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
+    a.d = ctx->hp.n_embd; a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
+    hipLaunchKernelGGL(k_resnorm, dim3(T), dim3(256), (size_t) kpad(a.d) * 4, ctx->stream, a);
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in) {
+    const auto & hp = ctx->hp;
+    int rc;
+    // router (exact contract)
+    RouterArgs r{};
+    r.x = ctx->cur; r.T = T; r.d = hp.n_embd; r.rd = ctx->rd; r.E = ly.E; r.k = ly.k;
+    r.w_down = ly.r_down; r.b_down = ly.r_down_b; r.eda = ly.r_eda; r.state_in = state_in;
+    r.rh = ctx->state + (size_t) L * ctx->Tmax * ctx->rd;
+    r.norm_w = ly.r_norm; r.eps = hp.rms_eps;
+    r.w0t = ly.r_m0t; r.b0 = ly.r_m0_b; r.w2t = ly.r_m2t; r.b2 = ly.r_m2_b; r.w4t = ly.r_m4t;
+    r.logit_bias = ly.logit_bias; r.mask = ly.mask; r.sc_bias = ly.r_bias;
+    r.sel = ctx->sel; r.wsel = ctx->wsel;
+    r.cap_logits = (float *) capp(ctx, Z2H_CAP_ROUTER_LOGITS, L);
+    r.cap_probs = (float *) capp(ctx, Z2H_CAP_PROBS, L);
+    hipLaunchKernelGGL(k_router_down, dim3((ctx->rd + 3) / 4), dim3(256), 0, ctx->stream, r);
+    HIPX(hipGetLastError());
+    hipLaunchKernelGGL(k_router_tail, dim3(T), dim3(64), 0, ctx->stream, r);
+    HIPX(hipGetLastError());
+    if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
+    if ((rc = cap_copy(ctx, Z2H_CAP_SEL, L, ctx->sel, T))) return rc;
+    if ((rc = cap_copy(ctx, Z2H_CAP_WEIGHTS, L, ctx->wsel, T))) return rc;
+    // gate + up (grouped by expert)
+    GemvArgs g{};
+    g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E;
+    g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_u; g.out_ld = hp.n_ff; g.epi = EPI_STORE;
+    if (ctx->capture) {
+        g.cap_counts = (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L);
+        g.cap_offsets = (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L);
+        g.cap_perm = (int32_t *) capp(ctx, Z2H_CAP_PERM, L);
+    }
+    if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ST_ACT, ly.E))) return rc;
+    // down, SwiGLU staging, route weight
+    GemvArgs dn{};
+    dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
+    dn.gu_g = ctx->gu_g; dn.gu_u = ctx->gu_u; dn.ff = hp.n_ff;
+    dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
+    if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ST_SWIGLU, ly.E))) return rc;
+    if ((rc = cap_copy(ctx, Z2H_CAP_EXPERT_OUT, L, ctx->eo, T))) return rc;
+    return Z2H_OK;
+}
+
+int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
+    const auto & hp = ctx->hp;
+    int rc;
+    GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
+    g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_u;
+    if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, ST_ACT, (T + NT - 1) / NT))) return rc;
+    GemvArgs dn{};
+    dn.grouped = 0; dn.n_tok = T; dn.gu_g = ctx->gu_g; dn.gu_u = ctx->gu_u; dn.ff = hp.n_ff;
+    dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_STORE;
+    return launch_gemv(ctx, ly.ffn_down, nullptr, dn, ST_SWIGLU, (T + NT - 1) / NT);
+}
+
+// The whole decode step on device-resident inputs in ctx->d_* (T tokens, host copy of n_past).
+int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
+             const int32_t * d_ids, const float * d_emb, float * d_logits) {
+    const auto & hp = ctx->hp;
+    const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
+    int rc;
+    ctx->cap_T = T;
+    // embeddings + emb_norm + layer-0 attn_norm
+    ResNormArgs e{};
+    e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb;
+    for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->tab[k]; e.tab_type[k] = ctx->tab_type[k]; e.tab_rows[k] = ctx->tab_rows[k]; }
+    e.res = ctx->res; e.norm_w = ctx->layers[0].attn_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_ATTN_IN, 0);
+    e.act = ctx->act; e.act_fmt = act_of(ctx->layers[0].qkvg.type);
+    if ((rc = launch_resnorm(ctx, T, e))) return rc;
+    if ((rc = cap_copy(ctx, Z2H_CAP_RES_IN, 0, ctx->res, T))) return rc;
+    int n_items = 0;
+    for (int t = 0; t < T; ++t) n_items += (h_npast[t] + 1 + ATT_CH - 1) / ATT_CH;
+    n_items *= nkv;
+    const int R = (nh + 2 * nkv) * hd + nh;
+    int prev_moe = -1;
+    for (int L = 0; L < hp.n_layer; ++L) {
+        Layer & ly = ctx->layers[L];
+        // fused QKV + gate projection
+        if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), ST_ACT, (T + NT - 1) / NT))) return rc;
+        AttnArgs a{};
+        a.qkvg = ctx->qkvg; a.R = R; a.nh = nh; a.nkv = nkv; a.hd = hd; a.temp = ly.attn_temp;
+        a.qk_eps = hp.qk_norm_eps; a.theta_scale = std::pow(hp.rope_freq_base, -2.0f / (float) hd);
+        a.scale = 1.0f / std::sqrt((float) hd);
+        a.slot_idx = d_slot; a.n_past = d_npast; a.T = T; a.S = ctx->S;
+        const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
+        a.kc = ctx->kv + (size_t) (2 * L) * lsz; a.vc = ctx->kv + (size_t) (2 * L + 1) * lsz;
+        a.q16 = ctx->q16; a.gate = ctx->gate;
+        a.cap_q = (float *) capp(ctx, Z2H_CAP_Q, L); a.cap_k = (float *) capp(ctx, Z2H_CAP_K, L); a.cap_v = (float *) capp(ctx, Z2H_CAP_V, L);
+        a.part_o = ctx->part_o; a.part_ml = ctx->part_ml; a.n_items = n_items;
+        a.o_out = (float *) capp(ctx, Z2H_CAP_ATTN_O, L);
+        a.act = ctx->act; a.act_fmt = act_of(ly.wo.type);
+        hipLaunchKernelGGL(k_qkv_post, dim3(T), dim3(256), 0, ctx->stream, a);
+        HIPX(hipGetLastError());
+        if ((rc = cap_copy(ctx, Z2H_CAP_GATE, L, ctx->gate, T))) return rc;
+        const int grp = nh / nkv;
+        const size_t lds_p = (size_t) 2 * ATT_CH * (hd + 8) * 2 + (size_t) (grp * hd + 8) * 2 + (size_t) grp * ATT_CH * 4 + 16;
+        hipLaunchKernelGGL(k_attn_partial, dim3(std::min(n_items, 4096)), dim3(256), lds_p, ctx->stream, a);
+        HIPX(hipGetLastError());
+        hipLaunchKernelGGL(k_attn_combine, dim3(T), dim3(256), (size_t) kpad(nh * hd) * 4, ctx->stream, a);
+        HIPX(hipGetLastError());
+        // W_o
+        if ((rc = launch_gemv(ctx, ly.wo, nullptr, gemv_dense(ctx, T, ctx->wo_out, d, EPI_STORE), ST_ACT, (T + NT - 1) / NT))) return rc;
+        if ((rc = cap_copy(ctx, Z2H_CAP_ATTN_OUT, L, ctx->wo_out, T))) return rc;
+        // res += attn; ffn_norm; encode for the FFN
+        ResNormArgs f{};
+        f.mode = RN_ADD; f.src = ctx->wo_out; f.res = ctx->res; f.norm_w = ly.ffn_norm; f.cur_out = ctx->cur;
+        f.act = ctx->act; f.act_fmt = act_of(ly.moe ? ly.up_exps.type : ly.ffn_up.type);
+        if ((rc = launch_resnorm(ctx, T, f))) return rc;
+        if ((rc = cap_copy(ctx, Z2H_CAP_FFN_IN, L, ctx->cur, T))) return rc;
+        if (ly.moe) {
+            const float * st = prev_moe >= 0 ? ctx->state + (size_t) prev_moe * ctx->Tmax * ctx->rd : nullptr;
+            if ((rc = expert_block(ctx, ly, L, T, st))) return rc;
+            prev_moe = L;
+        } else if ((rc = dense_block(ctx, ly, T))) return rc;
+        // fold the FFN output into the residual; next layer's attn_norm (or output_norm)
+        ResNormArgs n{};
+        n.mode = RN_ACCUM; n.src = ctx->eo; n.k = ly.moe ? ly.k : 1; n.res = ctx->res;
+        n.cap_x = (float *) capp(ctx, Z2H_CAP_FFN_OUT, L);
+        const bool last = L + 1 == hp.n_layer;
+        n.norm_w = last ? ctx->output_norm : ctx->layers[L + 1].attn_norm;
+        n.cur_out = last ? (float *) capp(ctx, Z2H_CAP_OUT_NORM, 0) : (float *) capp(ctx, Z2H_CAP_ATTN_IN, L + 1);
+        n.act = ctx->act; n.act_fmt = act_of(last ? ctx->head.type : ctx->layers[L + 1].qkvg.type);
+        if ((rc = launch_resnorm(ctx, T, n))) return rc;
+        if (!last && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, L + 1, ctx->res, T))) return rc;
+    }
+    // output head + softcap
+    const int nout = hp.n_codebooks * hp.audio_vocab;
+    return launch_gemv(ctx, ctx->head, nullptr, gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE),
+                       ST_ACT, (T + NT - 1) / NT);
+}
+
+int check_err_flag(z2h_ctx * ctx) {
+    int h = 0;
+    HIPX(hipMemcpy(&h, ctx->d_err, 4, hipMemcpyDeviceToHost));
+    if (h) {
+        HIPX(hipMemset(ctx->d_err, 0, 4));
+        return seterr(ctx, Z2H_EINVAL, "token id out of range");
+    }
+    return Z2H_OK;
+}
+
+int validate_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_past) {
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
+    for (int t = 0; t < T; ++t) {
+        if (slot_idx && (slot_idx[t] < 0 || slot_idx[t] >= ctx->n_slots)) return seterr(ctx, Z2H_EINVAL, "slot index out of range");
+        if (n_past[t] < 0 || n_past[t] >= ctx->S) return seterr(ctx, Z2H_EINVAL, "n_past out of range (slot full)");
+        if (slot_idx) for (int u = 0; u < t; ++u) if (slot_idx[u] == slot_idx[t]) return seterr(ctx, Z2H_EINVAL, "duplicate slot in step");
+    }
+    return Z2H_OK;
+}
+
+} // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int device, z2h_ctx ** out) {
+    if (!out) return Z2H_EINVAL;
+    *out = nullptr;
+    if (!hp || !hp->expert_used || hp->n_layer <= 0 || n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
+    if (hp->n_head <= 0 || hp->n_head_kv <= 0 || hp->n_head % hp->n_head_kv || hp->head_dim % 8 || hp->head_dim > 256)
+        return Z2H_EINVAL;
+    if (hp->n_codebooks + 1 > MAX_TABLES) return Z2H_ENOTSUP;
+    auto ctx = std::make_unique<z2h_ctx>();
+    ctx->hp = *hp;
+    ctx->expert_used.assign(hp->expert_used, hp->expert_used + hp->n_layer);
+    ctx->hp.expert_used = ctx->expert_used.data();
+    ctx->device = device; ctx->n_slots = n_slots;
+    ctx->S = ((slot_cap_frames + 255) / 256) * 256;
+    ctx->W = hp->n_codebooks + 1;
+    ctx->rd = hp->router_dim;
+    for (int L = 0; L < hp->n_layer; ++L) ctx->kmax = std::max(ctx->kmax, hp->expert_used[L]);
+    z2h_ctx * c = ctx.get();
+    if (hipSetDevice(device) != hipSuccess) return Z2H_EDEVICE;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return Z2H_EDEVICE;
+    const size_t kv_elems = (size_t) hp->n_layer * 2 * n_slots * hp->n_head_kv * c->S * hp->head_dim;
+    if (dalloc(c, &c->kv, kv_elems * 2, c->bytes_kv)) { (void) hipStreamDestroy(c->stream); return Z2H_ENOMEM; }
+    if (hipMemset(c->kv, 0, kv_elems * 2) != hipSuccess) return Z2H_EDEVICE;
+    c->layers.resize(hp->n_layer);
+    c->tab.assign(c->W, nullptr); c->tab_type.assign(c->W, -1); c->tab_rows.assign(c->W, 0);
+    *out = ctx.release();
+    return Z2H_OK;
+}
+
+int z2h_slot_cap(const z2h_ctx * ctx) { return ctx ? ctx->S : 0; }
+
+int z2h_upload_tensor(z2h_ctx * ctx, const char * name_c, int type, const int64_t ne_in[4], const void * data, size_t nbytes) {
+    if (!ctx || !name_c || !ne_in || !data) return Z2H_EINVAL;
+    if (ctx->finalized) return seterr(ctx, Z2H_ESTATE, "context already finalized");
+    if (!z2::type_known(type)) return seterr(ctx, Z2H_ENOTSUP, std::string("unsupported tensor type for ") + name_c);
+    HostTensor t; t.type = type;
+    for (int i = 0; i < 4; ++i) t.ne[i] = ne_in[i] > 0 ? ne_in[i] : 1;
+    if (t.ne[0] % z2::type_block(type)) return seterr(ctx, Z2H_EINVAL, std::string("row not block aligned: ") + name_c);
+    const int64_t expect = z2::row_bytes(type, t.ne[0]) * t.ne[1] * t.ne[2] * t.ne[3];
+    if ((int64_t) nbytes != expect) return seterr(ctx, Z2H_EINVAL, std::string("byte size mismatch for ") + name_c);
+    if (hipSetDevice(ctx->device) != hipSuccess) return Z2H_EDEVICE;
+    const std::string name(name_c);
+    const auto & hp = ctx->hp;
+    const uint8_t * src = (const uint8_t *) data;
+    auto copy_host = [&]() { t.bytes.assign(src, src + nbytes); };
+    ctx->seen[name] = true;
+    int L; std::string rest;
+    if (parse_layer(name, L, rest)) {
+        if (L < 0 || L >= hp.n_layer) return seterr(ctx, Z2H_EINVAL, "layer index out of range: " + name);
+        Layer & ly = ctx->layers[L];
+        if (rest == "attn_q.weight" || rest == "attn_k.weight" || rest == "attn_v.weight" || rest == "attn_gate.weight") {
+            copy_host();
+            ly.stash[rest] = std::move(t);
+            return fuse_qkvg(ctx, ly);
+        }
+        if (rest == "attn_output.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.wo);
+        if (rest == "ffn_up.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_up);
+        if (rest == "ffn_gate.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_gate);
+        if (rest == "ffn_down.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_down);
+        if (rest == "ffn_gate_exps.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps);
+        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps); }
+        if (rest == "ffn_down_exps.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps);
+        copy_host();
+        if (rest == "attn_norm.weight") return upload_f32(ctx, t, &ly.attn_norm, hp.n_embd);
+        if (rest == "ffn_norm.weight") return upload_f32(ctx, t, &ly.ffn_norm, hp.n_embd);
+        if (rest == "attn_temp") return upload_f32(ctx, t, &ly.attn_temp, hp.n_head);
+        if (rest == "router_down.weight") {
+            if (t.ne[1] != ctx->rd) return seterr(ctx, Z2H_EINVAL, "router_dim mismatch: " + name);
+            return upload_f32(ctx, t, &ly.r_down, -1);
+        }
+        if (rest == "router_down.bias") return upload_f32(ctx, t, &ly.r_down_b, ctx->rd);
+        if (rest == "router_mlp0.weight") return upload_f32_transposed(ctx, t, &ly.r_m0t);
+        if (rest == "router_mlp0.bias") return upload_f32(ctx, t, &ly.r_m0_b, ctx->rd);
+        if (rest == "router_mlp2.weight") return upload_f32_transposed(ctx, t, &ly.r_m2t);
+        if (rest == "router_mlp2.bias") return upload_f32(ctx, t, &ly.r_m2_b, ctx->rd);
+        if (rest == "router_mlp4.weight") return upload_f32_transposed(ctx, t, &ly.r_m4t);
+        if (rest == "router_norm.weight") return upload_f32(ctx, t, &ly.r_norm, ctx->rd);
+        if (rest == "router_bias") return upload_f32(ctx, t, &ly.r_bias, -1);
+        if (rest == "router_eda_scale") return upload_f32(ctx, t, &ly.r_eda, ctx->rd);
+        return seterr(ctx, Z2H_EINVAL, "unknown tensor " + name);
+    }
+    if (name.rfind("audio_embd.", 0) == 0 || name == "text_embd.weight") {
+        const int k = name == "text_embd.weight" ? hp.n_codebooks : std::atoi(name.c_str() + 11);
+        if (k < 0 || k > hp.n_codebooks || t.ne[0] != hp.n_embd) return seterr(ctx, Z2H_EINVAL, "bad embedding table " + name);
+        if (type != Z2H_F32 && type != Z2H_F16 && type != Z2H_Q8_0 && type != Z2H_Q4_K && type != Z2H_Q6_K)
+            return seterr(ctx, Z2H_ENOTSUP, "embedding type");
+        uint8_t * p = nullptr;
+        if (int rc = dalloc(ctx, &p, nbytes, ctx->bytes_w)) return rc;
+        HIPX(hipMemcpy(p, data, nbytes, hipMemcpyHostToDevice));
+        ctx->tab[k] = p; ctx->tab_type[k] = type; ctx->tab_rows[k] = t.ne[1];
+        return Z2H_OK;
+    }
+    if (name == "output.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->head);
+    if (name == "spk_lda.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->spk_lda);
+    if (name == "spk_proj.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->spk_proj);
+    copy_host();
+    if (name == "output_norm.weight") return upload_f32(ctx, t, &ctx->output_norm, hp.n_embd);
+    if (name == "spk_lda.bias") return upload_f32(ctx, t, &ctx->spk_lda_b, -1);
+    if (name == "spk_proj.bias") return upload_f32(ctx, t, &ctx->spk_proj_b, hp.n_embd);
+    return seterr(ctx, Z2H_EINVAL, "unknown tensor " + name);
+}
+
+int z2h_finalize(z2h_ctx * ctx) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->finalized) return Z2H_OK;
+    const auto & hp = ctx->hp;
+    std::string missing;
+    for (int k = 0; k < ctx->W; ++k) if (!ctx->tab[k]) missing += (k < hp.n_codebooks ? "audio_embd." + std::to_string(k) : std::string("text_embd")) + " ";
+    if (!ctx->head.ok()) missing += "output.weight ";
+    if (!ctx->output_norm) missing += "output_norm.weight ";
+    for (int L = 0; L < hp.n_layer; ++L) {
+        Layer & ly = ctx->layers[L];
+        const std::string b = "blk." + std::to_string(L) + ".";
+        ly.k = hp.expert_used[L]; ly.moe = ly.k > 0;
+        if (!ly.qkvg.ok()) missing += b + "attn_{q,k,v,gate} ";
+        if (!ly.wo.ok()) missing += b + "attn_output ";
+        if (!ly.attn_norm) missing += b + "attn_norm ";
+        if (!ly.ffn_norm) missing += b + "ffn_norm ";
+        if (!ly.attn_temp) missing += b + "attn_temp ";
+        if (ly.moe) {
+            if (!ly.gate_exps.ok() || !ly.up_exps.ok() || !ly.down_exps.ok()) missing += b + "ffn_*_exps ";
+            if (!ly.r_down || !ly.r_down_b || !ly.r_m0t || !ly.r_m0_b || !ly.r_m2t || !ly.r_m2_b || !ly.r_m4t || !ly.r_norm || !ly.r_bias)
+                missing += b + "router_* ";
+            if (ly.up_exps.ok() && ly.k > ly.E) return seterr(ctx, Z2H_EINVAL, b + "top-k exceeds the expert count");
+            if (ly.up_exps.ok() && ly.E > 256) return seterr(ctx, Z2H_ENOTSUP, "more than 256 experts");
+            if (ly.up_exps.ok() && (ly.up_exps.rows != hp.n_ff || ly.down_exps.K != hp.n_ff)) return seterr(ctx, Z2H_EINVAL, b + "expert shape mismatch");
+        } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
+    }
+    if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
+    if (ctx->rd > 512) return seterr(ctx, Z2H_ENOTSUP, "router_dim > 512");
+    if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
+    if (int rc = alloc_scratch(ctx)) return rc;
+    HIPX(hipMemset(ctx->d_err, 0, 16));
+    // allow the GEMV kernels the full 160 KiB of gfx950 LDS for their dynamic carve-up
+    const int lds_max = 160 * 1024 - 8 * 1024;
+#define LDS_ATTR(WF_) \
+    (void) hipFuncSetAttribute((const void *) &k_gemv<WF_, ST_ACT>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max); \
+    (void) hipFuncSetAttribute((const void *) &k_gemv<WF_, ST_SWIGLU>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
+    LDS_ATTR(WF_Q4_K) LDS_ATTR(WF_Q6_K) LDS_ATTR(WF_Q8_0) LDS_ATTR(WF_F16)
+#undef LDS_ATTR
+    ctx->finalized = true;
+    return Z2H_OK;
+}
+
+int z2h_kv_write(z2h_ctx * ctx, int layer, int slot, int row0, int n, const uint16_t * k, const uint16_t * v) {
+    if (!ctx) return Z2H_EINVAL;
+    const auto & hp = ctx->hp;
+    if (layer < 0 || layer >= hp.n_layer || slot < 0 || slot >= ctx->n_slots || row0 < 0 || n < 0 || row0 + n > ctx->S)
+        return seterr(ctx, Z2H_EINVAL, "kv_write out of range");
+    if (n == 0) return Z2H_OK;
+    const int nkv = hp.n_head_kv, hd = hp.head_dim;
+    const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
+    for (int which = 0; which < 2; ++which) {
+        const uint16_t * src = which ? v : k;
+        if (!src) continue;
+        uint16_t * base = ctx->kv + (size_t) (2 * layer + which) * lsz;
+        for (int g = 0; g < nkv; ++g)
+            HIPX(hipMemcpy2D(base + (((size_t) slot * nkv + g) * ctx->S + row0) * hd, (size_t) hd * 2,
+                             src + (size_t) g * hd, (size_t) nkv * hd * 2, (size_t) hd * 2, n, hipMemcpyHostToDevice));
+    }
+    return Z2H_OK;
+}
+
+int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n, uint16_t * k, uint16_t * v) {
+    if (!ctx) return Z2H_EINVAL;
+    const auto & hp = ctx->hp;
+    if (layer < 0 || layer >= hp.n_layer || slot < 0 || slot >= ctx->n_slots || row0 < 0 || n < 0 || row0 + n > ctx->S)
+        return seterr(ctx, Z2H_EINVAL, "kv_read out of range");
+    if (n == 0) return Z2H_OK;
+    HIPX(hipStreamSynchronize(ctx->stream));
+    const int nkv = hp.n_head_kv, hd = hp.head_dim;
+    const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
+    for (int which = 0; which < 2; ++which) {
+        uint16_t * dst = which ? v : k;
+        if (!dst) continue;
+        const uint16_t * base = ctx->kv + (size_t) (2 * layer + which) * lsz;
+        for (int g = 0; g < nkv; ++g)
+            HIPX(hipMemcpy2D(dst + (size_t) g * hd, (size_t) nkv * hd * 2, base + (((size_t) slot * nkv + g) * ctx->S + row0) * hd,
+                             (size_t) hd * 2, (size_t) hd * 2, n, hipMemcpyDeviceToHost));
+    }
+    return Z2H_OK;
+}
+
+int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
+             const float * emb, float * out_logits) {
+    if (!ctx || !slot_idx || !n_past || (!ids && !emb) || !out_logits) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (int rc = validate_step(ctx, T, slot_idx, n_past)) return rc;
+    if (ids) {
+        for (int t = 0; t < T; ++t)
+            for (int k = 0; k < ctx->W; ++k) {
+                const int id = ids[(size_t) t * ctx->W + k];
+                if (id < 0 || id >= ctx->tab_rows[k]) return seterr(ctx, Z2H_EINVAL, "token id out of range");
+            }
+    }
+    HIPX(hipSetDevice(ctx->device));
+    int32_t * hp_ = ctx->h_pin;
+    std::memcpy(hp_, slot_idx, (size_t) T * 4);
+    std::memcpy(hp_ + T, n_past, (size_t) T * 4);
+    if (ids) std::memcpy(hp_ + 2 * T, ids, (size_t) T * ctx->W * 4);
+    HIPX(hipMemcpyAsync(ctx->d_slot, hp_, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + T, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (ids) HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * ctx->W * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (emb) HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int rc = run_step(ctx, T, n_past, ctx->d_slot, ctx->d_npast, ids ? ctx->d_ids : nullptr, emb ? ctx->d_emb : nullptr, ctx->logits)) return rc;
+    const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
+    HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipStreamSynchronize(ctx->stream));
+    return check_err_flag(ctx);
+}
+
+int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t * d_npast, const int32_t * h_npast,
+                    const int32_t * d_ids, const float * d_emb, float * d_logits, void * stream) {
+    if (!ctx || !d_slot || !d_npast || !h_npast || (!d_ids && !d_emb) || !d_logits) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (int rc = validate_step(ctx, T, nullptr, h_npast)) return rc;
+    hipStream_t keep = ctx->stream;
+    if (stream) ctx->stream = (hipStream_t) stream;
+    const int rc = run_step(ctx, T, h_npast, d_slot, d_npast, d_ids, d_emb, d_logits);
+    ctx->stream = keep;
+    return rc;
+}
+
+int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
+                const float * delta, float * last_logits) {
+    if (!ctx || !ids || !last_logits) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (slot < 0 || slot >= ctx->n_slots) return seterr(ctx, Z2H_EINVAL, "slot out of range");
+    if (n0 <= 0 || n0 > ctx->S) return seterr(ctx, Z2H_EINVAL, "prefill n0 exceeds slot_cap");
+    if (spk) return seterr(ctx, Z2H_ENOTSUP, "speaker injection in prefill is not implemented on the device yet");
+    (void) spk_pos; (void) delta;
+    // causal prefill as n0 single-row decode steps over the empty band: row t attends rows [0, t]
+    std::vector<float> lg((size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab);
+    for (int t = 0; t < n0; ++t) {
+        const int32_t si = slot, np = t;
+        if (int rc = z2h_step(ctx, 1, &si, &np, ids + (size_t) t * ctx->W, nullptr, t + 1 == n0 ? last_logits : lg.data())) return rc;
+    }
+    return Z2H_OK;
+}
+
+int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int T, const float * d_x, const float * d_state_in, float * d_out, void * stream) {
+    if (!ctx || !d_x || !d_out) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].moe) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
+    if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_tokens out of range");
+    hipStream_t keep = ctx->stream;
+    if (stream) ctx->stream = (hipStream_t) stream;
+    ctx->cap_T = T;
+    Layer & ly = ctx->layers[layer];
+    int rc;
+    HIPX(hipMemcpyAsync(ctx->cur, d_x, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    ResNormArgs e{};
+    e.mode = RN_ENCODE; e.src = ctx->cur; e.act = ctx->act; e.act_fmt = act_of(ly.up_exps.type);
+    if ((rc = launch_resnorm(ctx, T, e))) { ctx->stream = keep; return rc; }
+    if ((rc = expert_block(ctx, ly, layer, T, d_state_in))) { ctx->stream = keep; return rc; }
+    ResNormArgs n{};
+    n.mode = RN_ACCUM; n.src = ctx->eo; n.k = ly.k; n.res = nullptr; n.cap_x = d_out; n.act_fmt = ACT_NONE;
+    rc = launch_resnorm(ctx, T, n);
+    if (!rc) rc = cap_copy(ctx, Z2H_CAP_FFN_OUT, layer, d_out, T);
+    ctx->stream = keep;
+    return rc;
+}
+
+int z2h_moe_forward(z2h_ctx * ctx, int layer, int T, const float * x, const float * state_in, float * out) {
+    if (!ctx || !x || !out) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_tokens out of range");
+    HIPX(hipSetDevice(ctx->device));
+    HIPX(hipMemcpyAsync(ctx->tmp_x, x, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (state_in) HIPX(hipMemcpyAsync(ctx->state_ext, state_in, (size_t) T * ctx->rd * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int rc = z2h_moe_forward_device(ctx, layer, T, ctx->tmp_x, state_in ? ctx->state_ext : nullptr, ctx->wo_out, nullptr)) return rc;
+    HIPX(hipMemcpyAsync(out, ctx->wo_out, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipStreamSynchronize(ctx->stream));
+    return Z2H_OK;
+}
+
+int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep) {
+    if (!ctx) return Z2H_EINVAL;
+    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].up_exps.ok()) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
+    Layer & ly = ctx->layers[layer];
+    if (!keep) { ly.mask = nullptr; return Z2H_OK; }
+    std::vector<float> m(ly.E);
+    for (int e = 0; e < ly.E; ++e) m[e] = keep[e] ? 0.0f : -INFINITY;
+    if (!ly.mask_buf) if (int rc = dalloc(ctx, &ly.mask_buf, (size_t) ly.E * 4, ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(ly.mask_buf, m.data(), m.size() * 4, hipMemcpyHostToDevice));
+    ly.mask = ly.mask_buf;
+    return Z2H_OK;
+}
+
+int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias) {
+    if (!ctx) return Z2H_EINVAL;
+    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].up_exps.ok()) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
+    Layer & ly = ctx->layers[layer];
+    if (!bias) { ly.logit_bias = nullptr; return Z2H_OK; }
+    if (!ly.bias_buf) if (int rc = dalloc(ctx, &ly.bias_buf, (size_t) ly.E * 4, ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(ly.bias_buf, bias, (size_t) ly.E * 4, hipMemcpyHostToDevice));
+    ly.logit_bias = ly.bias_buf;
+    return Z2H_OK;
+}
+
+int z2h_set_capture(z2h_ctx * ctx, int enable) {
+    if (!ctx) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (enable && ctx->cap.empty()) {
+        ctx->cap.assign(Z2H_CAP_COUNT_, nullptr);
+        for (int w = 0; w < Z2H_CAP_COUNT_; ++w) {
+            const size_t n = (size_t) cap_width(ctx, w, ctx->Tmax) * 4 * ctx->hp.n_layer;
+            if (int rc = dalloc(ctx, &ctx->cap[w], n, ctx->bytes_scratch)) return rc;
+            HIPX(hipMemset(ctx->cap[w], 0, n));
+        }
+    }
+    ctx->capture = enable != 0;
+    return Z2H_OK;
+}
+
+int64_t z2h_capture_bytes(z2h_ctx * ctx, int what, int n_tokens) {
+    if (!ctx || what < 0 || what >= Z2H_CAP_COUNT_) return -1;
+    return cap_width(ctx, what, n_tokens) * 4;
+}
+
+int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nbytes) {
+    if (!ctx || !host) return Z2H_EINVAL;
+    if (ctx->cap.empty()) return seterr(ctx, Z2H_ESTATE, "capture was never enabled");
+    if (what < 0 || what >= Z2H_CAP_COUNT_ || layer < 0 || layer >= ctx->hp.n_layer) return seterr(ctx, Z2H_EINVAL, "bad capture id");
+    const size_t n = (size_t) cap_width(ctx, what, ctx->cap_T) * 4;
+    if (nbytes < n) return seterr(ctx, Z2H_EINVAL, "capture buffer too small");
+    HIPX(hipStreamSynchronize(ctx->stream));
+    const int L = what == Z2H_CAP_OUT_NORM ? 0 : layer;
+    HIPX(hipMemcpy(host, ctx->cap[what] + (size_t) L * cap_width(ctx, what, ctx->Tmax) * 4, n, hipMemcpyDeviceToHost));
+    return Z2H_OK;
+}
+
+int64_t z2h_device_bytes(const z2h_ctx * ctx, int what) {
+    if (!ctx) return -1;
+    return what == 0 ? ctx->bytes_w : what == 1 ? ctx->bytes_kv : ctx->bytes_scratch;
+}
+
+const char * z2h_last_error(const z2h_ctx * ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+void z2h_destroy(z2h_ctx * ctx) {
+    if (!ctx) return;
+    (void) hipSetDevice(ctx->device);
+    if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    for (void * p : ctx->allocs) (void) hipFree(p);
+    if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);
+    if (ctx->stream) (void) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+} // extern "C"

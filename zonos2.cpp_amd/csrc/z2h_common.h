@@ -1,0 +1,94 @@
+// z2h_common.h — device-side helpers shared by the decode-step kernels (gfx950, wave64).
+//
+// The exp / erf / GELU / SiLU implementations and the xor-butterfly reductions are part of the
+// router's bit-exact contract (the CPU oracle restates them operation for operation): every source
+// file is compiled with -ffp-contract=off, and fused multiply-adds are only the explicit fmaf calls.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace z2d {
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// exp: Cody-Waite reduction by ln2 (high part exact in the fma) + degree-7 Taylor polynomial.
+__device__ __forceinline__ float z_expf(float x) {
+    if (x > 88.72283f) return __builtin_inff();
+    if (x < -103.97208f) return 0.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    r = __builtin_fmaf(n, -1.428606765330187e-06f, r);
+    float p = 1.98412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return ldexpf(p, (int) n);
+}
+
+// erf: Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7).
+__device__ __forceinline__ float z_erff(float x) {
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+    p = __builtin_fmaf(p, t, 1.421413741f);
+    p = __builtin_fmaf(p, t, -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.254829592f);
+    p = p * t;
+    const float y = 1.0f - p * z_expf(-(ax * ax));
+    return copysignf(y, x);
+}
+
+__device__ __forceinline__ float z_gelu(float x) { return (0.5f * x) * (1.0f + z_erff(x * 0.70710678118654752f)); }
+__device__ __forceinline__ float z_silu(float x) { return x / (1.0f + z_expf(-x)); }
+__device__ __forceinline__ float z_sigmoid(float x) { return 1.0f / (1.0f + z_expf(-x)); }
+
+// xor butterfly over the 64 lanes; every lane ends with the same value.
+__device__ __forceinline__ float wave_tree_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, WAVE);
+    return v;
+}
+__device__ __forceinline__ double wave_tree_d(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
+    half2_t ha, hb;
+    __builtin_memcpy(&ha, &a, 4);
+    __builtin_memcpy(&hb, &b, 4);
+    return __builtin_amdgcn_fdot2(ha, hb, c, false);
+}
+
+// Q4_K 6-bit scale / min of sub-block j from the 12 packed bytes (GGUF K-quant layout).
+__device__ __forceinline__ void q4k_sm(const uint8_t * sc, int j, int & s, int & m) {
+    if (j < 4) { s = sc[j] & 63; m = sc[j + 4] & 63; }
+    else {
+        s = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+        m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+}
+
+} // namespace z2d

@@ -1,0 +1,191 @@
+"""Synthetic model / workload configurations of the decode-step benchmarks.
+
+Tensor names and shapes follow the reference's GGUF layout (src/zonos2.cpp:137-183,
+scripts/make-dummy-model.py:95-136); ne is ggml order (ne0 fastest). Per-tensor storage types follow
+the reference's quantize policy (src/quantize.cpp:49-131, pick_qtype non-experts-only mode): 1-D
+tensors F32; the high-precision set (output head, text/audio embeddings, speaker projections) one
+tier above the bulk type (F16 over Q8_0, Q8_0 over K-quants); every other matrix the bulk type. The
+routers are kept F32 because the decode step's router is specified as fp32.
+
+Init: matrices N(0, 0.02); norm weights 1; attn_temp |N(0,1)| (the checkpoint stores |temp|,
+models/convert-zonos2-to-gguf.py:207); router_bias N(0, 1e-3); other 1-D biases N(0, 0.02).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+TYPE_NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def row_bytes(t: int, n: int) -> int:
+    be, bb = BLOCK[t]
+    assert n % be == 0, (t, n)
+    return n // be * bb
+
+
+@dataclass
+class ModelConfig:
+    name: str
+    n_layer: int
+    n_embd: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    n_expert: int
+    top_k: int
+    n_ff: int
+    bulk: int
+    router_dim: int = 128
+    n_codebooks: int = 9
+    audio_vocab: int = 1025
+    text_vocab: int = 519
+    spk_dim: int = 64
+    spk_lda_dim: int = 32
+    n_ctx_train: int = 4096
+    rope_freq_base: float = 10000.0
+    rms_eps: float = 1e-5
+    qk_norm_eps: float = 1e-6
+    logit_softcap: float = 15.0
+    expert_used: list[int] | None = None     # per layer; default all MoE with top_k
+
+    def __post_init__(self):
+        if self.expert_used is None:
+            self.expert_used = [self.top_k] * self.n_layer
+
+    @property
+    def codebook_size(self) -> int:
+        return self.audio_vocab - 2
+
+    def hparams(self) -> dict:
+        return dict(
+            n_layer=self.n_layer, n_embd=self.n_embd, head_dim=self.head_dim, n_head=self.n_head,
+            n_head_kv=self.n_head_kv, n_ff=self.n_ff, n_expert=self.n_expert,
+            n_ctx_train=self.n_ctx_train, rope_freq_base=self.rope_freq_base, rms_eps=self.rms_eps,
+            qk_norm_eps=self.qk_norm_eps, logit_softcap=self.logit_softcap,
+            n_codebooks=self.n_codebooks, codebook_size=self.codebook_size,
+            audio_vocab=self.audio_vocab, eoa_id=self.codebook_size, audio_pad_id=self.codebook_size + 1,
+            text_vocab=self.text_vocab, spk_dim=self.spk_dim, spk_lda_dim=self.spk_lda_dim,
+            router_dim=self.router_dim if any(self.expert_used) else 0,
+            expert_used=list(self.expert_used))
+
+    def high_tier(self) -> int:
+        if self.bulk in (Q8_0, F16):
+            return F16
+        return Q8_0
+
+    def tensors(self) -> list[tuple[str, int, tuple[int, ...], tuple]]:
+        """[(name, type, ne, init)] with init = (kind, a, b): 0 normal(a,b), 1 b*|N(0,1)|, 2 const a."""
+        d, hd, nh, nkv, ff, rd = self.n_embd, self.head_dim, self.n_head, self.n_head_kv, self.n_ff, self.router_dim
+        W, hi = (0, 0.0, 0.02), self.high_tier()
+        out: list = []
+        for i in range(self.n_codebooks):
+            out.append((f"audio_embd.{i}.weight", hi, (d, self.audio_vocab), W))
+        out.append(("text_embd.weight", hi, (d, self.text_vocab + 1), W))
+        out.append(("spk_lda.weight", hi, (self.spk_dim, self.spk_lda_dim), W))
+        out.append(("spk_lda.bias", F32, (self.spk_lda_dim,), W))
+        out.append(("spk_proj.weight", hi, (self.spk_lda_dim, d), W))
+        out.append(("spk_proj.bias", F32, (d,), W))
+        out.append(("output_norm.weight", F32, (d,), (2, 1.0, 0.0)))
+        out.append(("output.weight", hi, (d, self.n_codebooks * self.audio_vocab), W))
+        seen_moe = False
+        for L in range(self.n_layer):
+            b = f"blk.{L}."
+            bt = self.bulk
+            out += [
+                (b + "attn_norm.weight", F32, (d,), (2, 1.0, 0.0)),
+                (b + "ffn_norm.weight", F32, (d,), (2, 1.0, 0.0)),
+                (b + "attn_q.weight", bt, (d, nh * hd), W),
+                (b + "attn_k.weight", bt, (d, nkv * hd), W),
+                (b + "attn_v.weight", bt, (d, nkv * hd), W),
+                (b + "attn_output.weight", bt, (nh * hd, d), W),
+                (b + "attn_temp", F32, (nh,), (1, 0.0, 1.0)),
+                (b + "attn_gate.weight", bt, (d, nh), W),
+            ]
+            if self.expert_used[L] == 0:
+                out += [
+                    (b + "ffn_up.weight", bt, (d, ff), W),
+                    (b + "ffn_gate.weight", bt, (d, ff), W),
+                    (b + "ffn_down.weight", bt, (ff, d), W),
+                ]
+                continue
+            E = self.n_expert
+            out += [
+                (b + "ffn_gate_exps.weight", bt, (d, ff, E), W),
+                (b + "ffn_up_exps.weight", bt, (d, ff, E), W),
+                (b + "ffn_down_exps.weight", bt, (ff, d, E), W),
+                (b + "router_down.weight", F32, (d, rd), W),
+                (b + "router_down.bias", F32, (rd,), W),
+                (b + "router_mlp0.weight", F32, (rd, rd), W),
+                (b + "router_mlp0.bias", F32, (rd,), W),
+                (b + "router_mlp2.weight", F32, (rd, rd), W),
+                (b + "router_mlp2.bias", F32, (rd,), W),
+                (b + "router_mlp4.weight", F32, (rd, E), W),
+                (b + "router_norm.weight", F32, (rd,), (2, 1.0, 0.0)),
+                (b + "router_bias", F32, (E,), (0, 0.0, 1e-3)),
+            ]
+            if seen_moe:
+                out.append((b + "router_eda_scale", F32, (rd,), W))
+            seen_moe = True
+        return out
+
+
+@dataclass
+class Workload:
+    name: str
+    n_slots: int
+    kv_lens: list[int]                  # n_past per active request (rows already in the cache)
+    slot_cap: int                       # frames per slot (rounded up to 256 by the runtime)
+    inject_embeddings: bool = False     # feed N(0,1) embeddings instead of token ids
+    zipf: float | None = None           # pre-softmax Zipf(s) expert-popularity bias
+    seed: int = 1234
+    extra: dict = field(default_factory=dict)
+
+
+def C1() -> tuple[ModelConfig, Workload]:
+    m = ModelConfig("tiny-moe-q8_0", n_layer=2, n_embd=256, n_head=8, n_head_kv=2, head_dim=32,
+                    n_expert=8, top_k=2, n_ff=512, bulk=Q8_0)
+    w = Workload("c1-4req", n_slots=4, kv_lens=[3, 17, 64, 130], slot_cap=131, inject_embeddings=True)
+    return m, w
+
+
+def C2() -> tuple[ModelConfig, Workload]:
+    m = ModelConfig("moe-layer-q4_k", n_layer=1, n_embd=2048, n_head=16, n_head_kv=4, head_dim=128,
+                    n_expert=32, top_k=4, n_ff=1536, bulk=Q4_K, spk_dim=2048, spk_lda_dim=1024)
+    w = Workload("c2-16tok", n_slots=16, kv_lens=[0] * 16, slot_cap=256, inject_embeddings=True)
+    return m, w
+
+
+def zonos2_24l(bulk: int) -> ModelConfig:
+    return ModelConfig(f"zonos2-24l-{TYPE_NAMES[bulk].lower()}", n_layer=24, n_embd=2048, n_head=16,
+                       n_head_kv=4, head_dim=128, n_expert=32, top_k=4, n_ff=1536, bulk=bulk,
+                       spk_dim=2048, spk_lda_dim=1024)
+
+
+def _rng(seed):
+    import numpy as np
+    return np.random.default_rng(seed)
+
+
+def C3() -> tuple[ModelConfig, Workload]:
+    rng = _rng(3)
+    lens = [int(x) for x in rng.integers(32, 2049, size=16)]
+    return zonos2_24l(Q4_K), Workload("c3-16req-ragged", n_slots=16, kv_lens=lens, slot_cap=2049)
+
+
+def C4(bulk: int) -> tuple[ModelConfig, Workload]:
+    import numpy as np
+    rng = _rng(4)
+    lens = [int(x) for x in np.exp(rng.uniform(np.log(16), np.log(4096), size=64))]
+    return zonos2_24l(bulk), Workload("c4-64req-zipf", n_slots=64, kv_lens=lens, slot_cap=4097, zipf=1.2)
+
+
+def zipf_bias(n_expert: int, s: float, layer: int, seed: int = 99):
+    """Additive log-popularity bias log(p_e) for p_e ~ 1/rank^s, rank permuted per layer."""
+    import numpy as np
+    rng = np.random.default_rng(seed + layer)
+    ranks = rng.permutation(n_expert) + 1
+    p = 1.0 / ranks.astype(np.float64) ** s
+    p /= p.sum()
+    return np.log(p).astype(np.float32)

@@ -1,0 +1,165 @@
+"""ctypes binding of include/z2h.h (libzonos2_hip.so). Loading fails loudly when the library is not
+built; there is no fallback path."""
+from __future__ import annotations
+
+import ctypes as C
+from functools import lru_cache
+
+import numpy as np
+
+from .lib import _load
+
+OK, EINVAL, ENOMEM, EDEVICE, ESTATE, ENOTSUP = range(6)
+CAP = {n: i for i, n in enumerate(
+    ("res_in", "attn_in", "q", "k", "v", "gate", "attn_o", "attn_out", "ffn_in", "router_state", "router_logits",
+     "probs", "sel", "weights", "ffn_out", "out_norm", "counts", "offsets", "perm", "expert_out"))}
+INT_CAPS = {"sel", "counts", "offsets", "perm"}
+
+
+class Hparams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_layer", "n_embd", "head_dim", "n_head", "n_head_kv", "n_ff",
+                                          "n_expert", "n_ctx_train")] + \
+               [(n, C.c_float) for n in ("rope_freq_base", "rms_eps", "qk_norm_eps", "logit_softcap")] + \
+               [(n, C.c_int32) for n in ("n_codebooks", "codebook_size", "audio_vocab", "eoa_id",
+                                          "audio_pad_id", "text_vocab", "spk_dim", "spk_lda_dim",
+                                          "router_dim")] + \
+               [("expert_used", C.POINTER(C.c_int32))]
+
+
+@lru_cache(None)
+def lib() -> C.CDLL:
+    L = _load("libzonos2_hip.so")
+    vp, i32, i64 = C.c_void_p, C.c_int, C.c_int64
+    sig = {
+        "z2h_create": (i32, [C.POINTER(Hparams), i32, i32, i32, C.POINTER(vp)]),
+        "z2h_upload_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_int64), vp, C.c_size_t]),
+        "z2h_finalize": (i32, [vp]),
+        "z2h_slot_cap": (i32, [vp]),
+        "z2h_kv_write": (i32, [vp, i32, i32, i32, i32, vp, vp]),
+        "z2h_kv_read": (i32, [vp, i32, i32, i32, i32, vp, vp]),
+        "z2h_step": (i32, [vp, i32, vp, vp, vp, vp, vp]),
+        "z2h_step_device": (i32, [vp, i32, vp, vp, vp, vp, vp, vp, vp]),
+        "z2h_prefill": (i32, [vp, i32, vp, i32, vp, i32, vp, vp]),
+        "z2h_moe_forward": (i32, [vp, i32, i32, vp, vp, vp]),
+        "z2h_moe_forward_device": (i32, [vp, i32, i32, vp, vp, vp, vp]),
+        "z2h_set_expert_mask": (i32, [vp, i32, vp]),
+        "z2h_set_logit_bias": (i32, [vp, i32, vp]),
+        "z2h_set_capture": (i32, [vp, i32]),
+        "z2h_capture_bytes": (i64, [vp, i32, i32]),
+        "z2h_read_capture": (i32, [vp, i32, i32, vp, C.c_size_t]),
+        "z2h_device_bytes": (i64, [vp, i32]),
+        "z2h_last_error": (C.c_char_p, [vp]),
+        "z2h_destroy": (None, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+    return L
+
+
+EXPORTS = ("z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
+           "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
+           "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
+           "z2h_read_capture", "z2h_device_bytes", "z2h_last_error", "z2h_destroy")
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Z2HError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"z2h error {code}: {msg}")
+        self.code = code
+
+
+class Context:
+    """One decode-step context on a device (mirrors zonos2_batch_ctx)."""
+
+    def __init__(self, hp: dict, n_slots: int, slot_cap: int, device: int = 0):
+        self.hp = dict(hp)
+        eu = (C.c_int32 * hp["n_layer"])(*hp["expert_used"])
+        h = Hparams(**{k: v for k, v in hp.items() if k != "expert_used"})
+        h.expert_used = C.cast(eu, C.POINTER(C.c_int32))
+        self._eu = eu
+        out = C.c_void_p()
+        rc = lib().z2h_create(C.byref(h), n_slots, slot_cap, device, C.byref(out))
+        if rc != OK:
+            raise Z2HError(rc, "z2h_create failed")
+        self.ctx = out
+        self.n_slots = n_slots
+        self.S = lib().z2h_slot_cap(self.ctx)
+        self.kmax = max([k for k in hp["expert_used"]] + [1])
+
+    def check(self, rc):
+        if rc != OK:
+            raise Z2HError(rc, lib().z2h_last_error(self.ctx).decode())
+
+    def upload(self, tensors: dict):
+        for t in tensors.values():
+            ne = (C.c_int64 * 4)(*t.ne4)
+            self.check(lib().z2h_upload_tensor(self.ctx, t.name.encode(), t.type, ne, _p(t.data), t.data.nbytes))
+        self.check(lib().z2h_finalize(self.ctx))
+
+    def kv_write(self, layer, slot, row0, k, v):
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        self.check(lib().z2h_kv_write(self.ctx, layer, slot, row0, k.shape[0], _p(k), _p(v)))
+
+    def kv_read(self, layer, slot, row0, n):
+        k = np.empty((n, self.hp["n_head_kv"], self.hp["head_dim"]), np.uint16)
+        v = np.empty_like(k)
+        self.check(lib().z2h_kv_read(self.ctx, layer, slot, row0, n, _p(k), _p(v)))
+        return k, v
+
+    def step(self, slot_idx, n_past, ids=None, emb=None):
+        si = np.ascontiguousarray(slot_idx, np.int32)
+        npast = np.ascontiguousarray(n_past, np.int32)
+        ids = None if ids is None else np.ascontiguousarray(ids, np.int32)
+        emb = None if emb is None else np.ascontiguousarray(emb, np.float32)
+        T = len(si)
+        out = np.empty((T, self.hp["n_codebooks"] * self.hp["audio_vocab"]), np.float32)
+        self.check(lib().z2h_step(self.ctx, T, _p(si), _p(npast), _p(ids), _p(emb), _p(out)))
+        return out
+
+    def prefill(self, slot, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.hp["n_codebooks"] * self.hp["audio_vocab"], np.float32)
+        self.check(lib().z2h_prefill(self.ctx, slot, _p(ids), ids.shape[0], None, -1, None, _p(out)))
+        return out
+
+    def moe_forward(self, layer, x, state_in=None):
+        x = np.ascontiguousarray(x, np.float32)
+        st = None if state_in is None else np.ascontiguousarray(state_in, np.float32)
+        out = np.empty_like(x)
+        self.check(lib().z2h_moe_forward(self.ctx, layer, x.shape[0], _p(x), _p(st), _p(out)))
+        return out
+
+    def set_logit_bias(self, layer, bias):
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.check(lib().z2h_set_logit_bias(self.ctx, layer, _p(b)))
+
+    def set_expert_mask(self, layer, keep):
+        k = None if keep is None else np.ascontiguousarray(keep, np.uint8)
+        self.check(lib().z2h_set_expert_mask(self.ctx, layer, _p(k)))
+
+    def set_capture(self, on: bool):
+        self.check(lib().z2h_set_capture(self.ctx, 1 if on else 0))
+
+    def read_capture(self, layer, what: str, n_tokens: int):
+        w = CAP[what]
+        nb = lib().z2h_capture_bytes(self.ctx, w, n_tokens)
+        out = np.empty(nb // 4, np.int32 if what in INT_CAPS else np.float32)
+        self.check(lib().z2h_read_capture(self.ctx, layer, w, _p(out), nb))
+        return out
+
+    def device_bytes(self, what: int) -> int:
+        return int(lib().z2h_device_bytes(self.ctx, what))
+
+    def close(self):
+        if getattr(self, "ctx", None):
+            lib().z2h_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        self.close()
