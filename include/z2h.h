@@ -121,6 +121,18 @@ int z2h_set_capture(z2h_ctx * ctx, int enable);
 int64_t z2h_capture_bytes(z2h_ctx * ctx, int what, int n_tokens);
 int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nbytes);
 
+/* Per-kernel-family timing with HIP events recorded around every launch on the context's stream
+ * (the reference's only equivalent is the ZONOS2_PROFILE_STEP phase split, src/zonos2-graph.cpp:768,
+ * 815-829). Between begin and end every launch is bracketed by an event pair; end synchronizes and
+ * writes the summed milliseconds and launch counts per family. Up to 16384 launches per window. */
+enum {
+    Z2H_KF_RESNORM = 0, Z2H_KF_GEMV_QKV, Z2H_KF_QKV_POST, Z2H_KF_ATTN, Z2H_KF_ATTN_COMBINE, Z2H_KF_GEMV_WO,
+    Z2H_KF_ROUTER_DOWN, Z2H_KF_ROUTER_TAIL, Z2H_KF_GEMV_GATEUP, Z2H_KF_GEMV_DOWN, Z2H_KF_GEMV_DENSE,
+    Z2H_KF_GEMV_HEAD, Z2H_KF_SWIGLU, Z2H_KF_COUNT_
+};
+int z2h_profile_begin(z2h_ctx * ctx);
+int z2h_profile_end(z2h_ctx * ctx, double * ms, int32_t * launches);
+
 /* Device memory held by weights, KV cache and scratch (bytes). */
 int64_t z2h_device_bytes(const z2h_ctx * ctx, int what /* 0 weights, 1 kv, 2 scratch */);
 

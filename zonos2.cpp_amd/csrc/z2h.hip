@@ -17,6 +17,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 using namespace z2d;
@@ -25,6 +26,7 @@ namespace {
 
 struct DevMat {
     int type = -1;
+    bool m16 = false;                 // 16-row MFMA layout (Q4_K, Q8_0) instead of 64-row tiles
     int rows = 0, K = 0, nsb = 0, tiles = 0, n_mats = 1;
     uint8_t * w = nullptr;            // tiled bytes
     uint16_t * dpl = nullptr;         // Q6_K d plane
@@ -84,7 +86,8 @@ struct z2h_ctx {
     float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * gate = nullptr, * wo_out = nullptr;
     uint16_t * q16 = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
-    ActBuf act{};
+    ActBuf act{}, act_y{};
+    float * attn_o = nullptr;         // [T][nh*hd] gated attention output
     float * state = nullptr;          // [L][T][rd]
     float * state_ext = nullptr;      // [T][rd] external state for moe_forward
     int32_t * sel = nullptr; float * wsel = nullptr;
@@ -92,6 +95,12 @@ struct z2h_ctx {
     int * d_err = nullptr;
     int32_t * h_pin = nullptr;        // pinned staging for step inputs
     size_t h_pin_bytes = 0;
+
+    // per-kernel event timing
+    bool prof = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<int> ev_fam;
+    int ev_used = 0;
 
     // capture
     bool capture = false;
@@ -102,6 +111,20 @@ struct z2h_ctx {
 namespace {
 
 int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; return code; }
+int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
+
+constexpr int PROF_MAX = 16384;
+
+struct prof_scope {
+    z2h_ctx * c; int idx = -1;
+    prof_scope(z2h_ctx * ctx, int fam) : c(ctx) {
+        if (!c->prof || c->ev_used >= PROF_MAX) return;
+        idx = c->ev_used++;
+        c->ev_fam[idx] = fam;
+        (void) hipEventRecord(c->ev[2 * idx], c->stream);
+    }
+    ~prof_scope() { if (idx >= 0) (void) hipEventRecord(c->ev[2 * idx + 1], c->stream); }
+};
 
 #define HIPX(expr) do { hipError_t e_ = (expr); if (e_ != hipSuccess) \
     return seterr(ctx, Z2H_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); } while (0)
@@ -163,8 +186,74 @@ int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
     return Z2H_OK;
 }
 
-// Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the row-tiled layout.
+// Repack into the 16-row MFMA layout (see k_gemv_mfma): per (group, unit) the lane-owned 8-byte
+// k-slices of every 32-element sub-block, chunk-major for the 64 lanes, then the rows' scale headers.
+int upload_mat_m16(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+    const int UB = type == Z2H_Q4_K ? 2304 : 4352, QS = type == Z2H_Q4_K ? 2 : 4;
+    dm.type = type; dm.m16 = true; dm.rows = (int) rows; dm.K = (int) K; dm.nsb = (int) ((K + 255) / 256);
+    dm.tiles = (int) ((rows + 15) / 16); dm.n_mats = n_mats;
+    dm.mat_bytes = (int64_t) dm.tiles * dm.nsb * UB;
+    const int64_t rb = z2::row_bytes(type, K);
+    std::vector<uint8_t> out((size_t) dm.mat_bytes * n_mats, 0);
+    auto do_rows = [&](int64_t g0, int64_t g1) {          // global 16-row group range over all matrices
+        for (int64_t gg = g0; gg < g1; ++gg) {
+            const int e = (int) (gg / dm.tiles), g = (int) (gg % dm.tiles);
+            uint8_t * mat = out.data() + (size_t) e * dm.mat_bytes;
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = (int64_t) g * 16 + r;
+                if (row >= rows) break;
+                const uint8_t * rp = src + ((int64_t) e * rows + row) * rb;
+                for (int sb = 0; sb < dm.nsb; ++sb) {
+                    uint8_t * unit = mat + ((size_t) g * dm.nsb + sb) * UB;
+                    for (int q = 0; q < 4; ++q) {
+                        const int lane = 16 * q + r;
+                        for (int c = 0; c < QS; ++c) {
+                            uint8_t * dst = unit + ((size_t) c * 64 + lane) * 16;
+                            for (int h = 0; h < 2; ++h) {           // two sub-block slices per chunk
+                                if (type == Z2H_Q4_K) {
+                                    const int pr = 2 * c + h;        // qs pair
+                                    std::memcpy(dst + 8 * h, rp + 144 * sb + 16 + 32 * pr + 8 * q, 8);
+                                } else {
+                                    const int64_t blk = (int64_t) sb * 8 + 2 * c + h;
+                                    if (blk * 32 < K) std::memcpy(dst + 8 * h, rp + 34 * blk + 2 + 8 * q, 8);
+                                }
+                            }
+                        }
+                    }
+                    uint8_t * hd = unit + (size_t) QS * 64 * 16 + (size_t) r * 16;
+                    if (type == Z2H_Q4_K) std::memcpy(hd, rp + 144 * sb, 16);
+                    else
+                        for (int b = 0; b < 8; ++b) {
+                            const int64_t blk = (int64_t) sb * 8 + b;
+                            if (blk * 32 < K) std::memcpy(hd + 2 * b, rp + 34 * blk, 2);
+                        }
+                }
+            }
+        }
+    };
+    const int64_t total = (int64_t) n_mats * dm.tiles;
+    const int nth = (int) std::max<int64_t>(1, std::min<int64_t>(16, total / 64));
+    std::vector<std::thread> th;
+    for (int i = 0; i < nth; ++i) th.emplace_back([&, i] { do_rows(total * i / nth, total * (i + 1) / nth); });
+    for (auto & t : th) t.join();
+    if (int rc = dalloc(ctx, &dm.w, out.size(), ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(dm.w, out.data(), out.size(), hipMemcpyHostToDevice));
+    return Z2H_OK;
+}
+
+// Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the device layout: the 16-row
+// MFMA layout for Q4_K / Q8_0, the 64-row tiles for Q6_K / F16.
 int upload_mat(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+    if (type == Z2H_Q4_K || type == Z2H_Q8_0) {
+        if (type == Z2H_Q4_K && K % 256) return seterr(ctx, Z2H_EINVAL, "K-quant row not a multiple of 256");
+        if (type == Z2H_Q8_0 && K % 32) return seterr(ctx, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
+        return upload_mat_m16(ctx, type, K, rows, n_mats, src, dm);
+    }
+    return upload_mat_t64(ctx, type, K, rows, n_mats, src, dm);
+}
+
+// Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the 64-row tiled layout.
+int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
     const int C = chunks_of(type);
     if (!C) return seterr(ctx, Z2H_ENOTSUP, "matrix type not supported on the device (F16, Q8_0, Q4_K, Q6_K)");
     if ((type == Z2H_Q4_K || type == Z2H_Q6_K) && K % 256) return seterr(ctx, Z2H_EINVAL, "K-quant row not a multiple of 256");
@@ -176,9 +265,9 @@ int upload_mat(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, con
     const int64_t rb = z2::row_bytes(type, K);
     std::vector<uint8_t> tiled((size_t) dm.mat_bytes * n_mats, 0);
     std::vector<uint16_t> dpl((size_t) dm.dpl_elems * n_mats, 0);
-    for (int e = 0; e < n_mats; ++e) {
+    auto repack_rows = [&](int e, int64_t r0, int64_t r1) {
         uint8_t * dst = tiled.data() + (size_t) e * dm.mat_bytes;
-        for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t r = r0; r < r1; ++r) {
             const uint8_t * row = src + ((int64_t) e * rows + r) * rb;
             const int64_t tile = r / TILE, lane = r % TILE;
             for (int sb = 0; sb < dm.nsb; ++sb) {
@@ -208,7 +297,20 @@ int upload_mat(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, con
                     std::memcpy(dst + ((((size_t) tile * dm.nsb + sb) * C + c) * TILE + lane) * 16, unit + 16 * c, 16);
             }
         }
-    }
+    };
+    const int64_t total = (int64_t) n_mats * rows;
+    const int nth = (int) std::max<int64_t>(1, std::min<int64_t>(16, total / 1024));
+    std::vector<std::thread> th;
+    for (int i = 0; i < nth; ++i)
+        th.emplace_back([&, i] {
+            for (int64_t g = total * i / nth; g < total * (i + 1) / nth; ) {
+                const int e = (int) (g / rows);
+                const int64_t r0 = g % rows, r1 = std::min<int64_t>(rows, r0 + (total * (i + 1) / nth - g));
+                repack_rows(e, r0, r1);
+                g += r1 - r0;
+            }
+        });
+    for (auto & t : th) t.join();
     if (int rc = dalloc(ctx, &dm.w, tiled.size(), ctx->bytes_w)) return rc;
     HIPX(hipMemcpy(dm.w, tiled.data(), tiled.size(), hipMemcpyHostToDevice));
     if (type == Z2H_Q6_K) {
@@ -268,6 +370,12 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->act.q, (size_t) T * KM, b)) || (rc = dalloc(ctx, &ctx->act.d32, (size_t) T * (KM / 32) * 4, b)) ||
         (rc = dalloc(ctx, &ctx->act.d256, (size_t) T * (KM / 256) * 4, b)) || (rc = dalloc(ctx, &ctx->act.bs, (size_t) T * (KM / 16) * 2, b)) ||
         (rc = dalloc(ctx, &ctx->act.h, (size_t) T * KM * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.q, (size_t) T * K * kpad(std::max(ff, 1)), b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.d32, (size_t) T * K * (kpad(std::max(ff, 1)) / 32) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.d256, (size_t) T * K * (kpad(std::max(ff, 1)) / 256) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.bs, (size_t) T * K * (kpad(std::max(ff, 1)) / 16) * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.h, (size_t) T * K * kpad(std::max(ff, 1)) * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->attn_o, (size_t) T * nh * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->state, (size_t) hp.n_layer * T * rd * 4, b)) || (rc = dalloc(ctx, &ctx->state_ext, (size_t) T * rd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->sel, (size_t) T * K * 4, b)) || (rc = dalloc(ctx, &ctx->wsel, (size_t) T * K * 4, b)) ||
         (rc = dalloc(ctx, &ctx->gu_g, (size_t) T * K * std::max(ff, 1) * 4, b)) || (rc = dalloc(ctx, &ctx->gu_u, (size_t) T * K * std::max(ff, 1) * 4, b)) ||
@@ -315,26 +423,65 @@ int cap_copy(z2h_ctx * ctx, int what, int L, const void * src, int T) {
 }
 
 // ---------------------------------------------------------------- launch helpers
-int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & base, int stage, int grid_y) {
+int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & base, int grid_y, int fam) {
+    prof_scope ps(ctx, fam);
     GemvArgs a = base;
     a.w[0] = m0.w; a.w[1] = m1 ? m1->w : m0.w;
     a.dpl[0] = m0.dpl; a.dpl[1] = m1 ? m1->dpl : m0.dpl;
     a.mat_bytes = m0.mat_bytes; a.dpl_elems = m0.dpl_elems;
-    a.nsb = m0.nsb; a.tiles = m0.tiles; a.rows = m0.rows; a.K = m0.K;
+    a.nsb = m0.nsb; a.tiles = m0.tiles; a.rows = m0.rows;
+    if (!a.grouped) {
+        // spread the tokens over enough blocks to cover the chip (weights are re-read from L2/MALL)
+        const int want = std::min(a.n_tok, std::max(1, (256 + m0.tiles - 1) / m0.tiles));
+        const int chunks = std::max(want, (a.n_tok + NT - 1) / NT);
+        a.tpb = (a.n_tok + chunks - 1) / chunks;
+        grid_y = (a.n_tok + a.tpb - 1) / a.tpb;
+    }
     const int af = act_of(m0.type);
-    const size_t lds = gemv_lds_bytes(af, m0.nsb * 256, stage);
+    a.n_mats = m1 ? 2 : 1;
+    if (m0.m16) {
+        const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256);
+        // grouped: an expert serves at most n_tok routes (each token picks it once) -> route passes
+        const int passes = a.grouped ? (a.n_tok + MT - 1) / MT : 1;
+        if (!a.grouped) grid_y = (a.n_tok + MT - 1) / MT;
+        dim3 grid((m0.tiles + 3) / 4, grid_y, a.n_mats * passes), block(256);
+        if (m0.type == Z2H_Q4_K) hipLaunchKernelGGL(k_gemv_mfma<WF_Q4_K>, grid, block, lds, ctx->stream, a);
+        else hipLaunchKernelGGL(k_gemv_mfma<WF_Q8_0>, grid, block, lds, ctx->stream, a);
+        HIPX(hipGetLastError());
+        return Z2H_OK;
+    }
+    if (a.grouped) {
+        // grouped expert matmuls: row-streaming kernel, 4 tiles per block
+        const size_t lds = gemv_rows_lds_bytes(af, m0.nsb * 256);
+        dim3 grid((m0.tiles + 3) / 4, grid_y, m1 ? 2 : 1), block(256);
+        switch (m0.type) {
+            case Z2H_Q4_K: hipLaunchKernelGGL(k_gemv_rows<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_Q6_K: hipLaunchKernelGGL(k_gemv_rows<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_Q8_0: hipLaunchKernelGGL(k_gemv_rows<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_F16:  hipLaunchKernelGGL(k_gemv_rows<WF_F16>, grid, block, lds, ctx->stream, a); break;
+            default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
+        }
+        HIPX(hipGetLastError());
+        return Z2H_OK;
+    }
+    const size_t lds = gemv_lds_bytes(af, m0.nsb * 256);
     dim3 grid(m0.tiles, grid_y, m1 ? 2 : 1), block(256);
-#define GEMV_CASE(WF_) \
-    if (stage == ST_ACT) hipLaunchKernelGGL((k_gemv<WF_, ST_ACT>), grid, block, lds, ctx->stream, a); \
-    else hipLaunchKernelGGL((k_gemv<WF_, ST_SWIGLU>), grid, block, lds, ctx->stream, a);
     switch (m0.type) {
-        case Z2H_Q4_K: GEMV_CASE(WF_Q4_K); break;
-        case Z2H_Q6_K: GEMV_CASE(WF_Q6_K); break;
-        case Z2H_Q8_0: GEMV_CASE(WF_Q8_0); break;
-        case Z2H_F16:  GEMV_CASE(WF_F16); break;
+        case Z2H_Q4_K: hipLaunchKernelGGL(k_gemv<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_Q6_K: hipLaunchKernelGGL(k_gemv<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_Q8_0: hipLaunchKernelGGL(k_gemv<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_F16:  hipLaunchKernelGGL(k_gemv<WF_F16>, grid, block, lds, ctx->stream, a); break;
         default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
     }
-#undef GEMV_CASE
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+int launch_swiglu(z2h_ctx * ctx, int n_rows, int act_fmt) {
+    prof_scope ps(ctx, Z2H_KF_SWIGLU);
+    SwigluArgs w{};
+    w.g = ctx->gu_g; w.u = ctx->gu_u; w.ff = ctx->hp.n_ff; w.act = ctx->act_y; w.act_fmt = act_fmt;
+    hipLaunchKernelGGL(k_swiglu_encode, dim3(n_rows), dim3(256), (size_t) kpad(ctx->hp.n_ff) * 4, ctx->stream, w);
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -347,7 +494,9 @@ GemvArgs gemv_dense(z2h_ctx * ctx, int T, float * out, int out_ld, int epi) {
 }
 
 int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
-    a.d = ctx->hp.n_embd; a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
+    prof_scope ps(ctx, Z2H_KF_RESNORM);
+    if (!a.d) a.d = ctx->hp.n_embd;
+    a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
     hipLaunchKernelGGL(k_resnorm, dim3(T), dim3(256), (size_t) kpad(a.d) * 4, ctx->stream, a);
     HIPX(hipGetLastError());
     return Z2H_OK;
@@ -367,10 +516,17 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     r.sel = ctx->sel; r.wsel = ctx->wsel;
     r.cap_logits = (float *) capp(ctx, Z2H_CAP_ROUTER_LOGITS, L);
     r.cap_probs = (float *) capp(ctx, Z2H_CAP_PROBS, L);
-    hipLaunchKernelGGL(k_router_down, dim3((ctx->rd + 3) / 4), dim3(256), 0, ctx->stream, r);
-    HIPX(hipGetLastError());
-    hipLaunchKernelGGL(k_router_tail, dim3(T), dim3(64), 0, ctx->stream, r);
-    HIPX(hipGetLastError());
+    {
+        prof_scope ps(ctx, Z2H_KF_ROUTER_DOWN);
+        hipLaunchKernelGGL(k_router_down, dim3((ctx->rd + 3) / 4, T), dim3(256), 0, ctx->stream, r);
+        HIPX(hipGetLastError());
+    }
+    {
+        prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
+        r.tpb = router_tail_tpb(ctx->rd, ly.E);
+        hipLaunchKernelGGL(k_router_tail, dim3((T + r.tpb - 1) / r.tpb), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        HIPX(hipGetLastError());
+    }
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_SEL, L, ctx->sel, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_WEIGHTS, L, ctx->wsel, T))) return rc;
@@ -383,13 +539,15 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         g.cap_offsets = (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L);
         g.cap_perm = (int32_t *) capp(ctx, Z2H_CAP_PERM, L);
     }
-    if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ST_ACT, ly.E))) return rc;
-    // down, SwiGLU staging, route weight
+    if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ly.E, Z2H_KF_GEMV_GATEUP))) return rc;
+    // y = up * silu(gate) per route, encoded once for the down matmul
+    if ((rc = launch_swiglu(ctx, T * ly.k, act_of(ly.down_exps.type)))) return rc;
+    // down, route weight
     GemvArgs dn{};
     dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
-    dn.gu_g = ctx->gu_g; dn.gu_u = ctx->gu_u; dn.ff = hp.n_ff;
+    dn.act = ctx->act_y; dn.act_by_route = 1;
     dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
-    if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ST_SWIGLU, ly.E))) return rc;
+    if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ly.E, Z2H_KF_GEMV_DOWN))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_EXPERT_OUT, L, ctx->eo, T))) return rc;
     return Z2H_OK;
 }
@@ -399,11 +557,11 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
     int rc;
     GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
     g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_u;
-    if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, ST_ACT, (T + NT - 1) / NT))) return rc;
-    GemvArgs dn{};
-    dn.grouped = 0; dn.n_tok = T; dn.gu_g = ctx->gu_g; dn.gu_u = ctx->gu_u; dn.ff = hp.n_ff;
-    dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_STORE;
-    return launch_gemv(ctx, ly.ffn_down, nullptr, dn, ST_SWIGLU, (T + NT - 1) / NT);
+    if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, 1, Z2H_KF_GEMV_DENSE))) return rc;
+    if ((rc = launch_swiglu(ctx, T, act_of(ly.ffn_down.type)))) return rc;
+    GemvArgs dn = gemv_dense(ctx, T, ctx->eo, hp.n_embd, EPI_STORE);
+    dn.act = ctx->act_y;
+    return launch_gemv(ctx, ly.ffn_down, nullptr, dn, 1, Z2H_KF_GEMV_DENSE);
 }
 
 // The whole decode step on device-resident inputs in ctx->d_* (T tokens, host copy of n_past).
@@ -429,7 +587,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     for (int L = 0; L < hp.n_layer; ++L) {
         Layer & ly = ctx->layers[L];
         // fused QKV + gate projection
-        if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), ST_ACT, (T + NT - 1) / NT))) return rc;
+        if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), 1, Z2H_KF_GEMV_QKV))) return rc;
         AttnArgs a{};
         a.qkvg = ctx->qkvg; a.R = R; a.nh = nh; a.nkv = nkv; a.hd = hd; a.temp = ly.attn_temp;
         a.qk_eps = hp.qk_norm_eps; a.theta_scale = std::pow(hp.rope_freq_base, -2.0f / (float) hd);
@@ -440,19 +598,39 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         a.q16 = ctx->q16; a.gate = ctx->gate;
         a.cap_q = (float *) capp(ctx, Z2H_CAP_Q, L); a.cap_k = (float *) capp(ctx, Z2H_CAP_K, L); a.cap_v = (float *) capp(ctx, Z2H_CAP_V, L);
         a.part_o = ctx->part_o; a.part_ml = ctx->part_ml; a.n_items = n_items;
-        a.o_out = (float *) capp(ctx, Z2H_CAP_ATTN_O, L);
-        a.act = ctx->act; a.act_fmt = act_of(ly.wo.type);
-        hipLaunchKernelGGL(k_qkv_post, dim3(T), dim3(256), 0, ctx->stream, a);
-        HIPX(hipGetLastError());
+        a.o_out = ctx->attn_o;
+        a.act = ctx->act;
+        const int wo_act = act_of(ly.wo.type);
+        const int span = (nh / nkv) * hd;                  // elements one combine block owns
+        const bool in_block = span % 256 == 0;             // whole encoding blocks, no padding
+        a.act_fmt = in_block ? wo_act : ACT_NONE;
+        {
+            prof_scope ps(ctx, Z2H_KF_QKV_POST);
+            hipLaunchKernelGGL(k_qkv_post, dim3((nh + 2 * nkv + 3) / 4, T), dim3(256), 0, ctx->stream, a);
+            HIPX(hipGetLastError());
+        }
         if ((rc = cap_copy(ctx, Z2H_CAP_GATE, L, ctx->gate, T))) return rc;
         const int grp = nh / nkv;
         const size_t lds_p = (size_t) 2 * ATT_CH * (hd + 8) * 2 + (size_t) (grp * hd + 8) * 2 + (size_t) grp * ATT_CH * 4 + 16;
-        hipLaunchKernelGGL(k_attn_partial, dim3(std::min(n_items, 4096)), dim3(256), lds_p, ctx->stream, a);
-        HIPX(hipGetLastError());
-        hipLaunchKernelGGL(k_attn_combine, dim3(T), dim3(256), (size_t) kpad(nh * hd) * 4, ctx->stream, a);
-        HIPX(hipGetLastError());
+        {
+            prof_scope ps(ctx, Z2H_KF_ATTN);
+            hipLaunchKernelGGL(k_attn_partial, dim3(std::min(n_items, 4096)), dim3(256), lds_p, ctx->stream, a);
+            HIPX(hipGetLastError());
+        }
+        {
+            prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
+            const int nc_max = (ctx->S + ATT_CH - 1) / ATT_CH;
+            hipLaunchKernelGGL(k_attn_combine, dim3(nkv, T), dim3(256), (size_t) ((nh / nkv) * hd + 4 * nc_max) * 4, ctx->stream, a);
+            HIPX(hipGetLastError());
+        }
+        if (!in_block) {
+            ResNormArgs en{};
+            en.mode = RN_ENCODE; en.d = nh * hd; en.src = ctx->attn_o; en.act = ctx->act; en.act_fmt = wo_act;
+            if ((rc = launch_resnorm(ctx, T, en))) return rc;
+        }
+        if ((rc = cap_copy(ctx, Z2H_CAP_ATTN_O, L, ctx->attn_o, T))) return rc;
         // W_o
-        if ((rc = launch_gemv(ctx, ly.wo, nullptr, gemv_dense(ctx, T, ctx->wo_out, d, EPI_STORE), ST_ACT, (T + NT - 1) / NT))) return rc;
+        if ((rc = launch_gemv(ctx, ly.wo, nullptr, gemv_dense(ctx, T, ctx->wo_out, d, EPI_STORE), 1, Z2H_KF_GEMV_WO))) return rc;
         if ((rc = cap_copy(ctx, Z2H_CAP_ATTN_OUT, L, ctx->wo_out, T))) return rc;
         // res += attn; ffn_norm; encode for the FFN
         ResNormArgs f{};
@@ -479,7 +657,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     // output head + softcap
     const int nout = hp.n_codebooks * hp.audio_vocab;
     return launch_gemv(ctx, ctx->head, nullptr, gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE),
-                       ST_ACT, (T + NT - 1) / NT);
+                       1, Z2H_KF_GEMV_HEAD);
 }
 
 int check_err_flag(z2h_ctx * ctx) {
@@ -636,17 +814,20 @@ int z2h_finalize(z2h_ctx * ctx) {
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
     if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
-    if (ctx->rd > 512) return seterr(ctx, Z2H_ENOTSUP, "router_dim > 512");
+    if (ctx->rd > 256) return seterr(ctx, Z2H_ENOTSUP, "router_dim > 256");
     if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));
     // allow the GEMV kernels the full 160 KiB of gfx950 LDS for their dynamic carve-up
     const int lds_max = 160 * 1024 - 8 * 1024;
-#define LDS_ATTR(WF_) \
-    (void) hipFuncSetAttribute((const void *) &k_gemv<WF_, ST_ACT>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max); \
-    (void) hipFuncSetAttribute((const void *) &k_gemv<WF_, ST_SWIGLU>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
-    LDS_ATTR(WF_Q4_K) LDS_ATTR(WF_Q6_K) LDS_ATTR(WF_Q8_0) LDS_ATTR(WF_F16)
+#define LDS_ATTR(K_) (void) hipFuncSetAttribute((const void *) &K_, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
+    LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
+    LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
+    LDS_ATTR(k_gemv_mfma<WF_Q4_K>) LDS_ATTR(k_gemv_mfma<WF_Q8_0>)
+    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
+    if (router_tail_lds(std::max(1, ctx->rd), std::max(1, hp.n_expert)) > (size_t) lds_max)
+        return seterr(ctx, Z2H_ENOTSUP, "router too large for one block's LDS");
     ctx->finalized = true;
     return Z2H_OK;
 }
@@ -837,6 +1018,36 @@ int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nby
     return Z2H_OK;
 }
 
+int z2h_profile_begin(z2h_ctx * ctx) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->ev.empty()) {
+        ctx->ev.resize(2 * PROF_MAX);
+        ctx->ev_fam.resize(PROF_MAX);
+        for (auto & e : ctx->ev) HIPX(hipEventCreate(&e));
+    }
+    HIPX(hipStreamSynchronize(ctx->stream));
+    ctx->ev_used = 0;
+    ctx->prof = true;
+    return Z2H_OK;
+}
+
+int z2h_profile_end(z2h_ctx * ctx, double * ms, int32_t * launches) {
+    if (!ctx || !ms || !launches) return Z2H_EINVAL;
+    if (!ctx->prof) return seterr(ctx, Z2H_ESTATE, "profile window not open");
+    ctx->prof = false;
+    // launches may have gone to a caller's stream (z2h_step_device): wait on the events themselves
+    for (int f = 0; f < Z2H_KF_COUNT_; ++f) { ms[f] = 0.0; launches[f] = 0; }
+    for (int i = 0; i < ctx->ev_used; ++i) {
+        float t = 0.0f;
+        HIPX(hipEventSynchronize(ctx->ev[2 * i + 1]));
+        HIPX(hipEventElapsedTime(&t, ctx->ev[2 * i], ctx->ev[2 * i + 1]));
+        ms[ctx->ev_fam[i]] += t;
+        launches[ctx->ev_fam[i]] += 1;
+    }
+    if (ctx->ev_used >= PROF_MAX) return seterr(ctx, Z2H_EINVAL, "profile window overflowed");
+    return Z2H_OK;
+}
+
 int64_t z2h_device_bytes(const z2h_ctx * ctx, int what) {
     if (!ctx) return -1;
     return what == 0 ? ctx->bytes_w : what == 1 ? ctx->bytes_kv : ctx->bytes_scratch;
@@ -848,6 +1059,7 @@ void z2h_destroy(z2h_ctx * ctx) {
     if (!ctx) return;
     (void) hipSetDevice(ctx->device);
     if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    for (auto & e : ctx->ev) (void) hipEventDestroy(e);
     for (void * p : ctx->allocs) (void) hipFree(p);
     if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);
     if (ctx->stream) (void) hipStreamDestroy(ctx->stream);

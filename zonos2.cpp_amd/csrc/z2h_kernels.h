@@ -4,9 +4,10 @@
 //   k_resnorm        embedding sum (248-260) / emb_norm (300) / residual folds (332, 345, 353) /
 //                    rms_w norms (92-95, 343, 347, 354), and the encoding of the normalised row in
 //                    the next matmul's activation type (ggml's vec_dot_type conversion)
-//   k_gemv<F, S>     every weight matmul: QKV+gate (107-111, fused into one matrix), W_o (175),
+//   k_gemv<F>        every weight matmul: QKV+gate (107-111, fused into one matrix), W_o (175),
 //                    expert gate/up and down (mul_mat_id 223-231, grouped by expert from the
 //                    top-k selection), dense FFN (179-185), output head + softcap (357-362)
+//   k_swiglu_encode  up * silu(gate) (183, 225) encoded for the down matmul
 //   k_qkv_post       QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137), sigmoid gate (107)
 //   k_attn_partial   ragged GQA decode attention over the slot's band, split into 64-row chunks (139-153)
 //   k_attn_combine   chunk merge, per-head sigmoid gate (173), encoding for W_o
@@ -123,6 +124,26 @@ __device__ __forceinline__ void encode_row_rt(int af, const float * x, int K, co
     else if (af == ACT_F16) encode_row<ACT_F16>(x, K, nullptr, nullptr, nullptr, nullptr, a.h + (int64_t) t * Kp);
 }
 
+// Block-wide copy of n 16-byte items with all loads of a batch issued before its stores (a loop
+// that loads and stores per iteration is not software-pipelined and pays one memory round trip per
+// iteration). src(i) / dst(i) give the item addresses.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <int NTH, class Src, class Dst>
+__device__ __forceinline__ void copy16(int n, Src src, Dst dst) {
+    constexpr int B = 8;
+    for (int base = 0; base < n; base += NTH * B) {
+        u32x4 v0, v1, v2, v3, v4, v5, v6, v7;
+        const int i0 = base + threadIdx.x;
+#define C16_LD(J) if (i0 + NTH * J < n) v##J = *(const u32x4 *) src(i0 + NTH * J);
+#define C16_ST(J) if (i0 + NTH * J < n) *(u32x4 *) dst(i0 + NTH * J) = v##J;
+        C16_LD(0) C16_LD(1) C16_LD(2) C16_LD(3) C16_LD(4) C16_LD(5) C16_LD(6) C16_LD(7)
+        C16_ST(0) C16_ST(1) C16_ST(2) C16_ST(3) C16_ST(4) C16_ST(5) C16_ST(6) C16_ST(7)
+#undef C16_LD
+#undef C16_ST
+        static_assert(B == 8, "copy16 batch");
+    }
+}
+
 // block-wide double sum (256 threads)
 __device__ __forceinline__ double block_sum_d(double v, double * red) {
     v = wave_tree_d(v);
@@ -216,18 +237,28 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
         const float scale = 1.0f / sqrtf((float) (tot / (double) d) + a.eps);
         for (int i = tid; i < d; i += 256) { const float v = xs[i] * scale; xs[i] = v; res[i] = v; }
     } else if (a.mode == RN_ACCUM) {
-        for (int i = tid; i < d; i += 256) {
-            const float * s = a.src + ((int64_t) t * a.k) * d + i;
-            float x = s[0];
-            for (int j = 1; j < a.k; ++j) x = x + s[(int64_t) j * d];
-            if (a.cap_x) a.cap_x[(int64_t) t * d + i] = x;
-            if (a.res) { const float r = x + res[i]; res[i] = r; xs[i] = r; }
-            else xs[i] = x;
+        const float * __restrict__ src = a.src + ((int64_t) t * a.k) * d;
+        for (int i0 = tid * 4; i0 < d; i0 += 1024) {            // d % 4 == 0
+            float4 x = *(const float4 *) (src + i0);
+            for (int j = 1; j < a.k; ++j) {
+                const float4 y = *(const float4 *) (src + (int64_t) j * d + i0);
+                x.x = x.x + y.x; x.y = x.y + y.y; x.z = x.z + y.z; x.w = x.w + y.w;
+            }
+            if (a.cap_x) *(float4 *) (a.cap_x + (int64_t) t * d + i0) = x;
+            if (res) {
+                const float4 r0 = *(const float4 *) (res + i0);
+                x.x = x.x + r0.x; x.y = x.y + r0.y; x.z = x.z + r0.z; x.w = x.w + r0.w;
+                *(float4 *) (res + i0) = x;
+            }
+            *(float4 *) (xs + i0) = x;
         }
     } else if (a.mode == RN_ADD) {
-        for (int i = tid; i < d; i += 256) {
-            const float r = a.src[(int64_t) t * d + i] + res[i];
-            res[i] = r; xs[i] = r;
+        const float * __restrict__ src = a.src + (int64_t) t * d;
+        for (int i0 = tid * 4; i0 < d; i0 += 1024) {
+            const float4 x = *(const float4 *) (src + i0), r0 = *(const float4 *) (res + i0);
+            const float4 r = make_float4(x.x + r0.x, x.y + r0.y, x.z + r0.z, x.w + r0.w);
+            *(float4 *) (res + i0) = r;
+            *(float4 *) (xs + i0) = r;
         }
     } else {
         for (int i = tid; i < d; i += 256) xs[i] = a.src[(int64_t) t * d + i];
@@ -249,7 +280,6 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
 }
 
 // ------------------------------------------------------------------ k_gemv
-enum { ST_ACT = 0, ST_SWIGLU = 1 };
 enum { EPI_STORE = 0, EPI_SOFTCAP = 1, EPI_ROUTE_W = 2 };
 
 struct GemvArgs {
@@ -257,13 +287,14 @@ struct GemvArgs {
     const uint16_t * dpl[2];           // Q6_K f16 d plane
     int64_t mat_bytes, dpl_elems;      // per-expert strides
     int nsb, tiles, rows;              // padded K = nsb*256
-    int K;                             // real K (SwiGLU staging encodes zeros beyond it)
     // token source
     int grouped;                       // 0: tokens [y*NT, ...) of n_tok; 1: routes with sel == blockIdx.y
     int n_tok;                         // dense token count / grouped: number of tokens T
     const int32_t * sel; int k;        // [T][k]
     ActBuf act;                        // ST_ACT source rows (indexed by token)
-    const float * gu_g; const float * gu_u; int ff;   // ST_SWIGLU source rows (indexed by route / token)
+    int act_by_route;                  // grouped: activation row = route (else token = route / k)
+    int n_mats;                        // matrices in the launch (gate+up = 2)
+    int tpb;                           // dense: tokens per block (<= NT)
     // output
     float * out[2]; int out_ld;        // out[m][row-index][rows]; row-index = token or route
     int epi; float cap; const float * route_w;
@@ -292,158 +323,170 @@ __device__ __forceinline__ int build_route_list(const int32_t * sel, int n_route
 }
 
 template <int WF>
-__device__ __forceinline__ void gemv_unit(const uint4 * __restrict__ u, const uint16_t * dp, int sb, int nsb, int K,
+__device__ __forceinline__ void load_unit(const uint4 * __restrict__ u, uint4 (&r)[wfmt<WF>::C]) {
+#pragma unroll
+    for (int c = 0; c < wfmt<WF>::C; ++c) r[c] = u[c * TILE];
+}
+
+// One 256-column unit of the lane's row against nt staged activation rows. The unit is decoded once
+// (outside the token loop); each token's block value is added to the wave's LDS accumulator
+// sacc[tt * TILE] (per lane), so the token loop carries no register arrays.
+template <int WF>
+__device__ __forceinline__ void gemv_unit(const uint4 (&u)[wfmt<WF>::C], const uint16_t * dp, int sb, int nsb, int K,
                                           const int8_t * sq, const float * sd32, const float * sd256,
-                                          const int16_t * sbs, const uint16_t * sh, int nt, float (&acc)[NT]) {
-    constexpr int C = wfmt<WF>::C;
+                                          const int16_t * sbs, const uint16_t * sh, int nt, float * sacc) {
     if constexpr (WF == WF_Q4_K) {
         const uint4 hdr = u[0];
-        uint32_t qw[32];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint4 v = u[(c + 1) * TILE];
-            qw[4 * c] = v.x; qw[4 * c + 1] = v.y; qw[4 * c + 2] = v.z; qw[4 * c + 3] = v.w;
-        }
         const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
         uint8_t scb[12];
         __builtin_memcpy(scb, &hdr.y, 4); __builtin_memcpy(scb + 4, &hdr.z, 4); __builtin_memcpy(scb + 8, &hdr.w, 4);
         int sc[8], mn[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) q4k_sm(scb, j, sc[j], mn[j]);
+        // qs chunk c (1..8) holds bytes 16(c-1)..: pair p = (c-1)/2; low nibbles -> sub-block 2p,
+        // high nibbles -> sub-block 2p+1, at element dword 16p + 4*((c-1)&1) (+8 for high) + m
         uint32_t lo[32], hi[32];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) { lo[i] = qw[i] & 0x0f0f0f0fu; hi[i] = (qw[i] >> 4) & 0x0f0f0f0fu; }
+        for (int c = 0; c < 8; ++c) {
+            const uint4 v = u[c + 1];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            if (tt < nt) {
-                const int * aq = (const int *) (sq + tt * K + sb * 256);
-                int isum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int m = 0; m < 4; ++m) { lo[4 * c + m] = w4[m] & 0x0f0f0f0fu; hi[4 * c + m] = (w4[m] >> 4) & 0x0f0f0f0fu; }
+        }
+        for (int tt = 0; tt < nt; ++tt) {
+            const int * aq = (const int *) (sq + tt * K + sb * 256);
+            int sumi = 0;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const int p = c >> 1, hf = c & 1;
+            for (int p = 0; p < 4; ++p) {
+                int il = 0, ih = 0;
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
-                        isum[2 * p]     = sdot4((int) lo[4 * c + m], aq[16 * p + 4 * hf + m], isum[2 * p]);
-                        isum[2 * p + 1] = sdot4((int) hi[4 * c + m], aq[16 * p + 8 + 4 * hf + m], isum[2 * p + 1]);
+                        il = sdot4((int) lo[8 * p + 4 * hf + m], aq[16 * p + 4 * hf + m], il);
+                        ih = sdot4((int) hi[8 * p + 4 * hf + m], aq[16 * p + 8 + 4 * hf + m], ih);
                     }
-                }
-                int sumi = 0, summ = 0;
-                const int16_t * bsr = sbs + tt * (K / 16) + sb * 16;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) { sumi += sc[j] * isum[j]; summ += mn[j] * ((int) bsr[2 * j] + (int) bsr[2 * j + 1]); }
-                const float dx = sd256[tt * nsb + sb];
-                acc[tt] += (d * dx) * (float) sumi - (dmin * dx) * (float) summ;
+                sumi += sc[2 * p] * il + sc[2 * p + 1] * ih;
             }
+            const int16_t * bsr = sbs + tt * (K / 16) + sb * 16;
+            int summ = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) summ += mn[j] * ((int) bsr[2 * j] + (int) bsr[2 * j + 1]);
+            const float dx = sd256[tt * nsb + sb];
+            sacc[tt * TILE] += (d * dx) * (float) sumi - (dmin * dx) * (float) summ;
         }
     } else if constexpr (WF == WF_Q6_K) {
-        uint32_t ql[32], qh[16];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint4 v = u[c * TILE];
-            ql[4 * c] = v.x; ql[4 * c + 1] = v.y; ql[4 * c + 2] = v.z; ql[4 * c + 3] = v.w;
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 v = u[(8 + c) * TILE];
-            qh[4 * c] = v.x; qh[4 * c + 1] = v.y; qh[4 * c + 2] = v.z; qh[4 * c + 3] = v.w;
-        }
-        const uint4 scv = u[12 * TILE];
+        const uint4 scv = u[12];
         int8_t sc[16];
         __builtin_memcpy(sc, &scv, 16);
         const float d = h2f(*dp);
-        // unsigned 6-bit values of the 4 element groups per (half, l4)
+        // unsigned 6-bit values per element dword dw = 32h + 8grp + l4 (grp = element quarter of the half)
         uint32_t qv[64];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int l4 = 0; l4 < 8; ++l4) {
-                const uint32_t L0 = ql[16 * h + l4], L1 = ql[16 * h + 8 + l4], H = qh[8 * h + l4];
+                const int a0 = 16 * h + l4, a1 = 16 * h + 8 + l4, ah = 8 * h + l4;
+                const uint4 v0 = u[a0 >> 2], v1 = u[a1 >> 2], vh = u[8 + (ah >> 2)];
+                const uint32_t L0 = (a0 & 3) == 0 ? v0.x : (a0 & 3) == 1 ? v0.y : (a0 & 3) == 2 ? v0.z : v0.w;
+                const uint32_t L1 = (a1 & 3) == 0 ? v1.x : (a1 & 3) == 1 ? v1.y : (a1 & 3) == 2 ? v1.z : v1.w;
+                const uint32_t H  = (ah & 3) == 0 ? vh.x : (ah & 3) == 1 ? vh.y : (ah & 3) == 2 ? vh.z : vh.w;
                 qv[32 * h + l4]      = (L0 & 0x0f0f0f0fu) | ((H & 0x03030303u) << 4);
                 qv[32 * h + 8 + l4]  = (L1 & 0x0f0f0f0fu) | (((H >> 2) & 0x03030303u) << 4);
                 qv[32 * h + 16 + l4] = ((L0 >> 4) & 0x0f0f0f0fu) | (((H >> 4) & 0x03030303u) << 4);
                 qv[32 * h + 24 + l4] = ((L1 >> 4) & 0x0f0f0f0fu) | (((H >> 6) & 0x03030303u) << 4);
             }
+        for (int tt = 0; tt < nt; ++tt) {
+            const int * aq = (const int *) (sq + tt * K + sb * 256);
+            const int16_t * bsr = sbs + tt * (K / 16) + sb * 16;
+            int sumi = 0;
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            if (tt < nt) {
-                const int * aq = (const int *) (sq + tt * K + sb * 256);
-                const int16_t * bsr = sbs + tt * (K / 16) + sb * 16;
-                int sumi = 0;
+            for (int g = 0; g < 16; ++g) {             // 16-element scale group = dwords 4g..4g+3
+                int is = 0;
 #pragma unroll
-                for (int g = 0; g < 16; ++g) {       // group g: elements 16g..16g+15 = dwords 4g..4g+3
-                    int is = 0;
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        const int dw = 4 * g + m;    // element dword index within the 256
-                        const int h = dw >> 5, r = dw & 31, grp = r >> 3, l4 = r & 7;
-                        is = sdot4((int) qv[32 * h + 8 * grp + l4], aq[dw], is);
-                    }
-                    sumi += (int) sc[g] * (is - 32 * (int) bsr[g]);
-                }
-                acc[tt] += (d * sd256[tt * nsb + sb]) * (float) sumi;
+                for (int m = 0; m < 4; ++m) is = sdot4((int) qv[4 * g + m], aq[4 * g + m], is);
+                sumi += (int) sc[g] * (is - 32 * (int) bsr[g]);
             }
+            sacc[tt * TILE] += (d * sd256[tt * nsb + sb]) * (float) sumi;
         }
     } else if constexpr (WF == WF_Q8_0) {
         uint32_t qw[64];
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            const uint4 v = u[c * TILE];
+            const uint4 v = u[c];
             qw[4 * c] = v.x; qw[4 * c + 1] = v.y; qw[4 * c + 2] = v.z; qw[4 * c + 3] = v.w;
         }
-        const uint4 dv = u[16 * TILE];
+        const uint4 dv = u[16];
         uint16_t dh[8];
         __builtin_memcpy(dh, &dv, 16);
+        for (int tt = 0; tt < nt; ++tt) {
+            const int * aq = (const int *) (sq + tt * K + sb * 256);
+            const float * dx = sd32 + tt * (K / 32) + sb * 8;
+            float a = sacc[tt * TILE];
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            if (tt < nt) {
-                const int * aq = (const int *) (sq + tt * K + sb * 256);
-                const float * dx = sd32 + tt * (K / 32) + sb * 8;
+            for (int b = 0; b < 8; ++b) {
+                int is = 0;
 #pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    int is = 0;
-#pragma unroll
-                    for (int m = 0; m < 8; ++m) is = sdot4((int) qw[8 * b + m], aq[8 * b + m], is);
-                    acc[tt] += (h2f(dh[b]) * dx[b]) * (float) is;
-                }
+                for (int m = 0; m < 8; ++m) is = sdot4((int) qw[8 * b + m], aq[8 * b + m], is);
+                a += (h2f(dh[b]) * dx[b]) * (float) is;
             }
+            sacc[tt * TILE] = a;
         }
     } else {   // F16
+        for (int tt = 0; tt < nt; ++tt) {
+            const uint32_t * ah = (const uint32_t *) (sh + tt * K + sb * 256);
+            float s = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            if (tt < nt) {
-                const uint32_t * ah = (const uint32_t *) (sh + tt * K + sb * 256);
-                float s = 0.0f;
-#pragma unroll 4
-                for (int c = 0; c < 32; ++c) {
-                    const uint4 v = u[c * TILE];
-                    s = fdot2(v.x, ah[4 * c], s); s = fdot2(v.y, ah[4 * c + 1], s);
-                    s = fdot2(v.z, ah[4 * c + 2], s); s = fdot2(v.w, ah[4 * c + 3], s);
-                }
-                acc[tt] += s;
+            for (int c = 0; c < 32; ++c) {
+                const uint4 v = u[c];
+                s = fdot2(v.x, ah[4 * c], s); s = fdot2(v.y, ah[4 * c + 1], s);
+                s = fdot2(v.z, ah[4 * c + 2], s); s = fdot2(v.w, ah[4 * c + 3], s);
             }
+            sacc[tt * TILE] += s;
         }
     }
-    (void) C; (void) dp; (void) nsb;
+    (void) dp; (void) nsb; (void) sd32; (void) sd256; (void) sbs; (void) sh;
 }
 
-// LDS budget of k_gemv for activations of K columns (+ SwiGLU staging row)
-__host__ __device__ inline size_t gemv_lds_bytes(int act, int K, int stage) {
+// Stage nt encoded activation rows (row tt = token tok(tt)) into the LDS planes of the row kernels.
+template <int AF, class TokFn>
+__device__ __forceinline__ void stage_acts(const GemvArgs & a, int nt, TokFn tok, int K, int8_t * sq, float * sd32,
+                                           float * sd256, int16_t * sbs, uint16_t * sh) {
+    const int tid = threadIdx.x;
+    if constexpr (AF == ACT_Q8_K || AF == ACT_Q8_0) {
+        const int per = K / 16;
+        copy16<256>(nt * per, [&](int i) { return (const uint4 *) (a.act.q + (int64_t) tok(i / per) * K) + i % per; },
+                    [&](int i) { return (uint4 *) (sq + (i / per) * K) + i % per; });
+        if constexpr (AF == ACT_Q8_K) {
+            for (int i = tid; i < nt * (K / 256); i += 256) sd256[i] = a.act.d256[(int64_t) tok(i / (K / 256)) * (K / 256) + i % (K / 256)];
+            for (int i = tid; i < nt * (K / 16); i += 256) sbs[i] = a.act.bs[(int64_t) tok(i / (K / 16)) * (K / 16) + i % (K / 16)];
+        } else {
+            for (int i = tid; i < nt * (K / 32); i += 256) sd32[i] = a.act.d32[(int64_t) tok(i / (K / 32)) * (K / 32) + i % (K / 32)];
+        }
+    } else {
+        const int per = K / 8;
+        copy16<256>(nt * per, [&](int i) { return (const uint4 *) (a.act.h + (int64_t) tok(i / per) * K) + i % per; },
+                    [&](int i) { return (uint4 *) (sh + (i / per) * K) + i % per; });
+    }
+}
+
+// LDS budget of k_gemv for activations of K (padded) columns
+__host__ __device__ inline size_t gemv_lds_bytes(int act, int K) {
     size_t b = (size_t) 4 * NT * TILE * 4;                         // reduction buffer
     if (act == ACT_Q8_K) b += (size_t) NT * K + (size_t) NT * (K / 256) * 4 + (size_t) NT * (K / 16) * 2;
     else if (act == ACT_Q8_0) b += (size_t) NT * K + (size_t) NT * (K / 32) * 4;
     else b += (size_t) NT * K * 2;
-    if (stage == ST_SWIGLU) b += (size_t) K * 4;
     return b + 64;
 }
 
-template <int WF, int STAGE>
+template <int WF>
 __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
     constexpr int AF = wfmt<WF>::ACT;
     constexpr int C = wfmt<WF>::C;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ int s_list[MAX_ROUTES];
     __shared__ int s_wcnt[4];
-    const int K = a.nsb * 256, Kr = a.K, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.nsb * 256, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.x, m = blockIdx.z;
     // LDS carve-up
     float * s_red = (float *) smem;                                  // [4][NT][64]
@@ -459,7 +502,6 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
     } else {
         sh = (uint16_t *) p; p += NT * K * 2;
     }
-    float * s_y = (float *) p;                                       // [K] SwiGLU staging
 
     // which rows (tokens / routes) this block serves
     int n_items, item0 = 0;
@@ -484,60 +526,49 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
         }
         if (n_items == 0) return;
     } else {
-        item0 = blockIdx.y * NT;
-        n_items = min(NT, a.n_tok - item0);
+        item0 = blockIdx.y * a.tpb;
+        n_items = min(a.tpb, a.n_tok - item0);
         if (n_items <= 0) return;
     }
     const uint8_t * wbase = a.w[m] + (int64_t) e * a.mat_bytes;
     const uint16_t * dbase = WF == WF_Q6_K ? a.dpl[m] + (int64_t) e * a.dpl_elems : nullptr;
     const uint4 * wt = (const uint4 *) wbase + (size_t) tile * a.nsb * C * TILE + lane;
+    // issue this wave's weight loads before the activations are staged (up to PF units stay in
+    // registers for every token chunk; further units are loaded in the compute loop)
+    constexpr int PF = 1;
+    uint4 wr[PF][C];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        const int sb = wave + 4 * j;
+        if (sb < a.nsb) load_unit<WF>(wt + (size_t) sb * C * TILE, wr[j]);
+    }
 
     for (int c0 = 0; c0 < n_items; c0 += NT) {
         const int nt = min(NT, n_items - c0);
         __syncthreads();
         // ---- stage the activation rows of this chunk into LDS
-        for (int tt = 0; tt < nt; ++tt) {
-            const int it = a.grouped ? s_list[c0 + tt] : item0 + c0 + tt;       // route or token
-            if constexpr (STAGE == ST_ACT) {
-                const int tok = a.grouped ? it / a.k : it;
-                if constexpr (AF == ACT_Q8_K || AF == ACT_Q8_0) {
-                    const uint4 * src = (const uint4 *) (a.act.q + (int64_t) tok * K);
-                    uint4 * dst = (uint4 *) (sq + tt * K);
-                    for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
-                    if constexpr (AF == ACT_Q8_K) {
-                        for (int i = tid; i < K / 256; i += 256) sd256[tt * (K / 256) + i] = a.act.d256[(int64_t) tok * (K / 256) + i];
-                        for (int i = tid; i < K / 16; i += 256) sbs[tt * (K / 16) + i] = a.act.bs[(int64_t) tok * (K / 16) + i];
-                    } else {
-                        for (int i = tid; i < K / 32; i += 256) sd32[tt * (K / 32) + i] = a.act.d32[(int64_t) tok * (K / 32) + i];
-                    }
-                } else {
-                    const uint4 * src = (const uint4 *) (a.act.h + (int64_t) tok * K);
-                    uint4 * dst = (uint4 *) (sh + tt * K);
-                    for (int i = tid; i < K / 8; i += 256) dst[i] = src[i];
-                }
-            } else {
-                // y = up * silu(gate) of this route (graph.cpp:225), then encode for the down matmul
-                const float * g = a.gu_g + (int64_t) it * a.ff;
-                const float * uu = a.gu_u + (int64_t) it * a.ff;
-                __syncthreads();
-                for (int i = tid; i < Kr; i += 256) s_y[i] = uu[i] * z_silu(g[i]);
-                __syncthreads();
-                if constexpr (AF == ACT_Q8_K) encode_row<AF>(s_y, Kr, sq + tt * K, nullptr, sd256 + tt * (K / 256), sbs + tt * (K / 16), nullptr);
-                else if constexpr (AF == ACT_Q8_0) encode_row<AF>(s_y, Kr, sq + tt * K, sd32 + tt * (K / 32), nullptr, nullptr, nullptr);
-                else encode_row<AF>(s_y, Kr, nullptr, nullptr, nullptr, nullptr, sh + tt * K);
+        stage_acts<AF>(a, nt, [&](int tt) { const int it = a.grouped ? s_list[c0 + tt] : item0 + c0 + tt;
+                                             return a.grouped && !a.act_by_route ? it / a.k : it; },
+                       K, sq, sd32, sd256, sbs, sh);
+        __syncthreads();
+        // ---- each wave: its share of the 256-column units, lane = row of the tile; partial sums
+        // accumulate in the wave's LDS slice s_red[wave][tt][lane] in unit order
+        float * sacc = s_red + (wave * NT) * TILE + lane;
+        for (int tt = 0; tt < nt; ++tt) sacc[tt * TILE] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int sb = wave + 4 * j;
+            if (sb < a.nsb) {
+                const uint16_t * dp = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb) * TILE + lane : nullptr;
+                gemv_unit<WF>(wr[j], dp, sb, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, sacc);
             }
         }
-        __syncthreads();
-        // ---- each wave: its share of the 256-column units, lane = row of the tile
-        float acc[NT];
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) acc[tt] = 0.0f;
-        for (int sb = wave; sb < a.nsb; sb += 4) {
+        for (int sb = wave + 4 * PF; sb < a.nsb; sb += 4) {
+            uint4 r[C];
+            load_unit<WF>(wt + (size_t) sb * C * TILE, r);
             const uint16_t * dp = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb) * TILE + lane : nullptr;
-            gemv_unit<WF>(wt + (size_t) sb * C * TILE, dp, sb, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, acc);
+            gemv_unit<WF>(r, dp, sb, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, sacc);
         }
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) s_red[(wave * NT + tt) * TILE + lane] = acc[tt];
         __syncthreads();
         // ---- reduce the 4 waves (in wave order) and store
         for (int o = tid; o < nt * TILE; o += 256) {
@@ -550,6 +581,278 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
             float y = v;
             if (a.epi == EPI_SOFTCAP) y = tanhf(v * (1.0f / a.cap)) * a.cap;
             else if (a.epi == EPI_ROUTE_W) y = v * a.route_w[it];
+            a.out[m][(int64_t) it * a.out_ld + row] = y;
+        }
+    }
+}
+
+// Row-streaming variant for the grouped expert matmuls: each wave owns one 64-row tile over the
+// full K (no cross-wave reduction), its 256-column units double-buffered in registers so one
+// unit's loads are in flight while the previous one is decoded; the 4 waves of a block (4 tiles of
+// the same expert matrix) share one activation staging of up to NTE routes.
+constexpr int NTE = 8;
+
+__host__ __device__ inline size_t gemv_rows_lds_bytes(int act, int K) {
+    size_t b = (size_t) 4 * NTE * TILE * 4;                        // per-wave accumulators
+    if (act == ACT_Q8_K) b += (size_t) NTE * K + (size_t) NTE * (K / 256) * 4 + (size_t) NTE * (K / 16) * 2;
+    else if (act == ACT_Q8_0) b += (size_t) NTE * K + (size_t) NTE * (K / 32) * 4;
+    else b += (size_t) NTE * K * 2;
+    return b + 64;
+}
+
+template <int WF>
+__global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
+    constexpr int AF = wfmt<WF>::ACT;
+    constexpr int C = wfmt<WF>::C;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_wcnt[4];
+    const int K = a.nsb * 256, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = blockIdx.x * 4 + wave, m = blockIdx.z, e = blockIdx.y;
+    float * s_acc = (float *) smem;                                  // [4][NTE][64]
+    char * p = smem + 4 * NTE * TILE * 4;
+    int8_t * sq = nullptr; float * sd32 = nullptr; float * sd256 = nullptr; int16_t * sbs = nullptr; uint16_t * sh = nullptr;
+    if constexpr (AF == ACT_Q8_K) {
+        sq = (int8_t *) p; p += NTE * K;
+        sd256 = (float *) p; p += NTE * (K / 256) * 4;
+        sbs = (int16_t *) p; p += NTE * (K / 16) * 2;
+    } else if constexpr (AF == ACT_Q8_0) {
+        sq = (int8_t *) p; p += NTE * K;
+        sd32 = (float *) p; p += NTE * (K / 32) * 4;
+    } else {
+        sh = (uint16_t *) p; p += NTE * K * 2;
+    }
+    const int n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
+    if (a.cap_counts && blockIdx.x == 0 && m == 0) {                // grouping capture, one block per expert
+        int off = 0;
+        for (int r = 0; r < a.n_tok * a.k; ++r) off += a.sel[r] < e;
+        for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
+        if (tid == 0) {
+            a.cap_counts[e] = n_items;
+            a.cap_offsets[e] = off;
+            if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
+        }
+    }
+    if (n_items == 0) return;
+    const bool has_tile = tile < a.tiles;
+    const uint8_t * wbase = a.w[m] + (int64_t) e * a.mat_bytes;
+    const uint16_t * dbase = WF == WF_Q6_K ? a.dpl[m] + (int64_t) e * a.dpl_elems : nullptr;
+    const uint4 * wt = (const uint4 *) wbase + (size_t) (has_tile ? tile : 0) * a.nsb * C * TILE + lane;
+    float * sacc = s_acc + (wave * NTE) * TILE + lane;
+
+    for (int c0 = 0; c0 < n_items; c0 += NTE) {
+        const int nt = min(NTE, n_items - c0);
+        uint4 u0[C], u1[C];
+        if (has_tile) {
+            load_unit<WF>(wt, u0);
+            if (a.nsb > 1) load_unit<WF>(wt + (size_t) C * TILE, u1);
+        }
+        __syncthreads();
+        stage_acts<AF>(a, nt, [&](int tt) { const int it = s_list[c0 + tt]; return a.act_by_route ? it : it / a.k; },
+                       K, sq, sd32, sd256, sbs, sh);
+        for (int tt = 0; tt < nt; ++tt) sacc[tt * TILE] = 0.0f;
+        __syncthreads();
+        if (has_tile) {
+            for (int sb = 0; sb < a.nsb; sb += 2) {
+                const uint16_t * dp0 = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb) * TILE + lane : nullptr;
+                gemv_unit<WF>(u0, dp0, sb, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, sacc);
+                if (sb + 2 < a.nsb) load_unit<WF>(wt + (size_t) (sb + 2) * C * TILE, u0);
+                if (sb + 1 < a.nsb) {
+                    const uint16_t * dp1 = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb + 1) * TILE + lane : nullptr;
+                    gemv_unit<WF>(u1, dp1, sb + 1, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, sacc);
+                    if (sb + 3 < a.nsb) load_unit<WF>(wt + (size_t) (sb + 3) * C * TILE, u1);
+                }
+            }
+            const int row = tile * TILE + lane;
+            if (row < a.rows)
+                for (int tt = 0; tt < nt; ++tt) {
+                    const int it = s_list[c0 + tt];
+                    float y = sacc[tt * TILE];
+                    if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
+                    a.out[m][(int64_t) it * a.out_ld + row] = y;
+                }
+        }
+    }
+}
+
+// MFMA variant for Q4_K and Q8_0 weights (v_mfma_i32_16x16x32_i8). The product is computed as
+// C[token][row] = A[token][k] . B[k][row] with A = the encoded activations (from LDS) and B = the
+// weights, so every lane ends with 4 tokens x 1 row and applies its own row's block scales. One
+// wave owns a 16-row group over the full K and accumulates its row in block order, which is the
+// CPU oracle's summation order. Layout "m16": per (16-row group, 256-column unit) the integer
+// values are stored chunk-major for the lanes (lane l = (k-slice l/16, row l%16) owns 8 bytes of
+// each 32-element sub-block), followed by the 16 rows' scale headers:
+//   Q4_K 2304 B = 2 x 1 KiB nibble chunks + 16 x 16 B (d, dmin, scales)
+//   Q8_0 4352 B = 4 x 1 KiB int8 chunks   + 16 x 16 B (eight f16 block scales)
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+template <int WF> struct m16fmt;
+template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constexpr int BYTES = 2304; static constexpr int PF = 8; };
+template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int PF = 4; };
+constexpr int MT = 16;                  // tokens per MFMA pass
+
+__host__ __device__ inline size_t gemv_mfma_lds_bytes(int wf, int K) {
+    const size_t KP = (size_t) K + 16;
+    if (wf == WF_Q4_K) return MT * KP + (size_t) MT * (K / 32) * 4 + (size_t) MT * (K / 256) * 4 + 64;
+    return MT * KP + (size_t) MT * (K / 32) * 4 + 64;
+}
+
+template <int WF>
+__device__ __forceinline__ void m16_load(const uint4 * __restrict__ unit, int lane, uint4 (&qs)[m16fmt<WF>::QS], uint4 & hd) {
+#pragma unroll
+    for (int c = 0; c < m16fmt<WF>::QS; ++c) qs[c] = unit[c * 64 + lane];
+    hd = unit[m16fmt<WF>::QS * 64 + (lane & 15)];
+}
+
+template <int WF>
+__device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], const uint4 & hd, int sb, int K, int lane,
+                                         const int8_t * sq, const int * sbs2, const float * sdx, int nsb, float (&acc)[4]) {
+    const int q = lane >> 4, r = lane & 15, KP = K + 16;
+    const int8_t * arow = sq + r * KP + sb * 256 + 8 * q;          // A: token r, k-slice q
+    const v4i_t zero = {0, 0, 0, 0};
+    if constexpr (WF == WF_Q4_K) {
+        const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+        // 6-bit scales / mins of sub-blocks 0-3 and 4-7, four per dword (GGUF K-quant packing)
+        const uint32_t sc03 = hd.y & 0x3f3f3f3fu, mn03 = hd.z & 0x3f3f3f3fu;
+        const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn47 = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+        const uint32_t w[8] = {qs[0].x, qs[0].y, qs[0].z, qs[0].w, qs[1].x, qs[1].y, qs[1].z, qs[1].w};
+        int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {                               // sub-block j = nibble half of pair j/2
+            const int pr = j >> 1;
+            const uint32_t b0 = (j & 1) ? (w[2 * pr] >> 4) & 0x0f0f0f0fu : w[2 * pr] & 0x0f0f0f0fu;
+            const uint32_t b1 = (j & 1) ? (w[2 * pr + 1] >> 4) & 0x0f0f0f0fu : w[2 * pr + 1] & 0x0f0f0f0fu;
+            const long B = (long) (((uint64_t) b1 << 32) | b0);
+            const long A = *(const long *) (arow + 32 * j);
+            const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+            const int scj = (int) (((j < 4 ? sc03 : sc47) >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sumi[i] += scj * C[i];
+        }
+        // min correction sum_j m_j[row] * bsum_j[token] as an fp32 16x16x4 product (two k-halves):
+        // integer products < 2^19 and sums < 2^23, so the fp32 result is exact
+        const int * bsr = sbs2 + r * (K / 32) + sb * 8;              // token r (A operand row)
+        const float a0 = (float) bsr[q], a1 = (float) bsr[q + 4];
+        const float b0 = (float) ((mn03 >> (8 * q)) & 0xffu), b1 = (float) ((mn47 >> (8 * q)) & 0xffu);
+        v4f_t S = {0.0f, 0.0f, 0.0f, 0.0f};
+        S = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, S, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float dx = sdx[(4 * q + i) * nsb + sb];
+            acc[i] += (d * dx) * (float) sumi[i] - (dmin * dx) * S[i];
+        }
+    } else {
+        uint16_t dh[8];
+        __builtin_memcpy(dh, &hd, 16);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint4 v = qs[b >> 1];
+            const uint32_t lo = (b & 1) ? v.z : v.x, hi = (b & 1) ? v.w : v.y;
+            const long B = (long) (((uint64_t) hi << 32) | lo);
+            const long A = *(const long *) (arow + 32 * b);
+            const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+            const float dw = h2f(dh[b]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += (dw * sdx[(4 * q + i) * (K / 32) + sb * 8 + b]) * (float) C[i];
+        }
+    }
+}
+
+// grid: x = 16-row group quads, y = expert (grouped) or 16-token chunk (dense), z = matrix + n_mats *
+// route pass (grouped: routes [16*pass, 16*pass+16) of the expert, so hot experts spread over blocks)
+template <int WF>
+__global__ void __launch_bounds__(256) k_gemv_mfma(GemvArgs a) {
+    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES, PF = m16fmt<WF>::PF;
+    constexpr int AF = wfmt<WF>::ACT;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_wcnt[4];
+    const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g16 = blockIdx.x * 4 + wave, m = blockIdx.z % a.n_mats, pass = blockIdx.z / a.n_mats;
+    int8_t * sq = (int8_t *) smem;                                   // [MT][K+16]
+    int * sbs2 = (int *) (smem + MT * KP);                           // Q4_K: [MT][K/32] sums of 32
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + MT * (K / 32))  // Q4_K: [MT][K/256]
+                                 : (float *) (smem + MT * KP);       // Q8_0: [MT][K/32]
+    int n_items, c0, e = 0;
+    if (a.grouped) {
+        e = blockIdx.y;
+        n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
+        if (a.cap_counts && blockIdx.x == 0 && blockIdx.z == 0) {
+            int off = 0;
+            for (int rr = 0; rr < a.n_tok * a.k; ++rr) off += a.sel[rr] < e;
+            for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
+            if (tid == 0) {
+                a.cap_counts[e] = n_items;
+                a.cap_offsets[e] = off;
+                if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
+            }
+        }
+        c0 = pass * MT;
+    } else {
+        n_items = a.n_tok;
+        c0 = blockIdx.y * MT;
+    }
+    if (c0 >= n_items) return;
+    const int nt = min(MT, n_items - c0);
+    const bool has = g16 < a.tiles;
+    const uint4 * ub = (const uint4 *) (a.w[m] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * a.nsb * UB);
+    // the wave's first PF units are requested before the activations are staged
+    uint4 pq[PF][QS], ph[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+        if (has && j < a.nsb) m16_load<WF>(ub + (size_t) j * (UB / 16), lane, pq[j], ph[j]);
+
+    {
+        __shared__ int s_tok[MT];
+        if (tid < MT) {
+            int tok = 0;
+            if (tid < nt) {
+                const int it = a.grouped ? s_list[c0 + tid] : c0 + tid;
+                tok = a.grouped && !a.act_by_route ? it / a.k : it;
+            }
+            s_tok[tid] = tok;
+        }
+        __syncthreads();
+        const int per = K / 16;                                      // 16-byte items per token row
+        copy16<256>(MT * per,
+            [&](int i) { return (const uint4 *) (a.act.q + (int64_t) s_tok[i / per] * K) + i % per; },
+            [&](int i) { return (uint4 *) (sq + (i / per) * KP) + i % per; });
+        if constexpr (AF == ACT_Q8_K) {
+            const int ns = K / 32, nd = K / 256;
+            for (int i = tid; i < MT * ns; i += 256) {
+                const int tt = i / ns, j = i % ns;
+                const int16_t * bs = a.act.bs + (int64_t) s_tok[tt] * (K / 16);
+                sbs2[i] = tt < nt ? (int) bs[2 * j] + (int) bs[2 * j + 1] : 0;
+            }
+            for (int i = tid; i < MT * nd; i += 256) sdx[i] = (i / nd) < nt ? a.act.d256[(int64_t) s_tok[i / nd] * nd + i % nd] : 0.0f;
+        } else {
+            const int nd = K / 32;
+            for (int i = tid; i < MT * nd; i += 256) sdx[i] = (i / nd) < nt ? a.act.d32[(int64_t) s_tok[i / nd] * nd + i % nd] : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (!has) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+        if (j < a.nsb) m16_unit<WF>(pq[j], ph[j], j, K, lane, sq, sbs2, sdx, a.nsb, acc);
+    for (int sb = PF; sb < a.nsb; ++sb) {
+        uint4 uq[QS], uh;
+        m16_load<WF>(ub + (size_t) sb * (UB / 16), lane, uq, uh);
+        m16_unit<WF>(uq, uh, sb, K, lane, sq, sbs2, sdx, a.nsb, acc);
+    }
+    const int q = lane >> 4, row = g16 * 16 + (lane & 15);
+    if (row < a.rows) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * q + i;
+            if (t >= nt) continue;
+            const int it = a.grouped ? s_list[c0 + t] : c0 + t;
+            float y = acc[i];
+            if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+            else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
             a.out[m][(int64_t) it * a.out_ld + row] = y;
         }
     }
@@ -577,11 +880,11 @@ struct AttnArgs {
 
 // QK-norm, |temp|, RoPE, KV append, sigmoid gate. One block per token, one wave per head.
 __global__ void __launch_bounds__(256) k_qkv_post(AttnArgs a) {
-    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int hd = a.hd, nh = a.nh, nkv = a.nkv;
-    const float * row = a.qkvg + (int64_t) t * a.R;
+    const float * __restrict__ row = a.qkvg + (int64_t) t * a.R;
     const int pos = a.n_past[t], slot = a.slot_idx[t];
-    for (int h = wave; h < nh + 2 * nkv; h += 4) {
+    for (int h = blockIdx.x * 4 + wave; h < nh + 2 * nkv; h += gridDim.x * 4) {
         const bool isq = h < nh, isk = h >= nh && h < nh + nkv;
         const float * src = row + (int64_t) h * hd;          // q heads, then k heads, then v heads
         if (!isq && !isk) {                                  // V: plain f16 store
@@ -593,8 +896,13 @@ __global__ void __launch_bounds__(256) k_qkv_post(AttnArgs a) {
             }
             continue;
         }
+        float xv[4];
         double ss = 0.0;
-        for (int i = lane; i < hd; i += 64) ss += (double) (src[i] * src[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { const int i = lane + 64 * j; xv[j] = i < hd ? src[i] : 0.0f; }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss += (double) (xv[j] * xv[j]);
+        for (int i = lane + 256; i < hd; i += 64) ss += (double) (src[i] * src[i]);
         ss = wave_tree_d(ss);
         const float sc = 1.0f / sqrtf((float) (ss / (double) hd) + a.qk_eps);
         const float tmp = isq ? a.temp[h] : 1.0f;
@@ -618,6 +926,7 @@ __global__ void __launch_bounds__(256) k_qkv_post(AttnArgs a) {
         }
     }
     // gate = sigmoid(W_g x): the last nh columns of the fused projection
+    if (blockIdx.x == 0)
     for (int h = threadIdx.x; h < nh; h += 256)
         a.gate[(int64_t) t * nh + h] = z_sigmoid(row[(int64_t) (nh + 2 * nkv) * hd + h]);
 }
@@ -652,11 +961,11 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
         const uint16_t * vb = a.vc + (((int64_t) slot * a.nkv + g) * a.S + r0) * hd;
         __syncthreads();
         const int vpr = hd / 8;                                      // uint4 per row
-        for (int i = tid; i < nr * vpr; i += 256) {
-            const int r = i / vpr, cc = i % vpr;
-            *(uint4 *) (sk + r * ldk + cc * 8) = ((const uint4 *) (kb + (int64_t) r * hd))[cc];
-            *(uint4 *) (sv + r * ldk + cc * 8) = ((const uint4 *) (vb + (int64_t) r * hd))[cc];
-        }
+        copy16<256>(2 * nr * vpr,
+            [&](int i) { const int w = i / (nr * vpr), j = i % (nr * vpr);
+                         return (const uint4 *) ((w ? vb : kb) + (int64_t) (j / vpr) * hd) + j % vpr; },
+            [&](int i) { const int w = i / (nr * vpr), j = i % (nr * vpr);
+                         return (uint4 *) ((w ? sv : sk) + (j / vpr) * ldk) + j % vpr; });
         for (int i = tid; i < grp * hd; i += 256) sq[i] = a.q16[((int64_t) t * a.nh + g * grp) * hd + i];
         __syncthreads();
         // scores: wave = head of the group (looped), lane = row
@@ -696,31 +1005,73 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     }
 }
 
-// Merge the chunks of every head of one token, apply the sigmoid gate, encode for W_o.
+// Merge the chunks of the query-head group of one KV head for one token, apply the per-head sigmoid
+// gate. grid (nkv, T), one wave per head of the group. The group's grp*hd outputs are contiguous in
+// the token's row; when they cover whole encoding blocks the block encodes them for W_o here,
+// otherwise a separate encode pass follows (a.act_fmt == ACT_NONE).
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     extern __shared__ float sm_ac[];
-    const int t = blockIdx.x, hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv, tid = threadIdx.x;
+    const int g = blockIdx.x, t = blockIdx.y, hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int item0 = 0;
     for (int u = 0; u < t; ++u) item0 += (a.n_past[u] + 1 + ATT_CH - 1) / ATT_CH;
     const int nc = (a.n_past[t] + 1 + ATT_CH - 1) / ATT_CH;
-    float * o = sm_ac;                                               // [nh*hd]
-    for (int idx = tid; idx < nh * hd; idx += 256) {
-        const int h = idx / hd, i = idx % hd, g = h / grp, hh = h % grp;
-        float M = -__builtin_inff();
-        for (int c = 0; c < nc; ++c) M = fmaxf(M, a.part_ml[((int64_t) ((item0 + c) * nkv + g) * grp + hh) * 2]);
-        float den = 0.0f, num = 0.0f;
-        for (int c = 0; c < nc; ++c) {
+    float * ob = sm_ac;                                              // [grp*hd]
+    float * sw = ob + grp * hd;                                      // [4][nc] chunk weights per wave
+    const float * __restrict__ ml = a.part_ml;
+    const float * __restrict__ po = a.part_o;
+    for (int hh = wave; hh < grp; hh += 4) {
+        float * w = sw + wave * nc;
+        float m = -__builtin_inff();
+        for (int c = lane; c < nc; c += 64) m = fmaxf(m, ml[((int64_t) ((item0 + c) * nkv + g) * grp + hh) * 2]);
+        const float M = wave_max_f(m);
+        float den = 0.0f;
+        for (int c = lane; c < nc; c += 64) {
             const int64_t it = (int64_t) (item0 + c) * nkv + g;
-            const float w = z_expf(a.part_ml[(it * grp + hh) * 2] - M);
-            den = __builtin_fmaf(w, a.part_ml[(it * grp + hh) * 2 + 1], den);
-            num = __builtin_fmaf(w, a.part_o[(it * grp + hh) * hd + i], num);
+            const float e = z_expf(ml[(it * grp + hh) * 2] - M);
+            w[c] = e;
+            den = __builtin_fmaf(e, ml[(it * grp + hh) * 2 + 1], den);
         }
-        const float v = (num / den) * a.gate[(int64_t) t * nh + h];
-        o[idx] = v;
-        if (a.o_out) a.o_out[(int64_t) t * nh * hd + idx] = v;
+        den = wave_tree_f(den);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        const float gt = a.gate[(int64_t) t * nh + g * grp + hh] / den;
+        for (int pi = lane; pi < hd / 2; pi += 64) {
+            float o0 = 0.0f, o1 = 0.0f;
+            int c = 0;
+            for (; c + 4 <= nc; c += 4) {
+                float2 v[4]; float ww[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[j] = *(const float2 *) (po + ((((int64_t) (item0 + c + j) * nkv + g) * grp + hh) * hd) + 2 * pi);
+                    ww[j] = w[c + j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { o0 = __builtin_fmaf(ww[j], v[j].x, o0); o1 = __builtin_fmaf(ww[j], v[j].y, o1); }
+            }
+            for (; c < nc; ++c) {
+                const float2 v = *(const float2 *) (po + ((((int64_t) (item0 + c) * nkv + g) * grp + hh) * hd) + 2 * pi);
+                o0 = __builtin_fmaf(w[c], v.x, o0); o1 = __builtin_fmaf(w[c], v.y, o1);
+            }
+            ob[hh * hd + 2 * pi] = o0 * gt;
+            ob[hh * hd + 2 * pi + 1] = o1 * gt;
+        }
     }
     __syncthreads();
-    encode_row_rt(a.act_fmt, o, nh * hd, a.act, t);
+    const int base = g * grp * hd;
+    for (int i = tid; i < grp * hd; i += 256) a.o_out[(int64_t) t * nh * hd + base + i] = ob[i];
+    if (a.act_fmt == ACT_NONE) return;
+    // the group's slice [base, base + grp*hd) of the token row, encoded in place of the row's blocks
+    const int Kp = kpad(nh * hd);
+    if (a.act_fmt == ACT_Q8_K)
+        encode_row<ACT_Q8_K>(ob, grp * hd, a.act.q + (int64_t) t * Kp + base, nullptr,
+                             a.act.d256 + (int64_t) t * (Kp / 256) + base / 256, a.act.bs + (int64_t) t * (Kp / 16) + base / 16, nullptr);
+    else if (a.act_fmt == ACT_Q8_0)
+        encode_row<ACT_Q8_0>(ob, grp * hd, a.act.q + (int64_t) t * Kp + base, a.act.d32 + (int64_t) t * (Kp / 32) + base / 32,
+                             nullptr, nullptr, nullptr);
+    else
+        encode_row<ACT_F16>(ob, grp * hd, nullptr, nullptr, nullptr, nullptr, a.act.h + (int64_t) t * Kp + base);
 }
 
 // ------------------------------------------------------------------ router (exact contract)
@@ -740,104 +1091,217 @@ struct RouterArgs {
     const float * logit_bias;               // [E] or null
     const float * mask;                     // [E] additive 0/-inf or null
     const float * sc_bias;                  // router_bias [E]
+    int tpb;                                // router_tail: tokens per block
     int32_t * sel; float * wsel;            // [T][k]
     float * cap_logits; float * cap_probs;  // [T][E] (nullable)
 };
 
 // rh[t][o] = lane-strided fma partials over d + xor butterfly, + bias (+ state * eda).
+// grid (ceil(rd/4), T): wave = output row, blockIdx.y = token. Loads are issued 8 at a time ahead
+// of the fma chain; the chain order (i = lane, lane+64, ... ascending) is the contract's.
 __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
-    const int lane = threadIdx.x & 63, o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, o = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
     if (o >= a.rd) return;
-    const float * w = a.w_down + (int64_t) o * a.d;
-    for (int t = 0; t < a.T; ++t) {
-        const float * x = a.x + (int64_t) t * a.d;
-        float acc = 0.0f;
-        for (int i = lane; i < a.d; i += 64) acc = __builtin_fmaf(w[i], x[i], acc);
-        float v = wave_tree_f(acc) + a.b_down[o];
-        if (a.eda && a.state_in) v = v + a.state_in[(int64_t) t * a.rd + o] * a.eda[o];
-        if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+    const float * __restrict__ w = a.w_down + (int64_t) o * a.d;
+    const float * __restrict__ x = a.x + (int64_t) t * a.d;
+    float acc = 0.0f;
+    int i = lane;
+    for (; i + 64 * 7 < a.d; i += 64 * 8) {
+        float wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { wv[j] = w[i + 64 * j]; xv[j] = x[i + 64 * j]; }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
+    }
+    for (; i < a.d; i += 64) acc = __builtin_fmaf(w[i], x[i], acc);
+    float v = wave_tree_f(acc) + a.b_down[o];
+    if (a.eda && a.state_in) v = v + a.state_in[(int64_t) t * a.rd + o] * a.eda[o];
+    if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+}
+
+// one fmaf chain per output over LDS-resident W^T (i ascending); 8 LDS loads issued per step
+__device__ __forceinline__ float chain_lds(const float * wt, int ld, int o, const float * x, int n) {
+    float acc = 0.0f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        float wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { wv[j] = wt[(i + j) * ld + o]; xv[j] = x[i + j]; }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
+    }
+    for (; i < n; ++i) acc = __builtin_fmaf(wt[i * ld + o], x[i], acc);
+    return acc;
+}
+
+// One block per RT_TOK tokens. Norm by one wave per token; the three MLP layers as per-output fmaf
+// chains (i ascending) over W^T staged through LDS in RT_CI-row chunks (one staging serves every
+// token of the block); softmax + top-k by one wave per token (ties to the lower expert index).
+constexpr int RT_TOK = 8;                // tokens per thread chain group (block serves 2*RT_TOK for rd=128)
+constexpr int RT_CI = 128;
+
+// out[t][o] = f(chain_i W^T[i][o] * x[t][i] + b[o]) for t < nt, o < n_out; W^T is [n_in][n_out] in HBM
+template <bool GELU>
+__device__ __forceinline__ void rt_layer(const float * __restrict__ wt, const float * __restrict__ b, int n_in, int n_out,
+                                         const float * x, int ldx, float * out, int ldo, int nt, float * s_w,
+                                         const float * __restrict__ bias2, const float * __restrict__ bias3) {
+    const int tid = threadIdx.x;
+    const int G = 256 / n_out;                      // thread groups over tokens
+    const int o = tid % n_out, tg = tid / n_out;
+    const bool active = tg < G;
+    float acc[RT_TOK];
+#pragma unroll
+    for (int j = 0; j < RT_TOK; ++j) acc[j] = 0.0f;
+    for (int i0 = 0; i0 < n_in; i0 += RT_CI) {
+        const int ci = min(RT_CI, n_in - i0);
+        __syncthreads();
+        {   // stage W^T rows [i0, i0+ci)
+            const int n = ci * n_out, nv = n / 4;
+            const float4 * src = (const float4 *) (wt + (int64_t) i0 * n_out);
+            copy16<256>(nv, [&](int v) { return (const uint4 *) (src + v); }, [&](int v) { return (uint4 *) ((float4 *) s_w + v); });
+            for (int e = nv * 4 + tid; e < n; e += 256) s_w[e] = wt[(int64_t) i0 * n_out + e];
+        }
+        __syncthreads();
+        if (active) {
+            // 8 inputs per batch: all LDS reads of the batch are issued before its fmas
+            int i = 0;
+            for (; i + 8 <= ci; i += 8) {
+                float w[8], xv[RT_TOK][8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) w[u] = s_w[(i + u) * n_out + o];
+#pragma unroll
+                for (int j = 0; j < RT_TOK; ++j) {
+                    const int t = min(tg + G * j, nt - 1);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) xv[j][u] = x[t * ldx + i0 + i + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+#pragma unroll
+                    for (int j = 0; j < RT_TOK; ++j) acc[j] = __builtin_fmaf(w[u], xv[j][u], acc[j]);
+            }
+            for (; i < ci; ++i) {
+                const float w = s_w[i * n_out + o];
+#pragma unroll
+                for (int j = 0; j < RT_TOK; ++j) acc[j] = __builtin_fmaf(w, x[min(tg + G * j, nt - 1) * ldx + i0 + i], acc[j]);
+            }
+        }
+    }
+    __syncthreads();
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < RT_TOK; ++j) {
+            const int t = tg + G * j;
+            if (t >= nt) continue;
+            float v = acc[j];
+            if (b) v = v + b[o];
+            if (GELU) v = z_gelu(v);
+            if (bias2) v = v + bias2[o];
+            if (bias3) v = v + bias3[o];
+            out[t * ldo + o] = v;
+        }
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
+    extern __shared__ float sm_rt[];
+    const int rd = a.rd, E = a.E;
+    float * s_a = sm_rt;                       // [tpb][rd]
+    float * s_b = s_a + a.tpb * rd;            // [tpb][max(rd, E)]
+    float * s_w = s_b + a.tpb * (rd > E ? rd : E);    // [RT_CI][max(rd, E)]
+    const int t0 = blockIdx.x * a.tpb, nt = min(a.tpb, a.T - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int tt = wave; tt < nt; tt += 4) {
+        const float * __restrict__ rh = a.rh + (int64_t) (t0 + tt) * rd;
+        double part = 0.0;
+        for (int i = lane; i < rd; i += 64) part += (double) (rh[i] * rh[i]);
+        const double ss = wave_tree_d(part);
+        const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
+        for (int i = lane; i < rd; i += 64) s_a[tt * rd + i] = (rh[i] * scale) * a.norm_w[i];
+    }
+    rt_layer<true>(a.w0t, a.b0, rd, rd, s_a, rd, s_b, rd, nt, s_w, nullptr, nullptr);
+    rt_layer<true>(a.w2t, a.b2, rd, rd, s_b, rd, s_a, rd, nt, s_w, nullptr, nullptr);
+    rt_layer<false>(a.w4t, nullptr, rd, E, s_a, rd, s_b, E, nt, s_w, a.logit_bias, a.mask);
+    for (int tt = wave; tt < nt; tt += 4) {
+        const int t = t0 + tt;
+        const float * lgs = s_b + tt * E;
+        float lg[4], ex[4], pr[4], sc[4];
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            lg[j] = e < E ? lgs[e] : -__builtin_inff();
+            mx = fmaxf(mx, lg[j]);
+        }
+        mx = wave_max_f(mx);
+        double ps = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            ex[j] = e < E ? z_expf(lg[j] - mx) : 0.0f;
+            if (e < E) ps += (double) ex[j];
+        }
+        const float inv = (float) (1.0 / wave_tree_d(ps));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            pr[j] = ex[j] * inv;
+            sc[j] = -__builtin_inff();
+            if (e < E) {
+                sc[j] = pr[j] + a.sc_bias[e];
+                if (a.mask) sc[j] = sc[j] + a.mask[e];
+                if (a.cap_logits) a.cap_logits[(int64_t) t * E + e] = lg[j];
+                if (a.cap_probs) a.cap_probs[(int64_t) t * E + e] = pr[j];
+            }
+        }
+        bool taken[4] = {false, false, false, false};
+        for (int j = 0; j < a.k; ++j) {
+            float bv = 0.0f; int bi = 0x7fffffff; float bp = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = lane + 64 * q;
+                if (e < E && !taken[q] && (bi == 0x7fffffff || sc[q] > bv)) { bv = sc[q]; bi = e; bp = pr[q]; }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, WAVE), op = __shfl_xor(bp, off, WAVE);
+                const int oi = __shfl_xor(bi, off, WAVE);
+                const bool better = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+                if (better) { bv = ov; bi = oi; bp = op; }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) if (lane + 64 * q == bi) taken[q] = true;
+            if (lane == 0) { a.sel[(int64_t) t * a.k + j] = bi; a.wsel[(int64_t) t * a.k + j] = bp; }
+        }
     }
 }
 
-// One wave per token: norm, MLP, softmax, top-k (ties to the lower expert index).
-__global__ void __launch_bounds__(64) k_router_tail(RouterArgs a) {
-    __shared__ float s_a[512], s_b[512];
-    const int t = blockIdx.x, lane = threadIdx.x, rd = a.rd, E = a.E;
-    const float * rh = a.rh + (int64_t) t * rd;
-    double part = 0.0;
-    for (int i = lane; i < rd; i += 64) part += (double) (rh[i] * rh[i]);
-    const double ss = wave_tree_d(part);
-    const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
-    for (int i = lane; i < rd; i += 64) s_a[i] = (rh[i] * scale) * a.norm_w[i];
+// tokens one router_tail block serves: every MLP layer's thread groups (256 / width) x RT_TOK
+__host__ inline int router_tail_tpb(int rd, int E) {
+    const int m = rd > E ? rd : E;
+    const int t = (256 / m) * RT_TOK;
+    return t < 16 ? t : 16;
+}
+__host__ inline size_t router_tail_lds(int rd, int E) {
+    const int m = rd > E ? rd : E, tpb = router_tail_tpb(rd, E);
+    return (size_t) (tpb * rd + tpb * m + RT_CI * m) * 4;
+}
+
+// y = up * silu(gate) of one route (or dense token) row, encoded for the down matmul.
+struct SwigluArgs {
+    const float * g; const float * u; int ff;
+    ActBuf act; int act_fmt;
+};
+
+__global__ void __launch_bounds__(256) k_swiglu_encode(SwigluArgs a) {
+    extern __shared__ float sm_sw[];
+    const int r = blockIdx.x, tid = threadIdx.x, Kp = kpad(a.ff);
+    const float * __restrict__ g = a.g + (int64_t) r * a.ff;
+    const float * __restrict__ u = a.u + (int64_t) r * a.ff;
+    for (int i = tid; i < Kp; i += 256) sm_sw[i] = i < a.ff ? u[i] * z_silu(g[i]) : 0.0f;
     __syncthreads();
-    for (int o = lane; o < rd; o += 64) {
-        float acc = 0.0f;
-        for (int i = 0; i < rd; ++i) acc = __builtin_fmaf(a.w0t[(int64_t) i * rd + o], s_a[i], acc);
-        s_b[o] = z_gelu(acc + a.b0[o]);
-    }
-    __syncthreads();
-    for (int o = lane; o < rd; o += 64) {
-        float acc = 0.0f;
-        for (int i = 0; i < rd; ++i) acc = __builtin_fmaf(a.w2t[(int64_t) i * rd + o], s_b[i], acc);
-        s_a[o] = z_gelu(acc + a.b2[o]);
-    }
-    __syncthreads();
-    // logits: up to 4 experts per lane (E <= 256)
-    float lg[4], ex[4], pr[4], sc[4];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j;
-        lg[j] = -__builtin_inff();
-        if (e < E) {
-            float acc = 0.0f;
-            for (int i = 0; i < rd; ++i) acc = __builtin_fmaf(a.w4t[(int64_t) i * E + e], s_a[i], acc);
-            if (a.logit_bias) acc = acc + a.logit_bias[e];
-            if (a.mask) acc = acc + a.mask[e];
-            lg[j] = acc;
-        }
-        mx = fmaxf(mx, lg[j]);
-    }
-    mx = wave_max_f(mx);
-    double ps = 0.0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j;
-        ex[j] = e < E ? z_expf(lg[j] - mx) : 0.0f;
-        if (e < E) ps += (double) ex[j];
-    }
-    const float inv = (float) (1.0 / wave_tree_d(ps));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j;
-        pr[j] = ex[j] * inv;
-        sc[j] = -__builtin_inff();
-        if (e < E) {
-            sc[j] = pr[j] + a.sc_bias[e];
-            if (a.mask) sc[j] = sc[j] + a.mask[e];
-            if (a.cap_logits) a.cap_logits[(int64_t) t * E + e] = lg[j];
-            if (a.cap_probs) a.cap_probs[(int64_t) t * E + e] = pr[j];
-        }
-    }
-    bool taken[4] = {false, false, false, false};
-    for (int j = 0; j < a.k; ++j) {
-        float bv = 0.0f; int bi = 0x7fffffff; float bp = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = lane + 64 * q;
-            if (e < E && !taken[q] && (bi == 0x7fffffff || sc[q] > bv)) { bv = sc[q]; bi = e; bp = pr[q]; }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, WAVE), op = __shfl_xor(bp, off, WAVE);
-            const int oi = __shfl_xor(bi, off, WAVE);
-            const bool better = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-            if (better) { bv = ov; bi = oi; bp = op; }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) if (lane + 64 * q == bi) taken[q] = true;
-        if (lane == 0) { a.sel[(int64_t) t * a.k + j] = bi; a.wsel[(int64_t) t * a.k + j] = bp; }
-    }
+    encode_row_rt(a.act_fmt, sm_sw, a.ff, a.act, r);
 }
 
 } // namespace z2d

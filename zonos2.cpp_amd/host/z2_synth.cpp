@@ -3,8 +3,9 @@
 // The benchmark configurations are random-init models (N(0, sigma) matrices quantized to a GGUF
 // block type), in the style of the reference's dummy-model generator
 // (scripts/make-dummy-model.py:53-142, tensor names/shapes mirrored there). Values are a pure
-// function of (seed, stream, element index): a splitmix64 counter feeds Box-Muller, so any slice
-// of any tensor can be regenerated independently and in parallel.
+// function of (seed, stream, element index): a splitmix64 counter feeds an inverse-CDF transform, so any slice
+// of any tensor can be regenerated independently and in parallel. Normal deviates come from the
+// inverse CDF of a 53-bit uniform.
 //
 // The quantizers are this project's own simple min/max fits. Parity is defined on the same
 // quantized bytes for the CPU oracle and the device, so they need not match ggml's quantizer.
@@ -28,6 +29,29 @@ inline uint64_t splitmix64(uint64_t x) {
     return x ^ (x >> 31);
 }
 
+// Standard normal by inversion of the CDF: P. J. Acklam's rational approximation (2003;
+// relative error < 1.2e-9), which needs a log/sqrt only in the 2 x 2.425% tails.
+inline double inv_norm_cdf(double p) {
+    static const double a[6] = {-3.969683028665376e+01, 2.209460984245205e+02, -2.759285104469687e+02,
+                                1.383577518672690e+02, -3.066479806614716e+01, 2.506628277459239e+00};
+    static const double b[5] = {-5.447609879822406e+01, 1.615858368580409e+02, -1.556989798598866e+02,
+                                6.680131188771972e+01, -1.328068155288572e+01};
+    static const double c[6] = {-7.784894002430293e-03, -3.223964580411365e-01, -2.400758277161838e+00,
+                                -2.549732539343734e+00, 4.374664141464968e+00, 2.938163982698783e+00};
+    static const double d[4] = {7.784695709041462e-03, 3.224671290700398e-01, 2.445134137142996e+00,
+                                3.754408661907416e+00};
+    const double plow = 0.02425;
+    if (p < plow || p > 1.0 - plow) {
+        const double q = std::sqrt(-2.0 * std::log(p < plow ? p : 1.0 - p));
+        const double x = (((((c[0] * q + c[1]) * q + c[2]) * q + c[3]) * q + c[4]) * q + c[5]) /
+                         ((((d[0] * q + d[1]) * q + d[2]) * q + d[3]) * q + 1.0);
+        return p < plow ? x : -x;
+    }
+    const double q = p - 0.5, r = q * q;
+    return (((((a[0] * r + a[1]) * r + a[2]) * r + a[3]) * r + a[4]) * r + a[5]) * q /
+           (((((b[0] * r + b[1]) * r + b[2]) * r + b[3]) * r + b[4]) * r + 1.0);
+}
+
 // kind: 0 normal(a, b) | 1 b*|normal(0,1)| | 2 constant a | 3 uniform integer in [a, b]
 inline float gen_value(uint64_t key, int64_t i, int kind, float a, float b) {
     if (kind == 2) return a;
@@ -36,9 +60,8 @@ inline float gen_value(uint64_t key, int64_t i, int kind, float a, float b) {
         const int64_t lo = (int64_t) a, hi = (int64_t) b;
         return (float) (lo + (int64_t) (x % (uint64_t) (hi - lo + 1)));
     }
-    const float u1 = (float) ((x >> 40) + 1) * (1.0f / 16777216.0f);      // (0, 1]
-    const float u2 = (float) (x & 0xffffffu) * (1.0f / 16777216.0f);     // [0, 1)
-    const float z = std::sqrt(-2.0f * std::log(u1)) * std::cos(6.28318530717958647692f * u2);
+    const double u = ((double) (x >> 11) + 0.5) * (1.0 / 9007199254740992.0);   // (0, 1)
+    const float z = (float) inv_norm_cdf(u);
     if (kind == 1) return b * std::fabs(z);
     return a + b * z;
 }

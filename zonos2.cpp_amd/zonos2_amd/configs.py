@@ -8,7 +8,9 @@ tier above the bulk type (F16 over Q8_0, Q8_0 over K-quants); every other matrix
 routers are kept F32 because the decode step's router is specified as fp32.
 
 Init: matrices N(0, 0.02); norm weights 1; attn_temp |N(0,1)| (the checkpoint stores |temp|,
-models/convert-zonos2-to-gguf.py:207); router_bias N(0, 1e-3); other 1-D biases N(0, 0.02).
+models/convert-zonos2-to-gguf.py:207); other 1-D biases N(0, 0.02). router_bias is N(0, router_bias_std)
+with std 0 by default: with N(0, 0.02) routers the softmax spread across experts is ~1e-4, so any
+larger selection bias would pin every token to the same few experts.
 """
 from __future__ import annotations
 
@@ -49,6 +51,7 @@ class ModelConfig:
     qk_norm_eps: float = 1e-6
     logit_softcap: float = 15.0
     expert_used: list[int] | None = None     # per layer; default all MoE with top_k
+    router_bias_std: float = 0.0
 
     def __post_init__(self):
         if self.expert_used is None:
@@ -123,7 +126,7 @@ class ModelConfig:
                 (b + "router_mlp2.bias", F32, (rd,), W),
                 (b + "router_mlp4.weight", F32, (rd, E), W),
                 (b + "router_norm.weight", F32, (rd,), (2, 1.0, 0.0)),
-                (b + "router_bias", F32, (E,), (0, 0.0, 1e-3)),
+                (b + "router_bias", F32, (E,), (0, 0.0, self.router_bias_std) if self.router_bias_std > 0 else (2, 0.0, 0.0)),
             ]
             if seen_moe:
                 out.append((b + "router_eda_scale", F32, (rd,), W))
@@ -145,7 +148,7 @@ class Workload:
 
 def C1() -> tuple[ModelConfig, Workload]:
     m = ModelConfig("tiny-moe-q8_0", n_layer=2, n_embd=256, n_head=8, n_head_kv=2, head_dim=32,
-                    n_expert=8, top_k=2, n_ff=512, bulk=Q8_0)
+                    n_expert=8, top_k=2, n_ff=512, bulk=Q8_0, router_bias_std=1e-4)
     w = Workload("c1-4req", n_slots=4, kv_lens=[3, 17, 64, 130], slot_cap=131, inject_embeddings=True)
     return m, w
 

@@ -1,7 +1,7 @@
 """Synthetic model weights, KV caches and step inputs (host memory, numpy).
 
 Every value is a pure function of (seed, tensor name, element index) computed by
-libzonos2_host.so (splitmix64 counter + Box-Muller, then the GGUF-format quantizers), so the CPU
+libzonos2_host.so (splitmix64 counter + inverse normal CDF, then the GGUF-format quantizers), so the CPU
 oracle and the device see identical bytes and any config can be regenerated on any host.
 """
 from __future__ import annotations

@@ -48,6 +48,8 @@ def lib() -> C.CDLL:
         "z2h_capture_bytes": (i64, [vp, i32, i32]),
         "z2h_read_capture": (i32, [vp, i32, i32, vp, C.c_size_t]),
         "z2h_device_bytes": (i64, [vp, i32]),
+        "z2h_profile_begin": (i32, [vp]),
+        "z2h_profile_end": (i32, [vp, vp, vp]),
         "z2h_last_error": (C.c_char_p, [vp]),
         "z2h_destroy": (None, [vp]),
     }
@@ -60,7 +62,10 @@ def lib() -> C.CDLL:
 EXPORTS = ("z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
-           "z2h_read_capture", "z2h_device_bytes", "z2h_last_error", "z2h_destroy")
+           "z2h_read_capture", "z2h_device_bytes", "z2h_profile_begin", "z2h_profile_end", "z2h_last_error",
+           "z2h_destroy")
+KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
+                   "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
 
 
 def _p(a):
@@ -152,6 +157,26 @@ class Context:
         out = np.empty(nb // 4, np.int32 if what in INT_CAPS else np.float32)
         self.check(lib().z2h_read_capture(self.ctx, layer, w, _p(out), nb))
         return out
+
+    def profile_begin(self):
+        self.check(lib().z2h_profile_begin(self.ctx))
+
+    def profile_end(self):
+        ms = np.zeros(len(KERNEL_FAMILIES), np.float64)
+        n = np.zeros(len(KERNEL_FAMILIES), np.int32)
+        self.check(lib().z2h_profile_end(self.ctx, _p(ms), _p(n)))
+        return {k: (float(ms[i]), int(n[i])) for i, k in enumerate(KERNEL_FAMILIES)}
+
+    def step_device(self, T, d_slot, d_npast, h_npast, d_ids, d_emb, d_logits, stream=None):
+        """Device pointers (ints) as produced by torch's data_ptr(); stream is a hipStream_t handle."""
+        h = np.ascontiguousarray(h_npast, np.int32)
+        self.check(lib().z2h_step_device(self.ctx, T, C.c_void_p(d_slot), C.c_void_p(d_npast), _p(h),
+                                         C.c_void_p(d_ids) if d_ids else None, C.c_void_p(d_emb) if d_emb else None,
+                                         C.c_void_p(d_logits), C.c_void_p(stream) if stream else None))
+
+    def moe_forward_device(self, layer, T, d_x, d_state, d_out, stream=None):
+        self.check(lib().z2h_moe_forward_device(self.ctx, layer, T, C.c_void_p(d_x), C.c_void_p(d_state) if d_state else None,
+                                                C.c_void_p(d_out), C.c_void_p(stream) if stream else None))
 
     def device_bytes(self, what: int) -> int:
         return int(lib().z2h_device_bytes(self.ctx, what))
