@@ -121,6 +121,11 @@ int z2h_set_capture(z2h_ctx * ctx, int enable);
 int64_t z2h_capture_bytes(z2h_ctx * ctx, int what, int n_tokens);
 int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nbytes);
 
+/* Replay each step from a HIP graph captured once per (batch width, id/embedding input) pair
+ * (default on; the counterpart of the reference's CUDA-graph replay of its decode-graph ladder,
+ * CMakeLists.txt:34, src/zonos2-graph.cpp:670-680). Steps with capture or profiling run eagerly. */
+int z2h_set_graphs(z2h_ctx * ctx, int enable);
+
 /* Per-kernel-family timing with HIP events recorded around every launch on the context's stream
  * (the reference's only equivalent is the ZONOS2_PROFILE_STEP phase split, src/zonos2-graph.cpp:768,
  * 815-829). Between begin and end every launch is bracketed by an event pair; end synchronizes and

@@ -121,3 +121,22 @@ def test_c2_moe_layer_vs_oracle():
     assert np.array_equal(ctx.read_capture(0, "perm", T), perm)
     eo, out = O.experts(om, 0, x, ref["sel"], ref["w"])
     assert_close("moe out", got, out)
+
+
+def test_graph_replay_matches_eager():
+    """Whole-step HIP-graph replays equal the eager launch sequence bit for bit, replay after replay,
+    with eager work and other batch widths interleaved."""
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl, seed=45)
+    inp = synth.step_inputs(cfg, wl)
+    ctx.set_graphs(False)
+    ref = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    ref2 = ctx.step(inp.slot_idx[:2], inp.n_past[:2], emb=inp.emb[:2])
+    ctx.set_graphs(True)
+    x = synth.gen_normal_f32((4, cfg.n_embd), 3, "x")
+    for rep in range(4):
+        got = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+        assert np.array_equal(got, ref), f"replay {rep}"
+        got2 = ctx.step(inp.slot_idx[:2], inp.n_past[:2], emb=inp.emb[:2])
+        assert np.array_equal(got2, ref2), f"replay {rep} (width 2)"
+        ctx.moe_forward(0, x)                      # eager work between replays

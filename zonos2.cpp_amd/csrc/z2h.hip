@@ -96,6 +96,10 @@ struct z2h_ctx {
     int32_t * h_pin = nullptr;        // pinned staging for step inputs
     size_t h_pin_bytes = 0;
 
+    // HIP graphs of the whole step, one per (batch width, embedding-injection) pair
+    bool use_graphs = true;
+    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+
     // per-kernel event timing
     bool prof = false;
     std::vector<hipEvent_t> ev;
@@ -579,9 +583,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     e.act = ctx->act; e.act_fmt = act_of(ctx->layers[0].qkvg.type);
     if ((rc = launch_resnorm(ctx, T, e))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_RES_IN, 0, ctx->res, T))) return rc;
-    int n_items = 0;
-    for (int t = 0; t < T; ++t) n_items += (h_npast[t] + 1 + ATT_CH - 1) / ATT_CH;
-    n_items *= nkv;
+    (void) h_npast;
+    // persistent attention grid: the item count comes from the device n_past table
+    const int attn_grid = std::min(ctx->items_max, 2048);
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int L = 0; L < hp.n_layer; ++L) {
@@ -597,7 +601,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         a.kc = ctx->kv + (size_t) (2 * L) * lsz; a.vc = ctx->kv + (size_t) (2 * L + 1) * lsz;
         a.q16 = ctx->q16; a.gate = ctx->gate;
         a.cap_q = (float *) capp(ctx, Z2H_CAP_Q, L); a.cap_k = (float *) capp(ctx, Z2H_CAP_K, L); a.cap_v = (float *) capp(ctx, Z2H_CAP_V, L);
-        a.part_o = ctx->part_o; a.part_ml = ctx->part_ml; a.n_items = n_items;
+        a.part_o = ctx->part_o; a.part_ml = ctx->part_ml;
         a.o_out = ctx->attn_o;
         a.act = ctx->act;
         const int wo_act = act_of(ly.wo.type);
@@ -614,7 +618,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         const size_t lds_p = (size_t) 2 * ATT_CH * (hd + 8) * 2 + (size_t) (grp * hd + 8) * 2 + (size_t) grp * ATT_CH * 4 + 16;
         {
             prof_scope ps(ctx, Z2H_KF_ATTN);
-            hipLaunchKernelGGL(k_attn_partial, dim3(std::min(n_items, 4096)), dim3(256), lds_p, ctx->stream, a);
+            hipLaunchKernelGGL(k_attn_partial, dim3(attn_grid), dim3(256), lds_p, ctx->stream, a);
             HIPX(hipGetLastError());
         }
         {
@@ -678,6 +682,32 @@ int validate_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t 
         if (n_past[t] < 0 || n_past[t] >= ctx->S) return seterr(ctx, Z2H_EINVAL, "n_past out of range (slot full)");
         if (slot_idx) for (int u = 0; u < t; ++u) if (slot_idx[u] == slot_idx[t]) return seterr(ctx, Z2H_EINVAL, "duplicate slot in step");
     }
+    return Z2H_OK;
+}
+
+// Step on the context's input buffers (d_slot, d_npast, d_ids | d_emb) into ctx->logits: replayed
+// from a captured HIP graph when graphs are on and neither capture nor profiling is active.
+int step_internal(z2h_ctx * ctx, int T, const int32_t * h_npast, bool use_ids) {
+    const int32_t * ids = use_ids ? ctx->d_ids : nullptr;
+    const float * emb = use_ids ? nullptr : ctx->d_emb;
+    if (!ctx->use_graphs || ctx->capture || ctx->prof)
+        return run_step(ctx, T, h_npast, ctx->d_slot, ctx->d_npast, ids, emb, ctx->logits);
+    const auto key = std::make_pair(T, use_ids ? 1 : 0);
+    auto it = ctx->graphs.find(key);
+    if (it == ctx->graphs.end()) {
+        hipGraph_t g = nullptr;
+        HIPX(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = run_step(ctx, T, h_npast, ctx->d_slot, ctx->d_npast, ids, emb, ctx->logits);
+        const hipError_t ec = hipStreamEndCapture(ctx->stream, &g);
+        if (rc) { if (g) (void) hipGraphDestroy(g); return rc; }
+        if (ec != hipSuccess) return seterr(ctx, Z2H_EDEVICE, std::string("graph capture: ") + hipGetErrorString(ec));
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(g);
+        if (ei != hipSuccess) return seterr(ctx, Z2H_EDEVICE, std::string("graph instantiate: ") + hipGetErrorString(ei));
+        it = ctx->graphs.emplace(key, ex).first;
+    }
+    HIPX(hipGraphLaunch(it->second, ctx->stream));
     return Z2H_OK;
 }
 
@@ -891,7 +921,7 @@ int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_p
     HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + T, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
     if (ids) HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * ctx->W * 4, hipMemcpyHostToDevice, ctx->stream));
     if (emb) HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (int rc = run_step(ctx, T, n_past, ctx->d_slot, ctx->d_npast, ids ? ctx->d_ids : nullptr, emb ? ctx->d_emb : nullptr, ctx->logits)) return rc;
+    if (int rc = step_internal(ctx, T, n_past, ids != nullptr)) return rc;
     const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
     HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
@@ -904,7 +934,22 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
     if (int rc = validate_step(ctx, T, nullptr, h_npast)) return rc;
     hipStream_t keep = ctx->stream;
     if (stream) ctx->stream = (hipStream_t) stream;
-    const int rc = run_step(ctx, T, h_npast, d_slot, d_npast, d_ids, d_emb, d_logits);
+    int rc = Z2H_OK;
+    if (ctx->use_graphs && !ctx->capture && !ctx->prof) {
+        // inputs into the context's fixed buffers, replay, logits out
+        const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
+        auto cp = [&](void * dst, const void * src, size_t n) {
+            return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, ctx->stream) == hipSuccess;
+        };
+        if (!cp(ctx->d_slot, d_slot, (size_t) T * 4) || !cp(ctx->d_npast, d_npast, (size_t) T * 4) ||
+            (d_ids && !cp(ctx->d_ids, d_ids, (size_t) T * ctx->W * 4)) ||
+            (d_emb && !cp(ctx->d_emb, d_emb, (size_t) T * ctx->hp.n_embd * 4)))
+            rc = seterr(ctx, Z2H_EDEVICE, "input copy failed");
+        if (!rc) rc = step_internal(ctx, T, h_npast, d_ids != nullptr);
+        if (!rc && !cp(d_logits, ctx->logits, nout * 4)) rc = seterr(ctx, Z2H_EDEVICE, "logits copy failed");
+    } else {
+        rc = run_step(ctx, T, h_npast, d_slot, d_npast, d_ids, d_emb, d_logits);
+    }
     ctx->stream = keep;
     return rc;
 }
@@ -1018,6 +1063,12 @@ int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nby
     return Z2H_OK;
 }
 
+int z2h_set_graphs(z2h_ctx * ctx, int enable) {
+    if (!ctx) return Z2H_EINVAL;
+    ctx->use_graphs = enable != 0;
+    return Z2H_OK;
+}
+
 int z2h_profile_begin(z2h_ctx * ctx) {
     if (!ctx) return Z2H_EINVAL;
     if (ctx->ev.empty()) {
@@ -1059,6 +1110,7 @@ void z2h_destroy(z2h_ctx * ctx) {
     if (!ctx) return;
     (void) hipSetDevice(ctx->device);
     if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    for (auto & g : ctx->graphs) (void) hipGraphExecDestroy(g.second);
     for (auto & e : ctx->ev) (void) hipEventDestroy(e);
     for (void * p : ctx->allocs) (void) hipFree(p);
     if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);

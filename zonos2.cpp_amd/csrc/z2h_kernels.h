@@ -873,7 +873,6 @@ struct AttnArgs {
     // partials
     float * part_o;          // [items][grp][hd]
     float * part_ml;         // [items][grp][2]
-    int n_items;             // sum over tokens of chunks, times nkv
     float * o_out;           // [T][nh*hd] (combine: gated output, fp32)
     ActBuf act; int act_fmt; // encoding of o_out for W_o
 };
@@ -931,6 +930,12 @@ __global__ void __launch_bounds__(256) k_qkv_post(AttnArgs a) {
         a.gate[(int64_t) t * nh + h] = z_sigmoid(row[(int64_t) (nh + 2 * nkv) * hd + h]);
 }
 
+__device__ __forceinline__ int attn_n_items(const int32_t * n_past, int T, int nkv) {
+    int n = 0;
+    for (int t = 0; t < T; ++t) n += (n_past[t] + 1 + ATT_CH - 1) / ATT_CH;
+    return n * nkv;
+}
+
 // item i -> (token, chunk, kv head): tokens in order, chunks of ATT_CH rows, kv heads innermost
 __device__ __forceinline__ bool attn_item(const int32_t * n_past, int T, int nkv, int i, int & t, int & c, int & g) {
     g = i % nkv;
@@ -952,7 +957,8 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     uint16_t * sv = sk + ATT_CH * ldk;                               // [ATT_CH][ldk]
     uint16_t * sq = sv + ATT_CH * ldk;                               // [grp][hd]
     float * sp = (float *) (sq + grp * hd + 8);                      // [grp][ATT_CH]
-    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+    const int n_items = attn_n_items(a.n_past, a.T, a.nkv);         // from the device tables
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
         int t, c, g;
         if (!attn_item(a.n_past, a.T, a.nkv, item, t, c, g)) break;
         const int L = a.n_past[t] + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
@@ -1170,10 +1176,12 @@ __device__ __forceinline__ void rt_layer(const float * __restrict__ wt, const fl
 #pragma unroll
                 for (int u = 0; u < 8; ++u) w[u] = s_w[(i + u) * n_out + o];
 #pragma unroll
-                for (int j = 0; j < RT_TOK; ++j) {
+                for (int j = 0; j < RT_TOK; ++j) {                 // x rows are 16-byte aligned
                     const int t = min(tg + G * j, nt - 1);
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) xv[j][u] = x[t * ldx + i0 + i + u];
+                    const float4 x0 = *(const float4 *) (x + t * ldx + i0 + i);
+                    const float4 x1 = *(const float4 *) (x + t * ldx + i0 + i + 4);
+                    xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
+                    xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u)

@@ -48,6 +48,7 @@ def lib() -> C.CDLL:
         "z2h_capture_bytes": (i64, [vp, i32, i32]),
         "z2h_read_capture": (i32, [vp, i32, i32, vp, C.c_size_t]),
         "z2h_device_bytes": (i64, [vp, i32]),
+        "z2h_set_graphs": (i32, [vp, i32]),
         "z2h_profile_begin": (i32, [vp]),
         "z2h_profile_end": (i32, [vp, vp, vp]),
         "z2h_last_error": (C.c_char_p, [vp]),
@@ -62,7 +63,7 @@ def lib() -> C.CDLL:
 EXPORTS = ("z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
-           "z2h_read_capture", "z2h_device_bytes", "z2h_profile_begin", "z2h_profile_end", "z2h_last_error",
+           "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_last_error",
            "z2h_destroy")
 KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
                    "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
@@ -157,6 +158,9 @@ class Context:
         out = np.empty(nb // 4, np.int32 if what in INT_CAPS else np.float32)
         self.check(lib().z2h_read_capture(self.ctx, layer, w, _p(out), nb))
         return out
+
+    def set_graphs(self, on: bool):
+        self.check(lib().z2h_set_graphs(self.ctx, 1 if on else 0))
 
     def profile_begin(self):
         self.check(lib().z2h_profile_begin(self.ctx))
