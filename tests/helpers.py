@@ -6,7 +6,8 @@ import numpy as np
 import oracle_py as O
 from zonos2_amd import configs, synth
 
-# north_star bar: hidden states and logits per layer
+# parity bar of the floating-point path: per-layer hidden states and logits reach cosine >= 0.9999
+# and max |difference| <= 1e-2 against the oracle
 COS_MIN = 0.9999
 MAXABS = 1e-2
 

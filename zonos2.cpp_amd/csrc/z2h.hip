@@ -170,9 +170,10 @@ int upload_f32(z2h_ctx * ctx, const HostTensor & t, float ** out, int64_t n_expe
     return Z2H_OK;
 }
 
+// W [out][in] -> W^T [in][ld] with the output dimension padded to ld = a multiple of 4 (zeros)
 int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
-    const int64_t in = t.ne[0], outn = t.ne[1];
-    std::vector<float> full((size_t) (in * outn)), tr((size_t) (in * outn));
+    const int64_t in = t.ne[0], outn = t.ne[1], ld = (outn + 3) & ~3;
+    std::vector<float> full((size_t) (in * outn)), tr((size_t) (in * ld), 0.0f);
     for (int64_t r = 0; r < outn; ++r) {
         const uint8_t * src = t.bytes.data() + r * z2::row_bytes(t.type, in);
         for (int64_t i = 0; i < in; ++i) {
@@ -184,7 +185,7 @@ int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
             full[r * in + i] = v;
         }
     }
-    for (int64_t r = 0; r < outn; ++r) for (int64_t i = 0; i < in; ++i) tr[i * outn + r] = full[r * in + i];
+    for (int64_t r = 0; r < outn; ++r) for (int64_t i = 0; i < in; ++i) tr[i * ld + r] = full[r * in + i];
     if (int rc = dalloc(ctx, out, tr.size() * 4, ctx->bytes_w)) return rc;
     HIPX(hipMemcpy(*out, tr.data(), tr.size() * 4, hipMemcpyHostToDevice));
     return Z2H_OK;
@@ -527,8 +528,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     }
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
-        r.tpb = router_tail_tpb(ctx->rd, ly.E);
-        hipLaunchKernelGGL(k_router_tail, dim3((T + r.tpb - 1) / r.tpb), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        hipLaunchKernelGGL(k_router_tail, dim3((T + RT_TPB - 1) / RT_TPB), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
@@ -844,7 +844,7 @@ int z2h_finalize(z2h_ctx * ctx) {
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
     if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
-    if (ctx->rd > 256) return seterr(ctx, Z2H_ENOTSUP, "router_dim > 256");
+    if (ctx->rd > 256 || ctx->rd % 4) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be a multiple of 4, at most 256");
     if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));

@@ -50,26 +50,66 @@ __device__ __forceinline__ float z_gelu(float x) { return (0.5f * x) * (1.0f + z
 __device__ __forceinline__ float z_silu(float x) { return x / (1.0f + z_expf(-x)); }
 __device__ __forceinline__ float z_sigmoid(float x) { return 1.0f / (1.0f + z_expf(-x)); }
 
-// xor butterfly over the 64 lanes; every lane ends with the same value.
+// Reductions over the 64 lanes with the tree of an xor butterfly (offsets 32, 16, 8, 4, 2, 1): at each
+// level a node adds the two nodes of the level below that differ in one lane bit. Only lane 0's
+// chain of the tree is formed (lane i < off adds lane i + off), the two cross-row levels by lane
+// shuffles and the four in-row levels by DPP row shifts; lane 0's value is then broadcast. Every
+// addition is the one the butterfly makes (a + b and b + a are the same IEEE value), so the result
+// equals the butterfly's bit for bit.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v))); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t) dpp_i<CTRL>((int) (uint32_t) u), hi = (uint32_t) dpp_i<CTRL>((int) (uint32_t) (u >> 32));
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
+}
+constexpr int DPP_ROW_SHL = 0x100;     // lane i reads lane i + n of its 16-lane row
+__device__ __forceinline__ float lane0_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)); }
+__device__ __forceinline__ double lane0_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) u, 0);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (u >> 32), 0);
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
+}
+
 __device__ __forceinline__ float wave_tree_f(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, WAVE);
-    return v;
+    v = v + __shfl_down(v, 32, WAVE);
+    v = v + __shfl_down(v, 16, WAVE);
+    v = v + dpp_f<DPP_ROW_SHL + 8>(v);
+    v = v + dpp_f<DPP_ROW_SHL + 4>(v);
+    v = v + dpp_f<DPP_ROW_SHL + 2>(v);
+    v = v + dpp_f<DPP_ROW_SHL + 1>(v);
+    return lane0_f(v);
 }
 __device__ __forceinline__ double wave_tree_d(double v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, WAVE);
-    return v;
+    v = v + __shfl_down(v, 32, WAVE);
+    v = v + __shfl_down(v, 16, WAVE);
+    v = v + dpp_d<DPP_ROW_SHL + 8>(v);
+    v = v + dpp_d<DPP_ROW_SHL + 4>(v);
+    v = v + dpp_d<DPP_ROW_SHL + 2>(v);
+    v = v + dpp_d<DPP_ROW_SHL + 1>(v);
+    return lane0_d(v);
 }
 __device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
-    return v;
+    v = fmaxf(v, __shfl_down(v, 32, WAVE));
+    v = fmaxf(v, __shfl_down(v, 16, WAVE));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHL + 8>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHL + 4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHL + 2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHL + 1>(v));
+    return lane0_f(v);
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
-    return v;
+    v += __shfl_down(v, 32, WAVE);
+    v += __shfl_down(v, 16, WAVE);
+    v += dpp_i<DPP_ROW_SHL + 8>(v);
+    v += dpp_i<DPP_ROW_SHL + 4>(v);
+    v += dpp_i<DPP_ROW_SHL + 2>(v);
+    v += dpp_i<DPP_ROW_SHL + 1>(v);
+    return __builtin_amdgcn_readlane(v, 0);
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

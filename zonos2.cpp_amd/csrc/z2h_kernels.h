@@ -1097,7 +1097,6 @@ struct RouterArgs {
     const float * logit_bias;               // [E] or null
     const float * mask;                     // [E] additive 0/-inf or null
     const float * sc_bias;                  // router_bias [E]
-    int tpb;                                // router_tail: tokens per block
     int32_t * sel; float * wsel;            // [T][k]
     float * cap_logits; float * cap_probs;  // [T][E] (nullable)
 };
@@ -1125,124 +1124,155 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
 }
 
-// one fmaf chain per output over LDS-resident W^T (i ascending); 8 LDS loads issued per step
-__device__ __forceinline__ float chain_lds(const float * wt, int ld, int o, const float * x, int n) {
-    float acc = 0.0f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        float wv[8], xv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) { wv[j] = wt[(i + j) * ld + o]; xv[j] = x[i + j]; }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
-    }
-    for (; i < n; ++i) acc = __builtin_fmaf(wt[i * ld + o], x[i], acc);
-    return acc;
+// Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k.
+// One block per RT_TPB tokens, all three W^T planes resident in LDS. Every global read the block
+// needs (the planes, by LDS-direct loads; the tokens' router states; each thread's biases) is issued
+// at entry, so the kernel waits on memory once. MLP outputs are per-output fmaf chains over i
+// ascending; the norm and softmax sums are wave trees; top-k ranks each expert against all others
+// (score descending, ties to the lower index), so no lane-shuffle chain is needed per pick.
+constexpr int RT_TPB = 4;                // tokens per block = waves per block
+
+__host__ __device__ inline int pad4(int n) { return (n + 3) & ~3; }
+// LDS: W0^T, W2^T [rd][rd], W4^T [rd][pad4(E)], two activation planes [RT_TPB][rd], logits and
+// scores [RT_TPB][pad4(E)]
+__host__ __device__ inline size_t router_tail_lds(int rd, int E) {
+    return (size_t) 4 * (2 * rd * rd + rd * pad4(E) + 2 * RT_TPB * rd + 2 * RT_TPB * pad4(E));
 }
 
-// One block per RT_TOK tokens. Norm by one wave per token; the three MLP layers as per-output fmaf
-// chains (i ascending) over W^T staged through LDS in RT_CI-row chunks (one staging serves every
-// token of the block); softmax + top-k by one wave per token (ties to the lower expert index).
-constexpr int RT_TOK = 8;                // tokens per thread chain group (block serves 2*RT_TOK for rd=128)
-constexpr int RT_CI = 128;
+// n16 16-byte items from src to LDS dst, by LDS-direct loads (64 items per wave instruction)
+__device__ __forceinline__ void lds_dma(const void * src, void * dst, int n16) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int c = wave; c * 64 < n16; c += 4) {
+        const int it = c * 64 + lane;
+        if (it < n16)
+            __builtin_amdgcn_global_load_lds((const uint4 *) src + it, (__attribute__((address_space(3))) void *) ((uint4 *) dst + c * 64), 16, 0, 0);
+    }
+}
 
-// out[t][o] = f(chain_i W^T[i][o] * x[t][i] + b[o]) for t < nt, o < n_out; W^T is [n_in][n_out] in HBM
-template <bool GELU>
-__device__ __forceinline__ void rt_layer(const float * __restrict__ wt, const float * __restrict__ b, int n_in, int n_out,
-                                         const float * x, int ldx, float * out, int ldo, int nt, float * s_w,
-                                         const float * __restrict__ bias2, const float * __restrict__ bias3) {
-    const int tid = threadIdx.x;
-    const int G = 256 / n_out;                      // thread groups over tokens
-    const int o = tid % n_out, tg = tid / n_out;
-    const bool active = tg < G;
-    float acc[RT_TOK];
+// out[t][o] = chain_i W^T[i][o] * x[t][i] (i ascending, from 0) for the block's tokens: thread
+// (o = tid % n_out, group tid / n_out) serves tokens group + G*j, j < TT.
+template <int TT>
+__device__ __forceinline__ void rt2_chain(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
+                                          float (&acc)[TT], int & o, int & tg) {
+    const int tid = threadIdx.x, G = 256 / n_out;
+    o = tid % n_out; tg = tid / n_out;
 #pragma unroll
-    for (int j = 0; j < RT_TOK; ++j) acc[j] = 0.0f;
-    for (int i0 = 0; i0 < n_in; i0 += RT_CI) {
-        const int ci = min(RT_CI, n_in - i0);
-        __syncthreads();
-        {   // stage W^T rows [i0, i0+ci)
-            const int n = ci * n_out, nv = n / 4;
-            const float4 * src = (const float4 *) (wt + (int64_t) i0 * n_out);
-            copy16<256>(nv, [&](int v) { return (const uint4 *) (src + v); }, [&](int v) { return (uint4 *) ((float4 *) s_w + v); });
-            for (int e = nv * 4 + tid; e < n; e += 256) s_w[e] = wt[(int64_t) i0 * n_out + e];
-        }
-        __syncthreads();
-        if (active) {
-            // 8 inputs per batch: all LDS reads of the batch are issued before its fmas
-            int i = 0;
-            for (; i + 8 <= ci; i += 8) {
-                float w[8], xv[RT_TOK][8];
+    for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
+    if (tg >= G) return;
+    const float * xr[TT];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) w[u] = s_w[(i + u) * n_out + o];
+    for (int j = 0; j < TT; ++j) xr[j] = x + min(tg + G * j, nt - 1) * n_in;
+    for (int i = 0; i < n_in; i += 4) {
+        const float w0 = wt[(i + 0) * ldw + o], w1 = wt[(i + 1) * ldw + o];
+        const float w2 = wt[(i + 2) * ldw + o], w3 = wt[(i + 3) * ldw + o];
 #pragma unroll
-                for (int j = 0; j < RT_TOK; ++j) {                 // x rows are 16-byte aligned
-                    const int t = min(tg + G * j, nt - 1);
-                    const float4 x0 = *(const float4 *) (x + t * ldx + i0 + i);
-                    const float4 x1 = *(const float4 *) (x + t * ldx + i0 + i + 4);
-                    xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
-                    xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-#pragma unroll
-                    for (int j = 0; j < RT_TOK; ++j) acc[j] = __builtin_fmaf(w[u], xv[j][u], acc[j]);
-            }
-            for (; i < ci; ++i) {
-                const float w = s_w[i * n_out + o];
-#pragma unroll
-                for (int j = 0; j < RT_TOK; ++j) acc[j] = __builtin_fmaf(w, x[min(tg + G * j, nt - 1) * ldx + i0 + i], acc[j]);
-            }
+        for (int j = 0; j < TT; ++j) {
+            const float4 xv = *(const float4 *) (xr[j] + i);
+            acc[j] = __builtin_fmaf(w0, xv.x, acc[j]);
+            acc[j] = __builtin_fmaf(w1, xv.y, acc[j]);
+            acc[j] = __builtin_fmaf(w2, xv.z, acc[j]);
+            acc[j] = __builtin_fmaf(w3, xv.w, acc[j]);
         }
     }
-    __syncthreads();
-    if (active) {
+}
+
+// one MLP layer: y[t][o] = post(chain + ...), for n_out <= 256
+template <int TT, int MODE>   // MODE 0: gelu(acc + b[o]); 1: acc (+ logit bias[o]) (+ mask[o])
+__device__ __forceinline__ void rt2_layer(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
+                                          float * y, int ldy, float pb, const float * pb2, const float * pb3) {
+    float acc[TT]; int o, tg;
+    rt2_chain<TT>(wt, ldw, x, n_in, n_out, nt, acc, o, tg);
+    const int G = 256 / n_out;
+    if (tg < G) {
 #pragma unroll
-        for (int j = 0; j < RT_TOK; ++j) {
+        for (int j = 0; j < TT; ++j) {
             const int t = tg + G * j;
             if (t >= nt) continue;
             float v = acc[j];
-            if (b) v = v + b[o];
-            if (GELU) v = z_gelu(v);
-            if (bias2) v = v + bias2[o];
-            if (bias3) v = v + bias3[o];
-            out[t * ldo + o] = v;
+            if (MODE == 0) v = z_gelu(v + pb);
+            else {
+                if (pb2) v = v + *pb2;
+                if (pb3) v = v + *pb3;
+            }
+            y[t * ldy + o] = v;
         }
     }
-    __syncthreads();
+}
+
+template <int MODE>
+__device__ __forceinline__ void rt2_layer_any(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
+                                              float * y, int ldy, float pb, const float * pb2, const float * pb3) {
+    const int G = 256 / n_out, tt = (RT_TPB + G - 1) / G;
+    if (tt >= 4) rt2_layer<4, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
+    else if (tt >= 2) rt2_layer<2, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
+    else rt2_layer<1, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
 }
 
 __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
-    extern __shared__ float sm_rt[];
-    const int rd = a.rd, E = a.E;
-    float * s_a = sm_rt;                       // [tpb][rd]
-    float * s_b = s_a + a.tpb * rd;            // [tpb][max(rd, E)]
-    float * s_w = s_b + a.tpb * (rd > E ? rd : E);    // [RT_CI][max(rd, E)]
-    const int t0 = blockIdx.x * a.tpb, nt = min(a.tpb, a.T - t0);
+    extern __shared__ __attribute__((aligned(16))) float sm_rt[];
+    const int rd = a.rd, E = a.E, E4 = pad4(E);
+    float * s_w0 = sm_rt;                       // [rd][rd]
+    float * s_w2 = s_w0 + rd * rd;              // [rd][rd]
+    float * s_w4 = s_w2 + rd * rd;              // [rd][E4]
+    float * s_a = s_w4 + rd * E4;               // [RT_TPB][rd]
+    float * s_b = s_a + RT_TPB * rd;            // [RT_TPB][rd]
+    float * s_l = s_b + RT_TPB * rd;            // [RT_TPB][E4] logits
+    float * s_s = s_l + RT_TPB * E4;            // [RT_TPB][E4] selection scores
+    const int t0 = blockIdx.x * RT_TPB, nt = min(RT_TPB, a.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int tt = wave; tt < nt; tt += 4) {
-        const float * __restrict__ rh = a.rh + (int64_t) (t0 + tt) * rd;
+    // every global read of the block, issued together
+    lds_dma(a.w0t, s_w0, rd * rd / 4);
+    lds_dma(a.w2t, s_w2, rd * rd / 4);
+    lds_dma(a.w4t, s_w4, rd * E4 / 4);
+    const int tw = t0 + min(wave, nt - 1);      // this wave's token (norm, softmax)
+    float rh[4], nw[4], sb[4], mk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane + 64 * j, e = lane + 64 * j;
+        rh[j] = i < rd ? a.rh[(int64_t) tw * rd + i] : 0.0f;
+        nw[j] = i < rd ? a.norm_w[i] : 0.0f;
+        sb[j] = e < E ? a.sc_bias[e] : 0.0f;
+        mk[j] = e < E && a.mask ? a.mask[e] : 0.0f;
+    }
+    const int o_r = tid % rd, o_e = tid % E;
+    const float b0 = a.b0[o_r], b2 = a.b2[o_r];
+    const float lb = a.logit_bias ? a.logit_bias[o_e] : 0.0f, lm = a.mask ? a.mask[o_e] : 0.0f;
+    const float * plb = a.logit_bias ? &lb : nullptr, * plm = a.mask ? &lm : nullptr;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // router RMS norm, one wave per token: double lane partials (i = lane, lane + 64, ...) + tree
+    if (wave < nt) {
         double part = 0.0;
-        for (int i = lane; i < rd; i += 64) part += (double) (rh[i] * rh[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
         const double ss = wave_tree_d(part);
         const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
-        for (int i = lane; i < rd; i += 64) s_a[tt * rd + i] = (rh[i] * scale) * a.norm_w[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = lane + 64 * j;
+            if (i < rd) s_a[wave * rd + i] = (rh[j] * scale) * nw[j];
+        }
     }
-    rt_layer<true>(a.w0t, a.b0, rd, rd, s_a, rd, s_b, rd, nt, s_w, nullptr, nullptr);
-    rt_layer<true>(a.w2t, a.b2, rd, rd, s_b, rd, s_a, rd, nt, s_w, nullptr, nullptr);
-    rt_layer<false>(a.w4t, nullptr, rd, E, s_a, rd, s_b, E, nt, s_w, a.logit_bias, a.mask);
-    for (int tt = wave; tt < nt; tt += 4) {
-        const int t = t0 + tt;
-        const float * lgs = s_b + tt * E;
-        float lg[4], ex[4], pr[4], sc[4];
+    __syncthreads();
+    rt2_layer_any<0>(s_w0, rd, s_a, rd, rd, nt, s_b, rd, b0, nullptr, nullptr);
+    __syncthreads();
+    rt2_layer_any<0>(s_w2, rd, s_b, rd, rd, nt, s_a, rd, b2, nullptr, nullptr);
+    __syncthreads();
+    rt2_layer_any<1>(s_w4, E4, s_a, rd, E, nt, s_l, E4, 0.0f, plb, plm);
+    __syncthreads();
+    // softmax (own exp, double tree sum) + selection scores, one wave per token
+    float pr[4];
+    if (wave < nt) {
+        const int t = t0 + wave;
+        float lg[4];
         float mx = -__builtin_inff();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = lane + 64 * j;
-            lg[j] = e < E ? lgs[e] : -__builtin_inff();
+            lg[j] = e < E ? s_l[wave * E4 + e] : -__builtin_inff();
             mx = fmaxf(mx, lg[j]);
         }
         mx = wave_max_f(mx);
+        float ex[4];
         double ps = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1255,45 +1285,36 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
         for (int j = 0; j < 4; ++j) {
             const int e = lane + 64 * j;
             pr[j] = ex[j] * inv;
-            sc[j] = -__builtin_inff();
             if (e < E) {
-                sc[j] = pr[j] + a.sc_bias[e];
-                if (a.mask) sc[j] = sc[j] + a.mask[e];
+                float sc = pr[j] + sb[j];
+                if (a.mask) sc = sc + mk[j];
+                s_s[wave * E4 + e] = sc;
                 if (a.cap_logits) a.cap_logits[(int64_t) t * E + e] = lg[j];
                 if (a.cap_probs) a.cap_probs[(int64_t) t * E + e] = pr[j];
             }
         }
-        bool taken[4] = {false, false, false, false};
-        for (int j = 0; j < a.k; ++j) {
-            float bv = 0.0f; int bi = 0x7fffffff; float bp = 0.0f;
+    }
+    __syncthreads();
+    // top-k: expert e's rank = #{e' : s[e'] > s[e] or (s[e'] == s[e] and e' < e)}
+    if (wave < nt) {
+        const int t = t0 + wave;
+        const float * ss = s_s + wave * E4;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = lane + 64 * q;
-                if (e < E && !taken[q] && (bi == 0x7fffffff || sc[q] > bv)) { bv = sc[q]; bi = e; bp = pr[q]; }
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            if (64 * j >= E) break;
+            const float me = e < E ? ss[e] : 0.0f;
+            int rank = 0;
+            for (int f = 0; f < E; ++f) {
+                const float v = ss[f];
+                rank += (v > me) || (v == me && f < e);
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, WAVE), op = __shfl_xor(bp, off, WAVE);
-                const int oi = __shfl_xor(bi, off, WAVE);
-                const bool better = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-                if (better) { bv = ov; bi = oi; bp = op; }
+            if (e < E && rank < a.k) {
+                a.sel[(int64_t) t * a.k + rank] = e;
+                a.wsel[(int64_t) t * a.k + rank] = pr[j];
             }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) if (lane + 64 * q == bi) taken[q] = true;
-            if (lane == 0) { a.sel[(int64_t) t * a.k + j] = bi; a.wsel[(int64_t) t * a.k + j] = bp; }
         }
     }
-}
-
-// tokens one router_tail block serves: every MLP layer's thread groups (256 / width) x RT_TOK
-__host__ inline int router_tail_tpb(int rd, int E) {
-    const int m = rd > E ? rd : E;
-    const int t = (256 / m) * RT_TOK;
-    return t < 16 ? t : 16;
-}
-__host__ inline size_t router_tail_lds(int rd, int E) {
-    const int m = rd > E ? rd : E, tpb = router_tail_tpb(rd, E);
-    return (size_t) (tpb * rd + tpb * m + RT_CI * m) * 4;
 }
 
 // y = up * silu(gate) of one route (or dense token) row, encoded for the down matmul.
