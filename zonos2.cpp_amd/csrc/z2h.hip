@@ -79,6 +79,7 @@ struct z2h_ctx {
 
     // KV cache [L][2][slot][kvh][S][hd]
     uint16_t * kv = nullptr;
+    uint4 * kv_stage = nullptr;       // one slot's rows of one layer, host layout (kv_write / kv_read)
 
     // scratch (sized for n_slots tokens)
     int Tmax = 0, Kmax = 0, items_max = 0;
@@ -445,13 +446,24 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     const int af = act_of(m0.type);
     a.n_mats = m1 ? 2 : 1;
     if (m0.m16) {
-        const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256);
-        // grouped: an expert serves at most n_tok routes (each token picks it once) -> route passes
-        const int passes = a.grouped ? (a.n_tok + MT - 1) / MT : 1;
-        if (!a.grouped) grid_y = (a.n_tok + MT - 1) / MT;
-        dim3 grid((m0.tiles + 3) / 4, grid_y, a.n_mats * passes), block(256);
-        if (m0.type == Z2H_Q4_K) hipLaunchKernelGGL(k_gemv_mfma<WF_Q4_K>, grid, block, lds, ctx->stream, a);
-        else hipLaunchKernelGGL(k_gemv_mfma<WF_Q8_0>, grid, block, lds, ctx->stream, a);
+        // grouped: ROWS = MT_G routes per pass (an expert serves at most n_tok routes); dense: all
+        // MT tokens of a chunk per pass, so each weight tile is read once
+        const int rows = a.grouped ? MT_G : MT;
+        const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
+        const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
+        if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
+        const bool dual = a.mode == MM_SWIGLU;
+        if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
+        dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
+#define MM16(W_, D_, R_) hipLaunchKernelGGL((k_gemv_mfma<W_, D_, R_>), grid, block, lds, ctx->stream, a)
+        if (m0.type == Z2H_Q4_K) {
+            if (a.grouped) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
+            else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
+        } else {
+            if (a.grouped) { if (dual) MM16(WF_Q8_0, true, MT_G); else MM16(WF_Q8_0, false, MT_G); }
+            else { if (dual) MM16(WF_Q8_0, true, MT); else MM16(WF_Q8_0, false, MT); }
+        }
+#undef MM16
         HIPX(hipGetLastError());
         return Z2H_OK;
     }
@@ -478,6 +490,20 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         case Z2H_F16:  hipLaunchKernelGGL(k_gemv<WF_F16>, grid, block, lds, ctx->stream, a); break;
         default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
     }
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+// SwiGLU fused into the gate/up matmul (both in the 16-row MFMA layout, same shape)
+bool fused_ffn(const DevMat & g, const DevMat & u) {
+    return g.m16 && u.m16 && g.type == u.type && g.nsb == u.nsb && g.tiles == u.tiles;
+}
+
+int launch_encode(z2h_ctx * ctx, const float * x, int ld, int K, int n_rows, int act_fmt, const ActBuf & act) {
+    prof_scope ps(ctx, Z2H_KF_SWIGLU);
+    EncodeArgs e{x, ld, K, n_rows, act_fmt, act};
+    const int items = n_rows * (kpad(K) / 256);
+    hipLaunchKernelGGL(k_encode_rows, dim3((items + 3) / 4), dim3(256), 0, ctx->stream, e);
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -534,6 +560,25 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_SEL, L, ctx->sel, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_WEIGHTS, L, ctx->wsel, T))) return rc;
+    if (fused_ffn(ly.gate_exps, ly.up_exps)) {
+        // gate + up + SwiGLU in one grouped launch -> y [route][ff] fp32, encoded once for down
+        GemvArgs g{};
+        g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E; g.mode = MM_SWIGLU;
+        g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_g; g.out_ld = hp.n_ff; g.epi = EPI_STORE;
+        if (ctx->capture) {
+            g.cap_counts = (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L);
+            g.cap_offsets = (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L);
+            g.cap_perm = (int32_t *) capp(ctx, Z2H_CAP_PERM, L);
+        }
+        if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ly.E, Z2H_KF_GEMV_GATEUP))) return rc;
+        if ((rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T * ly.k, act_of(ly.down_exps.type), ctx->act_y))) return rc;
+        GemvArgs dn{};
+        dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
+        dn.act = ctx->act_y; dn.act_by_route = 1;
+        dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
+        if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ly.E, Z2H_KF_GEMV_DOWN))) return rc;
+        return cap_copy(ctx, Z2H_CAP_EXPERT_OUT, L, ctx->eo, T);
+    }
     // gate + up (grouped by expert)
     GemvArgs g{};
     g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E;
@@ -559,6 +604,15 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
 int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
     const auto & hp = ctx->hp;
     int rc;
+    if (fused_ffn(ly.ffn_gate, ly.ffn_up)) {
+        GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
+        g.mode = MM_SWIGLU;
+        if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, 1, Z2H_KF_GEMV_DENSE))) return rc;
+        if ((rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T, act_of(ly.ffn_down.type), ctx->act_y))) return rc;
+        GemvArgs dn = gemv_dense(ctx, T, ctx->eo, hp.n_embd, EPI_STORE);
+        dn.act = ctx->act_y;
+        return launch_gemv(ctx, ly.ffn_down, nullptr, dn, 1, Z2H_KF_GEMV_DENSE);
+    }
     GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
     g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_u;
     if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, 1, Z2H_KF_GEMV_DENSE))) return rc;
@@ -737,7 +791,8 @@ int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int dev
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return Z2H_EDEVICE;
     const size_t kv_elems = (size_t) hp->n_layer * 2 * n_slots * hp->n_head_kv * c->S * hp->head_dim;
     if (dalloc(c, &c->kv, kv_elems * 2, c->bytes_kv)) { (void) hipStreamDestroy(c->stream); return Z2H_ENOMEM; }
-    if (hipMemset(c->kv, 0, kv_elems * 2) != hipSuccess) return Z2H_EDEVICE;
+    if (dalloc(c, &c->kv_stage, (size_t) c->S * hp->n_head_kv * hp->head_dim * 2, c->bytes_scratch)) { z2h_destroy(ctx.release()); return Z2H_ENOMEM; }
+    if (hipMemset(c->kv, 0, kv_elems * 2) != hipSuccess) { z2h_destroy(ctx.release()); return Z2H_EDEVICE; }
     c->layers.resize(hp->n_layer);
     c->tab.assign(c->W, nullptr); c->tab_type.assign(c->W, -1); c->tab_rows.assign(c->W, 0);
     *out = ctx.release();
@@ -850,10 +905,13 @@ int z2h_finalize(z2h_ctx * ctx) {
     HIPX(hipMemset(ctx->d_err, 0, 16));
     // allow the GEMV kernels the full 160 KiB of gfx950 LDS for their dynamic carve-up
     const int lds_max = 160 * 1024 - 8 * 1024;
-#define LDS_ATTR(K_) (void) hipFuncSetAttribute((const void *) &K_, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
+#define LDS_ATTR(K_) (void) hipFuncSetAttribute((const void *) &(K_), hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
     LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
     LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
-    LDS_ATTR(k_gemv_mfma<WF_Q4_K>) LDS_ATTR(k_gemv_mfma<WF_Q8_0>)
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G>))
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     if (router_tail_lds(std::max(1, ctx->rd), std::max(1, hp.n_expert)) > (size_t) lds_max)
@@ -868,15 +926,18 @@ int z2h_kv_write(z2h_ctx * ctx, int layer, int slot, int row0, int n, const uint
     if (layer < 0 || layer >= hp.n_layer || slot < 0 || slot >= ctx->n_slots || row0 < 0 || n < 0 || row0 + n > ctx->S)
         return seterr(ctx, Z2H_EINVAL, "kv_write out of range");
     if (n == 0) return Z2H_OK;
+    HIPX(hipSetDevice(ctx->device));
     const int nkv = hp.n_head_kv, hd = hp.head_dim;
     const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
+    const int grid = (int) std::min<int64_t>(1024, ((int64_t) n * nkv * (hd / 8) + 255) / 256);
     for (int which = 0; which < 2; ++which) {
         const uint16_t * src = which ? v : k;
         if (!src) continue;
-        uint16_t * base = ctx->kv + (size_t) (2 * layer + which) * lsz;
-        for (int g = 0; g < nkv; ++g)
-            HIPX(hipMemcpy2D(base + (((size_t) slot * nkv + g) * ctx->S + row0) * hd, (size_t) hd * 2,
-                             src + (size_t) g * hd, (size_t) nkv * hd * 2, (size_t) hd * 2, n, hipMemcpyHostToDevice));
+        HIPX(hipMemcpyAsync(ctx->kv_stage, src, (size_t) n * nkv * hd * 2, hipMemcpyHostToDevice, ctx->stream));
+        hipLaunchKernelGGL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
+                           ctx->kv + (size_t) (2 * layer + which) * lsz, n, nkv, hd, ctx->S, row0, slot, 0);
+        HIPX(hipGetLastError());
+        HIPX(hipStreamSynchronize(ctx->stream));      // the staging buffer is reused by the next copy
     }
     return Z2H_OK;
 }
@@ -887,16 +948,18 @@ int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n, uint16_t * 
     if (layer < 0 || layer >= hp.n_layer || slot < 0 || slot >= ctx->n_slots || row0 < 0 || n < 0 || row0 + n > ctx->S)
         return seterr(ctx, Z2H_EINVAL, "kv_read out of range");
     if (n == 0) return Z2H_OK;
-    HIPX(hipStreamSynchronize(ctx->stream));
+    HIPX(hipSetDevice(ctx->device));
     const int nkv = hp.n_head_kv, hd = hp.head_dim;
     const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
+    const int grid = (int) std::min<int64_t>(1024, ((int64_t) n * nkv * (hd / 8) + 255) / 256);
     for (int which = 0; which < 2; ++which) {
         uint16_t * dst = which ? v : k;
         if (!dst) continue;
-        const uint16_t * base = ctx->kv + (size_t) (2 * layer + which) * lsz;
-        for (int g = 0; g < nkv; ++g)
-            HIPX(hipMemcpy2D(dst + (size_t) g * hd, (size_t) nkv * hd * 2, base + (((size_t) slot * nkv + g) * ctx->S + row0) * hd,
-                             (size_t) hd * 2, (size_t) hd * 2, n, hipMemcpyDeviceToHost));
+        hipLaunchKernelGGL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
+                           ctx->kv + (size_t) (2 * layer + which) * lsz, n, nkv, hd, ctx->S, row0, slot, 1);
+        HIPX(hipGetLastError());
+        HIPX(hipMemcpyAsync(dst, ctx->kv_stage, (size_t) n * nkv * hd * 2, hipMemcpyDeviceToHost, ctx->stream));
+        HIPX(hipStreamSynchronize(ctx->stream));
     }
     return Z2H_OK;
 }

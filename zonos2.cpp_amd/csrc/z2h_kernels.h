@@ -52,13 +52,18 @@ struct ActBuf {
 // ------------------------------------------------------------------ activation encoders
 // Q8_K of one 256-block by one wave (4 elements per lane). The element of largest |x| (first
 // occurrence) fixes iscale = -127/x; q = min(127, rint(iscale*x)); d = 1/iscale; sums of 16.
+__device__ __forceinline__ void q8k_block_v(const float (&vin)[4], int8_t * q, float * d, int16_t * bs, int lane);
 __device__ __forceinline__ void q8k_block(const float * x, int8_t * q, float * d, int16_t * bs, int lane) {
+    const float v[4] = {x[lane * 4], x[lane * 4 + 1], x[lane * 4 + 2], x[lane * 4 + 3]};
+    q8k_block_v(v, q, d, bs, lane);
+}
+__device__ __forceinline__ void q8k_block_v(const float (&vin)[4], int8_t * q, float * d, int16_t * bs, int lane) {
     float v[4];
     float bax = -1.0f, bval = 0.0f;
     int bidx = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[i] = x[lane * 4 + i];
+        v[i] = vin[i];
         const float ax = fabsf(v[i]);
         if (ax > bax) { bax = ax; bval = v[i]; bidx = lane * 4 + i; }
     }
@@ -281,6 +286,7 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
 
 // ------------------------------------------------------------------ k_gemv
 enum { EPI_STORE = 0, EPI_SOFTCAP = 1, EPI_ROUTE_W = 2 };
+enum { MM_PLAIN = 0, MM_SWIGLU = 1 };   // m16 kernel variants (host-side choice)
 
 struct GemvArgs {
     const uint8_t * w[2];              // tiled weights (matrix m = blockIdx.z)
@@ -292,6 +298,7 @@ struct GemvArgs {
     int n_tok;                         // dense token count / grouped: number of tokens T
     const int32_t * sel; int k;        // [T][k]
     ActBuf act;                        // ST_ACT source rows (indexed by token)
+    int mode;                          // MM_* (m16 kernels)
     int act_by_route;                  // grouped: activation row = route (else token = route / k)
     int n_mats;                        // matrices in the launch (gate+up = 2)
     int tpb;                           // dense: tokens per block (<= NT)
@@ -687,14 +694,17 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 template <int WF> struct m16fmt;
-template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constexpr int BYTES = 2304; static constexpr int PF = 8; };
-template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int PF = 4; };
+template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constexpr int BYTES = 2304; static constexpr int WPE = 5; };
+template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int WPE = 4; };
 constexpr int MT = 16;                  // tokens per MFMA pass
 
-__host__ __device__ inline size_t gemv_mfma_lds_bytes(int wf, int K) {
+// token rows per pass of the m16 kernels: grouped expert launches stage up to MT_G routes (an
+// expert serves ~2 at 16 requests), dense launches all MT tokens so each weight tile is read once
+constexpr int MT_G = 8;
+__host__ __device__ inline size_t gemv_mfma_lds_bytes(int wf, int K, int rows) {
     const size_t KP = (size_t) K + 16;
-    if (wf == WF_Q4_K) return MT * KP + (size_t) MT * (K / 32) * 4 + (size_t) MT * (K / 256) * 4 + 64;
-    return MT * KP + (size_t) MT * (K / 32) * 4 + 64;
+    if (wf == WF_Q4_K) return rows * KP + (size_t) rows * (K / 32) * 4 + (size_t) rows * (K / 256) * 4 + 64;
+    return rows * KP + (size_t) rows * (K / 32) * 4 + 64;
 }
 
 template <int WF>
@@ -704,10 +714,13 @@ __device__ __forceinline__ void m16_load(const uint4 * __restrict__ unit, int la
     hd = unit[m16fmt<WF>::QS * 64 + (lane & 15)];
 }
 
+// One 256-column unit of a wave's 16 rows against the staged token rows. Token rows beyond the last
+// valid one (ntm1) read that row instead (their results are discarded), so LDS holds only the valid
+// rows.
 template <int WF>
 __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], const uint4 & hd, int sb, int K, int lane,
-                                         const int8_t * sq, const int * sbs2, const float * sdx, int nsb, float (&acc)[4]) {
-    const int q = lane >> 4, r = lane & 15, KP = K + 16;
+                                         const int8_t * sq, const int * sbs2, const float * sdx, int nsb, int ntm1, float (&acc)[4]) {
+    const int q = lane >> 4, r = min(lane & 15, ntm1), KP = K + 16;
     const int8_t * arow = sq + r * KP + sb * 256 + 8 * q;          // A: token r, k-slice q
     const v4i_t zero = {0, 0, 0, 0};
     if constexpr (WF == WF_Q4_K) {
@@ -728,7 +741,7 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
             const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
             const int scj = (int) (((j < 4 ? sc03 : sc47) >> (8 * (j & 3))) & 0xffu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sumi[i] += scj * C[i];
+            for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scj, C[i]);   // |products| < 2^22
         }
         // min correction sum_j m_j[row] * bsum_j[token] as an fp32 16x16x4 product (two k-halves):
         // integer products < 2^19 and sums < 2^23, so the fp32 result is exact
@@ -740,7 +753,7 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
         S = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, S, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float dx = sdx[(4 * q + i) * nsb + sb];
+            const float dx = sdx[min(4 * q + i, ntm1) * nsb + sb];
             acc[i] += (d * dx) * (float) sumi[i] - (dmin * dx) * S[i];
         }
     } else {
@@ -755,26 +768,81 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
             const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
             const float dw = h2f(dh[b]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += (dw * sdx[(4 * q + i) * (K / 32) + sb * 8 + b]) * (float) C[i];
+            for (int i = 0; i < 4; ++i) acc[i] += (dw * sdx[min(4 * q + i, ntm1) * (K / 32) + sb * 8 + b]) * (float) C[i];
         }
     }
 }
 
-// grid: x = 16-row group quads, y = expert (grouped) or 16-token chunk (dense), z = matrix + n_mats *
-// route pass (grouped: routes [16*pass, 16*pass+16) of the expert, so hot experts spread over blocks)
-template <int WF>
-__global__ void __launch_bounds__(256) k_gemv_mfma(GemvArgs a) {
-    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES, PF = m16fmt<WF>::PF;
+// Stage the encoded activation rows of nt tokens (LDS row tt = token tok(tt)) for the m16 kernels:
+// int8 values [rows][K+16], Q8_K sums of 32 [rows][K/32] and scales [rows][K/256], or Q8_0 scales
+// [rows][K/32]. Every global load of a batch is issued before its first LDS store.
+template <int AF, class TokFn>
+__device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2, float * sdx) {
+    const int tid = threadIdx.x, KP = K + 16;
+    const int per = K / 16, nq = nt * per;                 // 16-byte items of the int8 rows
+    const int ns = K / 32, nsd = nt * ns;                  // sums of 32 (Q8_K) / scales (Q8_0)
+    const int nd = K / 256, ndd = nt * nd;                 // Q8_K block scales
+    const int iters = max(max((nq + 2047) / 2048, (nsd + 1023) / 1024), (ndd + 255) / 256);
+    for (int it = 0; it < iters; ++it) {
+        u32x4 v[8];
+        uint32_t sv[4];
+        float dv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = it * 2048 + tid + 256 * j;
+            if (i < nq) v[j] = *(const u32x4 *) (act.q + (int64_t) tok(i / per) * K + (i % per) * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = it * 1024 + tid + 256 * j;
+            sv[j] = 0;
+            if (i < nsd) {
+                if constexpr (AF == ACT_Q8_K) sv[j] = *(const uint32_t *) (act.bs + (int64_t) tok(i / ns) * (K / 16) + 2 * (i % ns));
+                else sv[j] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tok(i / ns) * ns + i % ns]);
+            }
+        }
+        const int id = it * 256 + tid;
+        if (AF == ACT_Q8_K && id < ndd) dv = act.d256[(int64_t) tok(id / nd) * nd + id % nd];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = it * 2048 + tid + 256 * j;
+            if (i < nq) *(u32x4 *) (sq + (i / per) * KP + (i % per) * 16) = v[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = it * 1024 + tid + 256 * j;
+            if (i < nsd) {
+                if constexpr (AF == ACT_Q8_K) sbs2[i] = (int) (int16_t) (sv[j] & 0xffffu) + (int) (int16_t) (sv[j] >> 16);
+                else sdx[i] = __builtin_bit_cast(float, sv[j]);
+            }
+        }
+        if (AF == ACT_Q8_K && id < ndd) sdx[id] = dv;
+    }
+}
+
+// grid: x = 16-row group quads, y = expert (grouped) or token chunk of ROWS (dense), z = matrix +
+// n_mats * route pass (grouped: routes [ROWS*pass, ROWS*pass+ROWS) of the expert, so hot experts
+// spread over blocks). DUAL: each wave computes the same 16 rows of two matrices (w[0] = gate,
+// w[1] = up) and stores up * silu(gate) (SwiGLU). The wave's weight units (both matrices for DUAL)
+// stream through a PF-deep register ring; the first PF are requested before the activations are
+// staged. Register use is capped for 5 (Q4_K) / 4 (Q8_0) waves per SIMD: the kernel is latency
+// bound, and occupancy hides more of it than a deeper per-wave ring.
+template <int WF, bool DUAL, int ROWS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(m16fmt<WF>::WPE, m16fmt<WF>::WPE))) k_gemv_mfma(GemvArgs a) {
+    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES, PF = 1;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ int s_list[MAX_ROUTES];
     __shared__ int s_wcnt[4];
+    __shared__ int s_tok[ROWS];
     const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g16 = blockIdx.x * 4 + wave, m = blockIdx.z % a.n_mats, pass = blockIdx.z / a.n_mats;
-    int8_t * sq = (int8_t *) smem;                                   // [MT][K+16]
-    int * sbs2 = (int *) (smem + MT * KP);                           // Q4_K: [MT][K/32] sums of 32
-    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + MT * (K / 32))  // Q4_K: [MT][K/256]
-                                 : (float *) (smem + MT * KP);       // Q8_0: [MT][K/32]
+    const int g16 = blockIdx.x * 4 + wave;
+    const int nm = DUAL ? 1 : a.n_mats;
+    const int m = blockIdx.z % nm, pass = blockIdx.z / nm;
+    int8_t * sq = (int8_t *) smem;                                   // [ROWS][K+16]
+    int * sbs2 = (int *) (smem + ROWS * KP);                         // Q4_K: [ROWS][K/32] sums of 32
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32))  // Q4_K: [ROWS][K/256]
+                                 : (float *) (smem + ROWS * KP);     // Q8_0: [ROWS][K/32]
     int n_items, c0, e = 0;
     if (a.grouped) {
         e = blockIdx.y;
@@ -789,59 +857,52 @@ __global__ void __launch_bounds__(256) k_gemv_mfma(GemvArgs a) {
                 if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
             }
         }
-        c0 = pass * MT;
+        c0 = pass * ROWS;
     } else {
         n_items = a.n_tok;
-        c0 = blockIdx.y * MT;
+        c0 = blockIdx.y * ROWS;
     }
     if (c0 >= n_items) return;
-    const int nt = min(MT, n_items - c0);
+    const int nt = min(ROWS, n_items - c0);
     const bool has = g16 < a.tiles;
-    const uint4 * ub = (const uint4 *) (a.w[m] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * a.nsb * UB);
-    // the wave's first PF units are requested before the activations are staged
+    const int nsb = a.nsb, U = (DUAL ? 2 : 1) * nsb;
+    const uint4 * ub0 = (const uint4 *) (a.w[DUAL ? 0 : m] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB);
+    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB) : ub0;
+    auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
     uint4 pq[PF][QS], ph[PF];
 #pragma unroll
     for (int j = 0; j < PF; ++j)
-        if (has && j < a.nsb) m16_load<WF>(ub + (size_t) j * (UB / 16), lane, pq[j], ph[j]);
+        if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
 
-    {
-        __shared__ int s_tok[MT];
-        if (tid < MT) {
-            int tok = 0;
-            if (tid < nt) {
-                const int it = a.grouped ? s_list[c0 + tid] : c0 + tid;
-                tok = a.grouped && !a.act_by_route ? it / a.k : it;
-            }
-            s_tok[tid] = tok;
+    if (tid < ROWS) {
+        int tok = 0;
+        if (tid < nt) {
+            const int it = a.grouped ? s_list[c0 + tid] : c0 + tid;
+            tok = a.grouped && !a.act_by_route ? it / a.k : it;
         }
-        __syncthreads();
-        const int per = K / 16;                                      // 16-byte items per token row
-        copy16<256>(MT * per,
-            [&](int i) { return (const uint4 *) (a.act.q + (int64_t) s_tok[i / per] * K) + i % per; },
-            [&](int i) { return (uint4 *) (sq + (i / per) * KP) + i % per; });
-        if constexpr (AF == ACT_Q8_K) {
-            const int ns = K / 32, nd = K / 256;
-            for (int i = tid; i < MT * ns; i += 256) {
-                const int tt = i / ns, j = i % ns;
-                const int16_t * bs = a.act.bs + (int64_t) s_tok[tt] * (K / 16);
-                sbs2[i] = tt < nt ? (int) bs[2 * j] + (int) bs[2 * j + 1] : 0;
-            }
-            for (int i = tid; i < MT * nd; i += 256) sdx[i] = (i / nd) < nt ? a.act.d256[(int64_t) s_tok[i / nd] * nd + i % nd] : 0.0f;
-        } else {
-            const int nd = K / 32;
-            for (int i = tid; i < MT * nd; i += 256) sdx[i] = (i / nd) < nt ? a.act.d32[(int64_t) s_tok[i / nd] * nd + i % nd] : 0.0f;
-        }
+        s_tok[tid] = tok;
     }
     __syncthreads();
+    m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
+    __syncthreads();
     if (!has) return;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < U; c += PF) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-        if (j < a.nsb) m16_unit<WF>(pq[j], ph[j], j, K, lane, sq, sbs2, sdx, a.nsb, acc);
-    for (int sb = PF; sb < a.nsb; ++sb) {
-        uint4 uq[QS], uh;
-        m16_load<WF>(ub + (size_t) sb * (UB / 16), lane, uq, uh);
-        m16_unit<WF>(uq, uh, sb, K, lane, sq, sbs2, sdx, a.nsb, acc);
+        for (int j = 0; j < PF; ++j) {
+            const int u = c + j;
+            if (u < U) {
+                float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
+                if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
+                const bool first = !DUAL || u < nsb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc0[i] = first ? acc0[i] + t4[i] : acc0[i];
+                    acc1[i] = first ? acc1[i] : acc1[i] + t4[i];
+                }
+            }
+        }
     }
     const int q = lane >> 4, row = g16 * 16 + (lane & 15);
     if (row < a.rows) {
@@ -850,11 +911,52 @@ __global__ void __launch_bounds__(256) k_gemv_mfma(GemvArgs a) {
             const int t = 4 * q + i;
             if (t >= nt) continue;
             const int it = a.grouped ? s_list[c0 + t] : c0 + t;
-            float y = acc[i];
-            if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+            float y = acc0[i];
+            if (DUAL) y = acc1[i] * z_silu(acc0[i]);
+            else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
             else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
             a.out[m][(int64_t) it * a.out_ld + row] = y;
         }
+    }
+}
+
+// Encode fp32 rows x[r][K] (row stride ld) in an activation type: one wave per (row, 256-block),
+// same arithmetic as encode_row. Grid: ceil(n_rows * ceil(K/256) / 4) blocks of 256 threads.
+struct EncodeArgs { const float * x; int ld, K, n_rows, act_fmt; ActBuf act; };
+__global__ void __launch_bounds__(256) k_encode_rows(EncodeArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int Kp = kpad(a.K), nb = Kp / 256;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= a.n_rows * nb) return;
+    const int r = item / nb, b = item % nb;
+    const float * x = a.x + (int64_t) r * a.ld + b * 256;
+    float v[4];
+    if (b * 256 + 256 <= a.K) {
+        const float4 f = *(const float4 *) (x + lane * 4);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = b * 256 + lane * 4 + e < a.K ? x[lane * 4 + e] : 0.0f;
+    }
+    if (a.act_fmt == ACT_Q8_K) {
+        q8k_block_v(v, a.act.q + (int64_t) r * Kp + b * 256, a.act.d256 + (int64_t) r * nb + b, a.act.bs + (int64_t) r * (Kp / 16) + b * 16, lane);
+    } else if (a.act_fmt == ACT_Q8_0) {
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+        const float dd = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        int qi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qi[e] = (int) rintf(v[e] * id);
+        const uint32_t packed = (uint32_t) (qi[0] & 255) | ((uint32_t) (qi[1] & 255) << 8) |
+                                ((uint32_t) (qi[2] & 255) << 16) | ((uint32_t) (qi[3] & 255) << 24);
+        *(uint32_t *) (a.act.q + (int64_t) r * Kp + b * 256 + lane * 4) = packed;
+        if ((lane & 7) == 0) a.act.d32[(int64_t) r * (Kp / 32) + b * 8 + (lane >> 3)] = h2f(f2h(dd));
+    } else {
+        uint16_t * h = a.act.h + (int64_t) r * Kp + b * 256 + lane * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f2h(v[e]);
     }
 }
 
@@ -1314,6 +1416,20 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
                 a.wsel[(int64_t) t * a.k + rank] = pr[j];
             }
         }
+    }
+}
+
+// KV rows between the host layout [n][nkv][hd] (staged in device memory) and the cache layout
+// [slot][kvh][S][hd]: dir 0 writes the cache, dir 1 reads it into the staging buffer.
+__global__ void __launch_bounds__(256) k_kv_move(uint4 * stage, uint16_t * cache, int n, int nkv, int hd, int S,
+                                                 int row0, int slot, int dir) {
+    const int cpr = hd / 8;                                        // 16-byte chunks per head row
+    const int64_t total = (int64_t) n * nkv * cpr;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        const int c = (int) (i % cpr), g = (int) ((i / cpr) % nkv), r = (int) (i / ((int64_t) cpr * nkv));
+        uint4 * cp = (uint4 *) (cache + (((int64_t) slot * nkv + g) * S + row0 + r) * hd) + c;
+        if (dir == 0) *cp = stage[i];
+        else stage[i] = *cp;
     }
 }
 
