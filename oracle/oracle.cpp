@@ -14,7 +14,7 @@
 //    probabilities, top-k indices and weights on the CPU and on the device:
 //      - n_embd-long dots: 64 lane partials (lane l sums i = l, l+64, ... with fmaf, ascending),
 //        then a xor butterfly (32,16,8,4,2,1) of fp32 adds;
-//      - router_dim-long dots (MLP layers): one fmaf chain over i ascending;
+//      - router_dim-long dots (MLP layers): 8 strided fmaf partial chains + xor butterfly (4,2,1);
 //      - RMSNorm sum of squares in double: 64 lane partials + xor butterfly;
 //      - softmax: max, exp via orc_expf, double sum with the same butterfly, p = e * (float)(1/sum);
 //      - top-k: score descending, ties to the lower expert index.
@@ -390,10 +390,21 @@ float lane_dot(const float * w, const float * x, int64_t n) {
     }
     return tree64(p);
 }
-float chain_dot(const float * w, const float * x, int64_t n) {
-    float acc = 0.0f;
-    for (int64_t i = 0; i < n; ++i) acc = std::fma(w[i], x[i], acc);
-    return acc;
+// router_dim-long dot: 8 strided partial fmaf chains (partial p: i = p, p+8, ... ascending), then
+// a xor butterfly over the partials (offsets 4, 2, 1): ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7))
+float chain8_dot(const float * w, const float * x, int64_t n) {
+    float p[8];
+    for (int l = 0; l < 8; ++l) {
+        float acc = 0.0f;
+        for (int64_t i = l; i < n; i += 8) acc = std::fma(w[i], x[i], acc);
+        p[l] = acc;
+    }
+    for (int off = 4; off >= 1; off >>= 1) {
+        float nxt[8];
+        for (int l = 0; l < 8; ++l) nxt[l] = p[l] + p[l ^ off];
+        std::memcpy(p, nxt, sizeof(nxt));
+    }
+    return p[0];
 }
 void router_rms(const float * x, const float * w, int64_t n, float eps, float * y) {
     double p[64];
@@ -486,10 +497,10 @@ void router_token(const orc_model & m, const orc_layer & ly, const float * x, co
     }
     std::vector<float> rn(rd), h1(rd), h2(rd), lg(E), pr(E);
     router_rms(rh, ly.r_norm.data(), rd, m.hp.rms_eps, rn.data());
-    for (int o = 0; o < rd; ++o) h1[o] = z_gelu(chain_dot(ly.r_m0.data() + (int64_t) o * rd, rn.data(), rd) + ly.r_m0_b[o]);
-    for (int o = 0; o < rd; ++o) h2[o] = z_gelu(chain_dot(ly.r_m2.data() + (int64_t) o * rd, h1.data(), rd) + ly.r_m2_b[o]);
+    for (int o = 0; o < rd; ++o) h1[o] = z_gelu(chain8_dot(ly.r_m0.data() + (int64_t) o * rd, rn.data(), rd) + ly.r_m0_b[o]);
+    for (int o = 0; o < rd; ++o) h2[o] = z_gelu(chain8_dot(ly.r_m2.data() + (int64_t) o * rd, h1.data(), rd) + ly.r_m2_b[o]);
     for (int e = 0; e < E; ++e) {
-        lg[e] = chain_dot(ly.r_m4.data() + (int64_t) e * rd, h2.data(), rd);
+        lg[e] = chain8_dot(ly.r_m4.data() + (int64_t) e * rd, h2.data(), rd);
         if (!ly.logit_bias.empty()) lg[e] = lg[e] + ly.logit_bias[e];
     }
     float mx = -INFINITY;

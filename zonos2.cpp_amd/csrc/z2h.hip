@@ -171,10 +171,10 @@ int upload_f32(z2h_ctx * ctx, const HostTensor & t, float ** out, int64_t n_expe
     return Z2H_OK;
 }
 
-// W [out][in] -> W^T [in][ld] with the output dimension padded to ld = a multiple of 4 (zeros)
-int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
-    const int64_t in = t.ne[0], outn = t.ne[1], ld = (outn + 3) & ~3;
-    std::vector<float> full((size_t) (in * outn)), tr((size_t) (in * ld), 0.0f);
+// W [out][in] as fp32 rows padded to in + 4 floats (the router tail's LDS layout)
+int upload_f32_rows_padded(z2h_ctx * ctx, const HostTensor & t, float ** out) {
+    const int64_t in = t.ne[0], outn = t.ne[1], ld = in + 4;
+    std::vector<float> rows((size_t) (ld * outn), 0.0f);
     for (int64_t r = 0; r < outn; ++r) {
         const uint8_t * src = t.bytes.data() + r * z2::row_bytes(t.type, in);
         for (int64_t i = 0; i < in; ++i) {
@@ -183,12 +183,11 @@ int upload_f32_transposed(z2h_ctx * ctx, const HostTensor & t, float ** out) {
             else if (t.type == Z2H_F16) { uint16_t h; std::memcpy(&h, src + 2 * i, 2); v = z2::f16_to_f32(h); }
             else if (t.type == Z2H_Q8_0) { uint16_t h; std::memcpy(&h, src + 34 * (i / 32), 2); v = (float) (int8_t) src[34 * (i / 32) + 2 + i % 32] * z2::f16_to_f32(h); }
             else return seterr(ctx, Z2H_ENOTSUP, "router matrices must be F32, F16 or Q8_0");
-            full[r * in + i] = v;
+            rows[r * ld + i] = v;
         }
     }
-    for (int64_t r = 0; r < outn; ++r) for (int64_t i = 0; i < in; ++i) tr[i * ld + r] = full[r * in + i];
-    if (int rc = dalloc(ctx, out, tr.size() * 4, ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(*out, tr.data(), tr.size() * 4, hipMemcpyHostToDevice));
+    if (int rc = dalloc(ctx, out, rows.size() * 4, ctx->bytes_w)) return rc;
+    HIPX(hipMemcpy(*out, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
     return Z2H_OK;
 }
 
@@ -454,6 +453,16 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
         const bool dual = a.mode == MM_SWIGLU;
         if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
+        if (!a.grouped && (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX) {
+            // few row groups: K split over the 4 waves of a block, one row group per block
+            dim3 grid(m0.tiles, grid_y, dual ? 1 : a.n_mats), block(256);
+#define SPL(W_, D_) hipLaunchKernelGGL((k_gemv_split<W_, D_>), grid, block, lds, ctx->stream, a)
+            if (m0.type == Z2H_Q4_K) { if (dual) SPL(WF_Q4_K, true); else SPL(WF_Q4_K, false); }
+            else { if (dual) SPL(WF_Q8_0, true); else SPL(WF_Q8_0, false); }
+#undef SPL
+            HIPX(hipGetLastError());
+            return Z2H_OK;
+        }
         dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
 #define MM16(W_, D_, R_) hipLaunchKernelGGL((k_gemv_mfma<W_, D_, R_>), grid, block, lds, ctx->stream, a)
         if (m0.type == Z2H_Q4_K) {
@@ -549,12 +558,19 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     r.cap_probs = (float *) capp(ctx, Z2H_CAP_PROBS, L);
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_DOWN);
-        hipLaunchKernelGGL(k_router_down, dim3((ctx->rd + 3) / 4, T), dim3(256), 0, ctx->stream, r);
+        const dim3 grid((ctx->rd + 3) / 4, T);
+        switch (hp.n_embd / 64) {
+            case 4: hipLaunchKernelGGL(k_router_down<4>, grid, dim3(256), 0, ctx->stream, r); break;
+            case 8: hipLaunchKernelGGL(k_router_down<8>, grid, dim3(256), 0, ctx->stream, r); break;
+            case 16: hipLaunchKernelGGL(k_router_down<16>, grid, dim3(256), 0, ctx->stream, r); break;
+            case 32: hipLaunchKernelGGL(k_router_down<32>, grid, dim3(256), 0, ctx->stream, r); break;
+            default: hipLaunchKernelGGL(k_router_down<64>, grid, dim3(256), 0, ctx->stream, r); break;
+        }
         HIPX(hipGetLastError());
     }
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
-        hipLaunchKernelGGL(k_router_tail, dim3((T + RT_TPB - 1) / RT_TPB), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        hipLaunchKernelGGL(k_router_tail, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
@@ -718,6 +734,15 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
                        1, Z2H_KF_GEMV_HEAD);
 }
 
+// Raise a kernel's dynamic-LDS limit to what gfx950's 160 KiB leaves beside its static LDS.
+int allow_lds(const void * fn, z2h_ctx * ctx) {
+    hipFuncAttributes fa{};
+    HIPX(hipFuncGetAttributes(&fa, fn));
+    const int dyn = 160 * 1024 - (int) fa.sharedSizeBytes;
+    HIPX(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+    return Z2H_OK;
+}
+
 int check_err_flag(z2h_ctx * ctx) {
     int h = 0;
     HIPX(hipMemcpy(&h, ctx->d_err, 4, hipMemcpyDeviceToHost));
@@ -777,6 +802,7 @@ int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int dev
     if (hp->n_head <= 0 || hp->n_head_kv <= 0 || hp->n_head % hp->n_head_kv || hp->head_dim % 8 || hp->head_dim > 256)
         return Z2H_EINVAL;
     if (hp->n_codebooks + 1 > MAX_TABLES) return Z2H_ENOTSUP;
+    if (hp->n_embd % 4 || hp->n_embd > 4 * 256 * RN_NV) return Z2H_ENOTSUP;   // k_resnorm row layout
     auto ctx = std::make_unique<z2h_ctx>();
     ctx->hp = *hp;
     ctx->expert_used.assign(hp->expert_used, hp->expert_used + hp->n_layer);
@@ -841,11 +867,11 @@ int z2h_upload_tensor(z2h_ctx * ctx, const char * name_c, int type, const int64_
             return upload_f32(ctx, t, &ly.r_down, -1);
         }
         if (rest == "router_down.bias") return upload_f32(ctx, t, &ly.r_down_b, ctx->rd);
-        if (rest == "router_mlp0.weight") return upload_f32_transposed(ctx, t, &ly.r_m0t);
+        if (rest == "router_mlp0.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m0t);
         if (rest == "router_mlp0.bias") return upload_f32(ctx, t, &ly.r_m0_b, ctx->rd);
-        if (rest == "router_mlp2.weight") return upload_f32_transposed(ctx, t, &ly.r_m2t);
+        if (rest == "router_mlp2.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m2t);
         if (rest == "router_mlp2.bias") return upload_f32(ctx, t, &ly.r_m2_b, ctx->rd);
-        if (rest == "router_mlp4.weight") return upload_f32_transposed(ctx, t, &ly.r_m4t);
+        if (rest == "router_mlp4.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m4t);
         if (rest == "router_norm.weight") return upload_f32(ctx, t, &ly.r_norm, ctx->rd);
         if (rest == "router_bias") return upload_f32(ctx, t, &ly.r_bias, -1);
         if (rest == "router_eda_scale") return upload_f32(ctx, t, &ly.r_eda, ctx->rd);
@@ -899,15 +925,23 @@ int z2h_finalize(z2h_ctx * ctx) {
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
     if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
-    if (ctx->rd > 256 || ctx->rd % 4) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be a multiple of 4, at most 256");
+    if (ctx->rd > 0) {
+        const int d = hp.n_embd;
+        if (ctx->rd != 64 && ctx->rd != 128 && ctx->rd != 192 && ctx->rd != 256) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be 64, 128, 192 or 256");
+        if (d != 256 && d != 512 && d != 1024 && d != 2048 && d != 4096) return seterr(ctx, Z2H_ENOTSUP, "MoE layers need n_embd in {256, 512, 1024, 2048, 4096}");
+        if (ctx->kmax > 8) return seterr(ctx, Z2H_ENOTSUP, "top-k above 8");
+    }
     if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));
-    // allow the GEMV kernels the full 160 KiB of gfx950 LDS for their dynamic carve-up
+    // allow each kernel the rest of gfx950's 160 KiB of LDS (beyond its static LDS) for its dynamic
+    // carve-up
     const int lds_max = 160 * 1024 - 8 * 1024;
-#define LDS_ATTR(K_) (void) hipFuncSetAttribute((const void *) &(K_), hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
+#define LDS_ATTR(K_) if (int rc_ = allow_lds((const void *) &(K_), ctx)) return rc_;
     LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
     LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
+    LDS_ATTR((k_gemv_split<WF_Q4_K, false>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false>))
+    LDS_ATTR((k_gemv_split<WF_Q4_K, true>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G>))

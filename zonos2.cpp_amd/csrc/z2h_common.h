@@ -67,6 +67,8 @@ __device__ __forceinline__ double dpp_d(double v) {
     return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
 }
 constexpr int DPP_ROW_SHL = 0x100;     // lane i reads lane i + n of its 16-lane row
+constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
 __device__ __forceinline__ float lane0_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)); }
 __device__ __forceinline__ double lane0_d(double v) {
     const uint64_t u = __builtin_bit_cast(uint64_t, v);

@@ -57,28 +57,25 @@ __device__ __forceinline__ void q8k_block(const float * x, int8_t * q, float * d
     const float v[4] = {x[lane * 4], x[lane * 4 + 1], x[lane * 4 + 2], x[lane * 4 + 3]};
     q8k_block_v(v, q, d, bs, lane);
 }
-__device__ __forceinline__ void q8k_block_v(const float (&vin)[4], int8_t * q, float * d, int16_t * bs, int lane) {
-    float v[4];
-    float bax = -1.0f, bval = 0.0f;
-    int bidx = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = vin[i];
-        const float ax = fabsf(v[i]);
-        if (ax > bax) { bax = ax; bval = v[i]; bidx = lane * 4 + i; }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oax = __shfl_xor(bax, off, WAVE), oval = __shfl_xor(bval, off, WAVE);
-        const int oidx = __shfl_xor(bidx, off, WAVE);
-        if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
-    }
+__device__ __forceinline__ void q8k_block_v(const float (&v)[4], int8_t * q, float * d, int16_t * bs, int lane) {
+    // largest |x| by a DPP max; its first occurrence (lowest element index lane*4+i) from ballots
+    const float lmax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float amax = wave_max_f(lmax);
     int qi[4];
-    if (bax == 0.0f) {
+    if (amax == 0.0f) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qi[i] = 0;
         if (lane == 0) *d = 0.0f;
     } else {
+        int best = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t m = __ballot(fabsf(v[i]) == amax);
+            if (m) best = min(best, (int) (__ffsll((unsigned long long) m) - 1) * 4 + i);
+        }
+        const int bi = best & 3;
+        const float vb = bi == 0 ? v[0] : bi == 1 ? v[1] : bi == 2 ? v[2] : v[3];
+        const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vb), best >> 2));
         const float iscale = -127.0f / bval;
 #pragma unroll
         for (int i = 0; i < 4; ++i) qi[i] = min(127, (int) rintf(iscale * v[i]));
@@ -88,8 +85,8 @@ __device__ __forceinline__ void q8k_block_v(const float (&vin)[4], int8_t * q, f
                             ((uint32_t) (qi[2] & 255) << 16) | ((uint32_t) (qi[3] & 255) << 24);
     *(uint32_t *) (q + lane * 4) = packed;
     int s = qi[0] + qi[1] + qi[2] + qi[3];
-    s += __shfl_xor(s, 1, WAVE);
-    s += __shfl_xor(s, 2, WAVE);
+    s += dpp_i<DPP_QUAD_XOR1>(s);                  // sum of the 4 lanes of a quad = 16 elements
+    s += dpp_i<DPP_QUAD_XOR2>(s);
     if ((lane & 3) == 0) bs[lane >> 2] = (int16_t) s;
 }
 
@@ -153,7 +150,7 @@ __device__ __forceinline__ void copy16(int n, Src src, Dst dst) {
 __device__ __forceinline__ double block_sum_d(double v, double * red) {
     v = wave_tree_d(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
+    __syncthreads();                               // earlier readers of red are done
     if (lane == 0) red[wave] = v;
     __syncthreads();
     return red[0] + red[1] + red[2] + red[3];
@@ -215,73 +212,143 @@ struct ResNormArgs {
     int * err;
 };
 
+// 4 consecutive elements of a dequantised table row (i0 % 4 == 0)
+__device__ __forceinline__ float4 table_elem4(const uint8_t * row, int type, int i0) {
+    switch (type) {
+        case 0: return *(const float4 *) (row + 4 * (int64_t) i0);
+        case 1: {
+            const uint2 h = *(const uint2 *) (row + 2 * (int64_t) i0);
+            return make_float4(h2f(h.x & 0xffffu), h2f(h.x >> 16), h2f(h.y & 0xffffu), h2f(h.y >> 16));
+        }
+        case 8: {
+            const uint8_t * b = row + 34 * (i0 >> 5);
+            const float dd = h2f(*(const uint16_t *) b);
+            const uint8_t * qv = b + 2 + (i0 & 31);
+            return make_float4((float) (int8_t) qv[0] * dd, (float) (int8_t) qv[1] * dd, (float) (int8_t) qv[2] * dd, (float) (int8_t) qv[3] * dd);
+        }
+    }
+    return make_float4(table_elem(row, type, i0), table_elem(row, type, i0 + 1), table_elem(row, type, i0 + 2), table_elem(row, type, i0 + 3));
+}
+
+// One block per token; thread tid owns elements 4*(tid + 256*j) .. +3 (d % 4 == 0, d <= 4096). Every
+// global read the block needs (norm weight, routes, residual, embedding rows) is issued before the
+// first reduction.
+constexpr int RN_NV = 4;
 __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     extern __shared__ float sm_rn[];
     float * xs = sm_rn;                // [d]
     __shared__ double red[4];
     const int t = blockIdx.x, d = a.d, tid = threadIdx.x;
     float * res = a.res ? a.res + (int64_t) t * d : nullptr;
+    float4 nw[RN_NV], xv[RN_NV];
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j) {
+        const int i0 = 4 * (tid + 256 * j);
+        if (a.norm_w && i0 < d) nw[j] = *(const float4 *) (a.norm_w + i0);
+    }
+    auto add4 = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
     if (a.mode == RN_EMBED) {
         if (a.emb_in) {
-            for (int i = tid; i < d; i += 256) xs[i] = a.emb_in[(int64_t) t * d + i];
+#pragma unroll
+            for (int j = 0; j < RN_NV; ++j) {
+                const int i0 = 4 * (tid + 256 * j);
+                if (i0 < d) xv[j] = *(const float4 *) (a.emb_in + (int64_t) t * d + i0);
+            }
         } else {
-            for (int i = tid; i < d; i += 256) xs[i] = 0.0f;
+            // sum of the W tables' rows in column order (kk = 0, 1, ...), each row gathered whole
+            const uint8_t * rows[MAX_TABLES];
             for (int kk = 0; kk < a.W; ++kk) {
                 const int id = a.ids[(int64_t) t * a.W + kk];
-                if (id < 0 || id >= a.tab_rows[kk]) { if (tid == 0) atomicOr(a.err, 1); continue; }
-                const uint8_t * row = a.tab[kk] + (int64_t) id * table_row_bytes(a.tab_type[kk], d);
-                for (int i = tid; i < d; i += 256) {
-                    const float e = table_elem(row, a.tab_type[kk], i);
-                    xs[i] = kk == 0 ? e : xs[i] + e;
-                }
+                const bool ok = id >= 0 && id < a.tab_rows[kk];
+                if (!ok && tid == 0) atomicOr(a.err, 1);
+                rows[kk] = a.tab[kk] + (int64_t) (ok ? id : 0) * table_row_bytes(a.tab_type[kk], d);
+            }
+#pragma unroll
+            for (int j = 0; j < RN_NV; ++j) {
+                const int i0 = 4 * (tid + 256 * j);
+                if (i0 >= d) continue;
+                float4 e[MAX_TABLES];
+#pragma unroll
+                for (int kk = 0; kk < MAX_TABLES; ++kk) if (kk < a.W) e[kk] = table_elem4(rows[kk], a.tab_type[kk], i0);
+                float4 x = e[0];
+#pragma unroll
+                for (int kk = 1; kk < MAX_TABLES; ++kk) if (kk < a.W) x = add4(x, e[kk]);
+                xv[j] = x;
             }
         }
+        // emb_norm (weightless); the normalised row seeds the residual stream
         double ss = 0.0;
-        for (int i = tid; i < d; i += 256) ss += (double) (xs[i] * xs[i]);
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j)
+            if (4 * (tid + 256 * j) < d) ss += (double) (xv[j].x * xv[j].x) + (double) (xv[j].y * xv[j].y) + (double) (xv[j].z * xv[j].z) + (double) (xv[j].w * xv[j].w);
         const double tot = block_sum_d(ss, red);
         const float scale = 1.0f / sqrtf((float) (tot / (double) d) + a.eps);
-        for (int i = tid; i < d; i += 256) { const float v = xs[i] * scale; xs[i] = v; res[i] = v; }
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 >= d) continue;
+            xv[j] = make_float4(xv[j].x * scale, xv[j].y * scale, xv[j].z * scale, xv[j].w * scale);
+            *(float4 *) (res + i0) = xv[j];
+        }
     } else if (a.mode == RN_ACCUM) {
+        // sum of the token's k routes in route order, + residual
         const float * __restrict__ src = a.src + ((int64_t) t * a.k) * d;
-        for (int i0 = tid * 4; i0 < d; i0 += 1024) {            // d % 4 == 0
-            float4 x = *(const float4 *) (src + i0);
-            for (int j = 1; j < a.k; ++j) {
-                const float4 y = *(const float4 *) (src + (int64_t) j * d + i0);
-                x.x = x.x + y.x; x.y = x.y + y.y; x.z = x.z + y.z; x.w = x.w + y.w;
-            }
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 >= d) continue;
+            float4 r[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) if (jj < a.k) r[jj] = *(const float4 *) (src + (int64_t) jj * d + i0);
+            const float4 r0 = res ? *(const float4 *) (res + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 x = r[0];
+#pragma unroll
+            for (int jj = 1; jj < 8; ++jj) if (jj < a.k) x = add4(x, r[jj]);
             if (a.cap_x) *(float4 *) (a.cap_x + (int64_t) t * d + i0) = x;
-            if (res) {
-                const float4 r0 = *(const float4 *) (res + i0);
-                x.x = x.x + r0.x; x.y = x.y + r0.y; x.z = x.z + r0.z; x.w = x.w + r0.w;
-                *(float4 *) (res + i0) = x;
-            }
-            *(float4 *) (xs + i0) = x;
+            if (res) { x = add4(x, r0); *(float4 *) (res + i0) = x; }
+            xv[j] = x;
         }
     } else if (a.mode == RN_ADD) {
         const float * __restrict__ src = a.src + (int64_t) t * d;
-        for (int i0 = tid * 4; i0 < d; i0 += 1024) {
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 >= d) continue;
             const float4 x = *(const float4 *) (src + i0), r0 = *(const float4 *) (res + i0);
-            const float4 r = make_float4(x.x + r0.x, x.y + r0.y, x.z + r0.z, x.w + r0.w);
-            *(float4 *) (res + i0) = r;
-            *(float4 *) (xs + i0) = r;
+            xv[j] = add4(x, r0);
+            *(float4 *) (res + i0) = xv[j];
         }
     } else {
-        for (int i = tid; i < d; i += 256) xs[i] = a.src[(int64_t) t * d + i];
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 < d) xv[j] = *(const float4 *) (a.src + (int64_t) t * d + i0);
+        }
     }
-    __syncthreads();
     if (a.norm_w) {
         double ss = 0.0;
-        for (int i = tid; i < d; i += 256) ss += (double) (xs[i] * xs[i]);
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j)
+            if (4 * (tid + 256 * j) < d) ss += (double) (xv[j].x * xv[j].x) + (double) (xv[j].y * xv[j].y) + (double) (xv[j].z * xv[j].z) + (double) (xv[j].w * xv[j].w);
         const double tot = block_sum_d(ss, red);
         const float scale = 1.0f / sqrtf((float) (tot / (double) d) + a.eps);
-        for (int i = tid; i < d; i += 256) {
-            const float v = (xs[i] * scale) * a.norm_w[i];
-            xs[i] = v;
-            if (a.cur_out) a.cur_out[(int64_t) t * d + i] = v;
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 >= d) continue;
+            xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
+            if (a.cur_out) *(float4 *) (a.cur_out + (int64_t) t * d + i0) = xv[j];
         }
-        __syncthreads();
     }
-    if (a.act_fmt != ACT_NONE) encode_row_rt(a.act_fmt, xs, d, a.act, t);
+    if (a.act_fmt == ACT_NONE) return;
+    // the encoders read the row from LDS (a 256-block spans the elements of 64 threads)
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j) {
+        const int i0 = 4 * (tid + 256 * j);
+        if (i0 < d) *(float4 *) (xs + i0) = xv[j];
+    }
+    __syncthreads();
+    encode_row_rt(a.act_fmt, xs, d, a.act, t);
 }
 
 // ------------------------------------------------------------------ k_gemv
@@ -920,6 +987,71 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(m16fmt
     }
 }
 
+// Dense (token-chunk) m16 GEMV with the K units split over the block's 4 waves: one 16-row group per
+// block (grid x), wave w takes units w, w+4, ... (all requested up front), partial sums are added in
+// LDS in wave order. Used where the matrix has few row groups (attention projections, output head),
+// so every wave has at most a few units in flight and the chip sees 4x more waves.
+constexpr int SPLIT_UMAX = 4;          // units per wave (U <= 16)
+template <int WF, bool DUAL>
+__global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
+    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
+    constexpr int AF = wfmt<WF>::ACT;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    __shared__ int s_tok[MT];
+    __shared__ float s_part[4][8][64];
+    const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g16 = blockIdx.x, m = DUAL ? 0 : blockIdx.z;
+    int8_t * sq = (int8_t *) smem;
+    int * sbs2 = (int *) (smem + MT * KP);
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + MT * (K / 32)) : (float *) (smem + MT * KP);
+    const int c0 = blockIdx.y * MT, nt = min(MT, a.n_tok - c0);
+    const int nsb = a.nsb, U = (DUAL ? 2 : 1) * nsb;
+    const uint4 * ub0 = (const uint4 *) (a.w[m] + (size_t) g16 * nsb * UB);
+    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (size_t) g16 * nsb * UB) : ub0;
+    auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
+    uint4 pq[SPLIT_UMAX][QS], ph[SPLIT_UMAX];
+#pragma unroll
+    for (int j = 0; j < SPLIT_UMAX; ++j)
+        if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
+    if (tid < MT) s_tok[tid] = c0 + min(tid, nt - 1);
+    __syncthreads();
+    m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
+    __syncthreads();
+    float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < SPLIT_UMAX; ++j) {
+        const int u = wave + 4 * j;
+        if (u < U) {
+            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
+            const bool first = !DUAL || u < nsb;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc0[i] = first ? acc0[i] + t4[i] : acc0[i];
+                acc1[i] = first ? acc1[i] : acc1[i] + t4[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { s_part[wave][i][lane] = acc0[i]; s_part[wave][4 + i][lane] = acc1[i]; }
+    __syncthreads();
+    if (wave != 0) return;
+    const int q = lane >> 4, row = g16 * 16 + (lane & 15);
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * q + i;
+        if (t >= nt) continue;
+        const float g = ((s_part[0][i][lane] + s_part[1][i][lane]) + s_part[2][i][lane]) + s_part[3][i][lane];
+        float y = g;
+        if (DUAL) {
+            const float u = ((s_part[0][4 + i][lane] + s_part[1][4 + i][lane]) + s_part[2][4 + i][lane]) + s_part[3][4 + i][lane];
+            y = u * z_silu(g);
+        } else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+        a.out[m][(int64_t) (c0 + t) * a.out_ld + row] = y;
+    }
+}
+
 // Encode fp32 rows x[r][K] (row stride ld) in an activation type: one wave per (row, 256-block),
 // same arithmetic as encode_row. Grid: ceil(n_rows * ceil(K/256) / 4) blocks of 256 threads.
 struct EncodeArgs { const float * x; int ld, K, n_rows, act_fmt; ActBuf act; };
@@ -1193,9 +1325,9 @@ struct RouterArgs {
     float * rh;               // [T][rd] (this layer's state)
     const float * norm_w;     // [rd]
     float eps;
-    const float * w0t; const float * b0;   // [rd_in][rd_out] (transposed), [rd]
+    const float * w0t; const float * b0;   // [rd][rd+4] (rows padded), [rd]
     const float * w2t; const float * b2;
-    const float * w4t;                      // [rd][E]
+    const float * w4t;                      // [E][rd+4]
     const float * logit_bias;               // [E] or null
     const float * mask;                     // [E] additive 0/-inf or null
     const float * sc_bias;                  // router_bias [E]
@@ -1204,41 +1336,37 @@ struct RouterArgs {
 };
 
 // rh[t][o] = lane-strided fma partials over d + xor butterfly, + bias (+ state * eda).
-// grid (ceil(rd/4), T): wave = output row, blockIdx.y = token. Loads are issued 8 at a time ahead
-// of the fma chain; the chain order (i = lane, lane+64, ... ascending) is the contract's.
+// grid (ceil(rd/4), T): wave = output row, blockIdx.y = token. All of a lane's loads are issued before
+// its fma chain; the chain order (i = lane, lane+64, ... ascending) is the contract's.
+template <int NI>   // NI = d / 64 elements per lane
 __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     const int lane = threadIdx.x & 63, o = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
     if (o >= a.rd) return;
-    const float * __restrict__ w = a.w_down + (int64_t) o * a.d;
-    const float * __restrict__ x = a.x + (int64_t) t * a.d;
+    const float * __restrict__ w = a.w_down + (int64_t) o * a.d + lane;
+    const float * __restrict__ x = a.x + (int64_t) t * a.d + lane;
+    float wv[NI], xv[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) { wv[j] = w[64 * j]; xv[j] = x[64 * j]; }
+    const float b = a.b_down[o];
+    const float st = a.eda && a.state_in ? a.state_in[(int64_t) t * a.rd + o] * a.eda[o] : 0.0f;
     float acc = 0.0f;
-    int i = lane;
-    for (; i + 64 * 7 < a.d; i += 64 * 8) {
-        float wv[8], xv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { wv[j] = w[i + 64 * j]; xv[j] = x[i + 64 * j]; }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
-    }
-    for (; i < a.d; i += 64) acc = __builtin_fmaf(w[i], x[i], acc);
-    float v = wave_tree_f(acc) + a.b_down[o];
-    if (a.eda && a.state_in) v = v + a.state_in[(int64_t) t * a.rd + o] * a.eda[o];
+    for (int j = 0; j < NI; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
+    float v = wave_tree_f(acc) + b;
+    if (a.eda && a.state_in) v = v + st;
     if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
 }
 
-// Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k.
-// One block per RT_TPB tokens, all three W^T planes resident in LDS. Every global read the block
-// needs (the planes, by LDS-direct loads; the tokens' router states; each thread's biases) is issued
-// at entry, so the kernel waits on memory once. MLP outputs are per-output fmaf chains over i
-// ascending; the norm and softmax sums are wave trees; top-k ranks each expert against all others
-// (score descending, ties to the lower index), so no lane-shuffle chain is needed per pick.
-constexpr int RT_TPB = 4;                // tokens per block = waves per block
-
+// Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k, one
+// block per token. The three weight planes (row-major, rows padded to rd + 4 floats) are copied into
+// LDS by LDS-direct loads at entry, together with every other global read of the block. An MLP output
+// is the dot of its weight row with the layer input as 8 strided fmaf partial chains (partial p sums
+// i = p, p+8, ... ascending) combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group;
+// the block's 32 groups take outputs g, g+32, ... The norm and softmax sums are wave trees; top-k ranks
+// each expert against all others (score descending, ties to the lower index).
 __host__ __device__ inline int pad4(int n) { return (n + 3) & ~3; }
-// LDS: W0^T, W2^T [rd][rd], W4^T [rd][pad4(E)], two activation planes [RT_TPB][rd], logits and
-// scores [RT_TPB][pad4(E)]
 __host__ __device__ inline size_t router_tail_lds(int rd, int E) {
-    return (size_t) 4 * (2 * rd * rd + rd * pad4(E) + 2 * RT_TPB * rd + 2 * RT_TPB * pad4(E));
+    return (size_t) 4 * ((size_t) (2 * rd + E) * (rd + 4) + 2 * rd + pad4(E) + 64);
 }
 
 // n16 16-byte items from src to LDS dst, by LDS-direct loads (64 items per wave instruction)
@@ -1251,98 +1379,77 @@ __device__ __forceinline__ void lds_dma(const void * src, void * dst, int n16) {
     }
 }
 
-// out[t][o] = chain_i W^T[i][o] * x[t][i] (i ascending, from 0) for the block's tokens: thread
-// (o = tid % n_out, group tid / n_out) serves tokens group + G*j, j < TT.
-template <int TT>
-__device__ __forceinline__ void rt2_chain(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
-                                          float (&acc)[TT], int & o, int & tg) {
-    const int tid = threadIdx.x, G = 256 / n_out;
-    o = tid % n_out; tg = tid / n_out;
+// y[o] = post(dot(W[o], x)) for o < n_out with n_in = 8 * NM; MODE 0: gelu(dot + b[o]); MODE 1: dot
+// (+ logit bias[o]) (+ mask[o]). NM is a compile-time count so the lane's loads are issued unguarded.
+template <int MODE, int NM>
+__device__ __forceinline__ void rt_layer(const float * w, int ldw, const float * x, int n_out, float * y,
+                                         const float * bias, const float * bias2) {
+    const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
+    float xr[NM];
 #pragma unroll
-    for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
-    if (tg >= G) return;
-    const float * xr[TT];
+    for (int m = 0; m < NM; ++m) xr[m] = x[p + 8 * m];
+    for (int o = g; o < n_out; o += 32) {
+        const float * wr = w + o * ldw + p;
+        float wv[NM];
 #pragma unroll
-    for (int j = 0; j < TT; ++j) xr[j] = x + min(tg + G * j, nt - 1) * n_in;
-    for (int i = 0; i < n_in; i += 4) {
-        const float w0 = wt[(i + 0) * ldw + o], w1 = wt[(i + 1) * ldw + o];
-        const float w2 = wt[(i + 2) * ldw + o], w3 = wt[(i + 3) * ldw + o];
+        for (int m = 0; m < NM; ++m) wv[m] = wr[8 * m];
+        float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < TT; ++j) {
-            const float4 xv = *(const float4 *) (xr[j] + i);
-            acc[j] = __builtin_fmaf(w0, xv.x, acc[j]);
-            acc[j] = __builtin_fmaf(w1, xv.y, acc[j]);
-            acc[j] = __builtin_fmaf(w2, xv.z, acc[j]);
-            acc[j] = __builtin_fmaf(w3, xv.w, acc[j]);
-        }
-    }
-}
-
-// one MLP layer: y[t][o] = post(chain + ...), for n_out <= 256
-template <int TT, int MODE>   // MODE 0: gelu(acc + b[o]); 1: acc (+ logit bias[o]) (+ mask[o])
-__device__ __forceinline__ void rt2_layer(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
-                                          float * y, int ldy, float pb, const float * pb2, const float * pb3) {
-    float acc[TT]; int o, tg;
-    rt2_chain<TT>(wt, ldw, x, n_in, n_out, nt, acc, o, tg);
-    const int G = 256 / n_out;
-    if (tg < G) {
-#pragma unroll
-        for (int j = 0; j < TT; ++j) {
-            const int t = tg + G * j;
-            if (t >= nt) continue;
-            float v = acc[j];
-            if (MODE == 0) v = z_gelu(v + pb);
+        for (int m = 0; m < NM; ++m) acc = __builtin_fmaf(wv[m], xr[m], acc);
+        acc = acc + __shfl_xor(acc, 4, 8);
+        acc = acc + __shfl_xor(acc, 2, 8);
+        acc = acc + __shfl_xor(acc, 1, 8);
+        if (p == 0) {
+            float v = acc;
+            if (MODE == 0) v = z_gelu(v + bias[o]);
             else {
-                if (pb2) v = v + *pb2;
-                if (pb3) v = v + *pb3;
+                if (bias) v = v + bias[o];
+                if (bias2) v = v + bias2[o];
             }
-            y[t * ldy + o] = v;
+            y[o] = v;
         }
     }
 }
 
-template <int MODE>
-__device__ __forceinline__ void rt2_layer_any(const float * wt, int ldw, const float * x, int n_in, int n_out, int nt,
-                                              float * y, int ldy, float pb, const float * pb2, const float * pb3) {
-    const int G = 256 / n_out, tt = (RT_TPB + G - 1) / G;
-    if (tt >= 4) rt2_layer<4, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
-    else if (tt >= 2) rt2_layer<2, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
-    else rt2_layer<1, MODE>(wt, ldw, x, n_in, n_out, nt, y, ldy, pb, pb2, pb3);
+// the router MLP for router_dim = 8 * NM
+template <int NM>
+__device__ __forceinline__ void rt_mlp(const RouterArgs & a, const float * s_w0, const float * s_w2, const float * s_w4, int ldw,
+                                       float * s_x, float * s_y, float * s_l) {
+    rt_layer<0, NM>(s_w0, ldw, s_x, a.rd, s_y, a.b0, nullptr);
+    __syncthreads();
+    rt_layer<0, NM>(s_w2, ldw, s_y, a.rd, s_x, a.b2, nullptr);
+    __syncthreads();
+    rt_layer<1, NM>(s_w4, ldw, s_x, a.E, s_l, a.logit_bias, a.mask);
 }
 
 __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
-    const int rd = a.rd, E = a.E, E4 = pad4(E);
-    float * s_w0 = sm_rt;                       // [rd][rd]
-    float * s_w2 = s_w0 + rd * rd;              // [rd][rd]
-    float * s_w4 = s_w2 + rd * rd;              // [rd][E4]
-    float * s_a = s_w4 + rd * E4;               // [RT_TPB][rd]
-    float * s_b = s_a + RT_TPB * rd;            // [RT_TPB][rd]
-    float * s_l = s_b + RT_TPB * rd;            // [RT_TPB][E4] logits
-    float * s_s = s_l + RT_TPB * E4;            // [RT_TPB][E4] selection scores
-    const int t0 = blockIdx.x * RT_TPB, nt = min(RT_TPB, a.T - t0);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rd = a.rd, E = a.E, ldw = rd + 4;
+    float * s_w0 = sm_rt;                       // [rd][rd+4]
+    float * s_w2 = s_w0 + rd * ldw;             // [rd][rd+4]
+    float * s_w4 = s_w2 + rd * ldw;             // [E][rd+4]
+    float * s_x = s_w4 + E * ldw;               // [rd]
+    float * s_y = s_x + rd;                     // [rd]
+    float * s_l = s_y + rd;                     // [E]
+    float * s_b = s_l + pad4(E);                // [64]: b0 / b2 staging not needed (read from global)
+    (void) s_b;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // every global read of the block, issued together
-    lds_dma(a.w0t, s_w0, rd * rd / 4);
-    lds_dma(a.w2t, s_w2, rd * rd / 4);
-    lds_dma(a.w4t, s_w4, rd * E4 / 4);
-    const int tw = t0 + min(wave, nt - 1);      // this wave's token (norm, softmax)
+    lds_dma(a.w0t, s_w0, rd * ldw / 4);
+    lds_dma(a.w2t, s_w2, rd * ldw / 4);
+    lds_dma(a.w4t, s_w4, E * ldw / 4);
     float rh[4], nw[4], sb[4], mk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int i = lane + 64 * j, e = lane + 64 * j;
-        rh[j] = i < rd ? a.rh[(int64_t) tw * rd + i] : 0.0f;
+        const int i = lane + 64 * j;
+        rh[j] = i < rd ? a.rh[(int64_t) t * rd + i] : 0.0f;
         nw[j] = i < rd ? a.norm_w[i] : 0.0f;
-        sb[j] = e < E ? a.sc_bias[e] : 0.0f;
-        mk[j] = e < E && a.mask ? a.mask[e] : 0.0f;
+        sb[j] = i < E ? a.sc_bias[i] : 0.0f;
+        mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
     }
-    const int o_r = tid % rd, o_e = tid % E;
-    const float b0 = a.b0[o_r], b2 = a.b2[o_r];
-    const float lb = a.logit_bias ? a.logit_bias[o_e] : 0.0f, lm = a.mask ? a.mask[o_e] : 0.0f;
-    const float * plb = a.logit_bias ? &lb : nullptr, * plm = a.mask ? &lm : nullptr;
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // router RMS norm, one wave per token: double lane partials (i = lane, lane + 64, ...) + tree
-    if (wave < nt) {
+    // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
+    if (wave == 0) {
         double part = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
@@ -1351,70 +1458,91 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int i = lane + 64 * j;
-            if (i < rd) s_a[wave * rd + i] = (rh[j] * scale) * nw[j];
+            if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
         }
     }
     __syncthreads();
-    rt2_layer_any<0>(s_w0, rd, s_a, rd, rd, nt, s_b, rd, b0, nullptr, nullptr);
-    __syncthreads();
-    rt2_layer_any<0>(s_w2, rd, s_b, rd, rd, nt, s_a, rd, b2, nullptr, nullptr);
-    __syncthreads();
-    rt2_layer_any<1>(s_w4, E4, s_a, rd, E, nt, s_l, E4, 0.0f, plb, plm);
-    __syncthreads();
-    // softmax (own exp, double tree sum) + selection scores, one wave per token
-    float pr[4];
-    if (wave < nt) {
-        const int t = t0 + wave;
-        float lg[4];
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            lg[j] = e < E ? s_l[wave * E4 + e] : -__builtin_inff();
-            mx = fmaxf(mx, lg[j]);
-        }
-        mx = wave_max_f(mx);
-        float ex[4];
-        double ps = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            ex[j] = e < E ? z_expf(lg[j] - mx) : 0.0f;
-            if (e < E) ps += (double) ex[j];
-        }
-        const float inv = (float) (1.0 / wave_tree_d(ps));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            pr[j] = ex[j] * inv;
-            if (e < E) {
-                float sc = pr[j] + sb[j];
-                if (a.mask) sc = sc + mk[j];
-                s_s[wave * E4 + e] = sc;
-                if (a.cap_logits) a.cap_logits[(int64_t) t * E + e] = lg[j];
-                if (a.cap_probs) a.cap_probs[(int64_t) t * E + e] = pr[j];
-            }
-        }
+    switch (rd) {                                    // router_dim in {64, 128, 192, 256} (host-checked)
+        case 64:  rt_mlp<8>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
+        case 128: rt_mlp<16>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
+        case 192: rt_mlp<24>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
+        default:  rt_mlp<32>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
     }
     __syncthreads();
-    // top-k: expert e's rank = #{e' : s[e'] > s[e] or (s[e'] == s[e] and e' < e)}
-    if (wave < nt) {
-        const int t = t0 + wave;
-        const float * ss = s_s + wave * E4;
+    if (wave != 0) return;
+    // softmax (own exp, double tree sum) + selection scores
+    float lg[4], pr[4], sc[4];
+    float mx = -__builtin_inff();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j;
-            if (64 * j >= E) break;
-            const float me = e < E ? ss[e] : 0.0f;
-            int rank = 0;
-            for (int f = 0; f < E; ++f) {
-                const float v = ss[f];
-                rank += (v > me) || (v == me && f < e);
-            }
-            if (e < E && rank < a.k) {
-                a.sel[(int64_t) t * a.k + rank] = e;
-                a.wsel[(int64_t) t * a.k + rank] = pr[j];
-            }
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        lg[j] = e < E ? s_l[e] : -__builtin_inff();
+        mx = fmaxf(mx, lg[j]);
+    }
+    mx = wave_max_f(mx);
+    float ex[4];
+    double ps = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        ex[j] = e < E ? z_expf(lg[j] - mx) : 0.0f;
+        if (e < E) ps += (double) ex[j];
+    }
+    const float inv = (float) (1.0 / wave_tree_d(ps));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        pr[j] = ex[j] * inv;
+        sc[j] = pr[j] + sb[j];
+        if (a.mask) sc[j] = sc[j] + mk[j];
+        if (e < E) {
+            if (a.cap_logits) a.cap_logits[(int64_t) t * E + e] = lg[j];
+            if (a.cap_probs) a.cap_probs[(int64_t) t * E + e] = pr[j];
+        }
+    }
+    // top-k: expert e's rank = #{e' : s[e'] > s[e] or (s[e'] == s[e] and e' < e)}. The scores go to
+    // LDS (padded with -inf, which never outranks a real score) and every lane compares against all.
+    float * s_s = s_y;                                                // [>= 64] (free after the MLP)
+    const int En = E <= 64 ? 64 : ((E + 3) & ~3);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        if (e < En) s_s[e] = e < E ? sc[j] : -__builtin_inff();
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (E <= 64) {
+        float4 sv[16];
+#pragma unroll
+        for (int f4 = 0; f4 < 16; ++f4) sv[f4] = *(const float4 *) (s_s + 4 * f4);
+        const float me = sc[0];
+        int rank = 0;
+#pragma unroll
+        for (int f4 = 0; f4 < 16; ++f4) {
+            const float vv[4] = {sv[f4].x, sv[f4].y, sv[f4].z, sv[f4].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rank += (vv[c] > me) || (vv[c] == me && 4 * f4 + c < lane);
+        }
+        if (lane < E && rank < a.k) {
+            a.sel[(int64_t) t * a.k + rank] = lane;
+            a.wsel[(int64_t) t * a.k + rank] = pr[0];
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (64 * j >= E) break;
+        const int e = lane + 64 * j;
+        const float me = sc[j];
+        int rank = 0;
+        for (int f = 0; f < E; ++f) {
+            const float v = s_s[f];
+            rank += (v > me) || (v == me && f < e);
+        }
+        if (e < E && rank < a.k) {
+            a.sel[(int64_t) t * a.k + rank] = e;
+            a.wsel[(int64_t) t * a.k + rank] = pr[j];
         }
     }
 }
