@@ -70,6 +70,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c3", "c4-q6_k", "c4-q8_0"])
     ap.add_argument("--cpu-steps", type=int, default=2, help="timed oracle steps for the CPU baseline (0: skip)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after the timed region, copy 256 MiB device to device once (a kernel of known traffic "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
@@ -223,6 +226,13 @@ def main() -> int:
     if args.config != "c3":
         line["metric"] = "batched-decode tok/s (MoE step); % of HBM peak GB/s"
     print(json.dumps(line), flush=True)
+    if args.calib_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 256 MiB read + 256 MiB written")
     ctx.close()
     return 0
 

@@ -14,7 +14,8 @@
 //    probabilities, top-k indices and weights on the CPU and on the device:
 //      - n_embd-long dots: 64 lane partials (lane l sums i = l, l+64, ... with fmaf, ascending),
 //        then a xor butterfly (32,16,8,4,2,1) of fp32 adds;
-//      - router_dim-long dots (MLP layers): 8 strided fmaf partial chains + xor butterfly (4,2,1);
+//      - router_dim-long dots (MLP layers): 8 fmaf partial chains over contiguous eighths + xor
+//        butterfly (4,2,1);
 //      - RMSNorm sum of squares in double: 64 lane partials + xor butterfly;
 //      - softmax: max, exp via orc_expf, double sum with the same butterfly, p = e * (float)(1/sum);
 //      - top-k: score descending, ties to the lower expert index.
@@ -390,13 +391,15 @@ float lane_dot(const float * w, const float * x, int64_t n) {
     }
     return tree64(p);
 }
-// router_dim-long dot: 8 strided partial fmaf chains (partial p: i = p, p+8, ... ascending), then
-// a xor butterfly over the partials (offsets 4, 2, 1): ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7))
+// router_dim-long dot: 8 partial fmaf chains over contiguous eighths (partial p: i = p*n/8 ...
+// (p+1)*n/8 - 1 ascending), then a xor butterfly over the partials (offsets 4, 2, 1):
+// ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7))
 float chain8_dot(const float * w, const float * x, int64_t n) {
+    const int64_t b = n / 8;
     float p[8];
     for (int l = 0; l < 8; ++l) {
         float acc = 0.0f;
-        for (int64_t i = l; i < n; i += 8) acc = std::fma(w[i], x[i], acc);
+        for (int64_t i = l * b; i < (l + 1) * b; ++i) acc = std::fma(w[i], x[i], acc);
         p[l] = acc;
     }
     for (int off = 4; off >= 1; off >>= 1) {

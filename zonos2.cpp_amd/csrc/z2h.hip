@@ -2,9 +2,10 @@
 //
 // One HIP stream per context; every device buffer is allocated at create / finalize time, so a
 // step performs no allocation. A step is a fixed sequence of kernels per layer (see z2h_kernels.h):
-//   k_resnorm -> k_gemv(QKV+gate) -> k_qkv_post -> k_attn_partial -> k_attn_combine -> k_gemv(W_o)
-//   -> k_resnorm(+attn, ffn_norm) -> [MoE] k_router_down -> k_router_tail -> k_gemv(gate/up, grouped)
-//   -> k_gemv(down, grouped, SwiGLU staging) | [dense] k_gemv(up/gate) -> k_gemv(down)
+//   k_resnorm -> k_gemv(QKV+gate) -> k_attn_decode (QK-norm, RoPE, KV append, partials) -> k_attn_combine
+//   -> k_gemv(W_o) -> k_resnorm(+attn, ffn_norm) -> [MoE] k_router_down -> k_router_tail
+//   -> k_gemv(gate/up + SwiGLU, grouped) -> k_encode_rows -> k_gemv(down, grouped) | [dense] the same
+//   FFN sequence ungrouped
 // and after the last layer k_resnorm(output_norm) -> k_gemv(head, softcap).
 #include "z2h.h"
 #include "z2h_kernels.h"
@@ -84,8 +85,7 @@ struct z2h_ctx {
     // scratch (sized for n_slots tokens)
     int Tmax = 0, Kmax = 0, items_max = 0;
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
-    float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * gate = nullptr, * wo_out = nullptr;
-    uint16_t * q16 = nullptr;
+    float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
     ActBuf act{}, act_y{};
     float * attn_o = nullptr;         // [T][nh*hd] gated attention output
@@ -117,6 +117,7 @@ namespace {
 
 int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; return code; }
 int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
+int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
 
 constexpr int PROF_MAX = 16384;
 
@@ -368,8 +369,8 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->d_ids, (size_t) T * W * 4, b)) || (rc = dalloc(ctx, &ctx->d_emb, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->res, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->cur, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->tmp_x, (size_t) T * d * 4, b)) ||
-        (rc = dalloc(ctx, &ctx->qkvg, (size_t) T * R * 4, b)) || (rc = dalloc(ctx, &ctx->gate, (size_t) T * nh * 4, b)) ||
-        (rc = dalloc(ctx, &ctx->wo_out, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->q16, (size_t) T * nh * hd * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->qkvg, (size_t) T * R * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->wo_out, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->part_o, (size_t) ctx->items_max * grp * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->part_ml, (size_t) ctx->items_max * grp * 2 * 4, b)) ||
         (rc = dalloc(ctx, &ctx->act.q, (size_t) T * KM, b)) || (rc = dalloc(ctx, &ctx->act.d32, (size_t) T * (KM / 32) * 4, b)) ||
@@ -655,7 +656,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     if ((rc = cap_copy(ctx, Z2H_CAP_RES_IN, 0, ctx->res, T))) return rc;
     (void) h_npast;
     // persistent attention grid: the item count comes from the device n_past table
-    const int attn_grid = std::min(ctx->items_max, 2048);
+    const int attn_grid = std::min(ctx->items_max, 4096);
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int L = 0; L < hp.n_layer; ++L) {
@@ -669,8 +670,8 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         a.slot_idx = d_slot; a.n_past = d_npast; a.T = T; a.S = ctx->S;
         const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;
         a.kc = ctx->kv + (size_t) (2 * L) * lsz; a.vc = ctx->kv + (size_t) (2 * L + 1) * lsz;
-        a.q16 = ctx->q16; a.gate = ctx->gate;
         a.cap_q = (float *) capp(ctx, Z2H_CAP_Q, L); a.cap_k = (float *) capp(ctx, Z2H_CAP_K, L); a.cap_v = (float *) capp(ctx, Z2H_CAP_V, L);
+        a.cap_gate = (float *) capp(ctx, Z2H_CAP_GATE, L);
         a.part_o = ctx->part_o; a.part_ml = ctx->part_ml;
         a.o_out = ctx->attn_o;
         a.act = ctx->act;
@@ -679,17 +680,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         const bool in_block = span % 256 == 0;             // whole encoding blocks, no padding
         a.act_fmt = in_block ? wo_act : ACT_NONE;
         {
-            prof_scope ps(ctx, Z2H_KF_QKV_POST);
-            hipLaunchKernelGGL(k_qkv_post, dim3((nh + 2 * nkv + 3) / 4, T), dim3(256), 0, ctx->stream, a);
-            HIPX(hipGetLastError());
-        }
-        if ((rc = cap_copy(ctx, Z2H_CAP_GATE, L, ctx->gate, T))) return rc;
-        const int grp = nh / nkv;
-        const size_t lds_p = (size_t) 2 * ATT_CH * (hd + 8) * 2 + (size_t) (grp * hd + 8) * 2 + (size_t) grp * ATT_CH * 4 + 16;
-        {
+            // QK-norm / RoPE / KV append fused in; item count from the device n_past table
             prof_scope ps(ctx, Z2H_KF_ATTN);
-            hipLaunchKernelGGL(k_attn_partial, dim3(attn_grid), dim3(256), lds_p, ctx->stream, a);
-            HIPX(hipGetLastError());
+            if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
         }
         {
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
@@ -740,6 +733,23 @@ int allow_lds(const void * fn, z2h_ctx * ctx) {
     HIPX(hipFuncGetAttributes(&fa, fn));
     const int dyn = 160 * 1024 - (int) fa.sharedSizeBytes;
     HIPX(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+    return Z2H_OK;
+}
+
+// one wave per (token, 64-row chunk, KV head) item, instantiated per head size and group size
+int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
+    const int grp = a.nh / a.nkv;
+#define ATT(H_, G_) hipLaunchKernelGGL((k_attn_decode<H_, G_>), dim3(grid), dim3(64), 0, ctx->stream, a)
+#define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
+    switch (a.hd) {
+        case 16: ATT_G(16) break;
+        case 32: ATT_G(32) break;
+        case 64: ATT_G(64) break;
+        default: ATT_G(128) break;
+    }
+#undef ATT_G
+#undef ATT
+    HIPX(hipGetLastError());
     return Z2H_OK;
 }
 
@@ -799,8 +809,11 @@ int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int dev
     if (!out) return Z2H_EINVAL;
     *out = nullptr;
     if (!hp || !hp->expert_used || hp->n_layer <= 0 || n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
-    if (hp->n_head <= 0 || hp->n_head_kv <= 0 || hp->n_head % hp->n_head_kv || hp->head_dim % 8 || hp->head_dim > 256)
-        return Z2H_EINVAL;
+    if (hp->n_head <= 0 || hp->n_head_kv <= 0 || hp->n_head % hp->n_head_kv) return Z2H_EINVAL;
+    {   // decode attention instantiations: head_dim 16/32/64/128, query heads per KV head 1/2/4/8
+        const int hd = hp->head_dim, grp = hp->n_head / hp->n_head_kv;
+        if ((hd != 16 && hd != 32 && hd != 64 && hd != 128) || (grp != 1 && grp != 2 && grp != 4 && grp != 8)) return Z2H_ENOTSUP;
+    }
     if (hp->n_codebooks + 1 > MAX_TABLES) return Z2H_ENOTSUP;
     if (hp->n_embd % 4 || hp->n_embd > 4 * 256 * RN_NV) return Z2H_ENOTSUP;   // k_resnorm row layout
     auto ctx = std::make_unique<z2h_ctx>();
@@ -920,14 +933,14 @@ int z2h_finalize(z2h_ctx * ctx) {
             if (!ly.r_down || !ly.r_down_b || !ly.r_m0t || !ly.r_m0_b || !ly.r_m2t || !ly.r_m2_b || !ly.r_m4t || !ly.r_norm || !ly.r_bias)
                 missing += b + "router_* ";
             if (ly.up_exps.ok() && ly.k > ly.E) return seterr(ctx, Z2H_EINVAL, b + "top-k exceeds the expert count");
-            if (ly.up_exps.ok() && ly.E > 256) return seterr(ctx, Z2H_ENOTSUP, "more than 256 experts");
+            if (ly.up_exps.ok() && ly.E > 128) return seterr(ctx, Z2H_ENOTSUP, "more than 128 experts");
             if (ly.up_exps.ok() && (ly.up_exps.rows != hp.n_ff || ly.down_exps.K != hp.n_ff)) return seterr(ctx, Z2H_EINVAL, b + "expert shape mismatch");
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
     if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
     if (ctx->rd > 0) {
         const int d = hp.n_embd;
-        if (ctx->rd != 64 && ctx->rd != 128 && ctx->rd != 192 && ctx->rd != 256) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be 64, 128, 192 or 256");
+        if (ctx->rd != 64 && ctx->rd != 128) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be 64 or 128");
         if (d != 256 && d != 512 && d != 1024 && d != 2048 && d != 4096) return seterr(ctx, Z2H_ENOTSUP, "MoE layers need n_embd in {256, 512, 1024, 2048, 4096}");
         if (ctx->kmax > 8) return seterr(ctx, Z2H_ENOTSUP, "top-k above 8");
     }

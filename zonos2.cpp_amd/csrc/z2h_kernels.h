@@ -1101,68 +1101,13 @@ struct AttnArgs {
     const int32_t * slot_idx, * n_past;
     int T, S;
     uint16_t * kc, * vc;     // this layer's cache [slot][kvh][S][hd]
-    uint16_t * q16;          // [T][nh][hd]
-    float * gate;            // [T][nh]
-    float * cap_q, * cap_k, * cap_v;   // fp32 captures (nullable)
+    float * cap_q, * cap_k, * cap_v, * cap_gate;   // fp32 captures (nullable)
     // partials
     float * part_o;          // [items][grp][hd]
     float * part_ml;         // [items][grp][2]
     float * o_out;           // [T][nh*hd] (combine: gated output, fp32)
     ActBuf act; int act_fmt; // encoding of o_out for W_o
 };
-
-// QK-norm, |temp|, RoPE, KV append, sigmoid gate. One block per token, one wave per head.
-__global__ void __launch_bounds__(256) k_qkv_post(AttnArgs a) {
-    const int t = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int hd = a.hd, nh = a.nh, nkv = a.nkv;
-    const float * __restrict__ row = a.qkvg + (int64_t) t * a.R;
-    const int pos = a.n_past[t], slot = a.slot_idx[t];
-    for (int h = blockIdx.x * 4 + wave; h < nh + 2 * nkv; h += gridDim.x * 4) {
-        const bool isq = h < nh, isk = h >= nh && h < nh + nkv;
-        const float * src = row + (int64_t) h * hd;          // q heads, then k heads, then v heads
-        if (!isq && !isk) {                                  // V: plain f16 store
-            const int g = h - nh - nkv;
-            uint16_t * dst = a.vc + (((int64_t) slot * nkv + g) * a.S + pos) * hd;
-            for (int i = lane; i < hd; i += 64) {
-                dst[i] = f2h(src[i]);
-                if (a.cap_v) a.cap_v[((int64_t) t * nkv + g) * hd + i] = src[i];
-            }
-            continue;
-        }
-        float xv[4];
-        double ss = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { const int i = lane + 64 * j; xv[j] = i < hd ? src[i] : 0.0f; }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ss += (double) (xv[j] * xv[j]);
-        for (int i = lane + 256; i < hd; i += 64) ss += (double) (src[i] * src[i]);
-        ss = wave_tree_d(ss);
-        const float sc = 1.0f / sqrtf((float) (ss / (double) hd) + a.qk_eps);
-        const float tmp = isq ? a.temp[h] : 1.0f;
-        for (int pi = lane; pi < hd / 2; pi += 64) {
-            float x0 = src[2 * pi] * sc, x1 = src[2 * pi + 1] * sc;
-            if (isq) { x0 = x0 * tmp; x1 = x1 * tmp; }
-            float theta = (float) pos;
-            for (int j = 0; j < pi; ++j) theta = theta * a.theta_scale;
-            const float cs = cosf(theta), sn = sinf(theta);
-            const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
-            if (isq) {
-                uint16_t * dq = a.q16 + ((int64_t) t * nh + h) * hd;
-                dq[2 * pi] = f2h(y0); dq[2 * pi + 1] = f2h(y1);
-                if (a.cap_q) { a.cap_q[((int64_t) t * nh + h) * hd + 2 * pi] = y0; a.cap_q[((int64_t) t * nh + h) * hd + 2 * pi + 1] = y1; }
-            } else {
-                const int g = h - nh;
-                uint16_t * dk = a.kc + (((int64_t) slot * nkv + g) * a.S + pos) * hd;
-                dk[2 * pi] = f2h(y0); dk[2 * pi + 1] = f2h(y1);
-                if (a.cap_k) { a.cap_k[((int64_t) t * nkv + g) * hd + 2 * pi] = y0; a.cap_k[((int64_t) t * nkv + g) * hd + 2 * pi + 1] = y1; }
-            }
-        }
-    }
-    // gate = sigmoid(W_g x): the last nh columns of the fused projection
-    if (blockIdx.x == 0)
-    for (int h = threadIdx.x; h < nh; h += 256)
-        a.gate[(int64_t) t * nh + h] = z_sigmoid(row[(int64_t) (nh + 2 * nkv) * hd + h]);
-}
 
 __device__ __forceinline__ int attn_n_items(const int32_t * n_past, int T, int nkv) {
     int n = 0;
@@ -1182,66 +1127,142 @@ __device__ __forceinline__ bool attn_item(const int32_t * n_past, int T, int nkv
     return false;
 }
 
-// One 64-row chunk of one token's band for one KV head and its query-head group.
-__global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    const int hd = a.hd, grp = a.nh / a.nkv, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ldk = hd + 8;                                          // padded f16 row stride
-    uint16_t * sk = (uint16_t *) smem;                               // [ATT_CH][ldk]
-    uint16_t * sv = sk + ATT_CH * ldk;                               // [ATT_CH][ldk]
-    uint16_t * sq = sv + ATT_CH * ldk;                               // [grp][hd]
-    float * sp = (float *) (sq + grp * hd + 8);                      // [grp][ATT_CH]
-    const int n_items = attn_n_items(a.n_past, a.T, a.nkv);         // from the device tables
+// Decode attention, one wave per item = (token, 64-row chunk of its band [0, n_past], KV head g). The
+// wave requests its chunk's K rows (lane = row) and V columns (lane = pair of head dims) first, then
+// forms the token's queries of group g from the fused projection output (per-head RMSNorm, |temp|,
+// interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, f16), and in the
+// chunk that holds the new row also k and v, which it appends to the f16 cache and uses directly.
+// Scores are f16 dot products with fp32 accumulation, then a per-chunk softmax partial (max, sum of
+// exp, unnormalised P.V) per head, merged by k_attn_combine.
+template <int HD, int GRP>
+__global__ void __launch_bounds__(64) k_attn_decode(AttnArgs a) {
+    constexpr int NP = HD / 2;                     // dim pairs (<= 64 lanes)
+    constexpr int KV4 = HD / 8;                    // uint4 per K row
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];      // f16 pairs
+    __shared__ __attribute__((aligned(16))) float s_p[ATT_CH][GRP];
+    __shared__ __attribute__((aligned(16))) uint32_t s_nk[NP], s_nv[NP];
+    const int lane = threadIdx.x, nkv = a.nkv;
+    const int n_items = attn_n_items(a.n_past, a.T, nkv);
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
         int t, c, g;
-        if (!attn_item(a.n_past, a.T, a.nkv, item, t, c, g)) break;
-        const int L = a.n_past[t] + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
+        if (!attn_item(a.n_past, a.T, nkv, item, t, c, g)) break;
+        const int np = a.n_past[t], L = np + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
+        const bool last = r0 + nr == L;                              // the chunk holds the new row
         const int slot = a.slot_idx[t];
-        const uint16_t * kb = a.kc + (((int64_t) slot * a.nkv + g) * a.S + r0) * hd;
-        const uint16_t * vb = a.vc + (((int64_t) slot * a.nkv + g) * a.S + r0) * hd;
-        __syncthreads();
-        const int vpr = hd / 8;                                      // uint4 per row
-        copy16<256>(2 * nr * vpr,
-            [&](int i) { const int w = i / (nr * vpr), j = i % (nr * vpr);
-                         return (const uint4 *) ((w ? vb : kb) + (int64_t) (j / vpr) * hd) + j % vpr; },
-            [&](int i) { const int w = i / (nr * vpr), j = i % (nr * vpr);
-                         return (uint4 *) ((w ? sv : sk) + (j / vpr) * ldk) + j % vpr; });
-        for (int i = tid; i < grp * hd; i += 256) sq[i] = a.q16[((int64_t) t * a.nh + g * grp) * hd + i];
-        __syncthreads();
-        // scores: wave = head of the group (looped), lane = row
-        for (int hh = wave; hh < grp; hh += 4) {
-            float s = -__builtin_inff();
-            if (lane < nr) {
-                const uint32_t * kr = (const uint32_t *) (sk + lane * ldk);
-                const uint32_t * qr = (const uint32_t *) (sq + hh * hd);
-                float acc = 0.0f;
-                for (int i = 0; i < hd / 2; ++i) acc = fdot2(kr[i], qr[i], acc);
-                s = acc * a.scale;
+        const uint16_t * kb = a.kc + (((int64_t) slot * nkv + g) * a.S + r0) * HD;
+        const uint16_t * vb = a.vc + (((int64_t) slot * nkv + g) * a.S + r0) * HD;
+        // ---- the chunk's K rows and V columns (rows past the chunk re-read its last row, weight 0)
+        uint4 kr[KV4];
+        const int rr = min(lane, nr - 1);
+#pragma unroll
+        for (int j = 0; j < KV4; ++j) kr[j] = *(const uint4 *) (kb + (int64_t) rr * HD + 8 * j);
+        const int pl = min(lane, NP - 1);
+        uint32_t vr[ATT_CH];
+#pragma unroll
+        for (int r = 0; r < ATT_CH; ++r) vr[r] = *(const uint32_t *) (vb + (int64_t) min(r, nr - 1) * HD + 2 * pl);
+        // ---- rotation of this lane's pair (pl) at position np
+        float th = (float) np;
+        for (int j = 0; j < pl; ++j) th = th * a.theta_scale;
+        const float cs = cosf(th), sn = sinf(th);
+        const float * row = a.qkvg + (int64_t) t * a.R;
+        auto norm_rope = [&](const float * src, float mul, float & y0, float & y1) {
+            const float x0 = lane < NP ? src[2 * lane] : 0.0f, x1 = lane < NP ? src[2 * lane + 1] : 0.0f;
+            const double ss = wave_tree_d((double) (x0 * x0) + (double) (x1 * x1));
+            const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + a.qk_eps);
+            float z0 = x0 * sc, z1 = x1 * sc;
+            if (mul != 1.0f) { z0 = z0 * mul; z1 = z1 * mul; }
+            y0 = z0 * cs - z1 * sn;
+            y1 = z0 * sn + z1 * cs;
+        };
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            const int qh = g * GRP + h;
+            float y0, y1;
+            norm_rope(row + (int64_t) qh * HD, a.temp[qh], y0, y1);
+            if (lane < NP) {
+                s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                if (a.cap_q && c == 0) {
+                    a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
+                    a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
+                }
             }
+        }
+        if (last) {
+            float k0, k1;
+            norm_rope(row + (int64_t) (a.nh + g) * HD, 1.0f, k0, k1);
+            const float * vsrc = row + (int64_t) (a.nh + nkv + g) * HD;
+            if (lane < NP) {
+                const float v0 = vsrc[2 * lane], v1 = vsrc[2 * lane + 1];
+                const uint32_t kp = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
+                const uint32_t vp = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
+                s_nk[lane] = kp; s_nv[lane] = vp;
+                *(uint32_t *) (a.kc + (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane) = kp;
+                *(uint32_t *) (a.vc + (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane) = vp;
+                if (a.cap_k) {
+                    a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane] = k0; a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = k1;
+                    a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane] = v0; a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = v1;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- scores (lane = row r0 + lane)
+        const bool isnew = last && lane == nr - 1;
+        if (isnew) {
+#pragma unroll
+            for (int j = 0; j < KV4; ++j) kr[j] = *(const uint4 *) &s_nk[4 * j];
+        }
+        float pr[GRP];
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KV4; ++j) {
+                const uint4 qv = *(const uint4 *) &s_q[h][4 * j];
+                acc = fdot2(kr[j].x, qv.x, acc); acc = fdot2(kr[j].y, qv.y, acc);
+                acc = fdot2(kr[j].z, qv.z, acc); acc = fdot2(kr[j].w, qv.w, acc);
+            }
+            const float s = lane < nr ? acc * a.scale : -__builtin_inff();
             const float mx = wave_max_f(s);
             const float pe = lane < nr ? z_expf(s - mx) : 0.0f;
             const float l = wave_tree_f(pe);
-            sp[hh * ATT_CH + lane] = pe;
+            pr[h] = pe;
             if (lane == 0) {
-                a.part_ml[((int64_t) item * grp + hh) * 2 + 0] = mx;
-                a.part_ml[((int64_t) item * grp + hh) * 2 + 1] = l;
+                a.part_ml[((int64_t) item * GRP + h) * 2 + 0] = mx;
+                a.part_ml[((int64_t) item * GRP + h) * 2 + 1] = l;
             }
         }
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) s_p[lane][h] = pr[h];
         __syncthreads();
-        // P.V: wave = head (looped), lane = pair of head dims
-        for (int hh = wave; hh < grp; hh += 4) {
-            for (int pi = lane; pi < hd / 2; pi += 64) {
-                float o0 = 0.0f, o1 = 0.0f;
-                for (int r = 0; r < nr; ++r) {
-                    const float pr = sp[hh * ATT_CH + r];
-                    const uint32_t vv = *(const uint32_t *) (sv + r * ldk + 2 * pi);
-                    o0 = __builtin_fmaf(pr, h2f(vv & 0xffffu), o0);
-                    o1 = __builtin_fmaf(pr, h2f(vv >> 16), o1);
+        // ---- P.V (lane = pair of head dims); rows past the chunk carry p = 0
+        float o0[GRP], o1[GRP];
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) { o0[h] = 0.0f; o1[h] = 0.0f; }
+        const uint32_t nv = s_nv[pl];
+#pragma unroll
+        for (int r = 0; r < ATT_CH; ++r) {
+            const uint32_t vv = (last && r == nr - 1) ? nv : vr[r];
+            const float va = h2f(vv & 0xffffu), vc = h2f(vv >> 16);
+            float pp[GRP];
+            if constexpr (GRP % 4 == 0) {
+#pragma unroll
+                for (int h4 = 0; h4 < GRP; h4 += 4) {
+                    const float4 p4 = *(const float4 *) &s_p[r][h4];
+                    pp[h4] = p4.x; pp[h4 + 1] = p4.y; pp[h4 + 2] = p4.z; pp[h4 + 3] = p4.w;
                 }
-                float * po = a.part_o + ((int64_t) item * grp + hh) * hd;
-                po[2 * pi] = o0; po[2 * pi + 1] = o1;
+            } else {
+#pragma unroll
+                for (int h = 0; h < GRP; ++h) pp[h] = s_p[r][h];
             }
+#pragma unroll
+            for (int h = 0; h < GRP; ++h) { o0[h] = __builtin_fmaf(pp[h], va, o0[h]); o1[h] = __builtin_fmaf(pp[h], vc, o1[h]); }
         }
+        if (lane < NP) {
+#pragma unroll
+            for (int h = 0; h < GRP; ++h)
+                *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * lane) = make_float2(o0[h], o1[h]);
+        }
+        __syncthreads();                                             // LDS reuse by the next item
     }
 }
 
@@ -1276,7 +1297,9 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        const float gt = a.gate[(int64_t) t * nh + g * grp + hh] / den;
+        const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd + g * grp + hh]);
+        if (a.cap_gate && lane == 0) a.cap_gate[(int64_t) t * nh + g * grp + hh] = gsig;
+        const float gt = gsig / den;
         for (int pi = lane; pi < hd / 2; pi += 64) {
             float o0 = 0.0f, o1 = 0.0f;
             int c = 0;
@@ -1358,86 +1381,94 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
 }
 
 // Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k, one
-// block per token. The three weight planes (row-major, rows padded to rd + 4 floats) are copied into
-// LDS by LDS-direct loads at entry, together with every other global read of the block. An MLP output
-// is the dot of its weight row with the layer input as 8 strided fmaf partial chains (partial p sums
-// i = p, p+8, ... ascending) combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group;
-// the block's 32 groups take outputs g, g+32, ... The norm and softmax sums are wave trees; top-k ranks
-// each expert against all others (score descending, ties to the lower index).
+// block per token. An MLP output is the dot of its weight row with the layer input as 8 fmaf partial
+// chains over contiguous eighths of the row (partial p sums i = p*rd/8 ... (p+1)*rd/8 - 1 ascending)
+// combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group; the block's 32 groups take
+// outputs g, g+32, g+64, g+96. Each lane's weights (rows padded to rd + 4 floats) go straight from
+// global memory to registers as float4s: W0 and W2 at entry, W4 during layer 1, so the weight traffic
+// overlaps the norm and the earlier layers. The
+// norm and softmax sums are wave trees; top-k ranks each expert against all others (score
+// descending, ties to the lower index).
 __host__ __device__ inline int pad4(int n) { return (n + 3) & ~3; }
 __host__ __device__ inline size_t router_tail_lds(int rd, int E) {
-    return (size_t) 4 * ((size_t) (2 * rd + E) * (rd + 4) + 2 * rd + pad4(E) + 64);
+    return (size_t) 4 * (2 * rd + (E <= 64 ? 64 : pad4(E)) + 64);
 }
 
-// n16 16-byte items from src to LDS dst, by LDS-direct loads (64 items per wave instruction)
-__device__ __forceinline__ void lds_dma(const void * src, void * dst, int n16) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int c = wave; c * 64 < n16; c += 4) {
-        const int it = c * 64 + lane;
-        if (it < n16)
-            __builtin_amdgcn_global_load_lds((const uint4 *) src + it, (__attribute__((address_space(3))) void *) ((uint4 *) dst + c * 64), 16, 0, 0);
+// the lane's weights of outputs g + 32u (u < 4) of a [n_out][ldw] matrix (rows beyond n_out clamp):
+// elements [p*NM, p*NM + NM) of each row
+template <int NM>
+__device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, float4 (&wv)[4][NM / 4]) {
+    const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float4 * wr = (const float4 *) (w + (int64_t) min(g + 32 * u, n_out - 1) * ldw + p * NM);
+#pragma unroll
+        for (int m = 0; m < NM / 4; ++m) wv[u][m] = wr[m];
     }
 }
 
-// y[o] = post(dot(W[o], x)) for o < n_out with n_in = 8 * NM; MODE 0: gelu(dot + b[o]); MODE 1: dot
-// (+ logit bias[o]) (+ mask[o]). NM is a compile-time count so the lane's loads are issued unguarded.
+// y[o] = post(dot(W[o], x)) for the lane group's outputs (n_out <= 128); MODE 0: gelu(dot + b[o]);
+// MODE 1: dot (+ logit bias[o]) (+ mask[o])
 template <int MODE, int NM>
-__device__ __forceinline__ void rt_layer(const float * w, int ldw, const float * x, int n_out, float * y,
+__device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const float * x, int n_out, float * y,
                                          const float * bias, const float * bias2) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
-    float xr[NM];
+    float4 xr[NM / 4];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) xr[m] = x[p + 8 * m];
-    for (int o = g; o < n_out; o += 32) {
-        const float * wr = w + o * ldw + p;
-        float wv[NM];
+    for (int m = 0; m < NM / 4; ++m) xr[m] = *(const float4 *) (x + p * NM + 4 * m);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int m = 0; m < NM; ++m) wv[m] = wr[8 * m];
-        float acc = 0.0f;
+    for (int m = 0; m < NM / 4; ++m)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) acc = __builtin_fmaf(wv[m], xr[m], acc);
-        acc = acc + __shfl_xor(acc, 4, 8);
-        acc = acc + __shfl_xor(acc, 2, 8);
-        acc = acc + __shfl_xor(acc, 1, 8);
-        if (p == 0) {
-            float v = acc;
-            if (MODE == 0) v = z_gelu(v + bias[o]);
-            else {
-                if (bias) v = v + bias[o];
-                if (bias2) v = v + bias2[o];
-            }
-            y[o] = v;
+        for (int u = 0; u < 4; ++u) {
+            acc[u] = __builtin_fmaf(wv[u][m].x, xr[m].x, acc[u]);
+            acc[u] = __builtin_fmaf(wv[u][m].y, xr[m].y, acc[u]);
+            acc[u] = __builtin_fmaf(wv[u][m].z, xr[m].z, acc[u]);
+            acc[u] = __builtin_fmaf(wv[u][m].w, xr[m].w, acc[u]);
         }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        acc[u] = acc[u] + __shfl_xor(acc[u], 4, 8);
+        acc[u] = acc[u] + __shfl_xor(acc[u], 2, 8);
+        acc[u] = acc[u] + __shfl_xor(acc[u], 1, 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int o = g + 32 * u;
+        if (o >= n_out) break;
+        float v = acc[u];                          // every lane of the group holds the sum
+        if (MODE == 0) v = z_gelu(v + bias[o]);
+        else {
+            if (bias) v = v + bias[o];
+            if (bias2) v = v + bias2[o];
+        }
+        if (p == 0) y[o] = v;
     }
 }
 
-// the router MLP for router_dim = 8 * NM
+// the router MLP for router_dim = 8 * NM (<= 128 outputs per layer)
 template <int NM>
-__device__ __forceinline__ void rt_mlp(const RouterArgs & a, const float * s_w0, const float * s_w2, const float * s_w4, int ldw,
-                                       float * s_x, float * s_y, float * s_l) {
-    rt_layer<0, NM>(s_w0, ldw, s_x, a.rd, s_y, a.b0, nullptr);
+__device__ __forceinline__ void rt_mlp(const RouterArgs & a, float * s_x, float * s_y, float * s_l) {
+    const int ldw = a.rd + 4;
+    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
+    rt_load<NM>(a.w0t, ldw, a.rd, w0);
+    rt_load<NM>(a.w2t, ldw, a.rd, w2);
+    __syncthreads();                               // s_x holds the normalised state
+    rt_load<NM>(a.w4t, ldw, a.E, w4);
+    rt_layer<0, NM>(w0, s_x, a.rd, s_y, a.b0, nullptr);
     __syncthreads();
-    rt_layer<0, NM>(s_w2, ldw, s_y, a.rd, s_x, a.b2, nullptr);
+    rt_layer<0, NM>(w2, s_y, a.rd, s_x, a.b2, nullptr);
     __syncthreads();
-    rt_layer<1, NM>(s_w4, ldw, s_x, a.E, s_l, a.logit_bias, a.mask);
+    rt_layer<1, NM>(w4, s_x, a.E, s_l, a.logit_bias, a.mask);
 }
 
 __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
-    const int rd = a.rd, E = a.E, ldw = rd + 4;
-    float * s_w0 = sm_rt;                       // [rd][rd+4]
-    float * s_w2 = s_w0 + rd * ldw;             // [rd][rd+4]
-    float * s_w4 = s_w2 + rd * ldw;             // [E][rd+4]
-    float * s_x = s_w4 + E * ldw;               // [rd]
-    float * s_y = s_x + rd;                     // [rd]
-    float * s_l = s_y + rd;                     // [E]
-    float * s_b = s_l + pad4(E);                // [64]: b0 / b2 staging not needed (read from global)
-    (void) s_b;
+    const int rd = a.rd, E = a.E;
+    float * s_x = sm_rt;                        // [rd]
+    float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
+    float * s_l = s_y + max(rd, 64);            // [E]
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // every global read of the block, issued together
-    lds_dma(a.w0t, s_w0, rd * ldw / 4);
-    lds_dma(a.w2t, s_w2, rd * ldw / 4);
-    lds_dma(a.w4t, s_w4, E * ldw / 4);
     float rh[4], nw[4], sb[4], mk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1447,7 +1478,6 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
         sb[j] = i < E ? a.sc_bias[i] : 0.0f;
         mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
     }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
     if (wave == 0) {
         double part = 0.0;
@@ -1461,12 +1491,9 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
             if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
         }
     }
-    __syncthreads();
-    switch (rd) {                                    // router_dim in {64, 128, 192, 256} (host-checked)
-        case 64:  rt_mlp<8>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
-        case 128: rt_mlp<16>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
-        case 192: rt_mlp<24>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
-        default:  rt_mlp<32>(a, s_w0, s_w2, s_w4, ldw, s_x, s_y, s_l); break;
+    switch (rd) {                                    // router_dim in {64, 128} (host-checked)
+        case 64:  rt_mlp<8>(a, s_x, s_y, s_l); break;
+        default:  rt_mlp<16>(a, s_x, s_y, s_l); break;
     }
     __syncthreads();
     if (wave != 0) return;
@@ -1522,7 +1549,7 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
         for (int f4 = 0; f4 < 16; ++f4) {
             const float vv[4] = {sv[f4].x, sv[f4].y, sv[f4].z, sv[f4].w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) rank += (vv[c] > me) || (vv[c] == me && 4 * f4 + c < lane);
+            for (int c = 0; c < 4; ++c) rank += (int) (vv[c] > me) | ((int) (vv[c] == me) & (int) (4 * f4 + c < lane));
         }
         if (lane < E && rank < a.k) {
             a.sel[(int64_t) t * a.k + rank] = lane;
@@ -1538,7 +1565,7 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
         int rank = 0;
         for (int f = 0; f < E; ++f) {
             const float v = s_s[f];
-            rank += (v > me) || (v == me && f < e);
+            rank += (int) (v > me) | ((int) (v == me) & (int) (f < e));
         }
         if (e < E && rank < a.k) {
             a.sel[(int64_t) t * a.k + rank] = e;
