@@ -6,15 +6,24 @@
  * No C++ exception crosses this boundary. A context is not reentrant: one thread drives it, as in
  * the reference (src/server.cpp:905-911, docs/INTERNALS.md:200).
  *
+ * Weights live in a reference-counted z2h_model (the reference's zonos2_model, loaded once); each
+ * z2h_ctx (the reference's zonos2_batch_ctx: KV cache, scratch, step graphs) holds one reference, so
+ * several batch contexts can share one model. z2h_create is the one-call form: model and context.
+ *
  * Reference interfaces replaced (file:line in Zyphra/zonos2.cpp):
- *   z2h_create            zonos2_batch_init            src/zonos2-graph.cpp:639-690 (KV alloc, S rounding)
- *   z2h_upload_tensor     zonos2_model_load tensor set src/zonos2.cpp:100-119, name map 137-183
- *   z2h_finalize          zonos2_model_load field map  src/zonos2.cpp:126-185
+ *   z2h_model_create      zonos2_model_load hparams    src/zonos2.cpp:15-97, src/zonos2.h:124
+ *   z2h_model_upload_tensor zonos2_model_load tensors  src/zonos2.cpp:100-119, name map 137-183
+ *   z2h_model_finalize    zonos2_model_load field map  src/zonos2.cpp:126-185
+ *   z2h_model_release     zonos2_model_free            src/zonos2.h:125, src/zonos2.cpp:188-195
+ *   z2h_create_batch      zonos2_batch_init            src/zonos2-graph.cpp:639-690 (KV alloc, S rounding)
+ *   z2h_create            zonos2_model_load + zonos2_batch_init in one call
+ *   z2h_upload_tensor     as z2h_model_upload_tensor on the context's model
+ *   z2h_finalize          as z2h_model_finalize, then the context's scratch
  *   z2h_step              zonos2_batch_step            src/zonos2-graph.cpp:762-837 (+ slot_logits 839-841)
  *   z2h_prefill           zonos2_batch_slot_prefill    src/zonos2-graph.cpp:703-760
  *   z2h_moe_forward       build_moe                    src/zonos2-graph.cpp:191-239 (one MoE layer)
- *   z2h_set_expert_mask   zonos2_set_expert_mask       src/zonos2.cpp:203-239
- *   z2h_destroy           zonos2_batch_free            src/zonos2-graph.cpp:692-701
+ *   z2h_set_expert_mask   zonos2_set_expert_mask       src/zonos2.cpp:203-239, src/zonos2.h:136
+ *   z2h_destroy           zonos2_batch_free            src/zonos2-graph.cpp:692-701 (+ drops the model reference)
  */
 #ifndef Z2H_H
 #define Z2H_H
@@ -48,10 +57,31 @@ typedef struct z2h_hparams {
     const int32_t * expert_used;   /* [n_layer]: 0 = dense FFN, else MoE top-k */
 } z2h_hparams;
 
+typedef struct z2h_model z2h_model;
 typedef struct z2h_ctx z2h_ctx;
 
-/* Create a context on HIP device `device` with n_slots decode slots of slot_cap_frames rows each
- * (rounded up to a multiple of 256, as the reference does). The KV cache is zero-filled. */
+/* Weights only, on HIP device `device`; refcount 1. Upload every tensor, then finalize. */
+int z2h_model_create(const z2h_hparams * hp, int device, z2h_model ** out);
+/* Tensor hand-over as for z2h_upload_tensor below. */
+int z2h_model_upload_tensor(z2h_model * m, const char * name, int type, const int64_t ne[4],
+                            const void * data, size_t nbytes);
+/* Checks that every tensor the forward pass needs is present; no uploads afterwards. */
+int z2h_model_finalize(z2h_model * m);
+/* Expert mask / router-logit bias (see z2h_set_expert_mask / z2h_set_logit_bias) on the model: every
+ * context sharing it sees the change at its next step. No step may be in flight on any of them. */
+int z2h_model_set_expert_mask(z2h_model * m, int layer, const uint8_t * keep);
+int z2h_model_set_logit_bias(z2h_model * m, int layer, const float * bias);
+const char * z2h_model_last_error(const z2h_model * m);
+/* Drops one reference; the weights are freed with the last one (contexts hold one each). */
+void z2h_model_release(z2h_model * m);
+
+/* A batch context over a model (takes a reference; the model may be finalized before or after, through
+ * z2h_finalize). n_slots decode slots of slot_cap_frames rows each (rounded up to a multiple of 256,
+ * as the reference does); the KV cache is zero-filled. */
+int z2h_create_batch(z2h_model * m, int n_slots, int slot_cap_frames, z2h_ctx ** out);
+
+/* A new model on HIP device `device` and a batch context over it (which then holds the model's only
+ * reference) in one call. */
 int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int device, z2h_ctx ** out);
 
 /* Hand over one GGUF tensor: name as in the reference GGUF, ggml ne order (ne0 fastest, unused = 1),
@@ -59,7 +89,7 @@ int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int dev
 int z2h_upload_tensor(z2h_ctx * ctx, const char * name, int type, const int64_t ne[4],
                       const void * data, size_t nbytes);
 
-/* After all uploads: checks that every tensor the forward pass needs is present. */
+/* After all uploads: finalizes the context's model (if not yet) and allocates the step scratch. */
 int z2h_finalize(z2h_ctx * ctx);
 
 /* Slot rows per slot after rounding (the reference's slot_cap). */
@@ -138,7 +168,7 @@ enum {
 int z2h_profile_begin(z2h_ctx * ctx);
 int z2h_profile_end(z2h_ctx * ctx, double * ms, int32_t * launches);
 
-/* Device memory held by weights, KV cache and scratch (bytes). */
+/* Device memory held by weights (the shared model), KV cache and scratch (bytes). */
 int64_t z2h_device_bytes(const z2h_ctx * ctx, int what /* 0 weights, 1 kv, 2 scratch */);
 
 /* Message of the context's last failure. */

@@ -450,6 +450,7 @@ struct orc_layer {
     bool is_moe = false;
     int top_k = 0, n_exp = 0;
     std::vector<float> logit_bias;                // harness-only
+    std::vector<float> mask;                      // runtime expert mask, 0 / -inf (src/zonos2.cpp:203-239)
     // router weights as fp32 (dequantized once)
     std::vector<float> r_down, r_down_b, r_m0, r_m0_b, r_m2, r_m2_b, r_m4, r_norm, r_bias, r_eda;
 };
@@ -505,6 +506,7 @@ void router_token(const orc_model & m, const orc_layer & ly, const float * x, co
     for (int e = 0; e < E; ++e) {
         lg[e] = chain8_dot(ly.r_m4.data() + (int64_t) e * rd, h2.data(), rd);
         if (!ly.logit_bias.empty()) lg[e] = lg[e] + ly.logit_bias[e];
+        if (!ly.mask.empty()) lg[e] = lg[e] + ly.mask[e];          // graph.cpp:212
     }
     float mx = -INFINITY;
     for (int e = 0; e < E; ++e) mx = std::max(mx, lg[e]);
@@ -516,6 +518,7 @@ void router_token(const orc_model & m, const orc_layer & ly, const float * x, co
     for (int e = 0; e < E; ++e) pr[e] = ex[e] * inv;
     std::vector<float> sc(E);
     for (int e = 0; e < E; ++e) sc[e] = pr[e] + ly.r_bias[e];
+    if (!ly.mask.empty()) for (int e = 0; e < E; ++e) sc[e] = sc[e] + ly.mask[e];   // graph.cpp:218
     std::vector<int> idx(E);
     std::iota(idx.begin(), idx.end(), 0);
     std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return sc[a] > sc[b]; });
@@ -743,6 +746,16 @@ int orc_model_set_logit_bias(orc_model * m, int layer, const float * bias) {
     orc_layer & ly = m->layers[layer];
     if (!ly.is_moe) return fail("layer is not MoE");
     if (bias) ly.logit_bias.assign(bias, bias + ly.n_exp); else ly.logit_bias.clear();
+    return 0;
+}
+
+// zonos2_set_expert_mask for one layer (src/zonos2.cpp:228-234): keep[e] != 0 -> 0, else -inf
+int orc_model_set_expert_mask(orc_model * m, int layer, const uint8_t * keep) {
+    if (int rc = check_layer(m, layer)) return rc;
+    orc_layer & ly = m->layers[layer];
+    if (!ly.is_moe) return fail("layer is not MoE");
+    ly.mask.clear();
+    if (keep) for (int e = 0; e < ly.n_exp; ++e) ly.mask.push_back(keep[e] ? 0.0f : -INFINITY);
     return 0;
 }
 

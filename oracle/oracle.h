@@ -62,6 +62,10 @@ int  orc_model_finalize(orc_model * m);
 // Harness-only additive pre-softmax router-logit bias for layer L (NULL clears). Not a reference
 // input; used to impose a skewed expert popularity.
 int  orc_model_set_logit_bias(orc_model * m, int layer, const float * bias);
+// Runtime expert mask of layer L (zonos2_set_expert_mask, src/zonos2.cpp:203-239): keep[e] == 0 adds
+// -inf to expert e's router logit before the softmax and to its selection score (graph.cpp:212, 218);
+// NULL clears.
+int  orc_model_set_expert_mask(orc_model * m, int layer, const uint8_t * keep);
 void orc_model_free(orc_model * m);
 const char * orc_last_error(void);
 

@@ -41,6 +41,7 @@ def lib() -> C.CDLL:
         "orc_model_set": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_int64), vp]),
         "orc_model_finalize": (i32, [vp]),
         "orc_model_set_logit_bias": (i32, [vp, i32, vp]),
+        "orc_model_set_expert_mask": (i32, [vp, i32, vp]),
         "orc_model_free": (None, [vp]),
         "orc_last_error": (C.c_char_p, []),
         "orc_kv_create": (vp, [vp, i32, i32]),
@@ -105,6 +106,10 @@ class OracleModel:
             self._keep.append(b)
             check(lib().orc_model_set_logit_bias(self.m, L, ptr(b)))
         self.kmax = max([k for k in hp["expert_used"]] + [1])
+
+    def set_expert_mask(self, layer, keep):
+        k = None if keep is None else np.ascontiguousarray(keep, dtype=np.uint8)
+        check(lib().orc_model_set_expert_mask(self.m, layer, ptr(k)))
 
     def __del__(self):
         if getattr(self, "m", None):

@@ -4,10 +4,13 @@ import re
 
 from zonos2_amd.lib import BUILD
 
+# function declarations only: a return type at the start of a line, then the z2h_ name and "("
+DECL = re.compile(r"^(?:int|int64_t|void|const char \*)\s+\**\s*(z2h_[a-z0-9_]+)\s*\(", re.M)
+
 
 def test_exports_match_header(root):
     hdr = (root / "include" / "z2h.h").read_text()
-    decl = set(re.findall(r"\b(z2h_[a-z_]+)\s*\(", hdr))
+    decl = set(DECL.findall(hdr))
     assert len(decl) >= 15
     lib = C.CDLL(str(BUILD / "libzonos2_hip.so"))
     missing = [n for n in sorted(decl) if not hasattr(lib, n)]
@@ -17,5 +20,5 @@ def test_exports_match_header(root):
 def test_python_binding_covers_header(root):
     from zonos2_amd import z2h
     hdr = (root / "include" / "z2h.h").read_text()
-    decl = set(re.findall(r"\b(z2h_[a-z_]+)\s*\(", hdr))
+    decl = set(DECL.findall(hdr))
     assert decl == set(z2h.EXPORTS)

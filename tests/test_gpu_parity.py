@@ -10,7 +10,7 @@ import pytest
 import oracle_py as O
 from helpers import COS_MIN, MAXABS, assert_close, fill_kv, oracle_pair, min_topk_margin
 from zonos2_amd import configs, synth
-from zonos2_amd.z2h import Context
+from zonos2_amd.z2h import Context, Model
 
 pytestmark = pytest.mark.gpu
 
@@ -140,3 +140,46 @@ def test_graph_replay_matches_eager():
         got2 = ctx.step(inp.slot_idx[:2], inp.n_past[:2], emb=inp.emb[:2])
         assert np.array_equal(got2, ref2), f"replay {rep} (width 2)"
         ctx.moe_forward(0, x)                      # eager work between replays
+
+
+def test_shared_model_contexts_and_mask_invalidation():
+    """Two batch contexts over one device model (zonos2_model loaded once, several zonos2_batch_ctx)
+    step exactly like a context with its own copy of the weights; a model-level expert mask reaches
+    every context, including through its already-captured step graphs."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 46)
+    shared = Model(cfg.hparams(), model)
+    a = Context(None, wl.n_slots, wl.slot_cap, model=shared)
+    b = Context(None, wl.n_slots, wl.slot_cap, model=shared)
+    shared.close()                                  # the contexts keep the weights alive
+    own = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    own.upload(model)
+    om, okv = oracle_pair(cfg, model, wl)
+    fill_kv(cfg, wl, [a.kv_write, b.kv_write, own.kv_write])
+    inp = synth.step_inputs(cfg, wl)
+    want = own.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    assert np.array_equal(a.step(inp.slot_idx, inp.n_past, emb=inp.emb), want)
+    assert np.array_equal(b.step(inp.slot_idx, inp.n_past, emb=inp.emb), want)
+    assert a.device_bytes(0) == b.device_bytes(0) == own.device_bytes(0)
+    # drop half the experts of the first MoE layer on the shared model only
+    L = next(i for i, k in enumerate(cfg.expert_used) if k > 0)
+    keep = np.zeros(cfg.n_expert, np.uint8)
+    keep[::2] = 1
+    a.set_expert_mask(L, keep)
+    own.set_expert_mask(L, keep)
+    own.set_graphs(False)
+    want_m = own.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    assert not np.array_equal(want_m, want)
+    assert np.array_equal(b.step(inp.slot_idx, inp.n_past, emb=inp.emb), want_m)
+    a.set_capture(True)
+    a.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    T = len(inp.slot_idx)
+    sel = a.read_capture(L, "sel", T).reshape(T, a.kmax)[:, :cfg.expert_used[L]]
+    assert np.all(sel % 2 == 0), "a masked expert was routed"
+    om.set_expert_mask(L, keep)
+    _check_routing(cfg, a, om, T)                   # masked routing bit-exact against the oracle
+    a.set_capture(False)
+    a.set_expert_mask(L, None)
+    assert np.array_equal(b.step(inp.slot_idx, inp.n_past, emb=inp.emb), want)
+    for c in (a, b, own):
+        c.close()

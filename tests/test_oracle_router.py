@@ -76,6 +76,38 @@ def test_topk_ties_go_to_lower_index():
     assert np.allclose(r["w"], 1.0 / 8)
 
 
+def test_expert_mask_renormalizes_and_never_routes_dropped():
+    """zonos2_set_expert_mask (src/zonos2.cpp:203-239; graph.cpp:212, 218): the survivors' probabilities
+    are the softmax over the survivors alone (as in a pruned model), a dropped expert gets probability 0
+    and is never selected even when its router_bias is the largest."""
+    cfg = _router_cfg(E=16, k=4)
+    model = synth.generate_model(cfg, 11)
+    bias = np.zeros(16, np.float32)
+    bias[3] = 10.0                                  # would always win the selection if not masked
+    model["blk.0.router_bias"].data[:] = np.frombuffer(bias.tobytes(), np.uint8)
+    om = O.OracleModel(cfg.hparams(), model)
+    x = synth.gen_normal_f32((24, cfg.n_embd), 3, "x")
+    r_open = O.router(om, 0, x, None)
+    assert np.all(r_open["sel"][:, 0] == 3)
+    keep = np.ones(16, np.uint8)
+    keep[[3, 5, 6, 11]] = 0
+    om.set_expert_mask(0, keep)
+    r = O.router(om, 0, x, None)
+    kept = keep.astype(bool)
+    assert np.all(r["probs"][:, ~kept] == 0.0)
+    assert not np.isin(r["sel"], np.flatnonzero(~kept)).any()
+    # float64: softmax over the kept logits only
+    _, lg, _, _ = _ref_router(model, 0, x.astype(np.float64), None)
+    lk = lg[:, kept]
+    pk = np.exp(lk - lk.max(1, keepdims=True))
+    pk /= pk.sum(1, keepdims=True)
+    assert np.allclose(r["probs"][:, kept], pk, rtol=1e-4, atol=1e-7)
+    assert np.array_equal(r["rh"].view(np.uint32), r_open["rh"].view(np.uint32))
+    om.set_expert_mask(0, None)
+    r2 = O.router(om, 0, x, None)
+    assert np.array_equal(r2["probs"].view(np.uint32), r_open["probs"].view(np.uint32))
+
+
 @pytest.mark.parametrize("T,k,E", [(1, 1, 4), (16, 4, 32), (64, 4, 32), (7, 2, 8)])
 def test_grouping_is_stable_counting_sort(T, k, E):
     rng = np.random.default_rng(T * 100 + E)

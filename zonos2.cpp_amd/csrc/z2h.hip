@@ -59,17 +59,18 @@ int chunks_of(int wtype) {
 
 } // namespace
 
-struct z2h_ctx {
+// Weights of one model on one device, shared by every batch context created from it (refcounted:
+// the creator's handle plus one reference per context).
+struct z2h_model {
     z2h_hparams hp{};
     std::vector<int32_t> expert_used;
-    int device = 0, n_slots = 0, S = 0, W = 0, kmax = 1, rd = 0;
-    hipStream_t stream = nullptr;
+    int device = 0, W = 0, kmax = 1, rd = 0;
     std::string err;
     bool finalized = false;
-    int64_t bytes_w = 0, bytes_kv = 0, bytes_scratch = 0;
+    int refs = 1;
+    int gen = 0;                      // bumped when a device pointer captured in step graphs changes
+    int64_t bytes_w = 0;
     std::vector<void *> allocs;
-
-    // weights
     std::vector<uint8_t *> tab; std::vector<int> tab_type; std::vector<int64_t> tab_rows;
     DevMat head;
     float * output_norm = nullptr;
@@ -77,6 +78,17 @@ struct z2h_ctx {
     float * spk_lda_b = nullptr, * spk_proj_b = nullptr;
     std::vector<Layer> layers;
     std::map<std::string, bool> seen;
+};
+
+struct z2h_ctx {
+    z2h_model * m = nullptr;
+    z2h_hparams hp{};                 // the model's (expert_used points into the model)
+    int device = 0, n_slots = 0, S = 0, W = 0, kmax = 1, rd = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    bool finalized = false;
+    int64_t bytes_kv = 0, bytes_scratch = 0;
+    std::vector<void *> allocs;
 
     // KV cache [L][2][slot][kvh][S][hd]
     uint16_t * kv = nullptr;
@@ -100,6 +112,7 @@ struct z2h_ctx {
     // HIP graphs of the whole step, one per (batch width, embedding-injection) pair
     bool use_graphs = true;
     std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+    int graph_gen = 0;                // the model generation the graphs were captured against
 
     // per-kernel event timing
     bool prof = false;
@@ -116,7 +129,8 @@ struct z2h_ctx {
 namespace {
 
 int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; return code; }
-int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
+int seterr(z2h_model * c, int code, const std::string & m) { if (c) c->err = m; return code; }
+int upload_mat_t64(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
 
 constexpr int PROF_MAX = 16384;
@@ -134,21 +148,23 @@ struct prof_scope {
 
 #define HIPX(expr) do { hipError_t e_ = (expr); if (e_ != hipSuccess) \
     return seterr(ctx, Z2H_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); } while (0)
+#define HIPM(expr) do { hipError_t e_ = (expr); if (e_ != hipSuccess) \
+    return seterr(mdl, Z2H_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); } while (0)
 
-template <class T>
-int dalloc(z2h_ctx * ctx, T ** p, size_t bytes, int64_t & counter) {
+template <class O, class T>
+int dalloc(O * owner, T ** p, size_t bytes, int64_t & counter) {
     void * v = nullptr;
     if (bytes == 0) bytes = 16;
-    if (hipMalloc(&v, bytes) != hipSuccess) return seterr(ctx, Z2H_ENOMEM, "hipMalloc failed (" + std::to_string(bytes) + " B)");
-    ctx->allocs.push_back(v);
+    if (hipMalloc(&v, bytes) != hipSuccess) return seterr(owner, Z2H_ENOMEM, "hipMalloc failed (" + std::to_string(bytes) + " B)");
+    owner->allocs.push_back(v);
     counter += (int64_t) bytes;
     *p = (T *) v;
     return Z2H_OK;
 }
 
-int upload_f32(z2h_ctx * ctx, const HostTensor & t, float ** out, int64_t n_expect) {
+int upload_f32(z2h_model * mdl, const HostTensor & t, float ** out, int64_t n_expect) {
     const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
-    if (n_expect >= 0 && n != n_expect) return seterr(ctx, Z2H_EINVAL, "unexpected vector length");
+    if (n_expect >= 0 && n != n_expect) return seterr(mdl, Z2H_EINVAL, "unexpected vector length");
     std::vector<float> f((size_t) n);
     const int64_t rows = n / t.ne[0];
     for (int64_t r = 0; r < rows; ++r) {
@@ -164,16 +180,16 @@ int upload_f32(z2h_ctx * ctx, const HostTensor & t, float ** out, int64_t n_expe
                     for (int j = 0; j < 32; ++j) y[32 * b + j] = (float) (int8_t) src[34 * b + 2 + j] * d;
                 }
                 break;
-            default: return seterr(ctx, Z2H_ENOTSUP, "router/vector tensors must be F32, F16 or Q8_0");
+            default: return seterr(mdl, Z2H_ENOTSUP, "router/vector tensors must be F32, F16 or Q8_0");
         }
     }
-    if (int rc = dalloc(ctx, out, f.size() * 4, ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(*out, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+    if (int rc = dalloc(mdl, out, f.size() * 4, mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(*out, f.data(), f.size() * 4, hipMemcpyHostToDevice));
     return Z2H_OK;
 }
 
 // W [out][in] as fp32 rows padded to in + 4 floats (the router tail's LDS layout)
-int upload_f32_rows_padded(z2h_ctx * ctx, const HostTensor & t, float ** out) {
+int upload_f32_rows_padded(z2h_model * mdl, const HostTensor & t, float ** out) {
     const int64_t in = t.ne[0], outn = t.ne[1], ld = in + 4;
     std::vector<float> rows((size_t) (ld * outn), 0.0f);
     for (int64_t r = 0; r < outn; ++r) {
@@ -183,18 +199,18 @@ int upload_f32_rows_padded(z2h_ctx * ctx, const HostTensor & t, float ** out) {
             if (t.type == Z2H_F32) std::memcpy(&v, src + 4 * i, 4);
             else if (t.type == Z2H_F16) { uint16_t h; std::memcpy(&h, src + 2 * i, 2); v = z2::f16_to_f32(h); }
             else if (t.type == Z2H_Q8_0) { uint16_t h; std::memcpy(&h, src + 34 * (i / 32), 2); v = (float) (int8_t) src[34 * (i / 32) + 2 + i % 32] * z2::f16_to_f32(h); }
-            else return seterr(ctx, Z2H_ENOTSUP, "router matrices must be F32, F16 or Q8_0");
+            else return seterr(mdl, Z2H_ENOTSUP, "router matrices must be F32, F16 or Q8_0");
             rows[r * ld + i] = v;
         }
     }
-    if (int rc = dalloc(ctx, out, rows.size() * 4, ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(*out, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+    if (int rc = dalloc(mdl, out, rows.size() * 4, mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(*out, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
     return Z2H_OK;
 }
 
 // Repack into the 16-row MFMA layout (see k_gemv_mfma): per (group, unit) the lane-owned 8-byte
 // k-slices of every 32-element sub-block, chunk-major for the 64 lanes, then the rows' scale headers.
-int upload_mat_m16(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+int upload_mat_m16(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
     const int UB = type == Z2H_Q4_K ? 2304 : 4352, QS = type == Z2H_Q4_K ? 2 : 4;
     dm.type = type; dm.m16 = true; dm.rows = (int) rows; dm.K = (int) K; dm.nsb = (int) ((K + 255) / 256);
     dm.tiles = (int) ((rows + 15) / 16); dm.n_mats = n_mats;
@@ -242,28 +258,28 @@ int upload_mat_m16(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats,
     std::vector<std::thread> th;
     for (int i = 0; i < nth; ++i) th.emplace_back([&, i] { do_rows(total * i / nth, total * (i + 1) / nth); });
     for (auto & t : th) t.join();
-    if (int rc = dalloc(ctx, &dm.w, out.size(), ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(dm.w, out.data(), out.size(), hipMemcpyHostToDevice));
+    if (int rc = dalloc(mdl, &dm.w, out.size(), mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(dm.w, out.data(), out.size(), hipMemcpyHostToDevice));
     return Z2H_OK;
 }
 
 // Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the device layout: the 16-row
 // MFMA layout for Q4_K / Q8_0, the 64-row tiles for Q6_K / F16.
-int upload_mat(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+int upload_mat(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
     if (type == Z2H_Q4_K || type == Z2H_Q8_0) {
-        if (type == Z2H_Q4_K && K % 256) return seterr(ctx, Z2H_EINVAL, "K-quant row not a multiple of 256");
-        if (type == Z2H_Q8_0 && K % 32) return seterr(ctx, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
-        return upload_mat_m16(ctx, type, K, rows, n_mats, src, dm);
+        if (type == Z2H_Q4_K && K % 256) return seterr(mdl, Z2H_EINVAL, "K-quant row not a multiple of 256");
+        if (type == Z2H_Q8_0 && K % 32) return seterr(mdl, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
+        return upload_mat_m16(mdl, type, K, rows, n_mats, src, dm);
     }
-    return upload_mat_t64(ctx, type, K, rows, n_mats, src, dm);
+    return upload_mat_t64(mdl, type, K, rows, n_mats, src, dm);
 }
 
 // Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the 64-row tiled layout.
-int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+int upload_mat_t64(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
     const int C = chunks_of(type);
-    if (!C) return seterr(ctx, Z2H_ENOTSUP, "matrix type not supported on the device (F16, Q8_0, Q4_K, Q6_K)");
-    if ((type == Z2H_Q4_K || type == Z2H_Q6_K) && K % 256) return seterr(ctx, Z2H_EINVAL, "K-quant row not a multiple of 256");
-    if (type == Z2H_Q8_0 && K % 32) return seterr(ctx, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
+    if (!C) return seterr(mdl, Z2H_ENOTSUP, "matrix type not supported on the device (F16, Q8_0, Q4_K, Q6_K)");
+    if ((type == Z2H_Q4_K || type == Z2H_Q6_K) && K % 256) return seterr(mdl, Z2H_EINVAL, "K-quant row not a multiple of 256");
+    if (type == Z2H_Q8_0 && K % 32) return seterr(mdl, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
     dm.type = type; dm.rows = (int) rows; dm.K = (int) K; dm.nsb = (int) ((K + 255) / 256);
     dm.tiles = (int) ((rows + TILE - 1) / TILE); dm.n_mats = n_mats;
     dm.mat_bytes = (int64_t) dm.tiles * dm.nsb * C * TILE * 16;
@@ -317,11 +333,11 @@ int upload_mat_t64(z2h_ctx * ctx, int type, int64_t K, int64_t rows, int n_mats,
             }
         });
     for (auto & t : th) t.join();
-    if (int rc = dalloc(ctx, &dm.w, tiled.size(), ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(dm.w, tiled.data(), tiled.size(), hipMemcpyHostToDevice));
+    if (int rc = dalloc(mdl, &dm.w, tiled.size(), mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(dm.w, tiled.data(), tiled.size(), hipMemcpyHostToDevice));
     if (type == Z2H_Q6_K) {
-        if (int rc = dalloc(ctx, &dm.dpl, dpl.size() * 2, ctx->bytes_w)) return rc;
-        HIPX(hipMemcpy(dm.dpl, dpl.data(), dpl.size() * 2, hipMemcpyHostToDevice));
+        if (int rc = dalloc(mdl, &dm.dpl, dpl.size() * 2, mdl->bytes_w)) return rc;
+        HIPM(hipMemcpy(dm.dpl, dpl.data(), dpl.size() * 2, hipMemcpyHostToDevice));
     }
     return Z2H_OK;
 }
@@ -335,7 +351,7 @@ bool parse_layer(const std::string & name, int & L, std::string & rest) {
     return true;
 }
 
-int fuse_qkvg(z2h_ctx * ctx, Layer & ly) {
+int fuse_qkvg(z2h_model * mdl, Layer & ly) {
     static const char * parts[4] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_gate.weight"};
     for (auto * p : parts) if (!ly.stash.count(p)) return Z2H_OK;   // not complete yet
     const int type = ly.stash["attn_q.weight"].type;
@@ -343,13 +359,13 @@ int fuse_qkvg(z2h_ctx * ctx, Layer & ly) {
     int64_t rows = 0;
     for (auto * p : parts) {
         const HostTensor & t = ly.stash[p];
-        if (t.type != type || t.ne[0] != K) return seterr(ctx, Z2H_ENOTSUP, "attention projections must share type and input size");
+        if (t.type != type || t.ne[0] != K) return seterr(mdl, Z2H_ENOTSUP, "attention projections must share type and input size");
         rows += t.ne[1];
     }
     std::vector<uint8_t> cat;
     for (auto * p : parts) cat.insert(cat.end(), ly.stash[p].bytes.begin(), ly.stash[p].bytes.end());
     ly.stash.clear();
-    return upload_mat(ctx, type, K, rows, 1, cat.data(), ly.qkvg);
+    return upload_mat(mdl, type, K, rows, 1, cat.data(), ly.qkvg);
 }
 
 int alloc_scratch(z2h_ctx * ctx) {
@@ -649,9 +665,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     // embeddings + emb_norm + layer-0 attn_norm
     ResNormArgs e{};
     e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb;
-    for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->tab[k]; e.tab_type[k] = ctx->tab_type[k]; e.tab_rows[k] = ctx->tab_rows[k]; }
-    e.res = ctx->res; e.norm_w = ctx->layers[0].attn_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_ATTN_IN, 0);
-    e.act = ctx->act; e.act_fmt = act_of(ctx->layers[0].qkvg.type);
+    for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->m->tab[k]; e.tab_type[k] = ctx->m->tab_type[k]; e.tab_rows[k] = ctx->m->tab_rows[k]; }
+    e.res = ctx->res; e.norm_w = ctx->m->layers[0].attn_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_ATTN_IN, 0);
+    e.act = ctx->act; e.act_fmt = act_of(ctx->m->layers[0].qkvg.type);
     if ((rc = launch_resnorm(ctx, T, e))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_RES_IN, 0, ctx->res, T))) return rc;
     (void) h_npast;
@@ -660,7 +676,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int L = 0; L < hp.n_layer; ++L) {
-        Layer & ly = ctx->layers[L];
+        Layer & ly = ctx->m->layers[L];
         // fused QKV + gate projection
         if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), 1, Z2H_KF_GEMV_QKV))) return rc;
         AttnArgs a{};
@@ -715,15 +731,15 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         n.mode = RN_ACCUM; n.src = ctx->eo; n.k = ly.moe ? ly.k : 1; n.res = ctx->res;
         n.cap_x = (float *) capp(ctx, Z2H_CAP_FFN_OUT, L);
         const bool last = L + 1 == hp.n_layer;
-        n.norm_w = last ? ctx->output_norm : ctx->layers[L + 1].attn_norm;
+        n.norm_w = last ? ctx->m->output_norm : ctx->m->layers[L + 1].attn_norm;
         n.cur_out = last ? (float *) capp(ctx, Z2H_CAP_OUT_NORM, 0) : (float *) capp(ctx, Z2H_CAP_ATTN_IN, L + 1);
-        n.act = ctx->act; n.act_fmt = act_of(last ? ctx->head.type : ctx->layers[L + 1].qkvg.type);
+        n.act = ctx->act; n.act_fmt = act_of(last ? ctx->m->head.type : ctx->m->layers[L + 1].qkvg.type);
         if ((rc = launch_resnorm(ctx, T, n))) return rc;
         if (!last && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, L + 1, ctx->res, T))) return rc;
     }
     // output head + softcap
     const int nout = hp.n_codebooks * hp.audio_vocab;
-    return launch_gemv(ctx, ctx->head, nullptr, gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE),
+    return launch_gemv(ctx, ctx->m->head, nullptr, gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE),
                        1, Z2H_KF_GEMV_HEAD);
 }
 
@@ -781,6 +797,11 @@ int step_internal(z2h_ctx * ctx, int T, const int32_t * h_npast, bool use_ids) {
     const float * emb = use_ids ? nullptr : ctx->d_emb;
     if (!ctx->use_graphs || ctx->capture || ctx->prof)
         return run_step(ctx, T, h_npast, ctx->d_slot, ctx->d_npast, ids, emb, ctx->logits);
+    if (ctx->graph_gen != ctx->m->gen) {             // a mask or bias buffer changed under the captured graphs
+        for (auto & g : ctx->graphs) (void) hipGraphExecDestroy(g.second);
+        ctx->graphs.clear();
+        ctx->graph_gen = ctx->m->gen;
+    }
     const auto key = std::make_pair(T, use_ids ? 1 : 0);
     auto it = ctx->graphs.find(key);
     if (it == ctx->graphs.end()) {
@@ -805,10 +826,10 @@ int step_internal(z2h_ctx * ctx, int T, const int32_t * h_npast, bool use_ids) {
 // ====================================================================== C ABI
 extern "C" {
 
-int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int device, z2h_ctx ** out) {
+int z2h_model_create(const z2h_hparams * hp, int device, z2h_model ** out) {
     if (!out) return Z2H_EINVAL;
     *out = nullptr;
-    if (!hp || !hp->expert_used || hp->n_layer <= 0 || n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
+    if (!hp || !hp->expert_used || hp->n_layer <= 0) return Z2H_EINVAL;
     if (hp->n_head <= 0 || hp->n_head_kv <= 0 || hp->n_head % hp->n_head_kv) return Z2H_EINVAL;
     {   // decode attention instantiations: head_dim 16/32/64/128, query heads per KV head 1/2/4/8
         const int hd = hp->head_dim, grp = hp->n_head / hp->n_head_kv;
@@ -816,111 +837,102 @@ int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int dev
     }
     if (hp->n_codebooks + 1 > MAX_TABLES) return Z2H_ENOTSUP;
     if (hp->n_embd % 4 || hp->n_embd > 4 * 256 * RN_NV) return Z2H_ENOTSUP;   // k_resnorm row layout
-    auto ctx = std::make_unique<z2h_ctx>();
-    ctx->hp = *hp;
-    ctx->expert_used.assign(hp->expert_used, hp->expert_used + hp->n_layer);
-    ctx->hp.expert_used = ctx->expert_used.data();
-    ctx->device = device; ctx->n_slots = n_slots;
-    ctx->S = ((slot_cap_frames + 255) / 256) * 256;
-    ctx->W = hp->n_codebooks + 1;
-    ctx->rd = hp->router_dim;
-    for (int L = 0; L < hp->n_layer; ++L) ctx->kmax = std::max(ctx->kmax, hp->expert_used[L]);
-    z2h_ctx * c = ctx.get();
     if (hipSetDevice(device) != hipSuccess) return Z2H_EDEVICE;
-    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return Z2H_EDEVICE;
-    const size_t kv_elems = (size_t) hp->n_layer * 2 * n_slots * hp->n_head_kv * c->S * hp->head_dim;
-    if (dalloc(c, &c->kv, kv_elems * 2, c->bytes_kv)) { (void) hipStreamDestroy(c->stream); return Z2H_ENOMEM; }
-    if (dalloc(c, &c->kv_stage, (size_t) c->S * hp->n_head_kv * hp->head_dim * 2, c->bytes_scratch)) { z2h_destroy(ctx.release()); return Z2H_ENOMEM; }
-    if (hipMemset(c->kv, 0, kv_elems * 2) != hipSuccess) { z2h_destroy(ctx.release()); return Z2H_EDEVICE; }
-    c->layers.resize(hp->n_layer);
-    c->tab.assign(c->W, nullptr); c->tab_type.assign(c->W, -1); c->tab_rows.assign(c->W, 0);
-    *out = ctx.release();
+    auto mdl = std::make_unique<z2h_model>();
+    mdl->hp = *hp;
+    mdl->expert_used.assign(hp->expert_used, hp->expert_used + hp->n_layer);
+    mdl->hp.expert_used = mdl->expert_used.data();
+    mdl->device = device;
+    mdl->W = hp->n_codebooks + 1;
+    mdl->rd = hp->router_dim;
+    for (int L = 0; L < hp->n_layer; ++L) mdl->kmax = std::max(mdl->kmax, hp->expert_used[L]);
+    mdl->layers.resize(hp->n_layer);
+    mdl->tab.assign(mdl->W, nullptr); mdl->tab_type.assign(mdl->W, -1); mdl->tab_rows.assign(mdl->W, 0);
+    *out = mdl.release();
     return Z2H_OK;
 }
 
-int z2h_slot_cap(const z2h_ctx * ctx) { return ctx ? ctx->S : 0; }
-
-int z2h_upload_tensor(z2h_ctx * ctx, const char * name_c, int type, const int64_t ne_in[4], const void * data, size_t nbytes) {
-    if (!ctx || !name_c || !ne_in || !data) return Z2H_EINVAL;
-    if (ctx->finalized) return seterr(ctx, Z2H_ESTATE, "context already finalized");
-    if (!z2::type_known(type)) return seterr(ctx, Z2H_ENOTSUP, std::string("unsupported tensor type for ") + name_c);
+int z2h_model_upload_tensor(z2h_model * mdl, const char * name_c, int type, const int64_t ne_in[4], const void * data, size_t nbytes) {
+    if (!mdl || !name_c || !ne_in || !data) return Z2H_EINVAL;
+    if (mdl->finalized) return seterr(mdl, Z2H_ESTATE, "model already finalized");
+    if (!z2::type_known(type)) return seterr(mdl, Z2H_ENOTSUP, std::string("unsupported tensor type for ") + name_c);
     HostTensor t; t.type = type;
     for (int i = 0; i < 4; ++i) t.ne[i] = ne_in[i] > 0 ? ne_in[i] : 1;
-    if (t.ne[0] % z2::type_block(type)) return seterr(ctx, Z2H_EINVAL, std::string("row not block aligned: ") + name_c);
+    if (t.ne[0] % z2::type_block(type)) return seterr(mdl, Z2H_EINVAL, std::string("row not block aligned: ") + name_c);
     const int64_t expect = z2::row_bytes(type, t.ne[0]) * t.ne[1] * t.ne[2] * t.ne[3];
-    if ((int64_t) nbytes != expect) return seterr(ctx, Z2H_EINVAL, std::string("byte size mismatch for ") + name_c);
-    if (hipSetDevice(ctx->device) != hipSuccess) return Z2H_EDEVICE;
+    if ((int64_t) nbytes != expect) return seterr(mdl, Z2H_EINVAL, std::string("byte size mismatch for ") + name_c);
+    if (hipSetDevice(mdl->device) != hipSuccess) return Z2H_EDEVICE;
     const std::string name(name_c);
-    const auto & hp = ctx->hp;
+    const auto & hp = mdl->hp;
     const uint8_t * src = (const uint8_t *) data;
     auto copy_host = [&]() { t.bytes.assign(src, src + nbytes); };
-    ctx->seen[name] = true;
+    mdl->seen[name] = true;
     int L; std::string rest;
     if (parse_layer(name, L, rest)) {
-        if (L < 0 || L >= hp.n_layer) return seterr(ctx, Z2H_EINVAL, "layer index out of range: " + name);
-        Layer & ly = ctx->layers[L];
+        if (L < 0 || L >= hp.n_layer) return seterr(mdl, Z2H_EINVAL, "layer index out of range: " + name);
+        Layer & ly = mdl->layers[L];
         if (rest == "attn_q.weight" || rest == "attn_k.weight" || rest == "attn_v.weight" || rest == "attn_gate.weight") {
             copy_host();
             ly.stash[rest] = std::move(t);
-            return fuse_qkvg(ctx, ly);
+            return fuse_qkvg(mdl, ly);
         }
-        if (rest == "attn_output.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.wo);
-        if (rest == "ffn_up.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_up);
-        if (rest == "ffn_gate.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_gate);
-        if (rest == "ffn_down.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ly.ffn_down);
-        if (rest == "ffn_gate_exps.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps);
-        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps); }
-        if (rest == "ffn_down_exps.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps);
+        if (rest == "attn_output.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.wo);
+        if (rest == "ffn_up.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_up);
+        if (rest == "ffn_gate.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_gate);
+        if (rest == "ffn_down.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_down);
+        if (rest == "ffn_gate_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps);
+        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps); }
+        if (rest == "ffn_down_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps);
         copy_host();
-        if (rest == "attn_norm.weight") return upload_f32(ctx, t, &ly.attn_norm, hp.n_embd);
-        if (rest == "ffn_norm.weight") return upload_f32(ctx, t, &ly.ffn_norm, hp.n_embd);
-        if (rest == "attn_temp") return upload_f32(ctx, t, &ly.attn_temp, hp.n_head);
+        if (rest == "attn_norm.weight") return upload_f32(mdl, t, &ly.attn_norm, hp.n_embd);
+        if (rest == "ffn_norm.weight") return upload_f32(mdl, t, &ly.ffn_norm, hp.n_embd);
+        if (rest == "attn_temp") return upload_f32(mdl, t, &ly.attn_temp, hp.n_head);
         if (rest == "router_down.weight") {
-            if (t.ne[1] != ctx->rd) return seterr(ctx, Z2H_EINVAL, "router_dim mismatch: " + name);
-            return upload_f32(ctx, t, &ly.r_down, -1);
+            if (t.ne[1] != mdl->rd) return seterr(mdl, Z2H_EINVAL, "router_dim mismatch: " + name);
+            return upload_f32(mdl, t, &ly.r_down, -1);
         }
-        if (rest == "router_down.bias") return upload_f32(ctx, t, &ly.r_down_b, ctx->rd);
-        if (rest == "router_mlp0.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m0t);
-        if (rest == "router_mlp0.bias") return upload_f32(ctx, t, &ly.r_m0_b, ctx->rd);
-        if (rest == "router_mlp2.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m2t);
-        if (rest == "router_mlp2.bias") return upload_f32(ctx, t, &ly.r_m2_b, ctx->rd);
-        if (rest == "router_mlp4.weight") return upload_f32_rows_padded(ctx, t, &ly.r_m4t);
-        if (rest == "router_norm.weight") return upload_f32(ctx, t, &ly.r_norm, ctx->rd);
-        if (rest == "router_bias") return upload_f32(ctx, t, &ly.r_bias, -1);
-        if (rest == "router_eda_scale") return upload_f32(ctx, t, &ly.r_eda, ctx->rd);
-        return seterr(ctx, Z2H_EINVAL, "unknown tensor " + name);
+        if (rest == "router_down.bias") return upload_f32(mdl, t, &ly.r_down_b, mdl->rd);
+        if (rest == "router_mlp0.weight") return upload_f32_rows_padded(mdl, t, &ly.r_m0t);
+        if (rest == "router_mlp0.bias") return upload_f32(mdl, t, &ly.r_m0_b, mdl->rd);
+        if (rest == "router_mlp2.weight") return upload_f32_rows_padded(mdl, t, &ly.r_m2t);
+        if (rest == "router_mlp2.bias") return upload_f32(mdl, t, &ly.r_m2_b, mdl->rd);
+        if (rest == "router_mlp4.weight") return upload_f32_rows_padded(mdl, t, &ly.r_m4t);
+        if (rest == "router_norm.weight") return upload_f32(mdl, t, &ly.r_norm, mdl->rd);
+        if (rest == "router_bias") return upload_f32(mdl, t, &ly.r_bias, -1);
+        if (rest == "router_eda_scale") return upload_f32(mdl, t, &ly.r_eda, mdl->rd);
+        return seterr(mdl, Z2H_EINVAL, "unknown tensor " + name);
     }
     if (name.rfind("audio_embd.", 0) == 0 || name == "text_embd.weight") {
         const int k = name == "text_embd.weight" ? hp.n_codebooks : std::atoi(name.c_str() + 11);
-        if (k < 0 || k > hp.n_codebooks || t.ne[0] != hp.n_embd) return seterr(ctx, Z2H_EINVAL, "bad embedding table " + name);
+        if (k < 0 || k > hp.n_codebooks || t.ne[0] != hp.n_embd) return seterr(mdl, Z2H_EINVAL, "bad embedding table " + name);
         if (type != Z2H_F32 && type != Z2H_F16 && type != Z2H_Q8_0 && type != Z2H_Q4_K && type != Z2H_Q6_K)
-            return seterr(ctx, Z2H_ENOTSUP, "embedding type");
+            return seterr(mdl, Z2H_ENOTSUP, "embedding type");
         uint8_t * p = nullptr;
-        if (int rc = dalloc(ctx, &p, nbytes, ctx->bytes_w)) return rc;
-        HIPX(hipMemcpy(p, data, nbytes, hipMemcpyHostToDevice));
-        ctx->tab[k] = p; ctx->tab_type[k] = type; ctx->tab_rows[k] = t.ne[1];
+        if (int rc = dalloc(mdl, &p, nbytes, mdl->bytes_w)) return rc;
+        HIPM(hipMemcpy(p, data, nbytes, hipMemcpyHostToDevice));
+        mdl->tab[k] = p; mdl->tab_type[k] = type; mdl->tab_rows[k] = t.ne[1];
         return Z2H_OK;
     }
-    if (name == "output.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->head);
-    if (name == "spk_lda.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->spk_lda);
-    if (name == "spk_proj.weight") return upload_mat(ctx, type, t.ne[0], t.ne[1], 1, src, ctx->spk_proj);
+    if (name == "output.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, mdl->head);
+    if (name == "spk_lda.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, mdl->spk_lda);
+    if (name == "spk_proj.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, mdl->spk_proj);
     copy_host();
-    if (name == "output_norm.weight") return upload_f32(ctx, t, &ctx->output_norm, hp.n_embd);
-    if (name == "spk_lda.bias") return upload_f32(ctx, t, &ctx->spk_lda_b, -1);
-    if (name == "spk_proj.bias") return upload_f32(ctx, t, &ctx->spk_proj_b, hp.n_embd);
-    return seterr(ctx, Z2H_EINVAL, "unknown tensor " + name);
+    if (name == "output_norm.weight") return upload_f32(mdl, t, &mdl->output_norm, hp.n_embd);
+    if (name == "spk_lda.bias") return upload_f32(mdl, t, &mdl->spk_lda_b, -1);
+    if (name == "spk_proj.bias") return upload_f32(mdl, t, &mdl->spk_proj_b, hp.n_embd);
+    return seterr(mdl, Z2H_EINVAL, "unknown tensor " + name);
 }
 
-int z2h_finalize(z2h_ctx * ctx) {
-    if (!ctx) return Z2H_EINVAL;
-    if (ctx->finalized) return Z2H_OK;
-    const auto & hp = ctx->hp;
+int z2h_model_finalize(z2h_model * mdl) {
+    if (!mdl) return Z2H_EINVAL;
+    if (mdl->finalized) return Z2H_OK;
+    const auto & hp = mdl->hp;
     std::string missing;
-    for (int k = 0; k < ctx->W; ++k) if (!ctx->tab[k]) missing += (k < hp.n_codebooks ? "audio_embd." + std::to_string(k) : std::string("text_embd")) + " ";
-    if (!ctx->head.ok()) missing += "output.weight ";
-    if (!ctx->output_norm) missing += "output_norm.weight ";
+    for (int k = 0; k < mdl->W; ++k) if (!mdl->tab[k]) missing += (k < hp.n_codebooks ? "audio_embd." + std::to_string(k) : std::string("text_embd")) + " ";
+    if (!mdl->head.ok()) missing += "output.weight ";
+    if (!mdl->output_norm) missing += "output_norm.weight ";
     for (int L = 0; L < hp.n_layer; ++L) {
-        Layer & ly = ctx->layers[L];
+        Layer & ly = mdl->layers[L];
         const std::string b = "blk." + std::to_string(L) + ".";
         ly.k = hp.expert_used[L]; ly.moe = ly.k > 0;
         if (!ly.qkvg.ok()) missing += b + "attn_{q,k,v,gate} ";
@@ -932,24 +944,87 @@ int z2h_finalize(z2h_ctx * ctx) {
             if (!ly.gate_exps.ok() || !ly.up_exps.ok() || !ly.down_exps.ok()) missing += b + "ffn_*_exps ";
             if (!ly.r_down || !ly.r_down_b || !ly.r_m0t || !ly.r_m0_b || !ly.r_m2t || !ly.r_m2_b || !ly.r_m4t || !ly.r_norm || !ly.r_bias)
                 missing += b + "router_* ";
-            if (ly.up_exps.ok() && ly.k > ly.E) return seterr(ctx, Z2H_EINVAL, b + "top-k exceeds the expert count");
-            if (ly.up_exps.ok() && ly.E > 128) return seterr(ctx, Z2H_ENOTSUP, "more than 128 experts");
-            if (ly.up_exps.ok() && (ly.up_exps.rows != hp.n_ff || ly.down_exps.K != hp.n_ff)) return seterr(ctx, Z2H_EINVAL, b + "expert shape mismatch");
+            if (ly.up_exps.ok() && ly.k > ly.E) return seterr(mdl, Z2H_EINVAL, b + "top-k exceeds the expert count");
+            if (ly.up_exps.ok() && ly.E > 128) return seterr(mdl, Z2H_ENOTSUP, "more than 128 experts");
+            if (ly.up_exps.ok() && (ly.up_exps.rows != hp.n_ff || ly.down_exps.K != hp.n_ff)) return seterr(mdl, Z2H_EINVAL, b + "expert shape mismatch");
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
-    if (!missing.empty()) return seterr(ctx, Z2H_EINVAL, "missing tensors: " + missing);
-    if (ctx->rd > 0) {
+    if (!missing.empty()) return seterr(mdl, Z2H_EINVAL, "missing tensors: " + missing);
+    if (mdl->rd > 0) {
         const int d = hp.n_embd;
-        if (ctx->rd != 64 && ctx->rd != 128) return seterr(ctx, Z2H_ENOTSUP, "router_dim must be 64 or 128");
-        if (d != 256 && d != 512 && d != 1024 && d != 2048 && d != 4096) return seterr(ctx, Z2H_ENOTSUP, "MoE layers need n_embd in {256, 512, 1024, 2048, 4096}");
-        if (ctx->kmax > 8) return seterr(ctx, Z2H_ENOTSUP, "top-k above 8");
+        if (mdl->rd != 64 && mdl->rd != 128) return seterr(mdl, Z2H_ENOTSUP, "router_dim must be 64 or 128");
+        if (d != 256 && d != 512 && d != 1024 && d != 2048 && d != 4096) return seterr(mdl, Z2H_ENOTSUP, "MoE layers need n_embd in {256, 512, 1024, 2048, 4096}");
+        if (mdl->kmax > 8) return seterr(mdl, Z2H_ENOTSUP, "top-k above 8");
     }
+    mdl->finalized = true;
+    return Z2H_OK;
+}
+
+const char * z2h_model_last_error(const z2h_model * mdl) { return mdl ? mdl->err.c_str() : "null model"; }
+
+void z2h_model_release(z2h_model * mdl) {
+    if (!mdl || --mdl->refs > 0) return;
+    (void) hipSetDevice(mdl->device);
+    for (void * p : mdl->allocs) (void) hipFree(p);
+    delete mdl;
+}
+
+int z2h_create_batch(z2h_model * mdl, int n_slots, int slot_cap_frames, z2h_ctx ** out) {
+    if (!out) return Z2H_EINVAL;
+    *out = nullptr;
+    if (!mdl || n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
+    if (hipSetDevice(mdl->device) != hipSuccess) return Z2H_EDEVICE;
+    auto ctx = std::make_unique<z2h_ctx>();
+    z2h_ctx * c = ctx.get();
+    c->m = mdl; ++mdl->refs;
+    c->hp = mdl->hp;
+    c->device = mdl->device; c->n_slots = n_slots;
+    c->S = ((slot_cap_frames + 255) / 256) * 256;
+    c->W = mdl->W; c->rd = mdl->rd; c->kmax = mdl->kmax;
+    const auto & hp = c->hp;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) { z2h_destroy(ctx.release()); return Z2H_EDEVICE; }
+    const size_t kv_elems = (size_t) hp.n_layer * 2 * n_slots * hp.n_head_kv * c->S * hp.head_dim;
+    if (dalloc(c, &c->kv, kv_elems * 2, c->bytes_kv) ||
+        dalloc(c, &c->kv_stage, (size_t) c->S * hp.n_head_kv * hp.head_dim * 2, c->bytes_scratch)) { z2h_destroy(ctx.release()); return Z2H_ENOMEM; }
+    if (hipMemset(c->kv, 0, kv_elems * 2) != hipSuccess) { z2h_destroy(ctx.release()); return Z2H_EDEVICE; }
+    if (mdl->finalized) {
+        if (int rc = z2h_finalize(c)) { z2h_destroy(ctx.release()); return rc; }
+    }
+    *out = ctx.release();
+    return Z2H_OK;
+}
+
+int z2h_create(const z2h_hparams * hp, int n_slots, int slot_cap_frames, int device, z2h_ctx ** out) {
+    if (!out) return Z2H_EINVAL;
+    *out = nullptr;
+    if (n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
+    z2h_model * mdl = nullptr;
+    if (int rc = z2h_model_create(hp, device, &mdl)) return rc;
+    const int rc = z2h_create_batch(mdl, n_slots, slot_cap_frames, out);
+    z2h_model_release(mdl);                          // the context holds the only reference now
+    return rc;
+}
+
+int z2h_slot_cap(const z2h_ctx * ctx) { return ctx ? ctx->S : 0; }
+
+int z2h_upload_tensor(z2h_ctx * ctx, const char * name, int type, const int64_t ne[4], const void * data, size_t nbytes) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->finalized) return seterr(ctx, Z2H_ESTATE, "context already finalized");
+    const int rc = z2h_model_upload_tensor(ctx->m, name, type, ne, data, nbytes);
+    if (rc) ctx->err = ctx->m->err;
+    return rc;
+}
+
+int z2h_finalize(z2h_ctx * ctx) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->finalized) return Z2H_OK;
+    if (int rc = z2h_model_finalize(ctx->m)) { ctx->err = ctx->m->err; return rc; }
+    const auto & hp = ctx->hp;
     if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));
     // allow each kernel the rest of gfx950's 160 KiB of LDS (beyond its static LDS) for its dynamic
     // carve-up
-    const int lds_max = 160 * 1024 - 8 * 1024;
 #define LDS_ATTR(K_) if (int rc_ = allow_lds((const void *) &(K_), ctx)) return rc_;
     LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
     LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
@@ -961,8 +1036,8 @@ int z2h_finalize(z2h_ctx * ctx) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G>))
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
-    if (router_tail_lds(std::max(1, ctx->rd), std::max(1, hp.n_expert)) > (size_t) lds_max)
-        return seterr(ctx, Z2H_ENOTSUP, "router too large for one block's LDS");
+    (void) hp;
+    ctx->graph_gen = ctx->m->gen;
     ctx->finalized = true;
     return Z2H_OK;
 }
@@ -1019,7 +1094,7 @@ int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_p
         for (int t = 0; t < T; ++t)
             for (int k = 0; k < ctx->W; ++k) {
                 const int id = ids[(size_t) t * ctx->W + k];
-                if (id < 0 || id >= ctx->tab_rows[k]) return seterr(ctx, Z2H_EINVAL, "token id out of range");
+                if (id < 0 || id >= ctx->m->tab_rows[k]) return seterr(ctx, Z2H_EINVAL, "token id out of range");
             }
     }
     HIPX(hipSetDevice(ctx->device));
@@ -1084,12 +1159,12 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
 int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int T, const float * d_x, const float * d_state_in, float * d_out, void * stream) {
     if (!ctx || !d_x || !d_out) return Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
-    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].moe) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
+    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->m->layers[layer].moe) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
     if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_tokens out of range");
     hipStream_t keep = ctx->stream;
     if (stream) ctx->stream = (hipStream_t) stream;
     ctx->cap_T = T;
-    Layer & ly = ctx->layers[layer];
+    Layer & ly = ctx->m->layers[layer];
     int rc;
     HIPX(hipMemcpyAsync(ctx->cur, d_x, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyDeviceToDevice, ctx->stream));
     ResNormArgs e{};
@@ -1117,28 +1192,48 @@ int z2h_moe_forward(z2h_ctx * ctx, int layer, int T, const float * x, const floa
     return Z2H_OK;
 }
 
-int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep) {
-    if (!ctx) return Z2H_EINVAL;
-    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].up_exps.ok()) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
-    Layer & ly = ctx->layers[layer];
+int z2h_model_set_expert_mask(z2h_model * mdl, int layer, const uint8_t * keep) {
+    if (!mdl) return Z2H_EINVAL;
+    if (layer < 0 || layer >= mdl->hp.n_layer || !mdl->layers[layer].up_exps.ok()) return seterr(mdl, Z2H_EINVAL, "layer is not MoE");
+    if (hipSetDevice(mdl->device) != hipSuccess) return Z2H_EDEVICE;
+    Layer & ly = mdl->layers[layer];
+    ++mdl->gen;                                      // captured graphs bake the mask pointer in
     if (!keep) { ly.mask = nullptr; return Z2H_OK; }
     std::vector<float> m(ly.E);
     for (int e = 0; e < ly.E; ++e) m[e] = keep[e] ? 0.0f : -INFINITY;
-    if (!ly.mask_buf) if (int rc = dalloc(ctx, &ly.mask_buf, (size_t) ly.E * 4, ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(ly.mask_buf, m.data(), m.size() * 4, hipMemcpyHostToDevice));
+    if (!ly.mask_buf) if (int rc = dalloc(mdl, &ly.mask_buf, (size_t) ly.E * 4, mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(ly.mask_buf, m.data(), m.size() * 4, hipMemcpyHostToDevice));
     ly.mask = ly.mask_buf;
     return Z2H_OK;
 }
 
-int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias) {
-    if (!ctx) return Z2H_EINVAL;
-    if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->layers[layer].up_exps.ok()) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
-    Layer & ly = ctx->layers[layer];
+int z2h_model_set_logit_bias(z2h_model * mdl, int layer, const float * bias) {
+    if (!mdl) return Z2H_EINVAL;
+    if (layer < 0 || layer >= mdl->hp.n_layer || !mdl->layers[layer].up_exps.ok()) return seterr(mdl, Z2H_EINVAL, "layer is not MoE");
+    if (hipSetDevice(mdl->device) != hipSuccess) return Z2H_EDEVICE;
+    Layer & ly = mdl->layers[layer];
+    ++mdl->gen;
     if (!bias) { ly.logit_bias = nullptr; return Z2H_OK; }
-    if (!ly.bias_buf) if (int rc = dalloc(ctx, &ly.bias_buf, (size_t) ly.E * 4, ctx->bytes_w)) return rc;
-    HIPX(hipMemcpy(ly.bias_buf, bias, (size_t) ly.E * 4, hipMemcpyHostToDevice));
+    if (!ly.bias_buf) if (int rc = dalloc(mdl, &ly.bias_buf, (size_t) ly.E * 4, mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(ly.bias_buf, bias, (size_t) ly.E * 4, hipMemcpyHostToDevice));
     ly.logit_bias = ly.bias_buf;
     return Z2H_OK;
+}
+
+int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    const int rc = z2h_model_set_expert_mask(ctx->m, layer, keep);
+    if (rc) ctx->err = ctx->m->err;
+    return rc;
+}
+
+int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    const int rc = z2h_model_set_logit_bias(ctx->m, layer, bias);
+    if (rc) ctx->err = ctx->m->err;
+    return rc;
 }
 
 int z2h_set_capture(z2h_ctx * ctx, int enable) {
@@ -1211,7 +1306,7 @@ int z2h_profile_end(z2h_ctx * ctx, double * ms, int32_t * launches) {
 
 int64_t z2h_device_bytes(const z2h_ctx * ctx, int what) {
     if (!ctx) return -1;
-    return what == 0 ? ctx->bytes_w : what == 1 ? ctx->bytes_kv : ctx->bytes_scratch;
+    return what == 0 ? ctx->m->bytes_w : what == 1 ? ctx->bytes_kv : ctx->bytes_scratch;
 }
 
 const char * z2h_last_error(const z2h_ctx * ctx) { return ctx ? ctx->err.c_str() : "null context"; }
@@ -1225,7 +1320,9 @@ void z2h_destroy(z2h_ctx * ctx) {
     for (void * p : ctx->allocs) (void) hipFree(p);
     if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);
     if (ctx->stream) (void) hipStreamDestroy(ctx->stream);
+    z2h_model * mdl = ctx->m;
     delete ctx;
+    z2h_model_release(mdl);
 }
 
 } // extern "C"

@@ -31,6 +31,14 @@ def lib() -> C.CDLL:
     L = _load("libzonos2_hip.so")
     vp, i32, i64 = C.c_void_p, C.c_int, C.c_int64
     sig = {
+        "z2h_model_create": (i32, [C.POINTER(Hparams), i32, C.POINTER(vp)]),
+        "z2h_model_upload_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_int64), vp, C.c_size_t]),
+        "z2h_model_finalize": (i32, [vp]),
+        "z2h_model_set_expert_mask": (i32, [vp, i32, vp]),
+        "z2h_model_set_logit_bias": (i32, [vp, i32, vp]),
+        "z2h_model_last_error": (C.c_char_p, [vp]),
+        "z2h_model_release": (None, [vp]),
+        "z2h_create_batch": (i32, [vp, i32, i32, C.POINTER(vp)]),
         "z2h_create": (i32, [C.POINTER(Hparams), i32, i32, i32, C.POINTER(vp)]),
         "z2h_upload_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_int64), vp, C.c_size_t]),
         "z2h_finalize": (i32, [vp]),
@@ -60,7 +68,9 @@ def lib() -> C.CDLL:
     return L
 
 
-EXPORTS = ("z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
+EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", "z2h_model_set_expert_mask",
+           "z2h_model_set_logit_bias", "z2h_model_last_error", "z2h_model_release", "z2h_create_batch",
+           "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
            "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_last_error",
@@ -79,19 +89,68 @@ class Z2HError(RuntimeError):
         self.code = code
 
 
-class Context:
-    """One decode-step context on a device (mirrors zonos2_batch_ctx)."""
+def _hparams(hp: dict):
+    eu = (C.c_int32 * hp["n_layer"])(*hp["expert_used"])
+    h = Hparams(**{k: v for k, v in hp.items() if k != "expert_used"})
+    h.expert_used = C.cast(eu, C.POINTER(C.c_int32))
+    return h, eu
 
-    def __init__(self, hp: dict, n_slots: int, slot_cap: int, device: int = 0):
+
+class Model:
+    """Device weights shared by any number of contexts (mirrors zonos2_model)."""
+
+    def __init__(self, hp: dict, tensors: dict | None = None, device: int = 0):
         self.hp = dict(hp)
-        eu = (C.c_int32 * hp["n_layer"])(*hp["expert_used"])
-        h = Hparams(**{k: v for k, v in hp.items() if k != "expert_used"})
-        h.expert_used = C.cast(eu, C.POINTER(C.c_int32))
-        self._eu = eu
+        h, _eu = _hparams(hp)
         out = C.c_void_p()
-        rc = lib().z2h_create(C.byref(h), n_slots, slot_cap, device, C.byref(out))
+        rc = lib().z2h_model_create(C.byref(h), device, C.byref(out))
         if rc != OK:
-            raise Z2HError(rc, "z2h_create failed")
+            raise Z2HError(rc, "z2h_model_create failed")
+        self.m = out
+        if tensors is not None:
+            self.upload(tensors)
+
+    def check(self, rc):
+        if rc != OK:
+            raise Z2HError(rc, lib().z2h_model_last_error(self.m).decode())
+
+    def upload(self, tensors: dict):
+        for t in tensors.values():
+            ne = (C.c_int64 * 4)(*t.ne4)
+            self.check(lib().z2h_model_upload_tensor(self.m, t.name.encode(), t.type, ne, _p(t.data), t.data.nbytes))
+        self.check(lib().z2h_model_finalize(self.m))
+
+    def set_expert_mask(self, layer, keep):
+        k = None if keep is None else np.ascontiguousarray(keep, dtype=np.uint8)
+        self.check(lib().z2h_model_set_expert_mask(self.m, layer, _p(k)))
+
+    def close(self):
+        if getattr(self, "m", None):
+            lib().z2h_model_release(self.m)
+            self.m = None
+
+    def __del__(self):
+        self.close()
+
+
+class Context:
+    """One decode-step context on a device (mirrors zonos2_batch_ctx). Built either from hparams (a
+    private model, weights uploaded through upload()) or over a shared Model."""
+
+    def __init__(self, hp: dict | None, n_slots: int, slot_cap: int, device: int = 0, model: Model | None = None):
+        out = C.c_void_p()
+        if model is not None:
+            self.hp = dict(model.hp)
+            rc = lib().z2h_create_batch(model.m, n_slots, slot_cap, C.byref(out))
+            if rc != OK:
+                raise Z2HError(rc, lib().z2h_model_last_error(model.m).decode())
+        else:
+            self.hp = dict(hp)
+            h, _eu = _hparams(hp)
+            rc = lib().z2h_create(C.byref(h), n_slots, slot_cap, device, C.byref(out))
+            if rc != OK:
+                raise Z2HError(rc, "z2h_create failed")
+        hp = self.hp
         self.ctx = out
         self.n_slots = n_slots
         self.S = lib().z2h_slot_cap(self.ctx)
