@@ -71,6 +71,11 @@ int z2h_model_finalize(z2h_model * m);
  * context sharing it sees the change at its next step. No step may be in flight on any of them. */
 int z2h_model_set_expert_mask(z2h_model * m, int layer, const uint8_t * keep);
 int z2h_model_set_logit_bias(z2h_model * m, int layer, const float * bias);
+/* Depth prune (zonos2_model::layer_skip, src/zonos2.h:116-121; src/zonos2-graph.cpp:334-341):
+ * skip[L] != 0 bypasses block L in every following step and prefill (attention, KV append and FFN are
+ * not run; the residual passes through unchanged; the router state threads past it). skip has
+ * n_layer entries; NULL clears. */
+int z2h_model_set_layer_skip(z2h_model * m, const uint8_t * skip);
 const char * z2h_model_last_error(const z2h_model * m);
 /* Drops one reference; the weights are freed with the last one (contexts hold one each). */
 void z2h_model_release(z2h_model * m);
@@ -133,6 +138,9 @@ int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int n_tokens, const float *
 /* Runtime expert mask for one MoE layer: keep[e] != 0 keeps expert e routable (logits and selection
  * scores of the others get -inf); keep == NULL clears the layer's mask. */
 int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep);
+
+/* Depth prune on the context's model (see z2h_model_set_layer_skip). */
+int z2h_set_layer_skip(z2h_ctx * ctx, const uint8_t * skip);
 
 /* Additive pre-softmax router-logit bias for one MoE layer ([n_expert] fp32, NULL clears). Not a
  * reference input: a benchmark hook to impose a skewed expert popularity. */

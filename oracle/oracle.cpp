@@ -462,6 +462,7 @@ struct orc_model {
     std::vector<tensor> audio_embd;
     tensor text_embd, spk_lda_w, spk_lda_b, spk_proj_w, spk_proj_b, output_norm, output;
     std::vector<orc_layer> layers;
+    std::vector<uint8_t> layer_skip;              // depth prune: nonzero = block bypassed (zonos2.h:116-121)
     int rd = 0, kmax = 0;
     bool finalized = false;
 };
@@ -759,6 +760,12 @@ int orc_model_set_expert_mask(orc_model * m, int layer, const uint8_t * keep) {
     return 0;
 }
 
+int orc_model_set_layer_skip(orc_model * m, const uint8_t * skip) {
+    if (!m) return fail("null model");
+    if (skip) m->layer_skip.assign(skip, skip + m->hp.n_layer); else m->layer_skip.clear();
+    return 0;
+}
+
 void orc_model_free(orc_model * m) { delete m; }
 
 orc_kv * orc_kv_create(const orc_model * m, int n_slots, int slot_cap_frames) {
@@ -832,6 +839,10 @@ int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const 
         const orc_layer & ly = m->layers[L];
         if (L == 0) res = x;
         else for (size_t i = 0; i < res.size(); ++i) res[i] = x[i] + res[i];
+        if (L < (int) m->layer_skip.size() && m->layer_skip[L]) {   // graph.cpp:334-341: identity block
+            for (size_t i = 0; i < res.size(); ++i) x[i] = 0.0f * res[i];
+            continue;
+        }
         if (cap && cap->res_in) std::memcpy(cap_at(cap->res_in, L, (int64_t) T * d), res.data(), res.size() * 4);
         for (int t = 0; t < T; ++t) rms_norm(&res[(int64_t) t * d], f32p(ly.attn_norm), d, hp.rms_eps, &cur[(int64_t) t * d]);
         if (cap && cap->attn_in) std::memcpy(cap_at(cap->attn_in, L, (int64_t) T * d), cur.data(), cur.size() * 4);
@@ -920,6 +931,10 @@ int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n
     for (int L = 0; L < hp.n_layer; ++L) {
         const orc_layer & ly = m->layers[L];
         if (L == 0) res = x; else for (size_t i = 0; i < res.size(); ++i) res[i] = x[i] + res[i];
+        if (L < (int) m->layer_skip.size() && m->layer_skip[L]) {
+            for (size_t i = 0; i < res.size(); ++i) x[i] = 0.0f * res[i];
+            continue;
+        }
         for (int t = 0; t < n; ++t) rms_norm(&res[(int64_t) t * d], f32p(ly.attn_norm), d, hp.rms_eps, &cur[(int64_t) t * d]);
         // manual causal attention over the n new rows with fp32 K/V (graph.cpp:155-169)
         std::vector<float> q((size_t) n * nh * hd), k((size_t) n * nkv * hd), v((size_t) n * nkv * hd), g((size_t) n * nh);

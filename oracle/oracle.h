@@ -66,6 +66,9 @@ int  orc_model_set_logit_bias(orc_model * m, int layer, const float * bias);
 // -inf to expert e's router logit before the softmax and to its selection score (graph.cpp:212, 218);
 // NULL clears.
 int  orc_model_set_expert_mask(orc_model * m, int layer, const uint8_t * keep);
+// Depth prune (zonos2_model::layer_skip, src/zonos2.h:116-121; graph.cpp:334-341): skip[L] != 0
+// bypasses block L (the residual passes through unchanged); NULL clears. skip has n_layer entries.
+int  orc_model_set_layer_skip(orc_model * m, const uint8_t * skip);
 void orc_model_free(orc_model * m);
 const char * orc_last_error(void);
 

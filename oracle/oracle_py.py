@@ -42,6 +42,7 @@ def lib() -> C.CDLL:
         "orc_model_finalize": (i32, [vp]),
         "orc_model_set_logit_bias": (i32, [vp, i32, vp]),
         "orc_model_set_expert_mask": (i32, [vp, i32, vp]),
+        "orc_model_set_layer_skip": (i32, [vp, vp]),
         "orc_model_free": (None, [vp]),
         "orc_last_error": (C.c_char_p, []),
         "orc_kv_create": (vp, [vp, i32, i32]),
@@ -110,6 +111,10 @@ class OracleModel:
     def set_expert_mask(self, layer, keep):
         k = None if keep is None else np.ascontiguousarray(keep, dtype=np.uint8)
         check(lib().orc_model_set_expert_mask(self.m, layer, ptr(k)))
+
+    def set_layer_skip(self, skip):
+        self._skip = None if skip is None else np.ascontiguousarray(skip, dtype=np.uint8)
+        check(lib().orc_model_set_layer_skip(self.m, ptr(self._skip)))
 
     def __del__(self):
         if getattr(self, "m", None):
@@ -222,3 +227,14 @@ def dequant(wtype, wbytes, n):
     y = np.empty(n, np.float32)
     check(lib().orc_dequant(wtype, ptr(np.ascontiguousarray(wbytes)), ptr(y), n))
     return y
+
+
+def prefill(model: OracleModel, kv: OracleKV, slot, ids, spk=None, spk_pos=0, delta=None):
+    """Causal prefill of ids [n0][W] into `slot`; returns the last row's logits [ncb * av]."""
+    hp = model.hp
+    ids = np.ascontiguousarray(ids, np.int32)
+    spk = None if spk is None else np.ascontiguousarray(spk, np.float32)
+    delta = None if delta is None else np.ascontiguousarray(delta, np.float32)
+    out = np.empty(hp["n_codebooks"] * hp["audio_vocab"], np.float32)
+    check(lib().orc_prefill(model.m, kv.kv, slot, ptr(ids), ids.shape[0], ptr(spk), spk_pos, ptr(delta), ptr(out)))
+    return out

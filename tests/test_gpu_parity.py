@@ -183,3 +183,70 @@ def test_shared_model_contexts_and_mask_invalidation():
     assert np.array_equal(b.step(inp.slot_idx, inp.n_past, emb=inp.emb), want)
     for c in (a, b, own):
         c.close()
+
+
+def _prompt(cfg, n0, seed):
+    rng = np.random.default_rng(seed)
+    return np.concatenate([rng.integers(0, cfg.audio_vocab, (n0, cfg.n_codebooks)),
+                           rng.integers(0, cfg.text_vocab + 1, (n0, 1))], axis=1).astype(np.int32)
+
+
+def test_prefill_with_speaker_vs_oracle():
+    """zonos2_batch_slot_prefill with a speaker row (graph.cpp:262-297, 703-760): the device prefill
+    (speaker projections on the device, then causal rows over the f16 band) against the oracle's
+    row-by-row decode of the same prompt with the oracle's speaker row (full bar), and against the
+    oracle's one-shot prefill, whose in-prompt K/V stay fp32 (f16 rounding bar)."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 47)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    om = O.OracleModel(cfg.hparams(), model)
+    n0, pos, slot = 12, 2, 1
+    ids = _prompt(cfg, n0, 8)
+    spk = synth.gen_normal_f32((cfg.spk_dim,), 3, "spk")
+    delta = synth.gen_normal_f32((cfg.n_embd,), 4, "delta") * 0.1
+    got = ctx.prefill(slot, ids, spk=spk, spk_pos=pos, delta=delta)
+    okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    want_pf = O.prefill(om, okv, slot, ids, spk=spk, spk_pos=pos, delta=delta)
+    assert_close("prefill(spk) vs oracle prefill", got, want_pf, cos_min=0.9999, maxabs=5e-2)
+    # the oracle's speaker row, injected into row-by-row oracle steps
+    kv2 = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    sp = None
+    for t in range(n0):
+        if t == pos:
+            sp = _speaker_row_f32(model, spk, delta)   # the oracle's W_lda / W_proj products
+            want = O.step(om, kv2, [slot], [t], emb=sp[None, :])
+        else:
+            want = O.step(om, kv2, [slot], [t], ids=ids[t:t + 1])
+    assert_close("prefill(spk) vs oracle steps", got, want[0])
+    for L in range(cfg.n_layer):
+        gk, gv = ctx.kv_read(L, slot, 0, n0)
+        ok, ov = kv2.read(L, slot, 0, n0)
+        assert_close(f"prefill K rows L{L}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32))
+        assert_close(f"prefill V rows L{L}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32))
+    ctx.close()
+
+
+def _speaker_row_f32(model, spk, delta):
+    """spk_proj(spk_lda(spk) + b_lda) + b_proj + delta with the oracle's quantized matmuls"""
+    lw, pw = model["spk_lda.weight"], model["spk_proj.weight"]
+    sl = O.matmul(lw.type, lw.data, lw.ne[0], lw.ne[1], spk[None, :])[0] + model["spk_lda.bias"].data.view(np.float32)
+    sp = O.matmul(pw.type, pw.data, pw.ne[0], pw.ne[1], sl[None, :])[0] + model["spk_proj.bias"].data.view(np.float32)
+    return (sp + delta).astype(np.float32)
+
+
+def test_layer_skip_vs_oracle():
+    """Depth prune (zonos2_model::layer_skip): block 0 bypassed, through captured graphs too."""
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl, seed=48)
+    inp = synth.step_inputs(cfg, wl)
+    full = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)        # captures the graph
+    ctx.set_layer_skip([1, 0])
+    om.set_layer_skip([1, 0])
+    got = ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb)
+    want = O.step(om, okv, inp.slot_idx, inp.n_past, emb=inp.emb)
+    assert_close("logits (block 0 skipped)", got, want)
+    assert not np.array_equal(got, full)
+    ctx.set_layer_skip(None)
+    assert np.array_equal(ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb), full)
+    ctx.close()

@@ -69,6 +69,7 @@ struct z2h_model {
     bool finalized = false;
     int refs = 1;
     int gen = 0;                      // bumped when a device pointer captured in step graphs changes
+    std::vector<uint8_t> layer_skip;  // depth prune: nonzero = block bypassed (empty = none)
     int64_t bytes_w = 0;
     std::vector<void *> allocs;
     std::vector<uint8_t *> tab; std::vector<int> tab_type; std::vector<int64_t> tab_rows;
@@ -97,6 +98,7 @@ struct z2h_ctx {
     // scratch (sized for n_slots tokens)
     int Tmax = 0, Kmax = 0, items_max = 0;
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
+    float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
     ActBuf act{}, act_y{};
@@ -405,6 +407,9 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->logits, (size_t) T * hp.n_codebooks * hp.audio_vocab * 4, b)) ||
         (rc = dalloc(ctx, &ctx->d_err, 16, b)))
         return rc;
+    if (hp.spk_dim > 0 && hp.spk_lda_dim > 0 &&
+        (rc = dalloc(ctx, &ctx->spk_io, (size_t) (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
+        return rc;
     (void) E;
     ctx->h_pin_bytes = (size_t) T * (2 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
@@ -576,13 +581,21 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_DOWN);
         const dim3 grid((ctx->rd + 3) / 4, T);
-        switch (hp.n_embd / 64) {
-            case 4: hipLaunchKernelGGL(k_router_down<4>, grid, dim3(256), 0, ctx->stream, r); break;
-            case 8: hipLaunchKernelGGL(k_router_down<8>, grid, dim3(256), 0, ctx->stream, r); break;
-            case 16: hipLaunchKernelGGL(k_router_down<16>, grid, dim3(256), 0, ctx->stream, r); break;
-            case 32: hipLaunchKernelGGL(k_router_down<32>, grid, dim3(256), 0, ctx->stream, r); break;
-            default: hipLaunchKernelGGL(k_router_down<64>, grid, dim3(256), 0, ctx->stream, r); break;
+        // elements per lane: the next power of two >= ceil(d / 64); unguarded when d fills every lane
+        const int ni = hp.n_embd <= 64 ? 1 : 1 << (32 - __builtin_clz((unsigned) ((hp.n_embd + 63) / 64 - 1)));
+        const bool exact = hp.n_embd == 64 * ni;
+#define RDN(N_) do { if (exact) hipLaunchKernelGGL((k_router_down<N_, false>), grid, dim3(256), 0, ctx->stream, r); \
+                     else hipLaunchKernelGGL((k_router_down<N_, true>), grid, dim3(256), 0, ctx->stream, r); } while (0)
+        switch (ni) {
+            case 1: RDN(1); break;
+            case 2: RDN(2); break;
+            case 4: RDN(4); break;
+            case 8: RDN(8); break;
+            case 16: RDN(16); break;
+            case 32: RDN(32); break;
+            default: RDN(64); break;
         }
+#undef RDN
         HIPX(hipGetLastError());
     }
     {
@@ -662,20 +675,33 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
     ctx->cap_T = T;
-    // embeddings + emb_norm + layer-0 attn_norm
+    // the blocks that run (depth prune: a skipped block passes the residual through unchanged)
+    std::vector<int> run;
+    for (int L = 0; L < hp.n_layer; ++L)
+        if (L >= (int) ctx->m->layer_skip.size() || !ctx->m->layer_skip[L]) run.push_back(L);
+    const int n_run = (int) run.size();
+    // embeddings + emb_norm + the first block's attn_norm (output_norm when every block is skipped)
     ResNormArgs e{};
     e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb;
     for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->m->tab[k]; e.tab_type[k] = ctx->m->tab_type[k]; e.tab_rows[k] = ctx->m->tab_rows[k]; }
-    e.res = ctx->res; e.norm_w = ctx->m->layers[0].attn_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_ATTN_IN, 0);
-    e.act = ctx->act; e.act_fmt = act_of(ctx->m->layers[0].qkvg.type);
+    e.res = ctx->res;
+    if (n_run) {
+        e.norm_w = ctx->m->layers[run[0]].attn_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_ATTN_IN, run[0]);
+        e.act_fmt = act_of(ctx->m->layers[run[0]].qkvg.type);
+    } else {
+        e.norm_w = ctx->m->output_norm; e.cur_out = (float *) capp(ctx, Z2H_CAP_OUT_NORM, 0);
+        e.act_fmt = act_of(ctx->m->head.type);
+    }
+    e.act = ctx->act;
     if ((rc = launch_resnorm(ctx, T, e))) return rc;
-    if ((rc = cap_copy(ctx, Z2H_CAP_RES_IN, 0, ctx->res, T))) return rc;
+    if (n_run && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, run[0], ctx->res, T))) return rc;
     (void) h_npast;
     // persistent attention grid: the item count comes from the device n_past table
     const int attn_grid = std::min(ctx->items_max, 4096);
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
-    for (int L = 0; L < hp.n_layer; ++L) {
+    for (int i = 0; i < n_run; ++i) {
+        const int L = run[i];
         Layer & ly = ctx->m->layers[L];
         // fused QKV + gate projection
         if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), 1, Z2H_KF_GEMV_QKV))) return rc;
@@ -730,12 +756,13 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         ResNormArgs n{};
         n.mode = RN_ACCUM; n.src = ctx->eo; n.k = ly.moe ? ly.k : 1; n.res = ctx->res;
         n.cap_x = (float *) capp(ctx, Z2H_CAP_FFN_OUT, L);
-        const bool last = L + 1 == hp.n_layer;
-        n.norm_w = last ? ctx->m->output_norm : ctx->m->layers[L + 1].attn_norm;
-        n.cur_out = last ? (float *) capp(ctx, Z2H_CAP_OUT_NORM, 0) : (float *) capp(ctx, Z2H_CAP_ATTN_IN, L + 1);
-        n.act = ctx->act; n.act_fmt = act_of(last ? ctx->m->head.type : ctx->m->layers[L + 1].qkvg.type);
+        const bool last = i + 1 == n_run;
+        const int nx = last ? -1 : run[i + 1];
+        n.norm_w = last ? ctx->m->output_norm : ctx->m->layers[nx].attn_norm;
+        n.cur_out = last ? (float *) capp(ctx, Z2H_CAP_OUT_NORM, 0) : (float *) capp(ctx, Z2H_CAP_ATTN_IN, nx);
+        n.act = ctx->act; n.act_fmt = act_of(last ? ctx->m->head.type : ctx->m->layers[nx].qkvg.type);
         if ((rc = launch_resnorm(ctx, T, n))) return rc;
-        if (!last && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, L + 1, ctx->res, T))) return rc;
+        if (!last && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, nx, ctx->res, T))) return rc;
     }
     // output head + softcap
     const int nout = hp.n_codebooks * hp.audio_vocab;
@@ -951,9 +978,7 @@ int z2h_model_finalize(z2h_model * mdl) {
     }
     if (!missing.empty()) return seterr(mdl, Z2H_EINVAL, "missing tensors: " + missing);
     if (mdl->rd > 0) {
-        const int d = hp.n_embd;
-        if (mdl->rd != 64 && mdl->rd != 128) return seterr(mdl, Z2H_ENOTSUP, "router_dim must be 64 or 128");
-        if (d != 256 && d != 512 && d != 1024 && d != 2048 && d != 4096) return seterr(mdl, Z2H_ENOTSUP, "MoE layers need n_embd in {256, 512, 1024, 2048, 4096}");
+        if (mdl->rd != 32 && mdl->rd != 64 && mdl->rd != 128) return seterr(mdl, Z2H_ENOTSUP, "router_dim must be 32, 64 or 128");
         if (mdl->kmax > 8) return seterr(mdl, Z2H_ENOTSUP, "top-k above 8");
     }
     mdl->finalized = true;
@@ -1139,19 +1164,52 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
     return rc;
 }
 
+// Speaker row (graph.cpp:262-297): sp = W_proj (W_lda spk + b_lda) + b_proj (+ delta) -> host [n_embd]
+static int speaker_row(z2h_ctx * ctx, const float * spk, const float * delta, float * out) {
+    z2h_model * m = ctx->m;
+    const auto & hp = ctx->hp;
+    if (!m->spk_lda.ok() || !m->spk_proj.ok() || !m->spk_lda_b || !m->spk_proj_b || !ctx->spk_io)
+        return seterr(ctx, Z2H_ESTATE, "speaker tensors (spk_lda / spk_proj) not uploaded");
+    const int sd = hp.spk_dim, ld = hp.spk_lda_dim, d = hp.n_embd;
+    if (m->spk_lda.K != sd || m->spk_lda.rows != ld || m->spk_proj.K != ld || m->spk_proj.rows != d)
+        return seterr(ctx, Z2H_EINVAL, "speaker tensor shapes do not match spk_dim / spk_lda_dim");
+    float * x = ctx->spk_io, * sl = x + kpad(sd), * sp = sl + kpad(ld), * dl = sp + kpad(d);
+    int rc;
+    HIPX(hipMemcpyAsync(x, spk, (size_t) sd * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (delta) HIPX(hipMemcpyAsync(dl, delta, (size_t) d * 4, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_encode(ctx, x, sd, sd, 1, act_of(m->spk_lda.type), ctx->act))) return rc;
+    if ((rc = launch_gemv(ctx, m->spk_lda, nullptr, gemv_dense(ctx, 1, sl, ld, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
+    hipLaunchKernelGGL(k_bias_add, dim3((ld + 255) / 256), dim3(256), 0, ctx->stream, sl, (const float *) m->spk_lda_b, (const float *) nullptr, ld);
+    HIPX(hipGetLastError());
+    if ((rc = launch_encode(ctx, sl, ld, ld, 1, act_of(m->spk_proj.type), ctx->act))) return rc;
+    if ((rc = launch_gemv(ctx, m->spk_proj, nullptr, gemv_dense(ctx, 1, sp, d, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
+    hipLaunchKernelGGL(k_bias_add, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, sp, (const float *) m->spk_proj_b, (const float *) (delta ? dl : nullptr), d);
+    HIPX(hipGetLastError());
+    HIPX(hipMemcpyAsync(out, sp, (size_t) d * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipStreamSynchronize(ctx->stream));
+    return Z2H_OK;
+}
+
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits) {
     if (!ctx || !ids || !last_logits) return Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
     if (slot < 0 || slot >= ctx->n_slots) return seterr(ctx, Z2H_EINVAL, "slot out of range");
     if (n0 <= 0 || n0 > ctx->S) return seterr(ctx, Z2H_EINVAL, "prefill n0 exceeds slot_cap");
-    if (spk) return seterr(ctx, Z2H_ENOTSUP, "speaker injection in prefill is not implemented on the device yet");
-    (void) spk_pos; (void) delta;
+    if (spk && (spk_pos < 0 || spk_pos >= n0)) return seterr(ctx, Z2H_EINVAL, "spk_pos outside the prompt");
+    HIPX(hipSetDevice(ctx->device));
+    std::vector<float> sp;
+    if (spk) {
+        sp.resize(ctx->hp.n_embd);
+        if (int rc = speaker_row(ctx, spk, delta, sp.data())) return rc;
+    }
     // causal prefill as n0 single-row decode steps over the empty band: row t attends rows [0, t]
     std::vector<float> lg((size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab);
     for (int t = 0; t < n0; ++t) {
         const int32_t si = slot, np = t;
-        if (int rc = z2h_step(ctx, 1, &si, &np, ids + (size_t) t * ctx->W, nullptr, t + 1 == n0 ? last_logits : lg.data())) return rc;
+        float * out = t + 1 == n0 ? last_logits : lg.data();
+        const bool spk_row = spk && t == spk_pos;
+        if (int rc = z2h_step(ctx, 1, &si, &np, spk_row ? nullptr : ids + (size_t) t * ctx->W, spk_row ? sp.data() : nullptr, out)) return rc;
     }
     return Z2H_OK;
 }
@@ -1218,6 +1276,21 @@ int z2h_model_set_logit_bias(z2h_model * mdl, int layer, const float * bias) {
     HIPM(hipMemcpy(ly.bias_buf, bias, (size_t) ly.E * 4, hipMemcpyHostToDevice));
     ly.logit_bias = ly.bias_buf;
     return Z2H_OK;
+}
+
+int z2h_model_set_layer_skip(z2h_model * mdl, const uint8_t * skip) {
+    if (!mdl) return Z2H_EINVAL;
+    std::vector<uint8_t> v;
+    if (skip) for (int L = 0; L < mdl->hp.n_layer; ++L) v.push_back(skip[L] ? 1 : 0);
+    if (std::find(v.begin(), v.end(), 1) == v.end()) v.clear();
+    if (v != mdl->layer_skip) { mdl->layer_skip = v; ++mdl->gen; }   // captured graphs bake the block list in
+    return Z2H_OK;
+}
+
+int z2h_set_layer_skip(z2h_ctx * ctx, const uint8_t * skip) {
+    if (!ctx) return Z2H_EINVAL;
+    if (ctx->stream) (void) hipStreamSynchronize(ctx->stream);
+    return z2h_model_set_layer_skip(ctx->m, skip);
 }
 
 int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep) {

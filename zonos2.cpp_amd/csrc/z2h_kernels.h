@@ -156,6 +156,15 @@ __device__ __forceinline__ double block_sum_d(double v, double * red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
+// y[i] = y[i] + b[i] (+ c[i]): the bias adds after the speaker projections (graph.cpp:272-278)
+__global__ void __launch_bounds__(256) k_bias_add(float * y, const float * b, const float * c, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = y[i] + b[i];
+    if (c) v = v + c[i];
+    y[i] = v;
+}
+
 // ------------------------------------------------------------------ dequantised table rows
 __device__ __forceinline__ float table_elem(const uint8_t * row, int type, int i) {
     switch (type) {
@@ -1360,8 +1369,9 @@ struct RouterArgs {
 
 // rh[t][o] = lane-strided fma partials over d + xor butterfly, + bias (+ state * eda).
 // grid (ceil(rd/4), T): wave = output row, blockIdx.y = token. All of a lane's loads are issued before
-// its fma chain; the chain order (i = lane, lane+64, ... ascending) is the contract's.
-template <int NI>   // NI = d / 64 elements per lane
+// its fma chain; the chain order (i = lane, lane+64, ... ascending) is the contract's. GUARD: d is
+// not a multiple of 64 (lanes past the row's end keep a zero partial).
+template <int NI, bool GUARD>   // NI = ceil(d / 64) elements per lane
 __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     const int lane = threadIdx.x & 63, o = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
     if (o >= a.rd) return;
@@ -1369,12 +1379,17 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     const float * __restrict__ x = a.x + (int64_t) t * a.d + lane;
     float wv[NI], xv[NI];
 #pragma unroll
-    for (int j = 0; j < NI; ++j) { wv[j] = w[64 * j]; xv[j] = x[64 * j]; }
+    for (int j = 0; j < NI; ++j) {
+        const bool in = !GUARD || lane + 64 * j < a.d;
+        wv[j] = in ? w[64 * j] : 0.0f;
+        xv[j] = in ? x[64 * j] : 0.0f;
+    }
     const float b = a.b_down[o];
     const float st = a.eda && a.state_in ? a.state_in[(int64_t) t * a.rd + o] * a.eda[o] : 0.0f;
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) acc = __builtin_fmaf(wv[j], xv[j], acc);
+    for (int j = 0; j < NI; ++j)
+        if (!GUARD || lane + 64 * j < a.d) acc = __builtin_fmaf(wv[j], xv[j], acc);
     float v = wave_tree_f(acc) + b;
     if (a.eda && a.state_in) v = v + st;
     if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
@@ -1491,7 +1506,8 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
             if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
         }
     }
-    switch (rd) {                                    // router_dim in {64, 128} (host-checked)
+    switch (rd) {                                    // router_dim in {32, 64, 128} (host-checked)
+        case 32:  rt_mlp<4>(a, s_x, s_y, s_l); break;
         case 64:  rt_mlp<8>(a, s_x, s_y, s_l); break;
         default:  rt_mlp<16>(a, s_x, s_y, s_l); break;
     }

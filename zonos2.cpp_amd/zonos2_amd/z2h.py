@@ -36,6 +36,8 @@ def lib() -> C.CDLL:
         "z2h_model_finalize": (i32, [vp]),
         "z2h_model_set_expert_mask": (i32, [vp, i32, vp]),
         "z2h_model_set_logit_bias": (i32, [vp, i32, vp]),
+        "z2h_model_set_layer_skip": (i32, [vp, vp]),
+        "z2h_set_layer_skip": (i32, [vp, vp]),
         "z2h_model_last_error": (C.c_char_p, [vp]),
         "z2h_model_release": (None, [vp]),
         "z2h_create_batch": (i32, [vp, i32, i32, C.POINTER(vp)]),
@@ -69,7 +71,7 @@ def lib() -> C.CDLL:
 
 
 EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", "z2h_model_set_expert_mask",
-           "z2h_model_set_logit_bias", "z2h_model_last_error", "z2h_model_release", "z2h_create_batch",
+           "z2h_model_set_logit_bias", "z2h_model_set_layer_skip", "z2h_set_layer_skip", "z2h_model_last_error", "z2h_model_release", "z2h_create_batch",
            "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
@@ -187,10 +189,12 @@ class Context:
         self.check(lib().z2h_step(self.ctx, T, _p(si), _p(npast), _p(ids), _p(emb), _p(out)))
         return out
 
-    def prefill(self, slot, ids):
+    def prefill(self, slot, ids, spk=None, spk_pos=-1, delta=None):
         ids = np.ascontiguousarray(ids, np.int32)
+        spk = None if spk is None else np.ascontiguousarray(spk, np.float32)
+        delta = None if delta is None else np.ascontiguousarray(delta, np.float32)
         out = np.empty(self.hp["n_codebooks"] * self.hp["audio_vocab"], np.float32)
-        self.check(lib().z2h_prefill(self.ctx, slot, _p(ids), ids.shape[0], None, -1, None, _p(out)))
+        self.check(lib().z2h_prefill(self.ctx, slot, _p(ids), ids.shape[0], _p(spk), spk_pos, _p(delta), _p(out)))
         return out
 
     def moe_forward(self, layer, x, state_in=None):
@@ -207,6 +211,10 @@ class Context:
     def set_expert_mask(self, layer, keep):
         k = None if keep is None else np.ascontiguousarray(keep, np.uint8)
         self.check(lib().z2h_set_expert_mask(self.ctx, layer, _p(k)))
+
+    def set_layer_skip(self, skip):
+        k = None if skip is None else np.ascontiguousarray(skip, np.uint8)
+        self.check(lib().z2h_set_layer_skip(self.ctx, _p(k)))
 
     def set_capture(self, on: bool):
         self.check(lib().z2h_set_capture(self.ctx, 1 if on else 0))
