@@ -1,0 +1,95 @@
+"""The reference's own fixture model (tests/golden/dummy-zonos2.gguf: 4 blocks, dense 0 and 3, MoE 1
+and 2 with top-1 / top-2 of 4 experts, router_dim 32, head_dim 16, F16 weights) through the device
+library: steps and a speaker prefill against the oracle on the same file, and the zonos2.h API's
+--batch-test / --decode-bench harness (F.1 / F.2 of src/main.cpp:158-285)."""
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+from gguf_read import hparams, read
+from helpers import assert_close
+from zonos2_amd.lib import BUILD
+from zonos2_amd.z2h import Context
+
+pytestmark = pytest.mark.gpu
+FIXTURE = "tests/golden/dummy-zonos2.gguf"
+
+
+@pytest.fixture(scope="module")
+def dummy(root):
+    _, kv, tensors = read(root / FIXTURE)
+    return hparams(kv, tensors), tensors
+
+
+def _ids(hp, T, seed):
+    rng = np.random.default_rng(seed)
+    return np.concatenate([rng.integers(0, hp["audio_vocab"], (T, hp["n_codebooks"])),
+                           rng.integers(0, hp["text_vocab"] + 1, (T, 1))], axis=1).astype(np.int32)
+
+
+def test_dummy_model_steps_vs_oracle(dummy):
+    hp, tensors = dummy
+    n_slots, cap = 4, 40
+    ctx = Context(hp, n_slots, cap)
+    ctx.upload(tensors)
+    om = O.OracleModel(hp, tensors)
+    okv = O.OracleKV(om, n_slots, cap)
+    # prefill ragged prompts row by row on both sides, then decode a few batched steps
+    lens = [3, 9, 1, 14]
+    for s, n in enumerate(lens):
+        ids = _ids(hp, n, 10 + s)
+        for t in range(n):
+            ctx.step([s], [t], ids=ids[t:t + 1])
+            O.step(om, okv, [s], [t], ids=ids[t:t + 1])
+    ctx.set_capture(True)
+    npast = list(lens)
+    for it in range(3):
+        ids = _ids(hp, n_slots, 50 + it)
+        got = ctx.step(list(range(n_slots)), npast, ids=ids)
+        want, cap_o = O.step(om, okv, list(range(n_slots)), npast, ids=ids, capture=True)
+        assert_close(f"dummy logits step {it}", got, want)
+        for L, k in enumerate(hp["expert_used"]):
+            if not k:
+                continue
+            sel = ctx.read_capture(L, "sel", n_slots).reshape(n_slots, ctx.kmax)[:, :k]
+            assert np.array_equal(sel, cap_o["sel"][L][:, :k]), f"layer {L} routing"
+        npast = [n + 1 for n in npast]
+    ctx.close()
+
+
+def test_dummy_model_speaker_prefill_vs_oracle(dummy):
+    hp, tensors = dummy
+    ctx = Context(hp, 2, 32)
+    ctx.upload(tensors)
+    om = O.OracleModel(hp, tensors)
+    ids = _ids(hp, 7, 3)
+    rng = np.random.default_rng(4)
+    spk = rng.standard_normal(hp["spk_dim"]).astype(np.float32)
+    delta = (0.1 * rng.standard_normal(hp["n_embd"])).astype(np.float32)
+    got = ctx.prefill(1, ids, spk=spk, spk_pos=0, delta=delta)
+    want = O.prefill(om, O.OracleKV(om, 2, 32), 1, ids, spk=spk, spk_pos=0, delta=delta)
+    assert_close("dummy prefill(spk)", got, want, cos_min=0.9999, maxabs=5e-2)
+    ctx.close()
+
+
+def _cli(*args):
+    r = subprocess.run([str(BUILD / "zonos2-batch"), *args], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:])
+    return r
+
+
+def test_batch_test_harness_on_fixture(root):
+    r = _cli("--model", str(root / FIXTURE), "--batch-test", "--greedy", "--slots", "5", "--requests", "4",
+             "--dup", "--max-frames", "24", "--prompt-len", "12")
+    assert r.returncode == 0 and "batch-test: OK" in r.stdout
+    assert "batch == alone for every request: yes" in r.stdout
+    r = _cli("--model", str(root / FIXTURE), "--batch-test", "--slots", "3", "--requests", "3",
+             "--max-frames", "16", "--prompt-len", "10", "--seed", "9")
+    assert r.returncode == 0 and "batch == alone for every request: yes" in r.stdout
+
+
+def test_decode_bench_harness_on_fixture(root):
+    r = _cli("--model", str(root / FIXTURE), "--decode-bench", "--slots", "4", "--steps", "16", "--prompt-len", "8")
+    assert r.returncode == 0 and "decode-bench: slots=4 steps=16" in r.stdout

@@ -71,7 +71,7 @@ def build_api(force: bool = True) -> tuple[Path, Path]:
     cli = BUILD / "zonos2-batch"
     host = PKG / "host"
     srcs = [host / "zonos2_batch.cpp", host / "gguf.cpp", host / "zonos2_sampler.cpp"]
-    deps = srcs + [ROOT / "include" / "zonos2.h", ROOT / "include" / "z2h.h", host / "gguf.h"]
+    deps = srcs + [ROOT / "include" / "zonos2.h", ROOT / "include" / "zonos2-sampler.h", ROOT / "include" / "z2h.h", host / "gguf.h"]
     inc = [f"-I{ROOT / 'include'}", f"-I{host}"]
     rpath = "-Wl,-rpath,$ORIGIN"
     if force or _stale(lib, deps):
