@@ -155,7 +155,8 @@ enum {
 };
 int z2h_set_capture(z2h_ctx * ctx, int enable);
 /* Copy capture `what` of `layer` (ignored for OUT_NORM) from the last step / moe_forward into host.
- * Sizes: see z2h_capture_bytes. */
+ * Sizes: see z2h_capture_bytes. SEL and WEIGHTS hold the layer's [n_tokens][top_k of that layer]
+ * rows at the start of a buffer sized for the model's largest top-k. */
 int64_t z2h_capture_bytes(z2h_ctx * ctx, int what, int n_tokens);
 int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nbytes);
 

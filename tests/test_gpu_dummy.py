@@ -53,7 +53,8 @@ def test_dummy_model_steps_vs_oracle(dummy):
         for L, k in enumerate(hp["expert_used"]):
             if not k:
                 continue
-            sel = ctx.read_capture(L, "sel", n_slots).reshape(n_slots, ctx.kmax)[:, :k]
+            # the layer's own top-k rows [T][k] lead the T * kmax capture buffer
+            sel = ctx.read_capture(L, "sel", n_slots).ravel()[:n_slots * k].reshape(n_slots, k)
             assert np.array_equal(sel, cap_o["sel"][L][:, :k]), f"layer {L} routing"
         npast = [n + 1 for n in npast]
     ctx.close()

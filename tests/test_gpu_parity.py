@@ -37,8 +37,8 @@ def _check_routing(cfg, ctx, om, T):
         rh = ctx.read_capture(L, "router_state", T).reshape(T, rd)
         lg = ctx.read_capture(L, "router_logits", T).reshape(T, E)
         pr = ctx.read_capture(L, "probs", T).reshape(T, E)
-        sel = ctx.read_capture(L, "sel", T).reshape(T, ctx.kmax)[:, :k]
-        w = ctx.read_capture(L, "weights", T).reshape(T, ctx.kmax)[:, :k]
+        sel = ctx.read_capture(L, "sel", T).ravel()[:T * k].reshape(T, k)
+        w = ctx.read_capture(L, "weights", T).ravel()[:T * k].reshape(T, k)
         for name, a, b in (("rh", rh, ref["rh"]), ("logits", lg, ref["logits"]), ("probs", pr, ref["probs"]),
                            ("w", w, ref["w"])):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"layer {L} {name} not bit-exact"
