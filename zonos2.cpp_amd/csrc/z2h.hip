@@ -476,17 +476,20 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         const bool dual = a.mode == MM_SWIGLU;
         if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
         if (!a.grouped && (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX) {
-            // few row groups: K split over the 4 waves of a block, one row group per block
-            dim3 grid(m0.tiles, grid_y, dual ? 1 : a.n_mats), block(256);
-#define SPL(W_, D_) hipLaunchKernelGGL((k_gemv_split<W_, D_>), grid, block, lds, ctx->stream, a)
-            if (m0.type == Z2H_Q4_K) { if (dual) SPL(WF_Q4_K, true); else SPL(WF_Q4_K, false); }
-            else { if (dual) SPL(WF_Q8_0, true); else SPL(WF_Q8_0, false); }
+            // K split over the 4 waves of a block, one 16-row group per block
+            const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, a.grouped ? MT_G : MT);
+            dim3 grid(m0.tiles, a.grouped ? a.E : grid_y, a.grouped ? passes : (dual ? 1 : a.n_mats)), block(256);
+#define SPL(W_, D_, R_) hipLaunchKernelGGL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
+#define SPL_R(W_, D_) do { if (a.grouped) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
+            if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
+            else { if (dual) SPL_R(WF_Q8_0, true); else SPL_R(WF_Q8_0, false); }
+#undef SPL_R
 #undef SPL
             HIPX(hipGetLastError());
             return Z2H_OK;
         }
         dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
-#define MM16(W_, D_, R_) hipLaunchKernelGGL((k_gemv_mfma<W_, D_, R_>), grid, block, lds, ctx->stream, a)
+#define MM16(W_, D_, R_) hipLaunchKernelGGL((k_gemv_mfma<W_, D_, R_, R_ == MT_G ? m16fmt<W_>::GPF : 1>), grid, block, lds, ctx->stream, a)
         if (m0.type == Z2H_Q4_K) {
             if (a.grouped) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
@@ -1053,12 +1056,12 @@ int z2h_finalize(z2h_ctx * ctx) {
 #define LDS_ATTR(K_) if (int rc_ = allow_lds((const void *) &(K_), ctx)) return rc_;
     LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
     LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
-    LDS_ATTR((k_gemv_split<WF_Q4_K, false>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false>))
-    LDS_ATTR((k_gemv_split<WF_Q4_K, true>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G>))
+    LDS_ATTR((k_gemv_split<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT>))
+    LDS_ATTR((k_gemv_split<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT, 1>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     (void) hp;

@@ -4,23 +4,27 @@
 //   k_resnorm        embedding sum (248-260) / emb_norm (300) / residual folds (332, 345, 353) /
 //                    rms_w norms (92-95, 343, 347, 354), and the encoding of the normalised row in
 //                    the next matmul's activation type (ggml's vec_dot_type conversion)
-//   k_gemv<F>        every weight matmul: QKV+gate (107-111, fused into one matrix), W_o (175),
-//                    expert gate/up and down (mul_mat_id 223-231, grouped by expert from the
-//                    top-k selection), dense FFN (179-185), output head + softcap (357-362)
-//   k_swiglu_encode  up * silu(gate) (183, 225) encoded for the down matmul
-//   k_qkv_post       QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137), sigmoid gate (107)
-//   k_attn_partial   ragged GQA decode attention over the slot's band, split into 64-row chunks (139-153)
-//   k_attn_combine   chunk merge, per-head sigmoid gate (173), encoding for W_o
+//   k_gemv_split     dense m16 matmuls with K split over a block's waves: fused QKV + gate
+//                    (107-111), W_o (175), output head + softcap (357-362), dense FFN (179-185)
+//   k_gemv_mfma      grouped expert matmuls on the m16 layout (mul_mat_id 223-231, routes grouped by
+//                    expert from the top-k selection): gate/up + SwiGLU in one launch, down x route
+//                    weight
+//   k_gemv / k_gemv_rows   the same on the 64-row tiled layout (Q6_K, F16)
+//   k_swiglu_encode / k_encode_rows   up * silu(gate) (183, 225) / fp32 rows encoded for the next matmul
+//   k_attn_decode    QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137) and ragged GQA
+//                    decode attention over the slot's band in 64-row chunks (139-153)
+//   k_attn_combine   chunk merge, per-head sigmoid gate (107, 173), encoding for W_o
 //   k_router_down    EDA router down-projection + state threading (199-203)
-//   k_router_tail    router norm, erf-GELU MLP, softmax, bias, top-k, weights (206-220)
+//   k_router_tail    router norm, erf-GELU MLP, softmax, bias, mask, top-k, weights (206-220)
+//   k_kv_move / k_bias_add   KV row staging for host reads and writes / speaker-projection biases
 //
-// Weight layout in HBM ("row-tiled"): a matrix of R rows x K columns is cut into 64-row tiles and
-// 256-column units. The bytes of unit (row, u) are split into 16-byte chunks; chunk c of the 64 rows
-// of a tile are stored contiguously, so every lane of a wave64 owns one row and each load
-// instruction of the wave reads 1 KiB of contiguous HBM. Unit sizes equal the GGUF storage sizes:
-//   Q4_K 144 B = 9 chunks (chunk 0 = d,dmin,scales; 1..8 = qs), Q8_0 8 blocks = 17 chunks
-//   (0..15 = qs, 16 = the 8 f16 scales), Q6_K 208 B = 13 chunks (ql, qh, scales) + an f16 d plane,
-//   F16 512 B = 32 chunks.
+// Weight layouts in HBM: "m16" for Q4_K and Q8_0 (see k_gemv_mfma) and "row-tiled" (t64) for Q6_K
+// and F16: a matrix of R rows x K columns is cut into 64-row tiles and 256-column units; the bytes
+// of unit (row, u) are split into 16-byte chunks and chunk c of the 64 rows of a tile is stored
+// contiguously, so every lane of a wave64 owns one row and each load instruction of the wave reads
+// 1 KiB of contiguous HBM. Unit sizes equal the GGUF storage sizes: Q4_K 144 B = 9 chunks, Q8_0 8
+// blocks = 17 chunks (16 of values, 1 of the 8 f16 scales), Q6_K 208 B = 13 chunks + an f16 d
+// plane, F16 512 B = 32 chunks.
 #pragma once
 #include "z2h_common.h"
 
@@ -770,8 +774,12 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 template <int WF> struct m16fmt;
-template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constexpr int BYTES = 2304; static constexpr int WPE = 5; };
-template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int WPE = 4; };
+// WPE: waves per SIMD of the PF = 1 kernels; GPF / GWPE: register-ring depth and waves per SIMD of
+// the grouped (expert) launches
+template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constexpr int BYTES = 2304; static constexpr int WPE = 5;
+                                     static constexpr int GPF = 1; static constexpr int GWPE = 5; };
+template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int WPE = 4;
+                                     static constexpr int GPF = 1; static constexpr int GWPE = 4; };
 constexpr int MT = 16;                  // tokens per MFMA pass
 
 // token rows per pass of the m16 kernels: grouped expert launches stage up to MT_G routes (an
@@ -796,55 +804,64 @@ __device__ __forceinline__ void m16_load(const uint4 * __restrict__ unit, int la
 template <int WF>
 __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], const uint4 & hd, int sb, int K, int lane,
                                          const int8_t * sq, const int * sbs2, const float * sdx, int nsb, int ntm1, float (&acc)[4]) {
+    // every operand load and all MFMAs of the unit are issued before the scale arithmetic, so the 8
+    // independent products pipeline instead of each waiting for its predecessor's scaling
     const int q = lane >> 4, r = min(lane & 15, ntm1), KP = K + 16;
     const int8_t * arow = sq + r * KP + sb * 256 + 8 * q;          // A: token r, k-slice q
     const v4i_t zero = {0, 0, 0, 0};
+    long A[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) A[j] = *(const long *) (arow + 32 * j);
+    v4i_t C[8];
     if constexpr (WF == WF_Q4_K) {
-        const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
-        // 6-bit scales / mins of sub-blocks 0-3 and 4-7, four per dword (GGUF K-quant packing)
-        const uint32_t sc03 = hd.y & 0x3f3f3f3fu, mn03 = hd.z & 0x3f3f3f3fu;
-        const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
-        const uint32_t mn47 = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+        const int * bsr = sbs2 + r * (K / 32) + sb * 8;              // token r (A operand row)
+        const float a0 = (float) bsr[q], a1 = (float) bsr[q + 4];
+        float dx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dx[i] = sdx[min(4 * q + i, ntm1) * nsb + sb];
         const uint32_t w[8] = {qs[0].x, qs[0].y, qs[0].z, qs[0].w, qs[1].x, qs[1].y, qs[1].z, qs[1].w};
-        int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {                               // sub-block j = nibble half of pair j/2
             const int pr = j >> 1;
             const uint32_t b0 = (j & 1) ? (w[2 * pr] >> 4) & 0x0f0f0f0fu : w[2 * pr] & 0x0f0f0f0fu;
             const uint32_t b1 = (j & 1) ? (w[2 * pr + 1] >> 4) & 0x0f0f0f0fu : w[2 * pr + 1] & 0x0f0f0f0fu;
-            const long B = (long) (((uint64_t) b1 << 32) | b0);
-            const long A = *(const long *) (arow + 32 * j);
-            const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
-            const int scj = (int) (((j < 4 ? sc03 : sc47) >> (8 * (j & 3))) & 0xffu);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scj, C[i]);   // |products| < 2^22
+            C[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j], (long) (((uint64_t) b1 << 32) | b0), zero, 0, 0, 0);
         }
         // min correction sum_j m_j[row] * bsum_j[token] as an fp32 16x16x4 product (two k-halves):
         // integer products < 2^19 and sums < 2^23, so the fp32 result is exact
-        const int * bsr = sbs2 + r * (K / 32) + sb * 8;              // token r (A operand row)
-        const float a0 = (float) bsr[q], a1 = (float) bsr[q + 4];
+        // (6-bit scales / mins of sub-blocks 0-3 and 4-7, four per dword: GGUF K-quant packing)
+        const uint32_t mn03 = hd.z & 0x3f3f3f3fu;
+        const uint32_t mn47 = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
         const float b0 = (float) ((mn03 >> (8 * q)) & 0xffu), b1 = (float) ((mn47 >> (8 * q)) & 0xffu);
         v4f_t S = {0.0f, 0.0f, 0.0f, 0.0f};
         S = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, S, 0, 0, 0);
         S = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, S, 0, 0, 0);
+        const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+        const uint32_t sc03 = hd.y & 0x3f3f3f3fu;
+        const uint32_t sc47 = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+        int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float dx = sdx[min(4 * q + i, ntm1) * nsb + sb];
-            acc[i] += (d * dx) * (float) sumi[i] - (dmin * dx) * S[i];
+        for (int j = 0; j < 8; ++j) {
+            const int scj = (int) (((j < 4 ? sc03 : sc47) >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scj, C[j][i]);   // |products| < 2^22
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += (d * dx[i]) * (float) sumi[i] - (dmin * dx[i]) * S[i];
     } else {
-        uint16_t dh[8];
-        __builtin_memcpy(dh, &hd, 16);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const uint4 v = qs[b >> 1];
             const uint32_t lo = (b & 1) ? v.z : v.x, hi = (b & 1) ? v.w : v.y;
-            const long B = (long) (((uint64_t) hi << 32) | lo);
-            const long A = *(const long *) (arow + 32 * b);
-            const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+            C[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[b], (long) (((uint64_t) hi << 32) | lo), zero, 0, 0, 0);
+        }
+        uint16_t dh[8];
+        __builtin_memcpy(dh, &hd, 16);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
             const float dw = h2f(dh[b]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += (dw * sdx[min(4 * q + i, ntm1) * (K / 32) + sb * 8 + b]) * (float) C[i];
+            for (int i = 0; i < 4; ++i) acc[i] += (dw * sdx[min(4 * q + i, ntm1) * (K / 32) + sb * 8 + b]) * (float) C[b][i];
         }
     }
 }
@@ -901,11 +918,14 @@ __device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok,
 // spread over blocks). DUAL: each wave computes the same 16 rows of two matrices (w[0] = gate,
 // w[1] = up) and stores up * silu(gate) (SwiGLU). The wave's weight units (both matrices for DUAL)
 // stream through a PF-deep register ring; the first PF are requested before the activations are
-// staged. Register use is capped for 5 (Q4_K) / 4 (Q8_0) waves per SIMD: the kernel is latency
-// bound, and occupancy hides more of it than a deeper per-wave ring.
-template <int WF, bool DUAL, int ROWS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(m16fmt<WF>::WPE, m16fmt<WF>::WPE))) k_gemv_mfma(GemvArgs a) {
-    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES, PF = 1;
+// staged. PF = 1 caps registers for 5 (Q4_K) / 4 (Q8_0) waves per SIMD; deeper rings (fewer waves
+// per SIMD) keep more bytes in flight per wave where few blocks are resident (the expert matmuls:
+// the touched experts x row-group quads come to under two blocks per CU).
+template <int WF, bool DUAL, int ROWS, int PF>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE,
+                                                                          PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE)))
+k_gemv_mfma(GemvArgs a) {
+    constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ int s_list[MAX_ROUTES];
@@ -996,33 +1016,67 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(m16fmt
     }
 }
 
-// Dense (token-chunk) m16 GEMV with the K units split over the block's 4 waves: one 16-row group per
-// block (grid x), wave w takes units w, w+4, ... (all requested up front), partial sums are added in
-// LDS in wave order. Used where the matrix has few row groups (attention projections, output head),
-// so every wave has at most a few units in flight and the chip sees 4x more waves.
+// m16 GEMV with the K units split over the block's 4 waves: one 16-row group per block (grid x), wave
+// w takes units w, w+4, ... (all requested up front, so a wave has all its weight bytes in flight at
+// once), partial sums are added in LDS in wave order. Dense: grid (groups, token chunks of ROWS, mats);
+// grouped (expert matmuls): grid (groups, experts, passes of ROWS routes), the expert's routes listed
+// first so blocks of untouched experts read no weights. Each 16-row group gives 4x more, shorter
+// waves than a wave streaming the whole K, which keeps enough bytes in flight to cover HBM latency.
 constexpr int SPLIT_UMAX = 4;          // units per wave (U <= 16)
-template <int WF, bool DUAL>
+template <int WF, bool DUAL, int ROWS>
 __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ int s_tok[MT];
+    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_wcnt[4];
+    __shared__ int s_tok[ROWS];
     __shared__ float s_part[4][8][64];
     const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g16 = blockIdx.x, m = DUAL ? 0 : blockIdx.z;
+    const int g16 = blockIdx.x;
     int8_t * sq = (int8_t *) smem;
-    int * sbs2 = (int *) (smem + MT * KP);
-    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + MT * (K / 32)) : (float *) (smem + MT * KP);
-    const int c0 = blockIdx.y * MT, nt = min(MT, a.n_tok - c0);
+    int * sbs2 = (int *) (smem + ROWS * KP);
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32)) : (float *) (smem + ROWS * KP);
+    int e = 0, m = 0, n_items, c0;
+    if (a.grouped) {
+        e = blockIdx.y;
+        n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
+        if (a.cap_counts && blockIdx.x == 0 && blockIdx.z == 0) {   // grouping capture, one block per expert
+            int off = 0;
+            for (int rr = 0; rr < a.n_tok * a.k; ++rr) off += a.sel[rr] < e;
+            for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
+            if (tid == 0) {
+                a.cap_counts[e] = n_items;
+                a.cap_offsets[e] = off;
+                if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
+            }
+        }
+        c0 = blockIdx.z * ROWS;
+    } else {
+        m = DUAL ? 0 : blockIdx.z;
+        n_items = a.n_tok;
+        c0 = blockIdx.y * ROWS;
+    }
+    if (c0 >= n_items) return;
+    const int nt = min(ROWS, n_items - c0);
     const int nsb = a.nsb, U = (DUAL ? 2 : 1) * nsb;
-    const uint4 * ub0 = (const uint4 *) (a.w[m] + (size_t) g16 * nsb * UB);
-    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (size_t) g16 * nsb * UB) : ub0;
+    const int64_t eoff = (int64_t) e * a.mat_bytes + (int64_t) g16 * nsb * UB;
+    const uint4 * ub0 = (const uint4 *) (a.w[m] + eoff);
+    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + eoff) : ub0;
     auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
     uint4 pq[SPLIT_UMAX][QS], ph[SPLIT_UMAX];
 #pragma unroll
     for (int j = 0; j < SPLIT_UMAX; ++j)
         if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
-    if (tid < MT) s_tok[tid] = c0 + min(tid, nt - 1);
+    if (tid < ROWS) {
+        const int tt = min(tid, nt - 1);
+        int tok = c0 + tt;
+        if (a.grouped) {
+            const int it = s_list[c0 + tt];
+            tok = a.act_by_route ? it : it / a.k;
+        }
+        s_tok[tid] = tok;
+    }
     __syncthreads();
     m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
     __syncthreads();
@@ -1051,13 +1105,15 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     for (int i = 0; i < 4; ++i) {
         const int t = 4 * q + i;
         if (t >= nt) continue;
+        const int it = a.grouped ? s_list[c0 + t] : c0 + t;
         const float g = ((s_part[0][i][lane] + s_part[1][i][lane]) + s_part[2][i][lane]) + s_part[3][i][lane];
         float y = g;
         if (DUAL) {
             const float u = ((s_part[0][4 + i][lane] + s_part[1][4 + i][lane]) + s_part[2][4 + i][lane]) + s_part[3][4 + i][lane];
             y = u * z_silu(g);
         } else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
-        a.out[m][(int64_t) (c0 + t) * a.out_ld + row] = y;
+        else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
+        a.out[m][(int64_t) it * a.out_ld + row] = y;
     }
 }
 
