@@ -16,6 +16,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -29,6 +30,16 @@ HBM_PEAK_GBPS = 8000.0
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def profiled_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/gemv_gateup_c3_traffic.md, copy-calibrated), or None."""
+    p = ROOT / "profiles" / "gemv_gateup_c3_traffic.md"
+    if config != "c3" or not p.exists():
+        return None
+    m = re.search(r"^gemv_gateup_traffic_bytes: (\d+)", p.read_text(), re.M)
+    return int(m.group(1)) if m else None
 
 
 def model_bytes(model, names):
@@ -149,7 +160,8 @@ def main() -> int:
     got = d_logits.cpu().numpy()
     assert np.array_equal(got, logits_gpu), "device-resident step differs from the host-API step"
 
-    # per-kernel HIP-event window (separate pass; events bracket every launch)
+    # per-kernel HIP-event window (separate pass over the same steps, eager launches): every launch
+    # carries a start / stop event pair timestamped at the kernel's own start and end
     ctx.profile_begin()
     for _ in range(args.steps):
         one()
@@ -215,9 +227,9 @@ def main() -> int:
                    "requests": T, "kv_lens": wl.kv_lens, "parallelism": "single GPU"},
         "step_hbm": {"bytes": B, "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
-        "roofline": {"kernel": "k_gemv<Q4_K> grouped expert gate/up", "bound": "hbm",
+        "roofline": {"kernel": "k_gemv_mfma<Q4_K, DUAL> grouped expert gate/up + SwiGLU", "bound": "hbm",
                      "achieved": round(dom_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(args.config),
                      "avg_launch_us": round(gu_ms / max(1, gu_n) * 1000.0, 2),
                      "bytes_per_launch": int((gu_w + act_b + gu_out) / cfg.n_layer)},
         "kernels_us_per_step": {k: round(t / args.steps * 1000.0, 1) for k, (t, n) in prof.items() if n},

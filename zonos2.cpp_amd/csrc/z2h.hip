@@ -9,6 +9,7 @@
 // and after the last layer k_resnorm(output_norm) -> k_gemv(head, softcap).
 #include "z2h.h"
 #include "z2h_kernels.h"
+#include <hip/hip_ext.h>
 #include "z2_formats.h"
 
 #include <algorithm>
@@ -121,6 +122,7 @@ struct z2h_ctx {
     std::vector<hipEvent_t> ev;
     std::vector<int> ev_fam;
     int ev_used = 0;
+    int prof_fam = -1;                // family of the launches being issued (profiling windows)
 
     // capture
     bool capture = false;
@@ -137,16 +139,25 @@ int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
 
 constexpr int PROF_MAX = 16384;
 
+// Profiling: while a window is open, every launch inside a prof_scope of family `fam` goes through
+// hipExtLaunchKernelGGL with its own start / stop event pair, which the runtime timestamps at the
+// kernel's own start and end (no extra packets between the launches of the step).
 struct prof_scope {
-    z2h_ctx * c; int idx = -1;
-    prof_scope(z2h_ctx * ctx, int fam) : c(ctx) {
-        if (!c->prof || c->ev_used >= PROF_MAX) return;
-        idx = c->ev_used++;
-        c->ev_fam[idx] = fam;
-        (void) hipEventRecord(c->ev[2 * idx], c->stream);
-    }
-    ~prof_scope() { if (idx >= 0) (void) hipEventRecord(c->ev[2 * idx + 1], c->stream); }
+    z2h_ctx * c; int keep;
+    prof_scope(z2h_ctx * ctx, int fam) : c(ctx), keep(ctx->prof_fam) { c->prof_fam = fam; }
+    ~prof_scope() { c->prof_fam = keep; }
 };
+// the event pair for the next launch, or nulls outside a window
+inline void prof_pair(z2h_ctx * c, hipEvent_t & e0, hipEvent_t & e1) {
+    e0 = e1 = nullptr;
+    if (!c->prof || c->prof_fam < 0 || c->ev_used >= PROF_MAX) return;
+    const int idx = c->ev_used++;
+    c->ev_fam[idx] = c->prof_fam;
+    e0 = c->ev[2 * idx]; e1 = c->ev[2 * idx + 1];
+}
+#define KL(K_, G_, B_, L_, S_, ...) do { hipEvent_t e0_, e1_; prof_pair(ctx, e0_, e1_); \
+    if (e0_) hipExtLaunchKernelGGL(K_, G_, B_, L_, S_, e0_, e1_, 0, __VA_ARGS__); \
+    else hipLaunchKernelGGL(K_, G_, B_, L_, S_, __VA_ARGS__); } while (0)
 
 #define HIPX(expr) do { hipError_t e_ = (expr); if (e_ != hipSuccess) \
     return seterr(ctx, Z2H_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); } while (0)
@@ -479,7 +490,7 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
             // K split over the 4 waves of a block, one 16-row group per block
             const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, a.grouped ? MT_G : MT);
             dim3 grid(m0.tiles, a.grouped ? a.E : grid_y, a.grouped ? passes : (dual ? 1 : a.n_mats)), block(256);
-#define SPL(W_, D_, R_) hipLaunchKernelGGL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
+#define SPL(W_, D_, R_) KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
 #define SPL_R(W_, D_) do { if (a.grouped) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
             if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
             else { if (dual) SPL_R(WF_Q8_0, true); else SPL_R(WF_Q8_0, false); }
@@ -489,7 +500,7 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
             return Z2H_OK;
         }
         dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
-#define MM16(W_, D_, R_) hipLaunchKernelGGL((k_gemv_mfma<W_, D_, R_, R_ == MT_G ? m16fmt<W_>::GPF : 1>), grid, block, lds, ctx->stream, a)
+#define MM16(W_, D_, R_) KL((k_gemv_mfma<W_, D_, R_, R_ == MT_G ? m16fmt<W_>::GPF : 1>), grid, block, lds, ctx->stream, a)
         if (m0.type == Z2H_Q4_K) {
             if (a.grouped) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
@@ -506,10 +517,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         const size_t lds = gemv_rows_lds_bytes(af, m0.nsb * 256);
         dim3 grid((m0.tiles + 3) / 4, grid_y, m1 ? 2 : 1), block(256);
         switch (m0.type) {
-            case Z2H_Q4_K: hipLaunchKernelGGL(k_gemv_rows<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
-            case Z2H_Q6_K: hipLaunchKernelGGL(k_gemv_rows<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
-            case Z2H_Q8_0: hipLaunchKernelGGL(k_gemv_rows<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
-            case Z2H_F16:  hipLaunchKernelGGL(k_gemv_rows<WF_F16>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_Q4_K: KL(k_gemv_rows<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_Q6_K: KL(k_gemv_rows<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_Q8_0: KL(k_gemv_rows<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
+            case Z2H_F16:  KL(k_gemv_rows<WF_F16>, grid, block, lds, ctx->stream, a); break;
             default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
         }
         HIPX(hipGetLastError());
@@ -518,10 +529,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     const size_t lds = gemv_lds_bytes(af, m0.nsb * 256);
     dim3 grid(m0.tiles, grid_y, m1 ? 2 : 1), block(256);
     switch (m0.type) {
-        case Z2H_Q4_K: hipLaunchKernelGGL(k_gemv<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
-        case Z2H_Q6_K: hipLaunchKernelGGL(k_gemv<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
-        case Z2H_Q8_0: hipLaunchKernelGGL(k_gemv<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
-        case Z2H_F16:  hipLaunchKernelGGL(k_gemv<WF_F16>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_Q4_K: KL(k_gemv<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_Q6_K: KL(k_gemv<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_Q8_0: KL(k_gemv<WF_Q8_0>, grid, block, lds, ctx->stream, a); break;
+        case Z2H_F16:  KL(k_gemv<WF_F16>, grid, block, lds, ctx->stream, a); break;
         default: return seterr(ctx, Z2H_ENOTSUP, "gemv type");
     }
     HIPX(hipGetLastError());
@@ -537,7 +548,7 @@ int launch_encode(z2h_ctx * ctx, const float * x, int ld, int K, int n_rows, int
     prof_scope ps(ctx, Z2H_KF_SWIGLU);
     EncodeArgs e{x, ld, K, n_rows, act_fmt, act};
     const int items = n_rows * (kpad(K) / 256);
-    hipLaunchKernelGGL(k_encode_rows, dim3((items + 3) / 4), dim3(256), 0, ctx->stream, e);
+    KL(k_encode_rows, dim3((items + 3) / 4), dim3(256), 0, ctx->stream, e);
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -546,7 +557,7 @@ int launch_swiglu(z2h_ctx * ctx, int n_rows, int act_fmt) {
     prof_scope ps(ctx, Z2H_KF_SWIGLU);
     SwigluArgs w{};
     w.g = ctx->gu_g; w.u = ctx->gu_u; w.ff = ctx->hp.n_ff; w.act = ctx->act_y; w.act_fmt = act_fmt;
-    hipLaunchKernelGGL(k_swiglu_encode, dim3(n_rows), dim3(256), (size_t) kpad(ctx->hp.n_ff) * 4, ctx->stream, w);
+    KL(k_swiglu_encode, dim3(n_rows), dim3(256), (size_t) kpad(ctx->hp.n_ff) * 4, ctx->stream, w);
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -562,7 +573,7 @@ int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
     prof_scope ps(ctx, Z2H_KF_RESNORM);
     if (!a.d) a.d = ctx->hp.n_embd;
     a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
-    hipLaunchKernelGGL(k_resnorm, dim3(T), dim3(256), (size_t) kpad(a.d) * 4, ctx->stream, a);
+    KL(k_resnorm, dim3(T), dim3(256), (size_t) kpad(a.d) * 4, ctx->stream, a);
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -587,8 +598,8 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         // elements per lane: the next power of two >= ceil(d / 64); unguarded when d fills every lane
         const int ni = hp.n_embd <= 64 ? 1 : 1 << (32 - __builtin_clz((unsigned) ((hp.n_embd + 63) / 64 - 1)));
         const bool exact = hp.n_embd == 64 * ni;
-#define RDN(N_) do { if (exact) hipLaunchKernelGGL((k_router_down<N_, false>), grid, dim3(256), 0, ctx->stream, r); \
-                     else hipLaunchKernelGGL((k_router_down<N_, true>), grid, dim3(256), 0, ctx->stream, r); } while (0)
+#define RDN(N_) do { if (exact) KL((k_router_down<N_, false>), grid, dim3(256), 0, ctx->stream, r); \
+                     else KL((k_router_down<N_, true>), grid, dim3(256), 0, ctx->stream, r); } while (0)
         switch (ni) {
             case 1: RDN(1); break;
             case 2: RDN(2); break;
@@ -603,7 +614,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     }
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
-        hipLaunchKernelGGL(k_router_tail, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        KL(k_router_tail, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
@@ -732,7 +743,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         {
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
             const int nc_max = (ctx->S + ATT_CH - 1) / ATT_CH;
-            hipLaunchKernelGGL(k_attn_combine, dim3(nkv, T), dim3(256), (size_t) ((nh / nkv) * hd + 4 * nc_max) * 4, ctx->stream, a);
+            KL(k_attn_combine, dim3(nkv, T), dim3(256), (size_t) ((nh / nkv) * hd + 4 * nc_max) * 4, ctx->stream, a);
             HIPX(hipGetLastError());
         }
         if (!in_block) {
@@ -785,7 +796,7 @@ int allow_lds(const void * fn, z2h_ctx * ctx) {
 // one wave per (token, 64-row chunk, KV head) item, instantiated per head size and group size
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
     const int grp = a.nh / a.nkv;
-#define ATT(H_, G_) hipLaunchKernelGGL((k_attn_decode<H_, G_>), dim3(grid), dim3(64), 0, ctx->stream, a)
+#define ATT(H_, G_) KL((k_attn_decode<H_, G_>), dim3(grid), dim3(64), 0, ctx->stream, a)
 #define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
     switch (a.hd) {
         case 16: ATT_G(16) break;
@@ -1084,7 +1095,7 @@ int z2h_kv_write(z2h_ctx * ctx, int layer, int slot, int row0, int n, const uint
         const uint16_t * src = which ? v : k;
         if (!src) continue;
         HIPX(hipMemcpyAsync(ctx->kv_stage, src, (size_t) n * nkv * hd * 2, hipMemcpyHostToDevice, ctx->stream));
-        hipLaunchKernelGGL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
+        KL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
                            ctx->kv + (size_t) (2 * layer + which) * lsz, n, nkv, hd, ctx->S, row0, slot, 0);
         HIPX(hipGetLastError());
         HIPX(hipStreamSynchronize(ctx->stream));      // the staging buffer is reused by the next copy
@@ -1105,7 +1116,7 @@ int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n, uint16_t * 
     for (int which = 0; which < 2; ++which) {
         uint16_t * dst = which ? v : k;
         if (!dst) continue;
-        hipLaunchKernelGGL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
+        KL(k_kv_move, dim3(grid), dim3(256), 0, ctx->stream, ctx->kv_stage,
                            ctx->kv + (size_t) (2 * layer + which) * lsz, n, nkv, hd, ctx->S, row0, slot, 1);
         HIPX(hipGetLastError());
         HIPX(hipMemcpyAsync(dst, ctx->kv_stage, (size_t) n * nkv * hd * 2, hipMemcpyDeviceToHost, ctx->stream));
@@ -1182,11 +1193,11 @@ static int speaker_row(z2h_ctx * ctx, const float * spk, const float * delta, fl
     if (delta) HIPX(hipMemcpyAsync(dl, delta, (size_t) d * 4, hipMemcpyHostToDevice, ctx->stream));
     if ((rc = launch_encode(ctx, x, sd, sd, 1, act_of(m->spk_lda.type), ctx->act))) return rc;
     if ((rc = launch_gemv(ctx, m->spk_lda, nullptr, gemv_dense(ctx, 1, sl, ld, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
-    hipLaunchKernelGGL(k_bias_add, dim3((ld + 255) / 256), dim3(256), 0, ctx->stream, sl, (const float *) m->spk_lda_b, (const float *) nullptr, ld);
+    KL(k_bias_add, dim3((ld + 255) / 256), dim3(256), 0, ctx->stream, sl, (const float *) m->spk_lda_b, (const float *) nullptr, ld);
     HIPX(hipGetLastError());
     if ((rc = launch_encode(ctx, sl, ld, ld, 1, act_of(m->spk_proj.type), ctx->act))) return rc;
     if ((rc = launch_gemv(ctx, m->spk_proj, nullptr, gemv_dense(ctx, 1, sp, d, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
-    hipLaunchKernelGGL(k_bias_add, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, sp, (const float *) m->spk_proj_b, (const float *) (delta ? dl : nullptr), d);
+    KL(k_bias_add, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, sp, (const float *) m->spk_proj_b, (const float *) (delta ? dl : nullptr), d);
     HIPX(hipGetLastError());
     HIPX(hipMemcpyAsync(out, sp, (size_t) d * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
