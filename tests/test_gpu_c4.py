@@ -1,0 +1,64 @@
+"""The 64-request configuration (KV lengths log-uniform in [16, 4096], Zipf(1.2) expert popularity as
+a pre-softmax router-logit bias mirrored in the oracle) with Q6_K and Q8_0 weights, on a 4-layer cut
+of the 24-layer model (same layer shapes): every layer teacher-forced against the oracle, the router
+bit-exact, and the end-to-end logits."""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+from helpers import assert_close, cos, fill_kv
+from zonos2_amd import configs, synth
+from zonos2_amd.z2h import Context
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+
+@pytest.mark.parametrize("bulk", [configs.Q6_K, configs.Q8_0], ids=["q6_k", "q8_0"])
+def test_c4_layers_teacher_forced(bulk):
+    cfg, wl = configs.C4(bulk)
+    cfg = dataclasses.replace(cfg, n_layer=4, expert_used=[cfg.top_k] * 4)
+    model = synth.generate_model(cfg, 7)
+    bias = {L: configs.zipf_bias(cfg.n_expert, wl.zipf, L) for L in range(cfg.n_layer)}
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    for L, b in bias.items():
+        ctx.set_logit_bias(L, b)
+    om = O.OracleModel(cfg.hparams(), model, logit_bias=bias)
+    okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    fill_kv(cfg, wl, [ctx.kv_write, okv.write])
+    T, d, E, k = len(wl.kv_lens), cfg.n_embd, cfg.n_expert, cfg.top_k
+    inp = synth.step_inputs(cfg, wl)
+    ctx.set_capture(True)
+    got = ctx.step(inp.slot_idx, inp.n_past, ids=inp.ids)
+    rd = lambda L, n: ctx.read_capture(L, n, T)
+    prev = None
+    for L in range(cfg.n_layer):
+        res_in = rd(L, "res_in").reshape(T, d)
+        attn_in = rd(L, "attn_in").reshape(T, d)
+        ffn_in = rd(L, "ffn_in").reshape(T, d)
+        attn_out = rd(L, "attn_out").reshape(T, d)
+        ffn_out = rd(L, "ffn_out").reshape(T, d)
+        ao = np.empty((T, cfg.n_head * cfg.head_dim), np.float32)
+        oo = np.empty((T, d), np.float32)
+        O.check(O.lib().orc_attention(om.m, okv.kv, L, T, O.ptr(inp.slot_idx), O.ptr(inp.n_past), O.ptr(attn_in),
+                                      O.ptr(ao), O.ptr(oo)))
+        assert_close(f"L{L} attn_out", attn_out, oo)
+        r = O.router(om, L, ffn_in, prev)
+        sel = rd(L, "sel").reshape(T, k)
+        assert np.array_equal(sel, r["sel"]), f"L{L} top-k ids"
+        assert np.array_equal(rd(L, "probs").reshape(T, E).view(np.uint32), r["probs"].view(np.uint32)), f"L{L} probs"
+        counts, offsets, perm = O.group(sel, E)
+        assert np.array_equal(rd(L, "counts"), counts) and np.array_equal(rd(L, "perm"), perm)
+        w = rd(L, "weights").reshape(T, k)
+        _, out = O.experts(om, L, ffn_in, sel, w)
+        assert_close(f"L{L} ffn_out", ffn_out, out)
+        if L + 1 < cfg.n_layer:
+            assert np.array_equal(rd(L + 1, "res_in").reshape(T, d), ffn_out + (attn_out + res_in)), f"L{L} residual fold"
+        prev = r["rh"]
+        print(f"L{L}: {len(set(sel.ravel().tolist()))} experts touched, max routes {counts.max()}")
+    want = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)
+    print(f"end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}")
+    assert cos(got, want) >= 0.9999
+    ctx.close()

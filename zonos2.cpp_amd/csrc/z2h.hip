@@ -711,7 +711,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     if (n_run && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, run[0], ctx->res, T))) return rc;
     (void) h_npast;
     // persistent attention grid: the item count comes from the device n_past table
-    const int attn_grid = std::min(ctx->items_max, 4096);
+    const int attn_grid = std::min(ctx->items_max, 2048);    // ~7 resident blocks per CU; more items loop
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int i = 0; i < n_run; ++i) {
@@ -796,7 +796,7 @@ int allow_lds(const void * fn, z2h_ctx * ctx) {
 // one wave per (token, 64-row chunk, KV head) item, instantiated per head size and group size
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
     const int grp = a.nh / a.nkv;
-#define ATT(H_, G_) KL((k_attn_decode<H_, G_>), dim3(grid), dim3(64), 0, ctx->stream, a)
+#define ATT(H_, G_) KL((k_attn_chunk<H_, G_>), dim3(grid), dim3(256), 0, ctx->stream, a)
 #define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
     switch (a.hd) {
         case 16: ATT_G(16) break;

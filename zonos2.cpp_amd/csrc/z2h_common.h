@@ -46,6 +46,32 @@ __device__ __forceinline__ float z_erff(float x) {
     return copysignf(y, x);
 }
 
+// sin and cos of a RoPE angle (0 <= x < 2^24): the angle is reduced modulo 2 pi in double
+// precision (the fp32 angle is exact in double; 2 pi in double is off by < 2.5e-16, so the reduced
+// angle is good to ~1e-13 for angles below 2^24), then by quadrant to [-pi/4, pi/4], where degree-9 /
+// degree-8 Taylor polynomials are accurate to < 4e-9. No library call, so no large-argument path.
+__device__ __forceinline__ void z_sincos(float x, float & s, float & c) {
+    const double xd = (double) x;
+    const double k2 = rint(xd * 0.15915494309189533577);                 // turns
+    const double rd = __builtin_fma(-k2, 6.28318530717958647692, xd);    // in [-pi, pi]
+    const double q = rint(rd * 0.63661977236758134308);                  // quadrant, |q| <= 2
+    const float r = (float) __builtin_fma(-q, 1.57079632679489661923, rd);
+    const float r2 = r * r;
+    float sp = 2.75573192e-6f;                                           // 1/9!
+    sp = __builtin_fmaf(sp, r2, -1.98412698e-4f);
+    sp = __builtin_fmaf(sp, r2, 8.33333333e-3f);
+    sp = __builtin_fmaf(sp, r2, -1.66666667e-1f);
+    const float sr = __builtin_fmaf(sp * r2, r, r);
+    float cp = 2.48015873e-5f;                                           // 1/8!
+    cp = __builtin_fmaf(cp, r2, -1.38888889e-3f);
+    cp = __builtin_fmaf(cp, r2, 4.16666667e-2f);
+    cp = __builtin_fmaf(cp, r2, -0.5f);
+    const float cr = __builtin_fmaf(cp, r2, 1.0f);
+    const int qi = ((int) q) & 3;
+    s = qi == 0 ? sr : qi == 1 ? cr : qi == 2 ? -sr : -cr;
+    c = qi == 0 ? cr : qi == 1 ? -sr : qi == 2 ? -cr : sr;
+}
+
 __device__ __forceinline__ float z_gelu(float x) { return (0.5f * x) * (1.0f + z_erff(x * 0.70710678118654752f)); }
 __device__ __forceinline__ float z_silu(float x) { return x / (1.0f + z_expf(-x)); }
 __device__ __forceinline__ float z_sigmoid(float x) { return 1.0f / (1.0f + z_expf(-x)); }

@@ -35,7 +35,7 @@ enum { ACT_NONE = -1, ACT_F16 = 1, ACT_Q8_0 = 8, ACT_Q8_K = 15 };
 
 constexpr int NT = 16;          // tokens (or routes) per GEMV pass
 constexpr int TILE = 64;        // rows per tile = lanes per wave
-constexpr int ATT_CH = 64;      // attention rows per chunk
+constexpr int ATT_CH = 32;      // attention rows per chunk (<= 64)
 constexpr int MAX_ROUTES = 1024; // top-k routes per step a grouped GEMV can list
 
 template <int WF> struct wfmt;
@@ -1174,158 +1174,224 @@ struct AttnArgs {
     ActBuf act; int act_fmt; // encoding of o_out for W_o
 };
 
-__device__ __forceinline__ int attn_n_items(const int32_t * n_past, int T, int nkv) {
-    int n = 0;
-    for (int t = 0; t < T; ++t) n += (n_past[t] + 1 + ATT_CH - 1) / ATT_CH;
-    return n * nkv;
-}
-
-// item i -> (token, chunk, kv head): tokens in order, chunks of ATT_CH rows, kv heads innermost
-__device__ __forceinline__ bool attn_item(const int32_t * n_past, int T, int nkv, int i, int & t, int & c, int & g) {
-    g = i % nkv;
-    int rem = i / nkv;
-    for (t = 0; t < T; ++t) {
-        const int nc = (n_past[t] + 1 + ATT_CH - 1) / ATT_CH;
-        if (rem < nc) { c = rem; return true; }
-        rem -= nc;
+// Wave-parallel item bookkeeping: lane u of each 64-token group loads n_past[u] (and slot_idx[u]) and
+// an inclusive scan of the per-token chunk counts locates an item, so the cost is one load per 64
+// tokens instead of a chain of dependent loads per token.
+__device__ __forceinline__ int wave_scan_incl(int v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(v, off, 64);
+        if (lane >= off) v += u;
     }
-    return false;
+    return v;
+}
+// item -> token t (with n_past np and slot), chunk c, kv head g; n_items = all items of the step
+__device__ __forceinline__ bool attn_locate(const int32_t * n_past, const int32_t * slot_idx, int T, int nkv, int item,
+                                            int & n_items, int & t, int & np, int & slot, int & c, int & g) {
+    const int lane = threadIdx.x & 63, want = item / nkv;
+    g = item % nkv;
+    int base = 0;
+    bool found = false;
+    for (int t0 = 0; t0 < T; t0 += 64) {
+        const int u = t0 + lane;
+        const int npu = u < T ? n_past[u] : 0, su = u < T ? slot_idx[u] : 0;
+        const int nc = u < T ? (npu + ATT_CH) / ATT_CH : 0;              // chunks of rows [0, n_past]
+        const int incl = wave_scan_incl(nc, lane), excl = incl - nc;
+        const uint64_t hit = __ballot(!found && want >= base + excl && want < base + incl);
+        if (hit) {
+            const int l = __ffsll((unsigned long long) hit) - 1;
+            t = t0 + l;
+            np = __shfl(npu, l, 64);
+            slot = __shfl(su, l, 64);
+            c = want - base - __shfl(excl, l, 64);
+            found = true;
+        }
+        base += __shfl(incl, 63, 64);
+    }
+    n_items = base * nkv;
+    return found;
+}
+// chunks before token t (exclusive prefix) and token t's own chunk count
+__device__ __forceinline__ void attn_chunks_of(const int32_t * n_past, int T, int t, int & before, int & nc_t) {
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    before = 0; nc_t = 0;
+    for (int t0 = 0; t0 < T && t0 <= t; t0 += 64) {
+        const int u = t0 + lane;
+        const int nc = u < T ? (n_past[u] + ATT_CH) / ATT_CH : 0;
+        const int incl = wave_scan_incl(nc, lane);
+        if (t < t0 + 64) {
+            before = base + __shfl(incl - nc, t - t0, 64);
+            nc_t = __shfl(nc, t - t0, 64);
+        }
+        base += __shfl(incl, 63, 64);
+    }
 }
 
-// Decode attention, one wave per item = (token, 64-row chunk of its band [0, n_past], KV head g). The
-// wave requests its chunk's K rows (lane = row) and V columns (lane = pair of head dims) first, then
-// forms the token's queries of group g from the fused projection output (per-head RMSNorm, |temp|,
-// interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, f16), and in the
-// chunk that holds the new row also k and v, which it appends to the f16 cache and uses directly.
-// Scores are f16 dot products with fp32 accumulation, then a per-chunk softmax partial (max, sum of
-// exp, unnormalised P.V) per head, merged by k_attn_combine.
+// Decode attention with a block of 4 waves per item = (token, ATT_CH-row chunk of its band [0, n_past],
+// KV head g). The block requests the chunk's K and V rows with coalesced 16-byte loads and, while
+// they are in flight, forms the group's queries from the fused projection output (per-head RMSNorm,
+// |temp|, interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, f16);
+// the chunk that holds the new row also forms k and v, appends them to the f16 cache and to the
+// LDS copy. Then every thread scores one (row, head) pair (f16 dot products, fp32 accumulation), one
+// wave per head reduces the chunk's softmax partial (max, sum of exp; lane = row), and every thread accumulates
+// one (head, dim pair) of the unnormalised P.V over the chunk's rows. k_attn_combine merges chunks.
 template <int HD, int GRP>
-__global__ void __launch_bounds__(64) k_attn_decode(AttnArgs a) {
-    constexpr int NP = HD / 2;                     // dim pairs (<= 64 lanes)
-    constexpr int KV4 = HD / 8;                    // uint4 per K row
-    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];      // f16 pairs
-    __shared__ __attribute__((aligned(16))) float s_p[ATT_CH][GRP];
-    __shared__ __attribute__((aligned(16))) uint32_t s_nk[NP], s_nv[NP];
-    const int lane = threadIdx.x, nkv = a.nkv;
-    const int n_items = attn_n_items(a.n_past, a.T, nkv);
+__global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
+    constexpr int NP = HD / 2;                     // dim pairs (<= 64)
+    constexpr int RW = HD / 8;                     // uint4 per K / V row
+    constexpr int KST = HD + 8;                    // LDS row stride of K (halfs): breaks bank aliasing
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];     // f16 pairs
+    __shared__ float s_p[ATT_CH][GRP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
+    int n_items, t, np, slot, c, g;
+    bool ok = attn_locate(a.n_past, a.slot_idx, a.T, nkv, blockIdx.x, n_items, t, np, slot, c, g);
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        int t, c, g;
-        if (!attn_item(a.n_past, a.T, nkv, item, t, c, g)) break;
-        const int np = a.n_past[t], L = np + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
+        if (item != (int) blockIdx.x) ok = attn_locate(a.n_past, a.slot_idx, a.T, nkv, item, n_items, t, np, slot, c, g);
+        if (!ok) break;
+        const int L = np + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
         const bool last = r0 + nr == L;                              // the chunk holds the new row
-        const int slot = a.slot_idx[t];
-        const uint16_t * kb = a.kc + (((int64_t) slot * nkv + g) * a.S + r0) * HD;
-        const uint16_t * vb = a.vc + (((int64_t) slot * nkv + g) * a.S + r0) * HD;
-        // ---- the chunk's K rows and V columns (rows past the chunk re-read its last row, weight 0)
-        uint4 kr[KV4];
-        const int rr = min(lane, nr - 1);
-#pragma unroll
-        for (int j = 0; j < KV4; ++j) kr[j] = *(const uint4 *) (kb + (int64_t) rr * HD + 8 * j);
-        const int pl = min(lane, NP - 1);
-        uint32_t vr[ATT_CH];
-#pragma unroll
-        for (int r = 0; r < ATT_CH; ++r) vr[r] = *(const uint32_t *) (vb + (int64_t) min(r, nr - 1) * HD + 2 * pl);
-        // ---- rotation of this lane's pair (pl) at position np
-        float th = (float) np;
-        for (int j = 0; j < pl; ++j) th = th * a.theta_scale;
-        const float cs = cosf(th), sn = sinf(th);
+        const int64_t band = (((int64_t) slot * nkv + g) * a.S + r0) * HD;
+        // ---- the projection values this wave normalises (its query heads; wave 3 also the new k and
+        // v), requested before the chunk so they arrive first
         const float * row = a.qkvg + (int64_t) t * a.R;
-        auto norm_rope = [&](const float * src, float mul, float & y0, float & y1) {
-            const float x0 = lane < NP ? src[2 * lane] : 0.0f, x1 = lane < NP ? src[2 * lane + 1] : 0.0f;
-            const double ss = wave_tree_d((double) (x0 * x0) + (double) (x1 * x1));
-            const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + a.qk_eps);
-            float z0 = x0 * sc, z1 = x1 * sc;
-            if (mul != 1.0f) { z0 = z0 * mul; z1 = z1 * mul; }
-            y0 = z0 * cs - z1 * sn;
-            y1 = z0 * sn + z1 * cs;
-        };
+        constexpr int HPW = (GRP + 3) / 4;                           // query heads per wave
+        float xq[HPW + 2][2];
 #pragma unroll
-        for (int h = 0; h < GRP; ++h) {
-            const int qh = g * GRP + h;
-            float y0, y1;
-            norm_rope(row + (int64_t) qh * HD, a.temp[qh], y0, y1);
-            if (lane < NP) {
-                s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
-                if (a.cap_q && c == 0) {
-                    a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
-                    a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
+        for (int j = 0; j < HPW; ++j) {
+            const int h = wave + 4 * j;
+            const float * src = row + (int64_t) (g * GRP + min(h, GRP - 1)) * HD;
+            xq[j][0] = lane < NP ? src[2 * lane] : 0.0f;
+            xq[j][1] = lane < NP ? src[2 * lane + 1] : 0.0f;
+        }
+        const bool mk = last && wave == 3;
+        {
+            const float * ksrc = row + (int64_t) (a.nh + g) * HD, * vsrc = row + (int64_t) (a.nh + nkv + g) * HD;
+            xq[HPW][0] = mk && lane < NP ? ksrc[2 * lane] : 0.0f;
+            xq[HPW][1] = mk && lane < NP ? ksrc[2 * lane + 1] : 0.0f;
+            xq[HPW + 1][0] = mk && lane < NP ? vsrc[2 * lane] : 0.0f;
+            xq[HPW + 1][1] = mk && lane < NP ? vsrc[2 * lane + 1] : 0.0f;
+        }
+        // ---- K and V rows of the chunk, requested now and written to LDS after the query
+        // arithmetic (rows past the chunk re-read its last row; the new row, still absent from the
+        // cache, is overwritten below)
+        constexpr int N4 = ATT_CH * RW;                              // uint4 per matrix
+        static_assert(N4 <= 512, "two 16-byte items per thread and matrix at most");
+        // (named registers: an array here is not promoted out of scratch)
+        uint4 k0, v0, k1 = {}, v1 = {};
+        auto kv_at = [&](int i, uint4 & kk, uint4 & vv) {           // threads past N4 repeat the last item
+            i = min(i, N4 - 1);
+            const int r = min(i / RW, nr - 1), q4 = i % RW;
+            kk = *(const uint4 *) (a.kc + band + (int64_t) r * HD + 8 * q4);
+            vv = *(const uint4 *) (a.vc + band + (int64_t) r * HD + 8 * q4);
+        };
+        kv_at(tid, k0, v0);
+        if constexpr (N4 > 256) kv_at(tid + 256, k1, v1);
+        // ---- queries of the group (one wave per head), and the new k / v row (wave 3)
+        uint32_t nk = 0, nv = 0;
+        {
+            const int pl = min(lane, NP - 1);
+            float th = (float) np;
+            for (int j = 0; j < pl; ++j) th = th * a.theta_scale;
+            float cs, sn;
+            z_sincos(th, sn, cs);
+            auto norm_rope = [&](float x0, float x1, float mul, float & y0, float & y1) {
+                const double ss = wave_tree_d((double) (x0 * x0) + (double) (x1 * x1));
+                const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + a.qk_eps);
+                float z0 = x0 * sc, z1 = x1 * sc;
+                if (mul != 1.0f) { z0 = z0 * mul; z1 = z1 * mul; }
+                y0 = z0 * cs - z1 * sn;
+                y1 = z0 * sn + z1 * cs;
+            };
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) {
+                const int h = wave + 4 * j;
+                if (h >= GRP) break;
+                const int qh = g * GRP + h;
+                float y0, y1;
+                norm_rope(xq[j][0], xq[j][1], a.temp[qh], y0, y1);
+                if (lane < NP) {
+                    s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                    if (a.cap_q && c == 0) {
+                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
+                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
+                    }
+                }
+            }
+            if (mk) {
+                float k0, k1;
+                norm_rope(xq[HPW][0], xq[HPW][1], 1.0f, k0, k1);
+                if (lane < NP) {
+                    const float v0 = xq[HPW + 1][0], v1 = xq[HPW + 1][1];
+                    nk = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
+                    nv = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
+                    *(uint32_t *) (a.kc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nk;
+                    *(uint32_t *) (a.vc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nv;
+                    if (a.cap_k) {
+                        a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane] = k0; a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = k1;
+                        a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane] = v0; a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = v1;
+                    }
                 }
             }
         }
-        if (last) {
-            float k0, k1;
-            norm_rope(row + (int64_t) (a.nh + g) * HD, 1.0f, k0, k1);
-            const float * vsrc = row + (int64_t) (a.nh + nkv + g) * HD;
-            if (lane < NP) {
-                const float v0 = vsrc[2 * lane], v1 = vsrc[2 * lane + 1];
-                const uint32_t kp = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
-                const uint32_t vp = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
-                s_nk[lane] = kp; s_nv[lane] = vp;
-                *(uint32_t *) (a.kc + (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane) = kp;
-                *(uint32_t *) (a.vc + (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane) = vp;
-                if (a.cap_k) {
-                    a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane] = k0; a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = k1;
-                    a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane] = v0; a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = v1;
-                }
+        if (tid < N4) {
+            *(uint4 *) &s_k[(tid / RW) * KST + 8 * (tid % RW)] = k0;
+            *(uint4 *) &s_v[(tid / RW) * HD + 8 * (tid % RW)] = v0;
+        }
+        if constexpr (N4 > 256) {
+            const int i = tid + 256;
+            if (i < N4) {
+                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = k1;
+                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = v1;
             }
+        }
+        __syncthreads();                                             // the chunk copy is in LDS
+        if (mk && lane < NP) {                                       // replace the stale new row
+            *(uint32_t *) &s_k[(nr - 1) * KST + 2 * lane] = nk;
+            *(uint32_t *) &s_v[(nr - 1) * HD + 2 * lane] = nv;
         }
         __syncthreads();
-        // ---- scores (lane = row r0 + lane)
-        const bool isnew = last && lane == nr - 1;
-        if (isnew) {
-#pragma unroll
-            for (int j = 0; j < KV4; ++j) kr[j] = *(const uint4 *) &s_nk[4 * j];
-        }
-        float pr[GRP];
-#pragma unroll
-        for (int h = 0; h < GRP; ++h) {
+        // ---- scores: one (row, head) per thread
+        for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
+            const int r = sidx / GRP, h = sidx % GRP;
             float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < KV4; ++j) {
-                const uint4 qv = *(const uint4 *) &s_q[h][4 * j];
-                acc = fdot2(kr[j].x, qv.x, acc); acc = fdot2(kr[j].y, qv.y, acc);
-                acc = fdot2(kr[j].z, qv.z, acc); acc = fdot2(kr[j].w, qv.w, acc);
+            for (int j = 0; j < RW; ++j) {
+                const uint4 kk = *(const uint4 *) &s_k[r * KST + 8 * j];
+                const uint4 qq = *(const uint4 *) &s_q[h][4 * j];
+                acc = fdot2(kk.x, qq.x, acc); acc = fdot2(kk.y, qq.y, acc);
+                acc = fdot2(kk.z, qq.z, acc); acc = fdot2(kk.w, qq.w, acc);
             }
-            const float s = lane < nr ? acc * a.scale : -__builtin_inff();
-            const float mx = wave_max_f(s);
-            const float pe = lane < nr ? z_expf(s - mx) : 0.0f;
+            s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
+        }
+        __syncthreads();
+        // ---- per-head chunk softmax partial (lane = row)
+        for (int h = wave; h < GRP; h += 4) {
+            const float sv = lane < ATT_CH ? s_p[min(lane, ATT_CH - 1)][h] : -__builtin_inff();
+            const float mx = wave_max_f(sv);
+            const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
             const float l = wave_tree_f(pe);
-            pr[h] = pe;
+            if (lane < ATT_CH) s_p[lane][h] = pe;
             if (lane == 0) {
                 a.part_ml[((int64_t) item * GRP + h) * 2 + 0] = mx;
                 a.part_ml[((int64_t) item * GRP + h) * 2 + 1] = l;
             }
         }
-#pragma unroll
-        for (int h = 0; h < GRP; ++h) s_p[lane][h] = pr[h];
         __syncthreads();
-        // ---- P.V (lane = pair of head dims); rows past the chunk carry p = 0
-        float o0[GRP], o1[GRP];
-#pragma unroll
-        for (int h = 0; h < GRP; ++h) { o0[h] = 0.0f; o1[h] = 0.0f; }
-        const uint32_t nv = s_nv[pl];
-#pragma unroll
-        for (int r = 0; r < ATT_CH; ++r) {
-            const uint32_t vv = (last && r == nr - 1) ? nv : vr[r];
-            const float va = h2f(vv & 0xffffu), vc = h2f(vv >> 16);
-            float pp[GRP];
-            if constexpr (GRP % 4 == 0) {
-#pragma unroll
-                for (int h4 = 0; h4 < GRP; h4 += 4) {
-                    const float4 p4 = *(const float4 *) &s_p[r][h4];
-                    pp[h4] = p4.x; pp[h4 + 1] = p4.y; pp[h4 + 2] = p4.z; pp[h4 + 3] = p4.w;
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < GRP; ++h) pp[h] = s_p[r][h];
+        // ---- P.V: one (head, dim pair) per thread, rows in order
+        for (int o = tid; o < GRP * NP; o += 256) {
+            const int h = o / NP, dp = o % NP;
+            float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 16
+            for (int r = 0; r < ATT_CH; ++r) {
+                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * dp];
+                const float pp = s_p[r][h];
+                o0 = __builtin_fmaf(pp, h2f(vv & 0xffffu), o0);
+                o1 = __builtin_fmaf(pp, h2f(vv >> 16), o1);
             }
-#pragma unroll
-            for (int h = 0; h < GRP; ++h) { o0[h] = __builtin_fmaf(pp[h], va, o0[h]); o1[h] = __builtin_fmaf(pp[h], vc, o1[h]); }
-        }
-        if (lane < NP) {
-#pragma unroll
-            for (int h = 0; h < GRP; ++h)
-                *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * lane) = make_float2(o0[h], o1[h]);
+            *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
         }
         __syncthreads();                                             // LDS reuse by the next item
     }
@@ -1339,9 +1405,8 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
     extern __shared__ float sm_ac[];
     const int g = blockIdx.x, t = blockIdx.y, hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int item0 = 0;
-    for (int u = 0; u < t; ++u) item0 += (a.n_past[u] + 1 + ATT_CH - 1) / ATT_CH;
-    const int nc = (a.n_past[t] + 1 + ATT_CH - 1) / ATT_CH;
+    int item0, nc;
+    attn_chunks_of(a.n_past, a.T, t, item0, nc);
     float * ob = sm_ac;                                              // [grp*hd]
     float * sw = ob + grp * hd;                                      // [4][nc] chunk weights per wave
     const float * __restrict__ ml = a.part_ml;
