@@ -113,11 +113,8 @@ def main() -> int:
             k, v = synth.kv_rows(cfg, L, s, n, 7)
             ctx.kv_write(L, s, 0, k, v)
             kv_cache[(L, s)] = (k, v)
-    bias = None
-    if wl.zipf:
-        bias = {L: configs.zipf_bias(cfg.n_expert, wl.zipf, L) for L in range(cfg.n_layer)}
-        for L, b in bias.items():
-            ctx.set_logit_bias(L, b)
+    # load-balanced routing (+ Zipf popularity for the 64-request configuration), calibrated on the device
+    bias = synth.router_biases(ctx, cfg, wl)
     log(f"uploaded + KV filled in {time.time() - t0:.1f}s; weights {ctx.device_bytes(0) / 1e9:.2f} GB, "
         f"KV {ctx.device_bytes(1) / 1e9:.2f} GB")
     inp = synth.step_inputs(cfg, wl)

@@ -467,13 +467,17 @@ struct orc_model {
     bool finalized = false;
 };
 
-struct orc_kv {
-    const orc_model * m = nullptr;
+struct orc_kv {                                   // shapes copied: any model of the same shape may use it
+    int n_layer = 0, nkv = 0, hd = 0;
     int n_slots = 0, S = 0;
     std::vector<std::vector<uint16_t>> k, v;      // per layer [slot][row][nkv][hd]
 };
 
 namespace {
+
+bool kv_fits(const orc_model & m, const orc_kv & kv) {
+    return kv.n_layer == (int) m.hp.n_layer && kv.nkv == (int) m.hp.n_head_kv && kv.hd == (int) m.hp.head_dim;
+}
 
 std::vector<float> to_f32(const tensor & t) {
     const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
@@ -771,7 +775,7 @@ void orc_model_free(orc_model * m) { delete m; }
 orc_kv * orc_kv_create(const orc_model * m, int n_slots, int slot_cap_frames) {
     if (!m || n_slots <= 0 || slot_cap_frames <= 0) { g_err = "bad kv args"; return nullptr; }
     auto * kv = new orc_kv();
-    kv->m = m; kv->n_slots = n_slots;
+    kv->n_layer = m->hp.n_layer; kv->nkv = m->hp.n_head_kv; kv->hd = m->hp.head_dim; kv->n_slots = n_slots;
     kv->S = ((slot_cap_frames + 255) / 256) * 256;            // graph.cpp:610, 644
     const int64_t per = (int64_t) n_slots * kv->S * m->hp.n_head_kv * m->hp.head_dim;
     kv->k.assign(m->hp.n_layer, std::vector<uint16_t>((size_t) per, 0));
@@ -782,9 +786,9 @@ orc_kv * orc_kv_create(const orc_model * m, int n_slots, int slot_cap_frames) {
 int orc_kv_slot_cap(const orc_kv * kv) { return kv ? kv->S : 0; }
 
 int orc_kv_write(orc_kv * kv, int L, int slot, int row0, int n, const uint16_t * k, const uint16_t * v) {
-    if (!kv || L < 0 || L >= kv->m->hp.n_layer || slot < 0 || slot >= kv->n_slots || row0 < 0 || n < 0 || row0 + n > kv->S)
+    if (!kv || L < 0 || L >= kv->n_layer || slot < 0 || slot >= kv->n_slots || row0 < 0 || n < 0 || row0 + n > kv->S)
         return fail("kv_write out of range");
-    const int64_t w = (int64_t) kv->m->hp.n_head_kv * kv->m->hp.head_dim;
+    const int64_t w = (int64_t) kv->nkv * kv->hd;
     const int64_t off = ((int64_t) slot * kv->S + row0) * w;
     if (k) std::memcpy(kv->k[L].data() + off, k, (size_t) n * w * 2);
     if (v) std::memcpy(kv->v[L].data() + off, v, (size_t) n * w * 2);
@@ -792,9 +796,9 @@ int orc_kv_write(orc_kv * kv, int L, int slot, int row0, int n, const uint16_t *
 }
 
 int orc_kv_read(const orc_kv * kv, int L, int slot, int row0, int n, uint16_t * k, uint16_t * v) {
-    if (!kv || L < 0 || L >= kv->m->hp.n_layer || slot < 0 || slot >= kv->n_slots || row0 < 0 || n < 0 || row0 + n > kv->S)
+    if (!kv || L < 0 || L >= kv->n_layer || slot < 0 || slot >= kv->n_slots || row0 < 0 || n < 0 || row0 + n > kv->S)
         return fail("kv_read out of range");
-    const int64_t w = (int64_t) kv->m->hp.n_head_kv * kv->m->hp.head_dim;
+    const int64_t w = (int64_t) kv->nkv * kv->hd;
     const int64_t off = ((int64_t) slot * kv->S + row0) * w;
     if (k) std::memcpy(k, kv->k[L].data() + off, (size_t) n * w * 2);
     if (v) std::memcpy(v, kv->v[L].data() + off, (size_t) n * w * 2);
@@ -806,6 +810,7 @@ void orc_kv_free(orc_kv * kv) { delete kv; }
 int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
              const int32_t * ids, const float * emb, float * logits, orc_capture * cap) {
     if (!m || !m->finalized || !kv) return fail("model/kv not ready");
+    if (!kv_fits(*m, *kv)) return fail("kv cache shape differs from the model");
     if (T <= 0 || !slot_idx || !n_past || (!ids && !emb) || !logits) return fail("bad step args");
     const auto & hp = m->hp;
     const int d = hp.n_embd, W = hp.n_codebooks + 1, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
@@ -894,6 +899,7 @@ int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const 
 int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n0,
                 const float * spk, int spk_pos, const float * delta, float * last_logits) {
     if (!m || !m->finalized || !kv) return fail("model/kv not ready");
+    if (!kv_fits(*m, *kv)) return fail("kv cache shape differs from the model");
     if (slot < 0 || slot >= kv->n_slots) return fail("slot out of range");
     if (n0 <= 0 || n0 > kv->S) return fail("n0 exceeds slot_cap");
     const auto & hp = m->hp;
@@ -1048,6 +1054,7 @@ int orc_dense_ffn(orc_model * m, int L, int T, const float * ffn_in, float * out
 int orc_attention(orc_model * m, orc_kv * kv, int L, int T, const int32_t * slot_idx, const int32_t * n_past,
                   const float * attn_in, float * attn_o, float * attn_out) {
     if (int rc = check_layer(m, L)) return rc;
+    if (!kv || !kv_fits(*m, *kv)) return fail("kv cache shape differs from the model");
     attention_fwd(*m, *kv, L, T, slot_idx, n_past, attn_in, nullptr, nullptr, nullptr, nullptr, attn_o, attn_out);
     return 0;
 }

@@ -22,8 +22,11 @@ def c3():
     model = synth.generate_model(cfg, 42)
     ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
     ctx.upload(model)
-    om, okv = oracle_pair(cfg, model, wl)
+    om0, okv = oracle_pair(cfg, model, wl)
     fill_kv(cfg, wl, [ctx.kv_write, okv.write])
+    bias = synth.router_biases(ctx, cfg, wl)         # load-balanced routing, also given to the oracle
+    om = O.OracleModel(cfg.hparams(), model, logit_bias=bias)
+    okv.model = om
     return cfg, wl, model, ctx, om, okv
 
 

@@ -1,6 +1,6 @@
 """The 64-request configuration (KV lengths log-uniform in [16, 4096], Zipf(1.2) expert popularity as
 a pre-softmax router-logit bias mirrored in the oracle) with Q6_K and Q8_0 weights, on a 4-layer cut
-of the 24-layer model (same layer shapes): every layer teacher-forced against the oracle, the router
+of the 24-layer model (same layer shapes; router logits load-balanced on a calibration batch): every layer teacher-forced against the oracle, the router
 bit-exact, and the end-to-end logits."""
 import dataclasses
 
@@ -20,14 +20,14 @@ def test_c4_layers_teacher_forced(bulk):
     cfg, wl = configs.C4(bulk)
     cfg = dataclasses.replace(cfg, n_layer=4, expert_used=[cfg.top_k] * 4)
     model = synth.generate_model(cfg, 7)
-    bias = {L: configs.zipf_bias(cfg.n_expert, wl.zipf, L) for L in range(cfg.n_layer)}
     ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
     ctx.upload(model)
-    for L, b in bias.items():
-        ctx.set_logit_bias(L, b)
-    om = O.OracleModel(cfg.hparams(), model, logit_bias=bias)
-    okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    om0 = O.OracleModel(cfg.hparams(), model)
+    okv = O.OracleKV(om0, wl.n_slots, wl.slot_cap)
     fill_kv(cfg, wl, [ctx.kv_write, okv.write])
+    bias = synth.router_biases(ctx, cfg, wl)         # balanced + Zipf, also given to the oracle
+    om = O.OracleModel(cfg.hparams(), model, logit_bias=bias)
+    okv.model = om
     T, d, E, k = len(wl.kv_lens), cfg.n_embd, cfg.n_expert, cfg.top_k
     inp = synth.step_inputs(cfg, wl)
     ctx.set_capture(True)

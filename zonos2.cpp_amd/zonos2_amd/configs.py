@@ -9,8 +9,10 @@ routers are kept F32 because the decode step's router is specified as fp32.
 
 Init: matrices N(0, 0.02); norm weights 1; attn_temp |N(0,1)| (the checkpoint stores |temp|,
 models/convert-zonos2-to-gguf.py:207); other 1-D biases N(0, 0.02). router_bias is N(0, router_bias_std)
-with std 0 by default: with N(0, 0.02) routers the softmax spread across experts is ~1e-4, so any
-larger selection bias would pin every token to the same few experts.
+with std 0 by default. The 24-layer configurations use a wider router MLP init (see zonos2_24l) and
+a load-balancing pre-softmax logit bias calibrated on the device (synth.router_biases), so routing
+spreads over the experts as a trained router's does; the 64-request configuration adds Zipf(1.2)
+log-popularity on top.
 """
 from __future__ import annotations
 
@@ -52,6 +54,8 @@ class ModelConfig:
     logit_softcap: float = 15.0
     expert_used: list[int] | None = None     # per layer; default all MoE with top_k
     router_bias_std: float = 0.0
+    router_mlp_std: float = 0.02               # router MLP matrices mlp0 / mlp2 N(0, std)
+    router_out_std: float = 0.02               # router output matrix mlp4 N(0, std)
 
     def __post_init__(self):
         if self.expert_used is None:
@@ -82,6 +86,7 @@ class ModelConfig:
         """[(name, type, ne, init)] with init = (kind, a, b): 0 normal(a,b), 1 b*|N(0,1)|, 2 const a."""
         d, hd, nh, nkv, ff, rd = self.n_embd, self.head_dim, self.n_head, self.n_head_kv, self.n_ff, self.router_dim
         W, hi = (0, 0.0, 0.02), self.high_tier()
+        RW = (0, 0.0, self.router_mlp_std)
         out: list = []
         for i in range(self.n_codebooks):
             out.append((f"audio_embd.{i}.weight", hi, (d, self.audio_vocab), W))
@@ -120,11 +125,11 @@ class ModelConfig:
                 (b + "ffn_down_exps.weight", bt, (ff, d, E), W),
                 (b + "router_down.weight", F32, (d, rd), W),
                 (b + "router_down.bias", F32, (rd,), W),
-                (b + "router_mlp0.weight", F32, (rd, rd), W),
+                (b + "router_mlp0.weight", F32, (rd, rd), RW),
                 (b + "router_mlp0.bias", F32, (rd,), W),
-                (b + "router_mlp2.weight", F32, (rd, rd), W),
+                (b + "router_mlp2.weight", F32, (rd, rd), RW),
                 (b + "router_mlp2.bias", F32, (rd,), W),
-                (b + "router_mlp4.weight", F32, (rd, E), W),
+                (b + "router_mlp4.weight", F32, (rd, E), (0, 0.0, self.router_out_std)),
                 (b + "router_norm.weight", F32, (rd,), (2, 1.0, 0.0)),
                 (b + "router_bias", F32, (E,), (0, 0.0, self.router_bias_std) if self.router_bias_std > 0 else (2, 0.0, 0.0)),
             ]
@@ -161,9 +166,12 @@ def C2() -> tuple[ModelConfig, Workload]:
 
 
 def zonos2_24l(bulk: int) -> ModelConfig:
+    # router MLP: hidden matrices N(0, 1/sqrt(router_dim)) keep unit-variance pre-activations through
+    # the erf-GELU layers, and the output matrix N(0, 0.3) gives per-token logit spreads of about 1,
+    # as in a trained router (with N(0, 0.02) throughout they vary by ~1e-3 between tokens)
     return ModelConfig(f"zonos2-24l-{TYPE_NAMES[bulk].lower()}", n_layer=24, n_embd=2048, n_head=16,
                        n_head_kv=4, head_dim=128, n_expert=32, top_k=4, n_ff=1536, bulk=bulk,
-                       spk_dim=2048, spk_lda_dim=1024)
+                       spk_dim=2048, spk_lda_dim=1024, router_mlp_std=128 ** -0.5, router_out_std=0.3)
 
 
 def _rng(seed):
@@ -174,14 +182,16 @@ def _rng(seed):
 def C3() -> tuple[ModelConfig, Workload]:
     rng = _rng(3)
     lens = [int(x) for x in rng.integers(32, 2049, size=16)]
-    return zonos2_24l(Q4_K), Workload("c3-16req-ragged", n_slots=16, kv_lens=lens, slot_cap=2049)
+    return zonos2_24l(Q4_K), Workload("c3-16req-ragged", n_slots=16, kv_lens=lens, slot_cap=2049,
+                                      extra={"balance": True})
 
 
 def C4(bulk: int) -> tuple[ModelConfig, Workload]:
     import numpy as np
     rng = _rng(4)
     lens = [int(x) for x in np.exp(rng.uniform(np.log(16), np.log(4096), size=64))]
-    return zonos2_24l(bulk), Workload("c4-64req-zipf", n_slots=64, kv_lens=lens, slot_cap=4097, zipf=1.2)
+    return zonos2_24l(bulk), Workload("c4-64req-zipf", n_slots=64, kv_lens=lens, slot_cap=4097, zipf=1.2,
+                                      extra={"balance": True})
 
 
 def zipf_bias(n_expert: int, s: float, layer: int, seed: int = 99):

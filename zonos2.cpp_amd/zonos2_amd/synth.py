@@ -97,3 +97,40 @@ def step_inputs(cfg: ModelConfig, wl: Workload) -> StepInputs:
     ids[:, cfg.n_codebooks] = rng.integers(0, cfg.text_vocab + 1, size=T)
     emb = gen_normal_f32((T, cfg.n_embd), wl.seed, "inputs.emb") if wl.inject_embeddings else None
     return StepInputs(np.arange(T, dtype=np.int32), np.array(wl.kv_lens, dtype=np.int32), ids, emb)
+
+
+def router_biases(ctx, cfg: ModelConfig, wl: Workload) -> dict | None:
+    """Pre-softmax router-logit biases of a workload, set on the device context and returned (so the
+    oracle can be given the same ones).
+
+    A random-init router gives every token nearly the same mean logit per expert, so a few experts
+    win every selection. A trained router is load-balanced, which we emulate by subtracting each
+    expert's mean logit over a calibration batch (different ids, same positions) run on the device
+    without biases. Workloads with a Zipf(s) popularity add log-popularity on top. Layers without
+    MoE get none. Only the 24-layer configurations ask for balancing (wl.extra["balance"])."""
+    if not wl.extra.get("balance") and not wl.zipf:
+        return None
+    T = len(wl.kv_lens)
+    E = cfg.n_expert
+    moe = [L for L in range(cfg.n_layer) if cfg.expert_used[L] > 0]
+    bias = {L: np.zeros(E, np.float32) for L in moe}
+    if wl.extra.get("balance"):
+        inp = step_inputs(cfg, wl)
+        rng = np.random.default_rng(wl.seed + 17)
+        ids = inp.ids.copy()
+        ids[:, :cfg.n_codebooks] = rng.integers(0, cfg.audio_vocab, size=(T, cfg.n_codebooks))
+        for L in moe:
+            ctx.set_logit_bias(L, None)
+        ctx.set_capture(True)
+        ctx.step(inp.slot_idx, inp.n_past, ids=ids)
+        for L in moe:
+            lg = ctx.read_capture(L, "router_logits", T).reshape(T, E)
+            bias[L] = (-lg.astype(np.float64).mean(0)).astype(np.float32)
+        ctx.set_capture(False)
+    if wl.zipf:
+        from .configs import zipf_bias
+        for L in moe:
+            bias[L] = (bias[L] + zipf_bias(E, wl.zipf, L)).astype(np.float32)
+    for L in moe:
+        ctx.set_logit_bias(L, bias[L])
+    return bias
