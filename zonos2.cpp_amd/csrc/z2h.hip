@@ -732,8 +732,13 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         a.o_out = ctx->attn_o;
         a.act = ctx->act;
         const int wo_act = act_of(ly.wo.type);
-        const int span = (nh / nkv) * hd;                  // elements one combine block owns
-        const bool in_block = span % 256 == 0;             // whole encoding blocks, no padding
+        // heads per combine block: the fewest (1, 2, 4 or 8, dividing the group) whose outputs cover
+        // whole encoding blocks, so the block encodes its slice for W_o; else a separate encode pass
+        int hpb = 0;
+        for (int h = 1; h <= 8 && !hpb; h *= 2)
+            if ((nh / nkv) % h == 0 && (h * hd) % 256 == 0) hpb = h;
+        const bool in_block = hpb != 0;
+        if (!hpb) hpb = 1;
         a.act_fmt = in_block ? wo_act : ACT_NONE;
         {
             // QK-norm / RoPE / KV append fused in; item count from the device n_past table
@@ -743,7 +748,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         {
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
             const int nc_max = (ctx->S + ATT_CH - 1) / ATT_CH;
-            KL(k_attn_combine, dim3(nkv, T), dim3(256), (size_t) ((nh / nkv) * hd + 4 * nc_max) * 4, ctx->stream, a);
+            KL(k_attn_combine, dim3(nh / hpb, T), dim3(512), attn_combine_lds(hpb, hd, nc_max), ctx->stream, a, hpb, nc_max);
             HIPX(hipGetLastError());
         }
         if (!in_block) {

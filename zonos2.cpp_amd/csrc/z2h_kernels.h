@@ -1397,74 +1397,108 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     }
 }
 
-// Merge the chunks of the query-head group of one KV head for one token, apply the per-head sigmoid
-// gate. grid (nkv, T), one wave per head of the group. The group's grp*hd outputs are contiguous in
-// the token's row; when they cover whole encoding blocks the block encodes them for W_o here,
-// otherwise a separate encode pass follows (a.act_fmt == ACT_NONE).
-__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
+// Merge the chunks of HPB query heads of one token and apply the per-head sigmoid gate. grid
+// (nh / HPB, T), 8 waves: WPH = 8 / HPB waves per head. Every wave of a head forms the chunk weights
+// exp(m_c - M) and the denominator sum_c w_c l_c over all of the token's chunks (lane = chunk); the
+// head's first wave keeps the weights in LDS. Wave `part` of a head then sums w_c o_c over chunks
+// c = part, part + WPH, ... (lane = dim pair) with 16 partial loads in flight per batch, and the
+// WPH partial sums are added in wave order. When the block's HPB * hd outputs cover whole encoding
+// blocks the block encodes them for W_o here, otherwise a separate encode pass follows
+// (a.act_fmt == ACT_NONE).
+constexpr int AM_B = 16;          // partial loads in flight per wave
+__global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int ncs) {
     extern __shared__ float sm_ac[];
-    const int g = blockIdx.x, t = blockIdx.y, hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv;
+    const int hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv, t = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wph = 8 / hpb, hl = wave / wph, part = wave % wph;
+    const int h0 = blockIdx.x * hpb, h = h0 + hl, g = h / grp, hh = h % grp;
+    float * ob = sm_ac;                                              // [hpb * hd]
+    float * pw = ob + hpb * hd;                                      // [8][hd] per-wave sums
+    float * sw = pw + 8 * hd;                                        // [hpb][ncs] chunk weights
+    float * sden = sw + hpb * ncs;                                   // [hpb]
     int item0, nc;
     attn_chunks_of(a.n_past, a.T, t, item0, nc);
-    float * ob = sm_ac;                                              // [grp*hd]
-    float * sw = ob + grp * hd;                                      // [4][nc] chunk weights per wave
-    const float * __restrict__ ml = a.part_ml;
-    const float * __restrict__ po = a.part_o;
-    for (int hh = wave; hh < grp; hh += 4) {
-        float * w = sw + wave * nc;
-        float m = -__builtin_inff();
-        for (int c = lane; c < nc; c += 64) m = fmaxf(m, ml[((int64_t) ((item0 + c) * nkv + g) * grp + hh) * 2]);
-        const float M = wave_max_f(m);
-        float den = 0.0f;
-        for (int c = lane; c < nc; c += 64) {
-            const int64_t it = (int64_t) (item0 + c) * nkv + g;
-            const float e = z_expf(ml[(it * grp + hh) * 2] - M);
-            w[c] = e;
-            den = __builtin_fmaf(e, ml[(it * grp + hh) * 2 + 1], den);
-        }
-        den = wave_tree_f(den);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd + g * grp + hh]);
-        if (a.cap_gate && lane == 0) a.cap_gate[(int64_t) t * nh + g * grp + hh] = gsig;
-        const float gt = gsig / den;
-        for (int pi = lane; pi < hd / 2; pi += 64) {
-            float o0 = 0.0f, o1 = 0.0f;
-            int c = 0;
-            for (; c + 4 <= nc; c += 4) {
-                float2 v[4]; float ww[4];
+    const float2 * __restrict__ ml2 = (const float2 *) a.part_ml;
+    const float2 * __restrict__ po2 = (const float2 *) a.part_o;
+    // partial (chunk c, this head) index: ((item0 + c) * nkv + g) * grp + hh
+    const int64_t pbase = ((int64_t) item0 * nkv + g) * grp + hh, pstep = (int64_t) nkv * grp;
+    float2 mr[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v[j] = *(const float2 *) (po + ((((int64_t) (item0 + c + j) * nkv + g) * grp + hh) * hd) + 2 * pi);
-                    ww[j] = w[c + j];
-                }
+    for (int j = 0; j < 4; ++j) {
+        const int c = lane + 64 * j;
+        mr[j] = c < nc ? ml2[pbase + c * pstep] : make_float2(-__builtin_inff(), 0.0f);
+    }
+    float m = fmaxf(fmaxf(mr[0].x, mr[1].x), fmaxf(mr[2].x, mr[3].x));
+    for (int c = lane + 256; c < nc; c += 64) m = fmaxf(m, ml2[pbase + c * pstep].x);
+    const float M = wave_max_f(m);
+    float den = 0.0f;
+    float * w = sw + hl * ncs;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) { o0 = __builtin_fmaf(ww[j], v[j].x, o0); o1 = __builtin_fmaf(ww[j], v[j].y, o1); }
-            }
-            for (; c < nc; ++c) {
-                const float2 v = *(const float2 *) (po + ((((int64_t) (item0 + c) * nkv + g) * grp + hh) * hd) + 2 * pi);
-                o0 = __builtin_fmaf(w[c], v.x, o0); o1 = __builtin_fmaf(w[c], v.y, o1);
-            }
-            ob[hh * hd + 2 * pi] = o0 * gt;
-            ob[hh * hd + 2 * pi + 1] = o1 * gt;
+    for (int j = 0; j < 4; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nc) {
+            const float e = z_expf(mr[j].x - M);
+            den = __builtin_fmaf(e, mr[j].y, den);
+            if (part == 0) w[c] = e;
         }
     }
+    for (int c = lane + 256; c < nc; c += 64) {
+        const float2 v = ml2[pbase + c * pstep];
+        const float e = z_expf(v.x - M);
+        den = __builtin_fmaf(e, v.y, den);
+        if (part == 0) w[c] = e;
+    }
+    den = wave_tree_f(den);
+    if (part == 0 && lane == 0) sden[hl] = den;
     __syncthreads();
-    const int base = g * grp * hd;
-    for (int i = tid; i < grp * hd; i += 256) a.o_out[(int64_t) t * nh * hd + base + i] = ob[i];
-    if (a.act_fmt == ACT_NONE) return;
-    // the group's slice [base, base + grp*hd) of the token row, encoded in place of the row's blocks
+    const int np2 = hd / 2;
+    for (int pi = lane; pi < np2; pi += 64) {
+        float o0 = 0.0f, o1 = 0.0f;
+        for (int c0 = part; c0 < nc; c0 += AM_B * wph) {
+            float2 v[AM_B];
+#pragma unroll
+            for (int j = 0; j < AM_B; ++j) {
+                const int c = min(c0 + j * wph, nc - 1);
+                v[j] = po2[(pbase + c * pstep) * np2 + pi];
+            }
+#pragma unroll
+            for (int j = 0; j < AM_B; ++j) {
+                const int c = c0 + j * wph;
+                const float ww = c < nc ? w[c] : 0.0f;
+                o0 = __builtin_fmaf(ww, v[j].x, o0);
+                o1 = __builtin_fmaf(ww, v[j].y, o1);
+            }
+        }
+        pw[wave * hd + 2 * pi] = o0;
+        pw[wave * hd + 2 * pi + 1] = o1;
+    }
+    __syncthreads();
+    const float * gate = a.qkvg + (int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd;
+    for (int i = tid; i < hpb * hd; i += 512) {
+        const int l = i / hd, dim = i - l * hd;
+        float s = 0.0f;
+        for (int p = 0; p < wph; ++p) s += pw[(l * wph + p) * hd + dim];
+        const float gsig = z_sigmoid(gate[h0 + l]);
+        if (a.cap_gate && dim == 0) a.cap_gate[(int64_t) t * nh + h0 + l] = gsig;
+        ob[i] = s * (gsig / sden[l]);
+    }
+    __syncthreads();
+    const int base = h0 * hd, span = hpb * hd;
+    for (int i = tid; i < span; i += 512) a.o_out[(int64_t) t * nh * hd + base + i] = ob[i];
+    if (a.act_fmt == ACT_NONE || tid >= 256) return;
+    // the block's slice [base, base + span) of the token row, encoded in place of the row's blocks
     const int Kp = kpad(nh * hd);
     if (a.act_fmt == ACT_Q8_K)
-        encode_row<ACT_Q8_K>(ob, grp * hd, a.act.q + (int64_t) t * Kp + base, nullptr,
+        encode_row<ACT_Q8_K>(ob, span, a.act.q + (int64_t) t * Kp + base, nullptr,
                              a.act.d256 + (int64_t) t * (Kp / 256) + base / 256, a.act.bs + (int64_t) t * (Kp / 16) + base / 16, nullptr);
     else if (a.act_fmt == ACT_Q8_0)
-        encode_row<ACT_Q8_0>(ob, grp * hd, a.act.q + (int64_t) t * Kp + base, a.act.d32 + (int64_t) t * (Kp / 32) + base / 32,
+        encode_row<ACT_Q8_0>(ob, span, a.act.q + (int64_t) t * Kp + base, a.act.d32 + (int64_t) t * (Kp / 32) + base / 32,
                              nullptr, nullptr, nullptr);
     else
-        encode_row<ACT_F16>(ob, grp * hd, nullptr, nullptr, nullptr, nullptr, a.act.h + (int64_t) t * Kp + base);
+        encode_row<ACT_F16>(ob, span, nullptr, nullptr, nullptr, nullptr, a.act.h + (int64_t) t * Kp + base);
+}
+__host__ __device__ inline size_t attn_combine_lds(int hpb, int hd, int ncs) {
+    return (size_t) 4 * (hpb * hd + 8 * hd + hpb * ncs + 8);
 }
 
 // ------------------------------------------------------------------ router (exact contract)
@@ -1521,10 +1555,9 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
 // chains over contiguous eighths of the row (partial p sums i = p*rd/8 ... (p+1)*rd/8 - 1 ascending)
 // combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group; the block's 32 groups take
 // outputs g, g+32, g+64, g+96. Each lane's weights (rows padded to rd + 4 floats) go straight from
-// global memory to registers as float4s: W0 and W2 at entry, W4 during layer 1, so the weight traffic
-// overlaps the norm and the earlier layers. The
-// norm and softmax sums are wave trees; top-k ranks each expert against all others (score
-// descending, ties to the lower index).
+// global memory to registers as float4s, all three matrices at entry, so the weight traffic overlaps
+// the state load and the norm. The norm and softmax sums are wave trees; top-k ranks each expert
+// against all others (score descending, ties to the lower index).
 __host__ __device__ inline int pad4(int n) { return (n + 3) & ~3; }
 __host__ __device__ inline size_t router_tail_lds(int rd, int E) {
     return (size_t) 4 * (2 * rd + (E <= 64 ? 64 : pad4(E)) + 64);
@@ -1543,11 +1576,18 @@ __device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, flo
     }
 }
 
-// y[o] = post(dot(W[o], x)) for the lane group's outputs (n_out <= 128); MODE 0: gelu(dot + b[o]);
-// MODE 1: dot (+ logit bias[o]) (+ mask[o])
+// bias entries of the lane group's outputs g + 32u (u < 4; rows beyond n_out clamp)
+__device__ __forceinline__ void rt_bias(const float * b, int n_out, float (&bv)[4]) {
+    const int g = threadIdx.x >> 3;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bv[u] = b ? b[min(g + 32 * u, n_out - 1)] : 0.0f;
+}
+
+// y[o] = post(dot(W[o], x)) for the lane group's outputs (n_out <= 128); MODE 0: gelu(dot + b1[u]);
+// MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
 template <int MODE, int NM>
 __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const float * x, int n_out, float * y,
-                                         const float * bias, const float * bias2) {
+                                         const float (&b1)[4], const float (&b2)[4], bool has1, bool has2) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
     float4 xr[NM / 4];
 #pragma unroll
@@ -1562,44 +1602,33 @@ __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const fl
             acc[u] = __builtin_fmaf(wv[u][m].z, xr[m].z, acc[u]);
             acc[u] = __builtin_fmaf(wv[u][m].w, xr[m].w, acc[u]);
         }
+    // lane p = 0 of the group ends with ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), the xor
+    // butterfly's (4, 2, 1) sum, from DPP row shifts (lane i reads lane i + n of its 16-lane row)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        acc[u] = acc[u] + __shfl_xor(acc[u], 4, 8);
-        acc[u] = acc[u] + __shfl_xor(acc[u], 2, 8);
-        acc[u] = acc[u] + __shfl_xor(acc[u], 1, 8);
+        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 4>(acc[u]);
+        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 2>(acc[u]);
+        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 1>(acc[u]);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int o = g + 32 * u;
         if (o >= n_out) break;
-        float v = acc[u];                          // every lane of the group holds the sum
-        if (MODE == 0) v = z_gelu(v + bias[o]);
+        float v = acc[u];                          // the group's sum (valid in lane p = 0)
+        if (MODE == 0) v = z_gelu(v + b1[u]);
         else {
-            if (bias) v = v + bias[o];
-            if (bias2) v = v + bias2[o];
+            if (has1) v = v + b1[u];
+            if (has2) v = v + b2[u];
         }
         if (p == 0) y[o] = v;
     }
 }
 
-// the router MLP for router_dim = 8 * NM (<= 128 outputs per layer)
+// One token's router tail for router_dim = 8 * NM (<= 128 outputs per layer). Every global load of
+// the block is issued at entry, the state row first: the norm waits only for it, and the three MLP
+// matrices, the biases and the mask arrive while it runs.
 template <int NM>
-__device__ __forceinline__ void rt_mlp(const RouterArgs & a, float * s_x, float * s_y, float * s_l) {
-    const int ldw = a.rd + 4;
-    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
-    rt_load<NM>(a.w0t, ldw, a.rd, w0);
-    rt_load<NM>(a.w2t, ldw, a.rd, w2);
-    __syncthreads();                               // s_x holds the normalised state
-    rt_load<NM>(a.w4t, ldw, a.E, w4);
-    rt_layer<0, NM>(w0, s_x, a.rd, s_y, a.b0, nullptr);
-    __syncthreads();
-    rt_layer<0, NM>(w2, s_y, a.rd, s_x, a.b2, nullptr);
-    __syncthreads();
-    rt_layer<1, NM>(w4, s_x, a.E, s_l, a.logit_bias, a.mask);
-}
-
-__global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float sm_rt[];
+__device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
     const int rd = a.rd, E = a.E;
     float * s_x = sm_rt;                        // [rd]
     float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
@@ -1611,6 +1640,20 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
         const int i = lane + 64 * j;
         rh[j] = i < rd ? a.rh[(int64_t) t * rd + i] : 0.0f;
         nw[j] = i < rd ? a.norm_w[i] : 0.0f;
+    }
+    const int ldw = rd + 4;
+    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
+    rt_load<NM>(a.w0t, ldw, rd, w0);
+    rt_load<NM>(a.w2t, ldw, rd, w2);
+    rt_load<NM>(a.w4t, ldw, E, w4);
+    float b0[4], b2[4], blg[4], bmk[4];
+    rt_bias(a.b0, rd, b0);
+    rt_bias(a.b2, rd, b2);
+    rt_bias(a.logit_bias, E, blg);
+    rt_bias(a.mask, E, bmk);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane + 64 * j;
         sb[j] = i < E ? a.sc_bias[i] : 0.0f;
         mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
     }
@@ -1627,11 +1670,12 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
             if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
         }
     }
-    switch (rd) {                                    // router_dim in {32, 64, 128} (host-checked)
-        case 32:  rt_mlp<4>(a, s_x, s_y, s_l); break;
-        case 64:  rt_mlp<8>(a, s_x, s_y, s_l); break;
-        default:  rt_mlp<16>(a, s_x, s_y, s_l); break;
-    }
+    __syncthreads();                               // s_x holds the normalised state
+    rt_layer<0, NM>(w0, s_x, rd, s_y, b0, b0, false, false);
+    __syncthreads();
+    rt_layer<0, NM>(w2, s_y, rd, s_x, b2, b2, false, false);
+    __syncthreads();
+    rt_layer<1, NM>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
     __syncthreads();
     if (wave != 0) return;
     // softmax (own exp, double tree sum) + selection scores
@@ -1708,6 +1752,17 @@ __global__ void __launch_bounds__(256) k_router_tail(RouterArgs a) {
             a.sel[(int64_t) t * a.k + rank] = e;
             a.wsel[(int64_t) t * a.k + rank] = pr[j];
         }
+    }
+}
+
+// one block per token; a single wave per SIMD suffices (16-ish blocks), so the three weight
+// matrices can all be register-resident
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_router_tail(RouterArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float sm_rt[];
+    switch (a.rd) {                                  // router_dim in {32, 64, 128} (host-checked)
+        case 32:  router_tail_body<4>(a, sm_rt); break;
+        case 64:  router_tail_body<8>(a, sm_rt); break;
+        default:  router_tail_body<16>(a, sm_rt); break;
     }
 }
 
