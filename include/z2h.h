@@ -146,6 +146,36 @@ int z2h_set_layer_skip(z2h_ctx * ctx, const uint8_t * skip);
  * reference input: a benchmark hook to impose a skewed expert popularity. */
 int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias);
 
+/* Frame sampling on the device, for callers that keep the logits in HBM. It follows the reference's
+ * per-codebook sampler (src/zonos2-sampler.cpp:16-77, called per slot by zonos2_slot_sample,
+ * src/zonos2-graph.cpp:843-870) with the random generator left on the host: column i, codebook cb
+ * applies the repetition penalty over hist, temperature, top-k (logit descending, ties to the lower
+ * id), softmax (float exp terms over a double sum), top-p, min-p and draws at u * kept mass along the
+ * candidates, where u[i][cb] is the canonical double in [0, 1) that the host sampler's
+ * std::uniform_real_distribution would take from its mt19937 (std::generate_canonical<double, 53>).
+ * The exp terms are exp(x) computed in double and rounded to float, so a draw can differ from the
+ * host sampler's (glibc expf) only where the two roundings differ by an ulp and u falls between the
+ * two cumulative sums.
+ *   d_logits  [n_active][n_codebooks][audio_vocab] on the device, NULL = the last z2h_step's logits
+ *   sp        [n_active] settings (greedy takes the first maximum of the raw logits)
+ *   hist      [n_active][n_codebooks][hist_cap] recent codes, oldest first (NULL: no penalty);
+ *             hist_len [n_active][n_codebooks] entries used; hist_cap <= Z2H_SAMPLE_HIST_MAX
+ *   u         [n_active][n_codebooks];  codes out [n_active][n_codebooks] (host memory)
+ * Synchronizes the context's stream. */
+#define Z2H_SAMPLE_HIST_MAX 256
+typedef struct z2h_sampling {
+    float   temperature;
+    int32_t top_k;            /* 0 or >= audio_vocab: every id is a candidate */
+    float   top_p;            /* 0 disables */
+    float   min_p;            /* 0 disables */
+    float   rep_penalty;
+    int32_t rep_codebooks;    /* codebooks cb < rep_codebooks get the penalty */
+    int32_t greedy;
+    int32_t reserved;
+} z2h_sampling;
+int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
+               const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes);
+
 /* Debug capture of per-layer intermediates of the following steps (off by default). */
 enum {
     Z2H_CAP_RES_IN = 0, Z2H_CAP_ATTN_IN, Z2H_CAP_Q, Z2H_CAP_K, Z2H_CAP_V, Z2H_CAP_GATE, Z2H_CAP_ATTN_O,

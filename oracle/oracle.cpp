@@ -1091,3 +1091,83 @@ uint16_t orc_f32_to_f16(float x) { return to_f16(x); }
 float orc_f16_to_f32(uint16_t h) { return from_f16(h); }
 
 } // extern "C"
+
+// ------------------------------------------------------------------ frame sampler
+// exp(x) in double: x = n ln2 + r (ln2 in two parts, Cody-Waite), exp(r) by the degree-13 Taylor
+// polynomial in Horner form with fma, times 2^n.
+double orc_exp_d(double x) {
+    if (x < -745.0) return 0.0;
+    const double n = std::rint(x * 0x1.71547652b82fep+0);
+    double r = std::fma(-n, 0x1.62e42fee00000p-1, x);
+    r = std::fma(-n, 0x1.a39ef35793c76p-33, r);
+    static const double c[14] = {0x1.6124613a86d09p-33, 0x1.1eed8eff8d898p-29, 0x1.ae64567f544e4p-26, 0x1.27e4fb7789f5cp-22,
+                                 0x1.71de3a556c734p-19, 0x1.a01a01a01a01ap-16, 0x1.a01a01a01a01ap-13, 0x1.6c16c16c16c17p-10,
+                                 0x1.1111111111111p-7, 0x1.5555555555555p-5, 0x1.5555555555555p-3, 0.5, 1.0, 1.0};
+    double p = c[0];
+    for (int i = 1; i < 14; ++i) p = std::fma(p, r, c[i]);
+    return std::ldexp(p, (int) n);
+}
+
+int orc_sample(const float * in, int vocab, float temperature, int top_k, float top_p, float min_p,
+               float rep_penalty, int rep_codebooks, int greedy, int cb, const int32_t * hist, int hist_len,
+               double u, int exp_mode) {
+    if (greedy) {
+        int best = 0;
+        for (int i = 1; i < vocab; ++i) if (in[i] > in[best]) best = i;
+        return best;
+    }
+    std::vector<float> lg(in, in + vocab);
+    if (rep_penalty != 1.0f && cb < rep_codebooks)
+        for (int i = 0; i < hist_len; ++i) {
+            const int t = hist[i];
+            if (t >= 0 && t < vocab) lg[t] = lg[t] > 0.0f ? lg[t] / rep_penalty : lg[t] * rep_penalty;
+        }
+    if (temperature > 0.0f)
+        for (float & v : lg) v /= temperature;
+    std::vector<int> cand(vocab);
+    for (int i = 0; i < vocab; ++i) cand[i] = i;
+    const int k = top_k > 0 && top_k < vocab ? top_k : vocab;
+    const auto by_logit = [&lg](int a, int b) { return lg[a] > lg[b]; };
+    if (k < vocab) {
+        std::partial_sort(cand.begin(), cand.begin() + k, cand.end(), by_logit);
+        cand.resize(k);
+    }
+    const size_t n = cand.size();
+    float mx = -1e30f;
+    for (const int i : cand) mx = std::max(mx, lg[i]);
+    std::vector<float> p(n);
+    double z = 0.0;
+    for (size_t j = 0; j < n; ++j) {
+        const float x = lg[cand[j]] - mx;
+        p[j] = exp_mode ? (float) orc_exp_d((double) x) : std::exp(x);
+        z += p[j];
+    }
+    for (float & v : p) v = (float) (v / z);
+    std::vector<int> rank(n);
+    for (size_t j = 0; j < n; ++j) rank[j] = (int) j;
+    std::sort(rank.begin(), rank.end(), [&p](int a, int b) { return p[a] > p[b]; });
+    std::vector<char> keep(n, 1);
+    if (top_p > 0.0f && top_p < 1.0f) {
+        double c = 0.0;
+        bool reached = false;
+        for (const int r : rank) {
+            if (reached) keep[r] = 0;
+            c += p[r];
+            if (c >= top_p) reached = true;
+        }
+    }
+    if (min_p > 0.0f) {
+        const float floor_p = min_p * p[rank[0]];
+        for (size_t j = 0; j < n; ++j) if (p[j] < floor_p) keep[j] = 0;
+    }
+    double mass = 0.0;
+    for (size_t j = 0; j < n; ++j) { if (!keep[j]) p[j] = 0.0f; mass += p[j]; }
+    if (mass <= 0.0) return cand[rank[0]];
+    const double r = u * (mass - 0.0) + 0.0;
+    double acc = 0.0;
+    for (size_t j = 0; j < n; ++j) {
+        acc += p[j];
+        if (acc >= r) return cand[j];
+    }
+    return cand[rank[0]];
+}

@@ -94,6 +94,13 @@ int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n
 int orc_router(orc_model * m, int layer, int T, const float * ffn_in, const float * state_in,
                float * rh, float * logits, float * probs, int32_t * sel, float * w);
 int orc_group(int T, int k, int E, const int32_t * sel, int32_t * counts, int32_t * offsets, int32_t * perm);
+// One frame code for one (column, codebook): the reference sampler's steps (src/zonos2-sampler.cpp:16-77)
+// with the uniform draw given as the canonical double u (r = u * kept mass). exp_mode 0: the terms are
+// std::exp(float) as in the reference; 1: exp in double (orc_exp_d) rounded to float.
+int orc_sample(const float * logits, int vocab, float temperature, int top_k, float top_p, float min_p,
+               float rep_penalty, int rep_codebooks, int greedy, int cb, const int32_t * hist, int hist_len,
+               double u, int exp_mode);
+double orc_exp_d(double x);
 int orc_experts(orc_model * m, int layer, int T, const float * ffn_in, const int32_t * sel,
                 const float * w, float * expert_out, float * out);
 int orc_dense_ffn(orc_model * m, int layer, int T, const float * ffn_in, float * out);

@@ -64,6 +64,8 @@ def lib() -> C.CDLL:
         "orc_silu": (f32, [f32]),
         "orc_rope": (i32, [vp, i32, i32, i32, f32]),
         "orc_f32_to_f16": (C.c_uint16, [f32]), "orc_f16_to_f32": (f32, [C.c_uint16]),
+        "orc_sample": (i32, [vp, i32, f32, i32, f32, f32, f32, i32, i32, i32, vp, i32, C.c_double, i32]),
+        "orc_exp_d": (C.c_double, [C.c_double]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -238,3 +240,17 @@ def prefill(model: OracleModel, kv: OracleKV, slot, ids, spk=None, spk_pos=0, de
     out = np.empty(hp["n_codebooks"] * hp["audio_vocab"], np.float32)
     check(lib().orc_prefill(model.m, kv.kv, slot, ptr(ids), ids.shape[0], ptr(spk), spk_pos, ptr(delta), ptr(out)))
     return out
+
+
+def sample(logits, sp: dict, cb: int, u: float, hist=None, exp_mode: int = 1) -> int:
+    """One frame code for one codebook (orc_sample); sp holds the z2h_sampling fields, hist the
+    codebook's recent codes (oldest first)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    h = np.ascontiguousarray(hist if hist is not None else [], np.int32)
+    return int(lib().orc_sample(ptr(lg), lg.size, sp["temperature"], sp["top_k"], sp["top_p"], sp["min_p"],
+                                sp["rep_penalty"], sp["rep_codebooks"], sp["greedy"], cb, ptr(h) if h.size else None,
+                                int(h.size), float(u), exp_mode))
+
+
+def exp_d(x: float) -> float:
+    return float(lib().orc_exp_d(float(x)))

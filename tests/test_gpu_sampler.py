@@ -1,0 +1,79 @@
+"""Device frame sampler (z2h_sample) against the oracle's restatement of the reference sampler.
+
+With the same logits, settings, histories and canonical draws u, the device codes equal orc_sample's
+with exp_mode 1 (exp in double rounded to float, the device's arithmetic) on every draw; against
+exp_mode 0 (std::exp on floats, the reference's arithmetic) they agree on all but a rare draw that
+falls between the two roundings' cumulative sums. Logits are distinct random values (no ties)."""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from zonos2_amd import configs, synth
+from zonos2_amd.z2h import Context
+
+pytestmark = pytest.mark.gpu
+
+SETTINGS = [
+    dict(temperature=1.15, top_k=106, top_p=0.0, min_p=0.18, rep_penalty=1.2, rep_codebooks=8, greedy=0),
+    dict(temperature=0.8, top_k=0, top_p=0.9, min_p=0.0, rep_penalty=1.0, rep_codebooks=8, greedy=0),
+    dict(temperature=1.0, top_k=20, top_p=0.7, min_p=0.05, rep_penalty=1.5, rep_codebooks=3, greedy=0),
+    dict(temperature=0.0, top_k=50, top_p=0.0, min_p=0.0, rep_penalty=1.3, rep_codebooks=9, greedy=0),
+    dict(temperature=1.0, top_k=0, top_p=0.0, min_p=0.0, rep_penalty=1.2, rep_codebooks=8, greedy=1),
+    dict(temperature=1.3, top_k=1025, top_p=0.95, min_p=0.02, rep_penalty=1.1, rep_codebooks=9, greedy=0),
+]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    cfg, wl = configs.C1()
+    c = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    c.upload(synth.generate_model(cfg, 42))
+    yield cfg, wl, c
+    c.close()
+
+
+def _oracle_codes(lg, sp, u, hist, hlen, exp_mode):
+    n, ncb = u.shape
+    return np.array([[O.sample(lg[i, cb], sp[i], cb, u[i, cb], hist[i, cb, :hlen[i, cb]], exp_mode)
+                      for cb in range(ncb)] for i in range(n)], np.int32)
+
+
+def test_device_sampler_matches_oracle(ctx):
+    import torch
+    cfg, wl, c = ctx
+    n, ncb, av = wl.n_slots, cfg.n_codebooks, cfg.audio_vocab
+    rng = np.random.default_rng(11)
+    agree0 = total = 0
+    for trial in range(24):
+        print(f"trial {trial}", flush=True)
+        lg = (rng.standard_normal((n, ncb, av)) * 2.5).astype(np.float32)
+        lg[..., 7] += 3.0
+        sp = [SETTINGS[(trial + i) % len(SETTINGS)] for i in range(n)]
+        hist = rng.integers(0, av, (n, ncb, 64)).astype(np.int32)
+        hist[..., ::5] = 7                                            # repeated codes: penalties stack
+        hlen = rng.integers(0, 65, (n, ncb)).astype(np.int32)
+        u = rng.random((n, ncb))
+        d = torch.from_numpy(lg).cuda()
+        torch.cuda.synchronize()
+        got = c.sample(sp, u, hist, hlen, d_logits=d.data_ptr())
+        want = _oracle_codes(lg, sp, u, hist, hlen, 1)
+        np.testing.assert_array_equal(got, want)
+        agree0 += int((got == _oracle_codes(lg, sp, u, hist, hlen, 0)).sum())
+        total += got.size
+    assert agree0 >= total - 2
+
+
+def test_device_sampler_on_step_logits(ctx):
+    cfg, wl, c = ctx
+    n = wl.n_slots
+    rng = np.random.default_rng(12)
+    emb = rng.standard_normal((n, cfg.n_embd)).astype(np.float32)
+    logits = c.step(np.arange(n), np.array(wl.kv_lens[:n]), emb=emb).reshape(n, cfg.n_codebooks, cfg.audio_vocab)
+    sp = [SETTINGS[0]] * n
+    u = rng.random((n, cfg.n_codebooks))
+    got = c.sample(sp, u)                                             # the last step's logits, no history
+    hist = np.zeros((n, cfg.n_codebooks, 1), np.int32)
+    hlen = np.zeros((n, cfg.n_codebooks), np.int32)
+    np.testing.assert_array_equal(got, _oracle_codes(logits, sp, u, hist, hlen, 1))
+    greedy = c.sample([SETTINGS[4]] * n, u)
+    np.testing.assert_array_equal(greedy, logits.argmax(axis=2))

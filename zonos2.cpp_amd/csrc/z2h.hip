@@ -112,6 +112,11 @@ struct z2h_ctx {
     int32_t * h_pin = nullptr;        // pinned staging for step inputs
     size_t h_pin_bytes = 0;
 
+    // frame sampler: per-column settings, histories, draws and codes (device + pinned staging)
+    SampleParams * d_sp = nullptr; int32_t * d_hist = nullptr, * d_hlen = nullptr, * d_codes = nullptr;
+    double * d_u = nullptr;
+    uint8_t * h_samp = nullptr;
+
     // HIP graphs of the whole step, one per (batch width, embedding-injection) pair
     bool use_graphs = true;
     std::map<std::pair<int, int>, hipGraphExec_t> graphs;
@@ -381,6 +386,11 @@ int fuse_qkvg(z2h_model * mdl, Layer & ly) {
     return upload_mat(mdl, type, K, rows, 1, cat.data(), ly.qkvg);
 }
 
+// pinned staging of one z2h_sample call: settings | histories | counts | draws | codes
+size_t samp_stage_bytes(int T, int ncb) {
+    return (size_t) T * sizeof(SampleParams) + (size_t) T * ncb * (Z2H_SAMPLE_HIST_MAX * 4 + 4 + 8 + 4) + 64;
+}
+
 int alloc_scratch(z2h_ctx * ctx) {
     const auto & hp = ctx->hp;
     const int T = ctx->n_slots, d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
@@ -424,6 +434,14 @@ int alloc_scratch(z2h_ctx * ctx) {
     (void) E;
     ctx->h_pin_bytes = (size_t) T * (2 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
+        return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
+    const int ncb = std::max(1, (int) hp.n_codebooks);
+    if ((rc = dalloc(ctx, &ctx->d_sp, (size_t) T * sizeof(SampleParams), b)) ||
+        (rc = dalloc(ctx, &ctx->d_hist, (size_t) T * ncb * Z2H_SAMPLE_HIST_MAX * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->d_hlen, (size_t) T * ncb * 4, b)) || (rc = dalloc(ctx, &ctx->d_u, (size_t) T * ncb * 8, b)) ||
+        (rc = dalloc(ctx, &ctx->d_codes, (size_t) T * ncb * 4, b)))
+        return rc;
+    if (hipHostMalloc((void **) &ctx->h_samp, samp_stage_bytes(T, ncb), hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     return Z2H_OK;
 }
@@ -1403,6 +1421,51 @@ int64_t z2h_device_bytes(const z2h_ctx * ctx, int what) {
 
 const char * z2h_last_error(const z2h_ctx * ctx) { return ctx ? ctx->err.c_str() : "null context"; }
 
+int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
+               const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes) {
+    static_assert(sizeof(z2h_sampling) == sizeof(SampleParams), "z2h_sampling layout");
+    if (!ctx || !sp || !u || !codes) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (n_active <= 0 || n_active > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
+    if (hist && (hist_cap < 0 || hist_cap > Z2H_SAMPLE_HIST_MAX || !hist_len))
+        return seterr(ctx, Z2H_EINVAL, "history capacity out of range (at most Z2H_SAMPLE_HIST_MAX)");
+    const int ncb = ctx->hp.n_codebooks, av = ctx->hp.audio_vocab;
+    int np2 = 1;
+    while (np2 < av) np2 <<= 1;
+    if (ncb <= 0 || av <= 0 || np2 > 4096) return seterr(ctx, Z2H_ENOTSUP, "audio vocabulary too large for the sampler");
+    const int hc = hist ? hist_cap : 0;
+    for (int i = 0; i < n_active * ncb; ++i)
+        if (hist && (hist_len[i] < 0 || hist_len[i] > hc)) return seterr(ctx, Z2H_EINVAL, "history length out of range");
+    HIPX(hipSetDevice(ctx->device));
+    // stage the inputs in pinned memory, then one copy each
+    uint8_t * h = ctx->h_samp;
+    SampleParams * hsp = (SampleParams *) h;
+    int32_t * hh = (int32_t *) (hsp + n_active);
+    int32_t * hl = hh + (size_t) n_active * ncb * std::max(hc, 1);
+    double * hu = (double *) (((uintptr_t) (hl + (size_t) n_active * ncb) + 7) & ~(uintptr_t) 7);
+    std::memcpy(hsp, sp, (size_t) n_active * sizeof(SampleParams));
+    if (hc) std::memcpy(hh, hist, (size_t) n_active * ncb * hc * 4);
+    if (hist) std::memcpy(hl, hist_len, (size_t) n_active * ncb * 4);
+    else std::memset(hl, 0, (size_t) n_active * ncb * 4);
+    std::memcpy(hu, u, (size_t) n_active * ncb * 8);
+    HIPX(hipMemcpyAsync(ctx->d_sp, hsp, (size_t) n_active * sizeof(SampleParams), hipMemcpyHostToDevice, ctx->stream));
+    if (hc) HIPX(hipMemcpyAsync(ctx->d_hist, hh, (size_t) n_active * ncb * hc * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPX(hipMemcpyAsync(ctx->d_hlen, hl, (size_t) n_active * ncb * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPX(hipMemcpyAsync(ctx->d_u, hu, (size_t) n_active * ncb * 8, hipMemcpyHostToDevice, ctx->stream));
+    SampleArgs a{};
+    a.logits = d_logits ? d_logits : ctx->logits;
+    a.ncb = ncb; a.av = av; a.np2 = np2;
+    a.sp = ctx->d_sp; a.hist = ctx->d_hist; a.hlen = ctx->d_hlen; a.hcap = std::max(hc, 1);
+    a.u = ctx->d_u; a.codes = ctx->d_codes;
+    KL(k_sample, dim3(ncb, n_active), dim3(256), sample_lds_bytes(av, np2), ctx->stream, a);
+    HIPX(hipGetLastError());
+    int32_t * hc_out = (int32_t *) (hu + (size_t) n_active * ncb);
+    HIPX(hipMemcpyAsync(hc_out, ctx->d_codes, (size_t) n_active * ncb * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipStreamSynchronize(ctx->stream));
+    std::memcpy(codes, hc_out, (size_t) n_active * ncb * 4);
+    return Z2H_OK;
+}
+
 void z2h_destroy(z2h_ctx * ctx) {
     if (!ctx) return;
     (void) hipSetDevice(ctx->device);
@@ -1411,6 +1474,7 @@ void z2h_destroy(z2h_ctx * ctx) {
     for (auto & e : ctx->ev) (void) hipEventDestroy(e);
     for (void * p : ctx->allocs) (void) hipFree(p);
     if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);
+    if (ctx->h_samp) (void) hipHostFree(ctx->h_samp);
     if (ctx->stream) (void) hipStreamDestroy(ctx->stream);
     z2h_model * mdl = ctx->m;
     delete ctx;

@@ -33,6 +33,33 @@ __device__ __forceinline__ float z_expf(float x) {
     return ldexpf(p, (int) n);
 }
 
+// exp in double for the sampler's softmax: x = n ln2 + r with ln2 split in two (Cody-Waite; n ln2_hi
+// is exact for |n| < 2^21), |r| <= ln2 / 2, exp(r) by its degree-13 Taylor polynomial (truncation
+// < 2^-58 relative) in Horner form with fma, scaled by 2^n. z_expf_cr rounds it to float: the
+// correctly rounded expf except where exp(x) lies within ~2 double ulps of a float rounding boundary.
+__device__ __forceinline__ double z_exp_d(double x) {
+    if (x < -745.0) return 0.0;
+    const double n = rint(x * 0x1.71547652b82fep+0);
+    double r = __builtin_fma(-n, 0x1.62e42fee00000p-1, x);
+    r = __builtin_fma(-n, 0x1.a39ef35793c76p-33, r);
+    double p = 0x1.6124613a86d09p-33;                                    // 1/13!
+    p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
+    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
+    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
+    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
+    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
+    p = __builtin_fma(p, r, 0x1.1111111111111p-7);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-5);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return ldexp(p, (int) n);
+}
+__device__ __forceinline__ float z_expf_cr(float x) { return (float) z_exp_d((double) x); }
+
 // erf: Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7).
 __device__ __forceinline__ float z_erff(float x) {
     const float ax = fabsf(x);

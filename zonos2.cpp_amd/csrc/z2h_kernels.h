@@ -1766,6 +1766,131 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
 }
 
+// ------------------------------------------------------------------ frame sampler
+// Per-column sampling settings (the layout of z2h_sampling).
+struct SampleParams { float temperature; int top_k; float top_p; float min_p; float rep_penalty; int rep_codebooks; int greedy; int pad; };
+struct SampleArgs {
+    const float * logits;             // [n][ncb][av]
+    int ncb, av, np2;                 // np2 = power of two >= av (sort width)
+    const SampleParams * sp;          // [n]
+    const int32_t * hist; const int32_t * hlen; int hcap;   // [n][ncb][hcap] codes, [n][ncb] counts
+    const double * u;                 // [n][ncb] canonical draws in [0, 1)
+    int32_t * codes;                  // [n][ncb]
+};
+__host__ __device__ inline size_t sample_lds_bytes(int av, int np2) { return (size_t) np2 * 8 + (size_t) av * 8 + av + 64; }
+
+// One block per (codebook, column), the steps of the reference's sampler (src/zonos2-sampler.cpp:16-77):
+// greedy = first maximum of the raw logits; otherwise the repetition penalty (each history occurrence
+// once, in order), temperature, candidates = the top_k ids by logit in descending order (or all ids in
+// id order), p = exp(l - max) over a double sum, top-p along the probability order, min-p against the
+// largest p, and the draw r = u * mass walked along the candidates. The ranking is a bitonic sort of
+// (logit descending, id ascending) over np2 entries in LDS; the order-dependent sums (normaliser, kept
+// mass, the walk) run in one thread in candidate order, as the reference's loops do.
+__global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char sm_s[];
+    float * s_key = (float *) sm_s;                              // [np2]
+    int * s_idx = (int *) (s_key + a.np2);                       // [np2]
+    float * s_lg = (float *) (s_idx + a.np2);                    // [av] penalised / tempered logits by id
+    float * s_p = s_lg + a.av;                                   // [av] probabilities by candidate
+    uint8_t * s_keep = (uint8_t *) (s_p + a.av);                 // [av]
+    __shared__ float s_bv[4]; __shared__ int s_bi[4];
+    const int cb = blockIdx.x, col = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int av = a.av, np2 = a.np2;
+    const SampleParams sp = a.sp[col];
+    const float * in = a.logits + ((size_t) col * a.ncb + cb) * av;
+    int32_t * out = a.codes + (size_t) col * a.ncb + cb;
+    if (sp.greedy) {                                             // first maximum
+        float bv = -__builtin_inff(); int bi = 0x7fffffff;
+        for (int j = tid; j < av; j += 256) { const float v = in[j]; if (bi == 0x7fffffff || v > bv) { bv = v; bi = j; } }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64); const int oi = __shfl_xor(bi, off, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < 4; ++w) if (s_bv[w] > bv || (s_bv[w] == bv && s_bi[w] < bi)) { bv = s_bv[w]; bi = s_bi[w]; }
+            *out = bi;
+        }
+        return;
+    }
+    for (int j = tid; j < av; j += 256) s_lg[j] = in[j];
+    __syncthreads();
+    if (tid == 0 && sp.rep_penalty != 1.0f && cb < sp.rep_codebooks) {
+        const int32_t * h = a.hist + ((size_t) col * a.ncb + cb) * a.hcap;
+        const int n = min(a.hlen[(size_t) col * a.ncb + cb], a.hcap);
+        for (int i = 0; i < n; ++i) {
+            const int t = h[i];
+            if (t >= 0 && t < av) s_lg[t] = s_lg[t] > 0.0f ? s_lg[t] / sp.rep_penalty : s_lg[t] * sp.rep_penalty;
+        }
+    }
+    __syncthreads();
+    for (int j = tid; j < np2; j += 256) {
+        float v = -__builtin_inff();
+        if (j < av) {
+            v = s_lg[j];
+            if (sp.temperature > 0.0f) { v = v / sp.temperature; s_lg[j] = v; }
+        }
+        s_key[j] = v; s_idx[j] = j;
+    }
+    __syncthreads();
+    // bitonic sort, descending by logit, ties to the lower id
+    for (int size = 2; size <= np2; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < np2 / 2; i += 256) {
+                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const float kl = s_key[lo], kh = s_key[hi];
+                const int il = s_idx[lo], ih = s_idx[hi];
+                const bool hi_first = kh > kl || (kh == kl && ih < il);
+                const bool desc = (lo & size) == 0;
+                if (desc ? hi_first : !hi_first) { s_key[lo] = kh; s_key[hi] = kl; s_idx[lo] = ih; s_idx[hi] = il; }
+            }
+            __syncthreads();
+        }
+    const bool topk = sp.top_k > 0 && sp.top_k < av;
+    const int n = topk ? sp.top_k : av;
+    // candidate j: id s_idx[j] (top-k) or j (all ids); probability-rank r: candidate r (top-k: the
+    // logit order is the probability order) or candidate s_idx[r]
+    auto cand = [&](int j) { return topk ? s_idx[j] : j; };
+    const float mx = s_key[0];
+    for (int j = tid; j < n; j += 256) { s_p[j] = z_expf_cr(s_lg[cand(j)] - mx); s_keep[j] = 1; }
+    __syncthreads();
+    __shared__ double s_z;
+    if (tid == 0) { double z = 0.0; for (int j = 0; j < n; ++j) z += (double) s_p[j]; s_z = z; }
+    __syncthreads();
+    const double z = s_z;
+    for (int j = tid; j < n; j += 256) s_p[j] = (float) ((double) s_p[j] / z);
+    __syncthreads();
+    if (tid != 0) return;
+    auto rank = [&](int r) { return topk ? r : s_idx[r]; };
+    if (sp.top_p > 0.0f && sp.top_p < 1.0f) {
+        double c = 0.0; bool reached = false;
+        for (int r = 0; r < n; ++r) {
+            const int j = rank(r);
+            if (reached) s_keep[j] = 0;
+            c += (double) s_p[j];
+            if (c >= (double) sp.top_p) reached = true;
+        }
+    }
+    const int j0 = rank(0);
+    if (sp.min_p > 0.0f) {
+        const float floor_p = sp.min_p * s_p[j0];
+        for (int j = 0; j < n; ++j) if (s_p[j] < floor_p) s_keep[j] = 0;
+    }
+    double mass = 0.0;
+    for (int j = 0; j < n; ++j) mass += s_keep[j] ? (double) s_p[j] : 0.0;
+    int code = cand(j0);
+    if (mass > 0.0) {
+        const double r = a.u[(size_t) col * a.ncb + cb] * (mass - 0.0) + 0.0;
+        double acc = 0.0;
+        for (int j = 0; j < n; ++j) {
+            acc += s_keep[j] ? (double) s_p[j] : 0.0;
+            if (acc >= r) { code = cand(j); break; }
+        }
+    }
+    *out = code;
+}
+
 // KV rows between the host layout [n][nkv][hd] (staged in device memory) and the cache layout
 // [slot][kvh][S][hd]: dir 0 writes the cache, dir 1 reads it into the staging buffer.
 __global__ void __launch_bounds__(256) k_kv_move(uint4 * stage, uint16_t * cache, int n, int nkv, int hd, int S,

@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
         "z2h_set_graphs": (i32, [vp, i32]),
         "z2h_profile_begin": (i32, [vp]),
         "z2h_profile_end": (i32, [vp, vp, vp]),
+        "z2h_sample": (i32, [vp, i32, vp, vp, vp, vp, i32, vp, vp]),
         "z2h_last_error": (C.c_char_p, [vp]),
         "z2h_destroy": (None, [vp]),
     }
@@ -75,14 +76,20 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
-           "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_last_error",
-           "z2h_destroy")
+           "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample",
+           "z2h_last_error", "z2h_destroy")
 KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
                    "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
 
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Sampling(C.Structure):
+    """z2h_sampling (include/z2h.h)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("rep_penalty", C.c_float), ("rep_codebooks", C.c_int32), ("greedy", C.c_int32), ("reserved", C.c_int32)]
 
 
 class Z2HError(RuntimeError):
@@ -248,6 +255,24 @@ class Context:
     def moe_forward_device(self, layer, T, d_x, d_state, d_out, stream=None):
         self.check(lib().z2h_moe_forward_device(self.ctx, layer, T, C.c_void_p(d_x), C.c_void_p(d_state) if d_state else None,
                                                 C.c_void_p(d_out), C.c_void_p(stream) if stream else None))
+
+    def sample(self, sp, u, hist=None, hist_len=None, d_logits=None):
+        """Device frame sampling: sp = list of dicts (one per column) with z2h_sampling fields, u
+        [n][ncb] canonical draws, hist [n][ncb][cap] / hist_len [n][ncb] (or None); d_logits a device
+        pointer (int) or None for the last step's logits. Returns codes [n][ncb]."""
+        n = len(sp)
+        arr = (Sampling * n)(*[Sampling(**d) for d in sp])
+        u = np.ascontiguousarray(u, np.float64)
+        ncb = self.hp["n_codebooks"]
+        codes = np.empty((n, ncb), np.int32)
+        cap = 0
+        if hist is not None:
+            hist = np.ascontiguousarray(hist, np.int32)
+            hist_len = np.ascontiguousarray(hist_len, np.int32)
+            cap = hist.shape[-1]
+        self.check(lib().z2h_sample(self.ctx, n, C.c_void_p(d_logits) if d_logits else None, C.cast(arr, C.c_void_p),
+                                    _p(hist), _p(hist_len), cap, _p(u), _p(codes)))
+        return codes
 
     def device_bytes(self, what: int) -> int:
         return int(lib().z2h_device_bytes(self.ctx, what))
