@@ -109,7 +109,8 @@ int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n_rows, uint16
  * row the new K/V are written at (the row count already in the cache), ids is [n_active][n_codebooks+1]
  * (audio codes then the text id), or NULL when emb ([n_active][n_embd] fp32, injected in place of the
  * summed embedding before emb_norm) is given. out_logits receives [n_active][n_codebooks][audio_vocab]
- * post-softcap logits. Unlike the reference, idle slots are simply not listed (no padded columns). */
+ * post-softcap logits, or stays on the device only (out_logits NULL) for z2h_sample. Unlike the
+ * reference, idle slots are simply not listed (no padded columns). */
 int z2h_step(z2h_ctx * ctx, int n_active, const int32_t * slot_idx, const int32_t * n_past,
              const int32_t * ids, const float * emb, float * out_logits);
 

@@ -20,3 +20,8 @@ struct zonos2_sampler {
     int  sample(const float * logits, int cb);        // logits: [vocab]
     void accept(const std::vector<int> & frame);      // push a sampled frame into the history
 };
+
+// The part of zonos2_slot_sample after the draws (history, eos / countdown, next_ids, step, done), for
+// a frame sampled elsewhere (zonos2_batch_sample). Returns on_frame's verdict.
+bool zonos2_slot_finish_frame(const zonos2_model & m, zonos2_slot & s, zonos2_sampler & smp, const std::vector<int> & frame,
+                              std::vector<int32_t> & out_codes, int max_frames, const zonos2_frame_cb & on_frame);

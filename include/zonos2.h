@@ -137,6 +137,8 @@ struct zonos2_batch_ctx {
     std::vector<int32_t> h_slot, h_npast, h_ids;
     std::vector<float>   h_logits;    // [n_slots][ncb][av], by slot index
     std::vector<float>   h_compact;   // [n_active][ncb][av] when the active slots are not 0..n-1
+    int last_n = 0;                   // columns of the last step (their slot indices: h_slot[0, last_n))
+    bool device_sampling = false;     // steps keep the logits on the GPU for zonos2_batch_sample
 };
 
 // Per-slot decode state (graph-facing only; the sampler and output codes live with the caller).
@@ -170,8 +172,20 @@ bool zonos2_batch_slot_prefill(zonos2_batch_ctx & bc, int slot, const float * pr
 // device failure a message goes to stderr and no n_past advances.
 void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> & active);
 
-// Slot `index`'s logits from the last step: [n_codebooks][audio_vocab], valid until the next step.
+// Slot `index`'s logits from the last step: [n_codebooks][audio_vocab], valid until the next step
+// (not filled while bc.device_sampling is set: the logits then stay on the GPU).
 const float * zonos2_batch_slot_logits(const zonos2_batch_ctx & bc, int index);
+
+// Device sampling (no counterpart in the reference, whose sampler runs on the host per slot): draws
+// the frame of every column of the last zonos2_batch_step on the GPU (include/z2h.h z2h_sample) with
+// slot i's sampler smps[i] (settings, repetition history, and its mt19937 for the draws), then does
+// zonos2_slot_sample's bookkeeping for each slot (history, eos / countdown, next_ids, step, done) and
+// appends its codes to *out_codes[i]. `slots` must be exactly the slots the last step ran. With
+// bc.device_sampling set, the step leaves the logits on the GPU (no host copy). Returns false (message
+// on stderr) on a mismatch or a device failure; keep[i] receives on_frame's verdict per slot.
+bool zonos2_batch_sample(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> & slots,
+                         const std::vector<zonos2_sampler *> & smps, const std::vector<std::vector<int32_t> *> & out_codes,
+                         int max_frames, const zonos2_frame_cb & on_frame, std::vector<char> * keep = nullptr);
 
 // Sample one frame for `slot` from `logits` with `smp`, append its codes to out_codes, advance the
 // slot's eos / countdown / step state and prepare next_ids; sets slot.done when finished (eos

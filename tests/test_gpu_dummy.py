@@ -94,3 +94,23 @@ def test_batch_test_harness_on_fixture(root):
 def test_decode_bench_harness_on_fixture(root):
     r = _cli("--model", str(root / FIXTURE), "--decode-bench", "--slots", "4", "--steps", "16", "--prompt-len", "8")
     assert r.returncode == 0 and "decode-bench: slots=4 steps=16" in r.stdout
+
+
+def test_batch_test_harness_with_gpu_sampling(root):
+    """The batched run samples on the GPU (zonos2_batch_sample), the per-request reference runs on
+    the host sampler: greedy codes must agree exactly (F.1 / F.2 as in the reference's harness); with
+    sampling, identical prompts in two slots must still draw identical codes (F.2)."""
+    r = _cli("--model", str(root / FIXTURE), "--batch-test", "--greedy", "--gpu-sample", "--slots", "5", "--requests", "4",
+             "--dup", "--max-frames", "24", "--prompt-len", "12")
+    assert r.returncode == 0 and "batch-test: OK" in r.stdout, r.stdout + r.stderr
+    assert "batch == alone for every request: yes" in r.stdout
+    r = _cli("--model", str(root / FIXTURE), "--batch-test", "--gpu-sample", "--slots", "4", "--requests", "4", "--dup",
+             "--max-frames", "20", "--prompt-len", "10", "--seed", "9")
+    assert r.returncode == 0 and "batch-test: OK" in r.stdout, r.stdout + r.stderr
+    assert "MISMATCH" not in r.stdout
+
+
+def test_decode_bench_harness_with_gpu_sampling(root):
+    for extra in (["--gpu-sample"], ["--gpu-sample", "--sampled"], ["--sampled"]):
+        r = _cli("--model", str(root / FIXTURE), "--decode-bench", "--slots", "4", "--steps", "16", "--prompt-len", "8", *extra)
+        assert r.returncode == 0 and "decode-bench: slots=4 steps=16" in r.stdout, r.stdout + r.stderr

@@ -1150,7 +1150,7 @@ int z2h_kv_read(z2h_ctx * ctx, int layer, int slot, int row0, int n, uint16_t * 
 
 int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
              const float * emb, float * out_logits) {
-    if (!ctx || !slot_idx || !n_past || (!ids && !emb) || !out_logits) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (!ctx || !slot_idx || !n_past || (!ids && !emb)) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
     if (int rc = validate_step(ctx, T, slot_idx, n_past)) return rc;
     if (ids) {
         for (int t = 0; t < T; ++t)
@@ -1170,7 +1170,7 @@ int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_p
     if (emb) HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
     if (int rc = step_internal(ctx, T, n_past, ids != nullptr)) return rc;
     const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
-    HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (out_logits) HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
     return check_err_flag(ctx);
 }

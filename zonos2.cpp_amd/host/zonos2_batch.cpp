@@ -7,11 +7,14 @@
 // of z2h_step / z2h_prefill (src/zonos2-graph.cpp:639-841).
 #include "zonos2.h"
 #include "gguf.h"
+#include "zonos2-sampler.h"
 
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <limits>
+#include <random>
 
 namespace {
 
@@ -266,11 +269,14 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
     if (!dense) bc.h_compact.resize((size_t) n * row);
     float * out = dense ? bc.h_logits.data() : bc.h_compact.data();
     if (!sync_layer_skip(*bc.model)) { fail("step: layer skip"); return; }
-    if (int rc = z2h_step(bc.dev, n, bc.h_slot.data(), bc.h_npast.data(), bc.h_ids.data(), nullptr, out)) {
+    bc.last_n = 0;
+    if (int rc = z2h_step(bc.dev, n, bc.h_slot.data(), bc.h_npast.data(), bc.h_ids.data(), nullptr,
+                          bc.device_sampling ? nullptr : out)) {
         fail("step failed (status " + std::to_string(rc) + "): " + z2h_last_error(bc.dev));
         return;
     }
-    if (!dense)
+    bc.last_n = n;
+    if (!dense && !bc.device_sampling)
         for (int i = 0; i < n; ++i)
             std::memcpy(&bc.h_logits[(size_t) run[i]->index * row], &out[(size_t) i * row], row * 4);
     for (zonos2_slot * sp : run) sp->n_past += 1;
@@ -278,4 +284,56 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
 
 const float * zonos2_batch_slot_logits(const zonos2_batch_ctx & bc, int index) {
     return bc.h_logits.data() + (size_t) index * bc.av * bc.ncb;
+}
+
+bool zonos2_batch_sample(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> & slots,
+                         const std::vector<zonos2_sampler *> & smps, const std::vector<std::vector<int32_t> *> & out_codes,
+                         int max_frames, const zonos2_frame_cb & on_frame, std::vector<char> * keep) {
+    if (!bc.dev || !bc.model) return fail("sample: batch context not initialised");
+    const int n = bc.last_n, ncb = bc.ncb;
+    if (n <= 0) return fail("sample: no step to sample from");
+    if ((int) slots.size() != n || smps.size() != slots.size() || out_codes.size() != slots.size())
+        return fail("sample: slots / samplers / outputs must list exactly the last step's slots");
+    // column of each slot in the last step, the per-column settings, histories and draws
+    std::vector<int> col(n, -1);
+    for (int i = 0; i < n; ++i) {
+        if (!slots[i] || !smps[i] || !out_codes[i]) return fail("sample: null slot / sampler / output");
+        for (int c = 0; c < n; ++c) if (bc.h_slot[c] == slots[i]->index) col[i] = c;
+        if (col[i] < 0) return fail("sample: slot " + std::to_string(slots[i]->index) + " was not in the last step");
+    }
+    int cap = 1;
+    for (int i = 0; i < n; ++i)
+        for (const auto & h : smps[i]->hist) cap = std::max(cap, (int) h.size());
+    if (cap > Z2H_SAMPLE_HIST_MAX) return fail("sample: repetition window above Z2H_SAMPLE_HIST_MAX");
+    std::vector<z2h_sampling> sp(n);
+    std::vector<int32_t> hist((size_t) n * ncb * cap, 0), hlen((size_t) n * ncb, 0), codes((size_t) n * ncb);
+    std::vector<double> u((size_t) n * ncb, 0.0);
+    for (int i = 0; i < n; ++i) {
+        const int c = col[i];
+        zonos2_sampler & smp = *smps[i];
+        if (smp.n_cb != ncb || smp.vocab != bc.av) return fail("sample: sampler shape differs from the model's");
+        z2h_sampling & s = sp[c];
+        s.temperature = smp.sp.temperature; s.top_k = smp.sp.top_k; s.top_p = smp.sp.top_p; s.min_p = smp.sp.min_p;
+        s.rep_penalty = smp.sp.rep_penalty; s.rep_codebooks = smp.sp.rep_codebooks; s.greedy = smp.sp.greedy ? 1 : 0;
+        s.reserved = 0;
+        for (int cb = 0; cb < ncb; ++cb) {
+            const auto & h = smp.hist[cb];
+            int j = 0;
+            for (const int t : h) hist[((size_t) c * ncb + cb) * cap + j++] = t;
+            hlen[(size_t) c * ncb + cb] = j;
+            // the host sampler's draw: uniform_real_distribution<double>(0, mass) on its mt19937 is
+            // generate_canonical<double, 53> times the mass, taken once per codebook in order
+            if (!smp.sp.greedy)
+                u[(size_t) c * ncb + cb] = std::generate_canonical<double, std::numeric_limits<double>::digits>(smp.rng);
+        }
+    }
+    if (int rc = z2h_sample(bc.dev, n, nullptr, sp.data(), hist.data(), hlen.data(), cap, u.data(), codes.data()))
+        return fail("sample failed (status " + std::to_string(rc) + "): " + z2h_last_error(bc.dev));
+    if (keep) keep->assign(n, 1);
+    for (int i = 0; i < n; ++i) {
+        const std::vector<int> frame(codes.begin() + (size_t) col[i] * ncb, codes.begin() + (size_t) (col[i] + 1) * ncb);
+        const bool k = zonos2_slot_finish_frame(*bc.model, *slots[i], *smps[i], frame, *out_codes[i], max_frames, on_frame);
+        if (keep) (*keep)[i] = k;
+    }
+    return true;
 }

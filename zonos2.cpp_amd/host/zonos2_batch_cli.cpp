@@ -11,6 +11,9 @@
 //                    prompts in two slots) must match.
 // Prompts are seeded random id rows of --prompt-len frames (the text prompt builder is not part of
 // this library); --requests R gives R prompts, request i reusing prompt i % 2 when --dup is set.
+// --gpu-sample samples the batched run's frames on the GPU from the step's logits
+// (zonos2_batch_sample) instead of the host sampler; --sampled makes --decode-bench use the default
+// sampling settings instead of greedy feedback.
 #include "zonos2.h"
 #include "zonos2-sampler.h"
 
@@ -28,6 +31,8 @@ namespace {
 struct Args {
     std::string model;
     bool info = false, bench = false, test = false, greedy = false, dup = false;
+    bool gpu_sample = false;          // sample on the GPU from the step's logits (zonos2_batch_sample)
+    bool sampled = false;             // decode-bench: default sampling settings instead of greedy
     int slots = 0, steps = 64, max_frames = 48, prompt_len = 32, requests = 3;
     uint32_t seed = 1;
 };
@@ -35,7 +40,7 @@ struct Args {
 int usage() {
     fprintf(stderr, "usage: zonos2-batch --model F.gguf (--info | --decode-bench | --batch-test)\n"
                     "       [--slots N] [--steps K] [--max-frames M] [--prompt-len N0] [--requests R]\n"
-                    "       [--greedy] [--dup] [--seed S]\n");
+                    "       [--greedy] [--dup] [--seed S] [--gpu-sample] [--sampled]\n");
     return 2;
 }
 
@@ -81,7 +86,7 @@ int run_decode_bench(zonos2_model & m, const Args & a) {
     const std::vector<float> idf = make_prompt(m, n0, a.seed);
     zonos2_batch_ctx bc;
     if (!zonos2_batch_init(bc, m, n_slots, n0 + n_steps + 16)) { fprintf(stderr, "decode-bench: batch init failed\n"); return 1; }
-    zonos2_sampling sp; sp.greedy = true;
+    zonos2_sampling sp; sp.greedy = !a.sampled; sp.seed = a.seed;
     std::vector<zonos2_sampler> smp(n_slots, zonos2_sampler(sp, ncb, av));
     std::vector<zonos2_slot> slots(n_slots);
     std::vector<std::vector<float>> lo(n_slots, std::vector<float>((size_t) av * ncb));
@@ -94,14 +99,25 @@ int run_decode_bench(zonos2_model & m, const Args & a) {
         }
         active[i] = &slots[i];
     }
+    // a frame = sampling (host: from the copied logits; --gpu-sample: on the GPU from the step's
+    // logits) + one batched step
+    std::vector<zonos2_sampler *> smp_p(n_slots);
+    std::vector<std::vector<int32_t> *> sink_p(n_slots, &sink);
+    for (int i = 0; i < n_slots; ++i) smp_p[i] = &smp[i];
+    for (int i = 0; i < n_slots; ++i) zonos2_slot_sample(m, slots[i], smp[i], lo[i].data(), sink, n_steps + n0 + 32, {});
+    bc.device_sampling = a.gpu_sample;
+    bool ok = true;
     auto step_once = [&]() {
-        for (int i = 0; i < n_slots; ++i) {
-            zonos2_slot_sample(m, slots[i], smp[i], lo[i].data(), sink, n_steps + n0 + 32, {});
-            slots[i].done = false;
-        }
+        for (int i = 0; i < n_slots; ++i) slots[i].done = false;
         zonos2_batch_step(bc, active);
-        for (int i = 0; i < n_slots; ++i)
-            std::memcpy(lo[i].data(), zonos2_batch_slot_logits(bc, i), (size_t) av * ncb * sizeof(float));
+        if (a.gpu_sample) {
+            ok = ok && zonos2_batch_sample(bc, active, smp_p, sink_p, n_steps + n0 + 32, {});
+        } else {
+            for (int i = 0; i < n_slots; ++i) {
+                std::memcpy(lo[i].data(), zonos2_batch_slot_logits(bc, i), (size_t) av * ncb * sizeof(float));
+                zonos2_slot_sample(m, slots[i], smp[i], lo[i].data(), sink, n_steps + n0 + 32, {});
+            }
+        }
         sink.clear();
     };
     for (int w = 0; w < 8; ++w) step_once();
@@ -109,8 +125,10 @@ int run_decode_bench(zonos2_model & m, const Args & a) {
     for (int s = 0; s < n_steps; ++s) step_once();
     const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     const double fps = (double) n_slots * n_steps / dt;
-    printf("decode-bench: slots=%d steps=%d  %.3fs  %.0f frames/s  %.1fx real-time  (%.1f frames/s/slot)\n",
-           n_slots, n_steps, dt, fps, fps / (44100.0 / 512.0), fps / n_slots);
+    if (!ok) { zonos2_batch_free(bc); return 1; }
+    printf("decode-bench: slots=%d steps=%d  %.3fs  %.0f frames/s  %.1fx real-time  (%.1f frames/s/slot)  [%s, sampling on the %s]\n",
+           n_slots, n_steps, dt, fps, fps / (44100.0 / 512.0), fps / n_slots, sp.greedy ? "greedy" : "sampled",
+           a.gpu_sample ? "GPU" : "host");
     zonos2_batch_free(bc);
     return 0;
 }
@@ -176,23 +194,35 @@ int run_batch_test(zonos2_model & m, const Args & a) {
             fprintf(stderr, "batch-test: prefill slot %d failed\n", i);
         }
     }
+    // the first frame comes from the prefill logits on the host; later frames are sampled on the host
+    // from the step's logits, or on the GPU (--gpu-sample) straight after the step
+    bc.device_sampling = a.gpu_sample;
+    for (Job & j : jobs) {
+        if (!j.slot.active || j.slot.done) continue;
+        zonos2_slot_sample(m, j.slot, *j.smp, j.logits.data(), j.codes, a.max_frames, {});
+        j.eos_frame = j.slot.eos_frame;
+    }
     for (;;) {
-        bool any = false;
-        for (Job & j : jobs) {
-            if (!j.slot.active || j.slot.done) continue;
-            zonos2_slot_sample(m, j.slot, *j.smp, j.logits.data(), j.codes, a.max_frames, {});
-            j.eos_frame = j.slot.eos_frame;
-            any = true;
-        }
-        if (!any) break;
         std::vector<zonos2_slot *> list;
         for (Job & j : jobs) if (j.slot.active && !j.slot.done) list.push_back(&j.slot);
         if (list.empty()) break;
         zonos2_batch_step(bc, list);
-        for (zonos2_slot * s : list)
-            std::memcpy(jobs[s->index].logits.data(), zonos2_batch_slot_logits(bc, s->index), (size_t) av * ncb * sizeof(float));
+        if (a.gpu_sample) {
+            std::vector<zonos2_sampler *> smps;
+            std::vector<std::vector<int32_t> *> outs;
+            for (zonos2_slot * s : list) { smps.push_back(jobs[s->index].smp.get()); outs.push_back(&jobs[s->index].codes); }
+            if (!zonos2_batch_sample(bc, list, smps, outs, a.max_frames, {})) { zonos2_batch_free(bc); return 1; }
+        } else {
+            for (zonos2_slot * s : list) {
+                Job & j = jobs[s->index];
+                std::memcpy(j.logits.data(), zonos2_batch_slot_logits(bc, s->index), (size_t) av * ncb * sizeof(float));
+                zonos2_slot_sample(m, j.slot, *j.smp, j.logits.data(), j.codes, a.max_frames, {});
+            }
+        }
+        for (zonos2_slot * s : list) jobs[s->index].eos_frame = s->eos_frame;
     }
-    printf("\n=== batch-test: %d requests in %d slots, %s, max=%d ===\n", n_req, n_slots, sp.greedy ? "greedy" : "sampling", a.max_frames);
+    printf("\n=== batch-test: %d requests in %d slots, %s%s, max=%d ===\n", n_req, n_slots, sp.greedy ? "greedy" : "sampling",
+           a.gpu_sample ? " on the GPU" : "", a.max_frames);
     int fails = 0, exact_all = 1;
     for (int i = 0; i < n_req; ++i) {
         const auto & b = jobs[i].codes;
@@ -237,6 +267,8 @@ int main(int argc, char ** argv) {
         else if (s == "--batch-test") a.test = true;
         else if (s == "--greedy") a.greedy = true;
         else if (s == "--dup") a.dup = true;
+        else if (s == "--gpu-sample") a.gpu_sample = true;
+        else if (s == "--sampled") a.sampled = true;
         else if (s == "--slots" && (v = next())) a.slots = std::atoi(v);
         else if (s == "--steps" && (v = next())) a.steps = std::atoi(v);
         else if (s == "--max-frames" && (v = next())) a.max_frames = std::atoi(v);

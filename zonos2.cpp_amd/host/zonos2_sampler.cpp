@@ -96,6 +96,12 @@ bool zonos2_slot_sample(const zonos2_model & m, zonos2_slot & s, zonos2_sampler 
     const int ncb = (int) m.hp.n_codebooks, av = (int) m.hp.audio_vocab;
     std::vector<int> frame(ncb);
     for (int cb = 0; cb < ncb; ++cb) frame[cb] = smp.sample(logits + (size_t) cb * av, cb);
+    return zonos2_slot_finish_frame(m, s, smp, frame, out_codes, max_frames, on_frame);
+}
+
+bool zonos2_slot_finish_frame(const zonos2_model & m, zonos2_slot & s, zonos2_sampler & smp, const std::vector<int> & frame,
+                              std::vector<int32_t> & out_codes, int max_frames, const zonos2_frame_cb & on_frame) {
+    const int ncb = (int) m.hp.n_codebooks;
     smp.accept(frame);
     out_codes.insert(out_codes.end(), frame.begin(), frame.end());
 
