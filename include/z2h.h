@@ -129,6 +129,14 @@ int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, con
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits);
 
+/* Rows per prefill chunk (1 .. Z2H_PREFILL_CHUNK_MAX, at most 1024 / max top-k; default the maximum).
+ * A chunk's rows go through each layer together (the projections and expert matmuls see them as one
+ * batch; every row appends its K/V before the chunk's attention), so a prompt of n0 rows takes
+ * ceil(n0 / rows) passes instead of n0 single-row steps. Any chunk size gives the same results. No
+ * reference counterpart: the reference builds one graph over the whole prompt. */
+#define Z2H_PREFILL_CHUNK_MAX 256
+int z2h_set_prefill_chunk(z2h_ctx * ctx, int rows);
+
 /* One MoE layer (build_moe) on n_tokens host rows x [n_tokens][n_embd] (the layer's ffn_in); state_in
  * ([n_tokens][router_dim], may be NULL) is the previous MoE layer's router state. out [n_tokens][n_embd]. */
 int z2h_moe_forward(z2h_ctx * ctx, int layer, int n_tokens, const float * x, const float * state_in, float * out);

@@ -250,3 +250,37 @@ def test_layer_skip_vs_oracle():
     ctx.set_layer_skip(None)
     assert np.array_equal(ctx.step(inp.slot_idx, inp.n_past, emb=inp.emb), full)
     ctx.close()
+
+
+def test_chunked_prefill_is_chunk_size_independent():
+    """Chunked prefill (every row of a chunk appends its K/V before the chunk's attention) gives the
+    same bits for any chunk size: one row at a time, 7-row chunks (ragged last chunk, the speaker
+    row inside a chunk) and the whole prompt in one chunk; the last-row logits also match the oracle's
+    row-by-row decode (full bar)."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 48)
+    om = O.OracleModel(cfg.hparams(), model)
+    n0, pos, slot = 61, 23, 2
+    ids = _prompt(cfg, n0, 9)
+    spk = synth.gen_normal_f32((cfg.spk_dim,), 5, "spk")
+    outs, kvs = [], []
+    for chunk in (1, 7, 256):
+        ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+        ctx.upload(model)
+        ctx.set_prefill_chunk(chunk)
+        print(f"prefill chunk {chunk}", flush=True)
+        outs.append(ctx.prefill(slot, ids, spk=spk, spk_pos=pos))
+        kvs.append([ctx.kv_read(L, slot, 0, n0) for L in range(cfg.n_layer)])
+        ctx.close()
+    for i in (1, 2):
+        np.testing.assert_array_equal(outs[i], outs[0])
+        for L in range(cfg.n_layer):
+            np.testing.assert_array_equal(kvs[i][L][0], kvs[0][L][0])
+            np.testing.assert_array_equal(kvs[i][L][1], kvs[0][L][1])
+    okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    for t in range(n0):
+        if t == pos:
+            want = O.step(om, okv, [slot], [t], emb=_speaker_row_f32(model, spk, np.zeros(cfg.n_embd, np.float32))[None, :])
+        else:
+            want = O.step(om, okv, [slot], [t], ids=ids[t:t + 1])
+    assert_close("chunked prefill vs oracle steps", outs[2], want[0])

@@ -97,7 +97,9 @@ struct z2h_ctx {
     uint4 * kv_stage = nullptr;       // one slot's rows of one layer, host layout (kv_write / kv_read)
 
     // scratch (sized for n_slots tokens)
-    int Tmax = 0, Kmax = 0, items_max = 0;
+    int Tmax = 0, Kmax = 0, items_max = 0;   // Tmax: token rows of the scratch (steps and prefill chunks)
+    int Tstep = 0;                    // columns a step may list (n_slots); captures are sized for it
+    int pch = 0;                      // prefill chunk rows (<= Tmax)
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
@@ -141,6 +143,7 @@ int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; re
 int seterr(z2h_model * c, int code, const std::string & m) { if (c) c->err = m; return code; }
 int upload_mat_t64(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
+int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T);
 
 constexpr int PROF_MAX = 16384;
 
@@ -393,9 +396,14 @@ size_t samp_stage_bytes(int T, int ncb) {
 
 int alloc_scratch(z2h_ctx * ctx) {
     const auto & hp = ctx->hp;
-    const int T = ctx->n_slots, d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
+    // rows: a step's columns, or a prefill chunk of up to Z2H_PREFILL_CHUNK_MAX prompt rows (capped so a
+    // chunk's routes fit the grouped GEMVs' route lists)
+    const int pmax = std::max(1, std::min(Z2H_PREFILL_CHUNK_MAX, MAX_ROUTES / std::max(1, ctx->kmax)));
+    const int T = std::max(ctx->n_slots, pmax), d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     const int ff = hp.n_ff, K = ctx->kmax, E = std::max(1, hp.n_expert), rd = std::max(1, ctx->rd);
     ctx->Tmax = T;
+    ctx->Tstep = ctx->n_slots;
+    ctx->pch = pmax;
     ctx->Kmax = std::max({kpad(d), kpad(nh * hd), kpad(ff), kpad(std::max(1, hp.spk_dim)), kpad(std::max(1, hp.spk_lda_dim))});
     const int R = (nh + 2 * nkv) * hd + nh;
     const int grp = nh / nkv;
@@ -469,7 +477,7 @@ int64_t cap_width(const z2h_ctx * c, int what, int T) {
 
 uint8_t * capp(z2h_ctx * c, int what, int L) {
     if (!c->capture) return nullptr;
-    return c->cap[what] + (size_t) L * cap_width(c, what, c->Tmax) * 4;
+    return c->cap[what] + (size_t) L * cap_width(c, what, c->Tstep) * 4;
 }
 
 int cap_copy(z2h_ctx * ctx, int what, int L, const void * src, int T) {
@@ -701,8 +709,10 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
 }
 
 // The whole decode step on device-resident inputs in ctx->d_* (T tokens, host copy of n_past).
+// kv_pre: append every token's K/V row before the attention (prefill chunks, whose rows attend to
+// each other); emb_row >= 0: only that token takes d_emb (one row), the others d_ids.
 int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
-             const int32_t * d_ids, const float * d_emb, float * d_logits) {
+             const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false, int emb_row = -1) {
     const auto & hp = ctx->hp;
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
@@ -714,7 +724,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     const int n_run = (int) run.size();
     // embeddings + emb_norm + the first block's attn_norm (output_norm when every block is skipped)
     ResNormArgs e{};
-    e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb;
+    e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb; e.emb_row = emb_row;
     for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->m->tab[k]; e.tab_type[k] = ctx->m->tab_type[k]; e.tab_rows[k] = ctx->m->tab_rows[k]; }
     e.res = ctx->res;
     if (n_run) {
@@ -761,6 +771,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         {
             // QK-norm / RoPE / KV append fused in; item count from the device n_past table
             prof_scope ps(ctx, Z2H_KF_ATTN);
+            if (kv_pre && (rc = launch_kv_append(ctx, a, T))) return rc;
             if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
         }
         {
@@ -817,6 +828,18 @@ int allow_lds(const void * fn, z2h_ctx * ctx) {
 }
 
 // one wave per (token, 64-row chunk, KV head) item, instantiated per head size and group size
+int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T) {
+    const dim3 grid(T, a.nkv);
+    switch (a.hd) {
+        case 16: KL(k_kv_append<16>, grid, dim3(64), 0, ctx->stream, a); break;
+        case 32: KL(k_kv_append<32>, grid, dim3(64), 0, ctx->stream, a); break;
+        case 64: KL(k_kv_append<64>, grid, dim3(64), 0, ctx->stream, a); break;
+        default: KL(k_kv_append<128>, grid, dim3(64), 0, ctx->stream, a); break;
+    }
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
     const int grp = a.nh / a.nkv;
 #define ATT(H_, G_) KL((k_attn_chunk<H_, G_>), dim3(grid), dim3(256), 0, ctx->stream, a)
@@ -845,7 +868,7 @@ int check_err_flag(z2h_ctx * ctx) {
 
 int validate_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_past) {
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
-    if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
+    if (T <= 0 || T > ctx->Tstep) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
     for (int t = 0; t < T; ++t) {
         if (slot_idx && (slot_idx[t] < 0 || slot_idx[t] >= ctx->n_slots)) return seterr(ctx, Z2H_EINVAL, "slot index out of range");
         if (n_past[t] < 0 || n_past[t] >= ctx->S) return seterr(ctx, Z2H_EINVAL, "n_past out of range (slot full)");
@@ -1234,20 +1257,49 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
     if (slot < 0 || slot >= ctx->n_slots) return seterr(ctx, Z2H_EINVAL, "slot out of range");
     if (n0 <= 0 || n0 > ctx->S) return seterr(ctx, Z2H_EINVAL, "prefill n0 exceeds slot_cap");
     if (spk && (spk_pos < 0 || spk_pos >= n0)) return seterr(ctx, Z2H_EINVAL, "spk_pos outside the prompt");
+    const int W = ctx->W;
+    for (int64_t i = 0; i < (int64_t) n0 * W; ++i) {
+        const int k = (int) (i % W);
+        if ((!spk || i / W != spk_pos) && (ids[i] < 0 || ids[i] >= ctx->m->tab_rows[k])) return seterr(ctx, Z2H_EINVAL, "token id out of range");
+    }
     HIPX(hipSetDevice(ctx->device));
     std::vector<float> sp;
     if (spk) {
         sp.resize(ctx->hp.n_embd);
         if (int rc = speaker_row(ctx, spk, delta, sp.data())) return rc;
     }
-    // causal prefill as n0 single-row decode steps over the empty band: row t attends rows [0, t]
-    std::vector<float> lg((size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab);
-    for (int t = 0; t < n0; ++t) {
-        const int32_t si = slot, np = t;
-        float * out = t + 1 == n0 ? last_logits : lg.data();
-        const bool spk_row = spk && t == spk_pos;
-        if (int rc = z2h_step(ctx, 1, &si, &np, spk_row ? nullptr : ids + (size_t) t * ctx->W, spk_row ? sp.data() : nullptr, out)) return rc;
+    // causal prefill in chunks of rows [r0, r0 + T): every row of a chunk appends its K/V before the
+    // chunk's attention, then row r attends rows [0, r] of the band. Each row's arithmetic is the
+    // decode step's for a column at n_past = r, so any chunk size gives the same bits. With capture on,
+    // chunks stay within the step width the capture buffers hold.
+    const int chunk = std::max(1, std::min(ctx->pch, ctx->capture ? ctx->Tstep : ctx->Tmax));
+    const size_t row = (size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab;
+    for (int r0 = 0; r0 < n0; r0 += chunk) {
+        const int T = std::min(chunk, n0 - r0);
+        const bool last = r0 + T == n0;
+        int32_t * hp_ = ctx->h_pin;
+        for (int t = 0; t < T; ++t) { hp_[t] = slot; hp_[T + t] = r0 + t; }
+        std::memcpy(hp_ + 2 * T, ids + (size_t) r0 * W, (size_t) T * W * 4);
+        const int er = spk && spk_pos >= r0 && spk_pos < r0 + T ? spk_pos - r0 : -1;
+        if (er >= 0) for (int k = 0; k < W; ++k) hp_[2 * T + er * W + k] = 0;      // the row's ids are unused
+        HIPX(hipMemcpyAsync(ctx->d_slot, hp_, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + T, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * W * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (er >= 0) HIPX(hipMemcpyAsync(ctx->d_emb, sp.data(), (size_t) ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (int rc = run_step(ctx, T, hp_ + T, ctx->d_slot, ctx->d_npast, ctx->d_ids, er >= 0 ? ctx->d_emb : nullptr,
+                              ctx->logits, /*kv_pre=*/true, er)) return rc;
+        if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits + (size_t) (T - 1) * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }
+    return check_err_flag(ctx);
+}
+
+int z2h_set_prefill_chunk(z2h_ctx * ctx, int rows) {
+    if (!ctx) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    const int pmax = std::max(1, std::min(Z2H_PREFILL_CHUNK_MAX, MAX_ROUTES / std::max(1, ctx->kmax)));
+    if (rows <= 0 || rows > pmax) return seterr(ctx, Z2H_EINVAL, "prefill chunk out of range");
+    ctx->pch = rows;
     return Z2H_OK;
 }
 
@@ -1255,7 +1307,7 @@ int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int T, const float * d_x, c
     if (!ctx || !d_x || !d_out) return Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
     if (layer < 0 || layer >= ctx->hp.n_layer || !ctx->m->layers[layer].moe) return seterr(ctx, Z2H_EINVAL, "layer is not MoE");
-    if (T <= 0 || T > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_tokens out of range");
+    if (T <= 0 || T > ctx->Tmax || (ctx->capture && T > ctx->Tstep)) return seterr(ctx, Z2H_EINVAL, "n_tokens out of range");
     hipStream_t keep = ctx->stream;
     if (stream) ctx->stream = (hipStream_t) stream;
     ctx->cap_T = T;
@@ -1352,7 +1404,7 @@ int z2h_set_capture(z2h_ctx * ctx, int enable) {
     if (enable && ctx->cap.empty()) {
         ctx->cap.assign(Z2H_CAP_COUNT_, nullptr);
         for (int w = 0; w < Z2H_CAP_COUNT_; ++w) {
-            const size_t n = (size_t) cap_width(ctx, w, ctx->Tmax) * 4 * ctx->hp.n_layer;
+            const size_t n = (size_t) cap_width(ctx, w, ctx->Tstep) * 4 * ctx->hp.n_layer;
             if (int rc = dalloc(ctx, &ctx->cap[w], n, ctx->bytes_scratch)) return rc;
             HIPX(hipMemset(ctx->cap[w], 0, n));
         }
@@ -1374,7 +1426,7 @@ int z2h_read_capture(z2h_ctx * ctx, int layer, int what, void * host, size_t nby
     if (nbytes < n) return seterr(ctx, Z2H_EINVAL, "capture buffer too small");
     HIPX(hipStreamSynchronize(ctx->stream));
     const int L = what == Z2H_CAP_OUT_NORM ? 0 : layer;
-    HIPX(hipMemcpy(host, ctx->cap[what] + (size_t) L * cap_width(ctx, what, ctx->Tmax) * 4, n, hipMemcpyDeviceToHost));
+    HIPX(hipMemcpy(host, ctx->cap[what] + (size_t) L * cap_width(ctx, what, ctx->Tstep) * 4, n, hipMemcpyDeviceToHost));
     return Z2H_OK;
 }
 
@@ -1426,7 +1478,7 @@ int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sa
     static_assert(sizeof(z2h_sampling) == sizeof(SampleParams), "z2h_sampling layout");
     if (!ctx || !sp || !u || !codes) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
-    if (n_active <= 0 || n_active > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
+    if (n_active <= 0 || n_active > ctx->Tstep) return seterr(ctx, Z2H_EINVAL, "n_active out of range");
     if (hist && (hist_cap < 0 || hist_cap > Z2H_SAMPLE_HIST_MAX || !hist_len))
         return seterr(ctx, Z2H_EINVAL, "history capacity out of range (at most Z2H_SAMPLE_HIST_MAX)");
     const int ncb = ctx->hp.n_codebooks, av = ctx->hp.audio_vocab;

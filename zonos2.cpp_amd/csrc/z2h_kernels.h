@@ -11,12 +11,14 @@
 //                    weight
 //   k_gemv / k_gemv_rows   the same on the 64-row tiled layout (Q6_K, F16)
 //   k_swiglu_encode / k_encode_rows   up * silu(gate) (183, 225) / fp32 rows encoded for the next matmul
-//   k_attn_decode    QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137) and ragged GQA
-//                    decode attention over the slot's band in 64-row chunks (139-153)
+//   k_attn_chunk     QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137) and ragged GQA
+//                    decode attention over the slot's band in 32-row chunks (139-153)
 //   k_attn_combine   chunk merge, per-head sigmoid gate (107, 173), encoding for W_o
 //   k_router_down    EDA router down-projection + state threading (199-203)
 //   k_router_tail    router norm, erf-GELU MLP, softmax, bias, mask, top-k, weights (206-220)
 //   k_kv_move / k_bias_add   KV row staging for host reads and writes / speaker-projection biases
+//   k_kv_append      K/V rows of every token of a prefill chunk, before the chunk's attention
+//   k_sample         frame sampler (src/zonos2-sampler.cpp:16-77) on the step's logits
 //
 // Weight layouts in HBM: "m16" for Q4_K and Q8_0 (see k_gemv_mfma) and "row-tiled" (t64) for Q6_K
 // and F16: a matrix of R rows x K columns is cut into 64-row tiles and 256-column units; the bytes
@@ -214,7 +216,8 @@ constexpr int MAX_TABLES = 16;
 struct ResNormArgs {
     int mode, d;
     const int32_t * ids; int W;
-    const float * emb_in;
+    const float * emb_in;              // [T][d] injected rows, or one row for token emb_row
+    int emb_row;                       // >= 0: only token emb_row takes emb_in (row 0), others ids
     const uint8_t * tab[MAX_TABLES]; int tab_type[MAX_TABLES]; int64_t tab_rows[MAX_TABLES];
     const float * src; int k;         // ACCUM: [T*k][d] routes; ADD / ENCODE: [T][d]
     float * res;                       // [T][d] (ACCUM may pass null: no residual)
@@ -261,11 +264,12 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     }
     auto add4 = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
     if (a.mode == RN_EMBED) {
-        if (a.emb_in) {
+        if (a.emb_in && (a.emb_row < 0 || t == a.emb_row)) {
+            const float * er = a.emb_in + (a.emb_row < 0 ? (int64_t) t * d : 0);
 #pragma unroll
             for (int j = 0; j < RN_NV; ++j) {
                 const int i0 = 4 * (tid + 256 * j);
-                if (i0 < d) xv[j] = *(const float4 *) (a.emb_in + (int64_t) t * d + i0);
+                if (i0 < d) xv[j] = *(const float4 *) (er + i0);
             }
         } else {
             // sum of the W tables' rows in column order (kk = 0, 1, ...), each row gathered whole
@@ -1228,6 +1232,25 @@ __device__ __forceinline__ void attn_chunks_of(const int32_t * n_past, int T, in
     }
 }
 
+// RoPE angle of the lane's dim pair (lane < HD/2) at position pos: theta = pos * theta_scale^i by
+// repeated fp32 multiplication, as the reference's rope_ext does; cs / sn its cosine and sine.
+__device__ __forceinline__ void rope_cs(int pos, int pl, float theta_scale, float & cs, float & sn) {
+    float th = (float) pos;
+    for (int j = 0; j < pl; ++j) th = th * theta_scale;
+    z_sincos(th, sn, cs);
+}
+// Per-head RMSNorm (one wave, lane = dim pair (x0, x1); lanes past the head hold zeros) times mul,
+// then RoPE with the lane's (cs, sn).
+template <int HD>
+__device__ __forceinline__ void norm_rope(float x0, float x1, float mul, float eps, float cs, float sn, float & y0, float & y1) {
+    const double ss = wave_tree_d((double) (x0 * x0) + (double) (x1 * x1));
+    const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + eps);
+    float z0 = x0 * sc, z1 = x1 * sc;
+    if (mul != 1.0f) { z0 = z0 * mul; z1 = z1 * mul; }
+    y0 = z0 * cs - z1 * sn;
+    y1 = z0 * sn + z1 * cs;
+}
+
 // Decode attention with a block of 4 waves per item = (token, ATT_CH-row chunk of its band [0, n_past],
 // KV head g). The block requests the chunk's K and V rows with coalesced 16-byte loads and, while
 // they are in flight, forms the group's queries from the fused projection output (per-head RMSNorm,
@@ -1292,26 +1315,15 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         // ---- queries of the group (one wave per head), and the new k / v row (wave 3)
         uint32_t nk = 0, nv = 0;
         {
-            const int pl = min(lane, NP - 1);
-            float th = (float) np;
-            for (int j = 0; j < pl; ++j) th = th * a.theta_scale;
             float cs, sn;
-            z_sincos(th, sn, cs);
-            auto norm_rope = [&](float x0, float x1, float mul, float & y0, float & y1) {
-                const double ss = wave_tree_d((double) (x0 * x0) + (double) (x1 * x1));
-                const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + a.qk_eps);
-                float z0 = x0 * sc, z1 = x1 * sc;
-                if (mul != 1.0f) { z0 = z0 * mul; z1 = z1 * mul; }
-                y0 = z0 * cs - z1 * sn;
-                y1 = z0 * sn + z1 * cs;
-            };
+            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
 #pragma unroll
             for (int j = 0; j < HPW; ++j) {
                 const int h = wave + 4 * j;
                 if (h >= GRP) break;
                 const int qh = g * GRP + h;
                 float y0, y1;
-                norm_rope(xq[j][0], xq[j][1], a.temp[qh], y0, y1);
+                norm_rope<HD>(xq[j][0], xq[j][1], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
                 if (lane < NP) {
                     s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
                     if (a.cap_q && c == 0) {
@@ -1322,7 +1334,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             }
             if (mk) {
                 float k0, k1;
-                norm_rope(xq[HPW][0], xq[HPW][1], 1.0f, k0, k1);
+                norm_rope<HD>(xq[HPW][0], xq[HPW][1], 1.0f, a.qk_eps, cs, sn, k0, k1);
                 if (lane < NP) {
                     const float v0 = xq[HPW + 1][0], v1 = xq[HPW + 1][1];
                     nk = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
@@ -1394,6 +1406,29 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
         }
         __syncthreads();                                             // LDS reuse by the next item
+    }
+}
+
+// K/V append for every token of a prefill chunk before its attention reads them: one wave per
+// (token, KV head) forms the new k (per-head RMSNorm, RoPE at n_past) and v rows in f16 exactly as the
+// attention kernel does for its new row, and stores them at row n_past of the slot's band.
+template <int HD>
+__global__ void __launch_bounds__(64) k_kv_append(AttnArgs a) {
+    constexpr int NP = HD / 2;
+    const int t = blockIdx.x, g = blockIdx.y, lane = threadIdx.x;
+    const int np = a.n_past[t], slot = a.slot_idx[t], nkv = a.nkv;
+    const float * row = a.qkvg + (int64_t) t * a.R;
+    const float * ksrc = row + (int64_t) (a.nh + g) * HD, * vsrc = row + (int64_t) (a.nh + nkv + g) * HD;
+    const float x0 = lane < NP ? ksrc[2 * lane] : 0.0f, x1 = lane < NP ? ksrc[2 * lane + 1] : 0.0f;
+    const float v0 = lane < NP ? vsrc[2 * lane] : 0.0f, v1 = lane < NP ? vsrc[2 * lane + 1] : 0.0f;
+    float cs, sn;
+    rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
+    float k0, k1;
+    norm_rope<HD>(x0, x1, 1.0f, a.qk_eps, cs, sn, k0, k1);
+    if (lane < NP) {
+        const int64_t at = (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane;
+        *(uint32_t *) (a.kc + at) = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
+        *(uint32_t *) (a.vc + at) = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
     }
 }
 

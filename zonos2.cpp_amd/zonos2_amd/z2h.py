@@ -62,6 +62,7 @@ def lib() -> C.CDLL:
         "z2h_profile_begin": (i32, [vp]),
         "z2h_profile_end": (i32, [vp, vp, vp]),
         "z2h_sample": (i32, [vp, i32, vp, vp, vp, vp, i32, vp, vp]),
+        "z2h_set_prefill_chunk": (i32, [vp, i32]),
         "z2h_last_error": (C.c_char_p, [vp]),
         "z2h_destroy": (None, [vp]),
     }
@@ -76,7 +77,7 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
-           "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample",
+           "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample", "z2h_set_prefill_chunk",
            "z2h_last_error", "z2h_destroy")
 KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
                    "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
@@ -203,6 +204,9 @@ class Context:
         out = np.empty(self.hp["n_codebooks"] * self.hp["audio_vocab"], np.float32)
         self.check(lib().z2h_prefill(self.ctx, slot, _p(ids), ids.shape[0], _p(spk), spk_pos, _p(delta), _p(out)))
         return out
+
+    def set_prefill_chunk(self, rows: int):
+        self.check(lib().z2h_set_prefill_chunk(self.ctx, rows))
 
     def moe_forward(self, layer, x, state_in=None):
         x = np.ascontiguousarray(x, np.float32)
