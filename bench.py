@@ -205,6 +205,32 @@ def main() -> int:
                          f"after 1 warm-up), C++ restatement of the ggml CPU path",
                "logits_cos_vs_gpu": round(cosv, 7)}
 
+    # the next rows of the path, outside the decode step: chunked prefill of one 1024-row prompt (it
+    # overwrites slot 0's first rows, after the step's measurements) and device sampling of the step's
+    # 16 columns with the default settings
+    rng_p = np.random.default_rng(5)
+    n_pf = 1024
+    pids = np.concatenate([rng_p.integers(0, cfg.audio_vocab, (n_pf, cfg.n_codebooks)),
+                           rng_p.integers(0, cfg.text_vocab + 1, (n_pf, 1))], axis=1).astype(np.int32)
+    ctx.prefill(0, pids[:16])
+    pf = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ctx.prefill(0, pids)
+        pf.append(time.perf_counter() - t0)
+    pf_ms = float(np.median(pf)) * 1000.0
+    log(f"prefill: {n_pf} rows in {pf_ms:.1f} ms ({n_pf / pf_ms * 1000.0:.0f} rows/s)")
+    sp_def = dict(temperature=1.15, top_k=106, top_p=0.0, min_p=0.18, rep_penalty=1.2, rep_codebooks=8, greedy=0)
+    hist = rng_p.integers(0, cfg.audio_vocab, (T, cfg.n_codebooks, 50)).astype(np.int32)
+    hlen = np.full((T, cfg.n_codebooks), 50, np.int32)
+    uu = rng_p.random((T, cfg.n_codebooks))
+    ctx.sample([sp_def] * T, uu, hist, hlen, d_logits=d_logits.data_ptr())
+    t0 = time.perf_counter()
+    for _ in range(20):
+        ctx.sample([sp_def] * T, uu, hist, hlen, d_logits=d_logits.data_ptr())
+    samp_us = (time.perf_counter() - t0) / 20 * 1e6
+    log(f"device sampling: {samp_us:.1f} us per frame of {T} columns (host round trip included)")
+
     line = {
         "metric": "batched-decode tok/s (Q4_K MoE step, 16 ragged reqs); % of HBM peak GB/s",
         "value": round(T / (ms / 1000.0), 1),
@@ -231,6 +257,9 @@ def main() -> int:
                      "bytes_per_launch": int((gu_w + act_b + gu_out) / cfg.n_layer)},
         "kernels_us_per_step": {k: round(t / args.steps * 1000.0, 1) for k, (t, n) in prof.items() if n},
         "cpu_baseline": cpu,
+        "prefill": {"rows": n_pf, "chunk_rows": 256, "ms": round(pf_ms, 2), "rows_per_s": round(n_pf / pf_ms * 1000.0, 1)},
+        "sampler": {"columns": T, "settings": "temperature 1.15, top-k 106, min-p 0.18, repetition 1.2 over 50",
+                    "us_per_frame_step": round(samp_us, 1)},
     }
     if args.config != "c3":
         line["metric"] = "batched-decode tok/s (MoE step); % of HBM peak GB/s"
