@@ -185,6 +185,17 @@ typedef struct z2h_sampling {
 int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
                const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes);
 
+/* Device-resident step tables (no reference counterpart; the reference repacks ids, positions and its
+ * mask on the host every step, src/zonos2-graph.cpp:773-813). z2h_sample_feed is z2h_sample on the
+ * last step's logits (which must come from z2h_step, z2h_step_resident or the graph path of
+ * z2h_step_device with ids) that also writes each column's next input frame (its codes + the text pad
+ * id text_vocab) and n_past + 1 into the context's step tables; z2h_step_resident(ctx, n) then runs
+ * the next step of the same n columns from those tables without any host upload, leaving the logits
+ * on the device (enqueued, not synchronized). Any other step, prefill or sample clears the tables. */
+int z2h_sample_feed(z2h_ctx * ctx, int n_active, const z2h_sampling * sp, const int32_t * hist, const int32_t * hist_len,
+                    int hist_cap, const double * u, int32_t * codes);
+int z2h_step_resident(z2h_ctx * ctx, int n_active);
+
 /* Debug capture of per-layer intermediates of the following steps (off by default). */
 enum {
     Z2H_CAP_RES_IN = 0, Z2H_CAP_ATTN_IN, Z2H_CAP_Q, Z2H_CAP_K, Z2H_CAP_V, Z2H_CAP_GATE, Z2H_CAP_ATTN_O,

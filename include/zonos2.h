@@ -139,6 +139,12 @@ struct zonos2_batch_ctx {
     std::vector<float>   h_compact;   // [n_active][ncb][av] when the active slots are not 0..n-1
     int last_n = 0;                   // columns of the last step (their slot indices: h_slot[0, last_n))
     bool device_sampling = false;     // steps keep the logits on the GPU for zonos2_batch_sample
+    // device-resident tables: zonos2_batch_sample left the next step's inputs of the last step's
+    // columns on the GPU (fed_ids [last_n][W]); a step over the same slots with those next_ids runs
+    // from them without host packing
+    bool resident = false;
+    std::vector<int32_t> fed_ids;
+    std::vector<int32_t> h_slot_prev, h_npast_prev;   // the last step's columns and rows
 };
 
 // Per-slot decode state (graph-facing only; the sampler and output codes live with the caller).

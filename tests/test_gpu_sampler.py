@@ -77,3 +77,41 @@ def test_device_sampler_on_step_logits(ctx):
     np.testing.assert_array_equal(got, _oracle_codes(logits, sp, u, hist, hlen, 1))
     greedy = c.sample([SETTINGS[4]] * n, u)
     np.testing.assert_array_equal(greedy, logits.argmax(axis=2))
+
+
+def test_resident_decode_loop_matches_host_loop():
+    """Device-resident tables: z2h_sample_feed + z2h_step_resident for 12 frames gives the same codes
+    (and K/V rows) as host steps fed with the same codes (next ids = codes + the text pad, n_past + 1)
+    and z2h_sample on their logits, with the same draws."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 43)
+    n, ncb, W = wl.n_slots, cfg.n_codebooks, cfg.n_codebooks + 1
+    a = Context(cfg.hparams(), wl.n_slots, wl.slot_cap); a.upload(model)
+    b = Context(cfg.hparams(), wl.n_slots, wl.slot_cap); b.upload(model)
+    rng = np.random.default_rng(21)
+    slots = np.arange(n)
+    npast = np.array([3, 17, 40, 9], np.int32)[:n]
+    ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (n, ncb)), np.full((n, 1), cfg.text_vocab)], axis=1).astype(np.int32)
+    sp = [SETTINGS[i % 4] for i in range(n)]
+    a.step(slots, npast, ids=ids)
+    b.step(slots, npast, ids=ids)
+    for f in range(12):
+        print(f"frame {f}", flush=True)
+        u = rng.random((n, ncb))
+        ca = a.sample_feed(sp, u)
+        cb_ = b.sample(sp, u)
+        np.testing.assert_array_equal(ca, cb_)
+        npast = npast + 1
+        a.step_resident(n)
+        b.step(slots, npast, ids=np.concatenate([cb_, np.full((n, 1), cfg.text_vocab, np.int32)], axis=1))
+    u = rng.random((n, ncb))
+    np.testing.assert_array_equal(a.sample(sp, u), b.sample(sp, u))
+    for L in range(cfg.n_layer):
+        for s in range(n):
+            ka, va = a.kv_read(L, s, 0, int(npast[s]) + 1)
+            kb, vb = b.kv_read(L, s, 0, int(npast[s]) + 1)
+            np.testing.assert_array_equal(ka, kb)
+            np.testing.assert_array_equal(va, vb)
+    with pytest.raises(Exception):
+        a.step_resident(n)                                           # the tables were consumed
+    a.close(); b.close()

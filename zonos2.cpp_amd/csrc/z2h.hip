@@ -118,6 +118,8 @@ struct z2h_ctx {
     SampleParams * d_sp = nullptr; int32_t * d_hist = nullptr, * d_hlen = nullptr, * d_codes = nullptr;
     double * d_u = nullptr;
     uint8_t * h_samp = nullptr;
+    int resident_T = 0;               // columns whose next-step inputs z2h_sample_feed left in d_ids / d_npast
+    int resident_last = 0;            // width of the last step whose inputs and logits are in d_* / logits
 
     // HIP graphs of the whole step, one per (batch width, embedding-injection) pair
     bool use_graphs = true;
@@ -1191,11 +1193,14 @@ int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_p
     HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + T, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
     if (ids) HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * ctx->W * 4, hipMemcpyHostToDevice, ctx->stream));
     if (emb) HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+    ctx->resident_T = ctx->resident_last = 0;
     if (int rc = step_internal(ctx, T, n_past, ids != nullptr)) return rc;
     const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
     if (out_logits) HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
-    return check_err_flag(ctx);
+    if (int rc = check_err_flag(ctx)) return rc;
+    ctx->resident_last = T;
+    return Z2H_OK;
 }
 
 int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t * d_npast, const int32_t * h_npast,
@@ -1205,6 +1210,7 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
     hipStream_t keep = ctx->stream;
     if (stream) ctx->stream = (hipStream_t) stream;
     int rc = Z2H_OK;
+    ctx->resident_T = ctx->resident_last = 0;
     if (ctx->use_graphs && !ctx->capture && !ctx->prof) {
         // inputs into the context's fixed buffers, replay, logits out
         const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
@@ -1217,6 +1223,7 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
             rc = seterr(ctx, Z2H_EDEVICE, "input copy failed");
         if (!rc) rc = step_internal(ctx, T, h_npast, d_ids != nullptr);
         if (!rc && !cp(d_logits, ctx->logits, nout * 4)) rc = seterr(ctx, Z2H_EDEVICE, "logits copy failed");
+        if (!rc && d_ids) ctx->resident_last = T;
     } else {
         rc = run_step(ctx, T, h_npast, d_slot, d_npast, d_ids, d_emb, d_logits);
     }
@@ -1263,6 +1270,7 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
         if ((!spk || i / W != spk_pos) && (ids[i] < 0 || ids[i] >= ctx->m->tab_rows[k])) return seterr(ctx, Z2H_EINVAL, "token id out of range");
     }
     HIPX(hipSetDevice(ctx->device));
+    ctx->resident_T = ctx->resident_last = 0;
     std::vector<float> sp;
     if (spk) {
         sp.resize(ctx->hp.n_embd);
@@ -1473,8 +1481,8 @@ int64_t z2h_device_bytes(const z2h_ctx * ctx, int what) {
 
 const char * z2h_last_error(const z2h_ctx * ctx) { return ctx ? ctx->err.c_str() : "null context"; }
 
-int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
-               const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes) {
+static int sample_impl(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
+                       const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes, bool feed) {
     static_assert(sizeof(z2h_sampling) == sizeof(SampleParams), "z2h_sampling layout");
     if (!ctx || !sp || !u || !codes) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
@@ -1511,10 +1519,41 @@ int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sa
     a.u = ctx->d_u; a.codes = ctx->d_codes;
     KL(k_sample, dim3(ncb, n_active), dim3(256), sample_lds_bytes(av, np2), ctx->stream, a);
     HIPX(hipGetLastError());
+    ctx->resident_T = 0;
+    if (feed) {
+        ctx->resident_last = 0;                      // the tables now hold the next step's inputs
+        KL(k_feed, dim3(n_active), dim3(64), 0, ctx->stream, ctx->d_codes, ncb, ctx->W, (int) ctx->hp.text_vocab,
+           ctx->d_ids, ctx->d_npast);
+        HIPX(hipGetLastError());
+    }
     int32_t * hc_out = (int32_t *) (hu + (size_t) n_active * ncb);
     HIPX(hipMemcpyAsync(hc_out, ctx->d_codes, (size_t) n_active * ncb * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
     std::memcpy(codes, hc_out, (size_t) n_active * ncb * 4);
+    if (feed) ctx->resident_T = n_active;
+    return Z2H_OK;
+}
+
+int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sampling * sp, const int32_t * hist,
+               const int32_t * hist_len, int hist_cap, const double * u, int32_t * codes) {
+    return sample_impl(ctx, n_active, d_logits, sp, hist, hist_len, hist_cap, u, codes, false);
+}
+
+int z2h_sample_feed(z2h_ctx * ctx, int n_active, const z2h_sampling * sp, const int32_t * hist, const int32_t * hist_len,
+                    int hist_cap, const double * u, int32_t * codes) {
+    if (ctx && (ctx->resident_last != n_active)) return seterr(ctx, Z2H_ESTATE, "z2h_sample_feed: the last step had another width or no device tables");
+    return sample_impl(ctx, n_active, nullptr, sp, hist, hist_len, hist_cap, u, codes, true);
+}
+
+int z2h_step_resident(z2h_ctx * ctx, int n_active) {
+    if (!ctx) return Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (n_active <= 0 || n_active != ctx->resident_T)
+        return seterr(ctx, Z2H_ESTATE, "z2h_step_resident: no fed device tables of this width (z2h_sample_feed)");
+    HIPX(hipSetDevice(ctx->device));
+    ctx->resident_T = 0;
+    if (int rc = step_internal(ctx, n_active, nullptr, true)) return rc;
+    ctx->resident_last = n_active;
     return Z2H_OK;
 }
 

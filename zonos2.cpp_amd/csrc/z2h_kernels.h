@@ -1926,6 +1926,14 @@ __global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
     *out = code;
 }
 
+// Device-resident step tables for the next step: column i's input frame = its sampled codes + the
+// text pad id, and its row n_past + 1 (the slot indices stay).
+__global__ void __launch_bounds__(64) k_feed(const int32_t * codes, int ncb, int W, int text_pad, int32_t * ids, int32_t * n_past) {
+    const int i = blockIdx.x, l = threadIdx.x;
+    if (l < W) ids[(int64_t) i * W + l] = l < ncb ? codes[(int64_t) i * ncb + l] : text_pad;
+    if (l == 0) n_past[i] = n_past[i] + 1;
+}
+
 // KV rows between the host layout [n][nkv][hd] (staged in device memory) and the cache layout
 // [slot][kvh][S][hd]: dir 0 writes the cache, dir 1 reads it into the staging buffer.
 __global__ void __launch_bounds__(256) k_kv_move(uint4 * stage, uint16_t * cache, int n, int nkv, int hd, int S,

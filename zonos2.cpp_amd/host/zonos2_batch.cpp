@@ -269,6 +269,23 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
     if (!dense) bc.h_compact.resize((size_t) n * row);
     float * out = dense ? bc.h_logits.data() : bc.h_compact.data();
     if (!sync_layer_skip(*bc.model)) { fail("step: layer skip"); return; }
+    // the same columns as the last step, each one row further, fed by the device sampler: run from
+    // the device-resident tables
+    bool resident = bc.resident && bc.device_sampling && n == bc.last_n && (int) bc.fed_ids.size() == n * W;
+    for (int i = 0; resident && i < n; ++i)
+        resident = run[i]->index == bc.h_slot_prev[i] && run[i]->n_past == bc.h_npast_prev[i] + 1 &&
+                   std::equal(run[i]->next_ids.begin(), run[i]->next_ids.begin() + W, bc.fed_ids.begin() + (size_t) i * W);
+    bc.resident = false;
+    if (resident) {
+        if (int rc = z2h_step_resident(bc.dev, n)) {
+            fail("step failed (status " + std::to_string(rc) + "): " + z2h_last_error(bc.dev));
+            return;
+        }
+        for (int i = 0; i < n; ++i) { bc.h_slot_prev[i] = run[i]->index; bc.h_npast_prev[i] = run[i]->n_past; }
+        bc.last_n = n;
+        for (zonos2_slot * sp : run) sp->n_past += 1;
+        return;
+    }
     bc.last_n = 0;
     if (int rc = z2h_step(bc.dev, n, bc.h_slot.data(), bc.h_npast.data(), bc.h_ids.data(), nullptr,
                           bc.device_sampling ? nullptr : out)) {
@@ -276,6 +293,8 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
         return;
     }
     bc.last_n = n;
+    bc.h_slot_prev.assign(bc.h_slot.begin(), bc.h_slot.begin() + n);
+    bc.h_npast_prev.assign(bc.h_npast.begin(), bc.h_npast.begin() + n);
     if (!dense && !bc.device_sampling)
         for (int i = 0; i < n; ++i)
             std::memcpy(&bc.h_logits[(size_t) run[i]->index * row], &out[(size_t) i * row], row * 4);
@@ -327,8 +346,13 @@ bool zonos2_batch_sample(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *>
                 u[(size_t) c * ncb + cb] = std::generate_canonical<double, std::numeric_limits<double>::digits>(smp.rng);
         }
     }
-    if (int rc = z2h_sample(bc.dev, n, nullptr, sp.data(), hist.data(), hlen.data(), cap, u.data(), codes.data()))
+    if (int rc = z2h_sample_feed(bc.dev, n, sp.data(), hist.data(), hlen.data(), cap, u.data(), codes.data()))
         return fail("sample failed (status " + std::to_string(rc) + "): " + z2h_last_error(bc.dev));
+    // the next step's inputs now wait on the GPU, by column
+    bc.fed_ids.assign((size_t) n * bc.W, (int32_t) bc.model->hp.text_vocab);
+    for (int c = 0; c < n; ++c)
+        for (int cb = 0; cb < ncb; ++cb) bc.fed_ids[(size_t) c * bc.W + cb] = codes[(size_t) c * ncb + cb];
+    bc.resident = true;
     if (keep) keep->assign(n, 1);
     for (int i = 0; i < n; ++i) {
         const std::vector<int> frame(codes.begin() + (size_t) col[i] * ncb, codes.begin() + (size_t) (col[i] + 1) * ncb);

@@ -63,6 +63,8 @@ def lib() -> C.CDLL:
         "z2h_profile_end": (i32, [vp, vp, vp]),
         "z2h_sample": (i32, [vp, i32, vp, vp, vp, vp, i32, vp, vp]),
         "z2h_set_prefill_chunk": (i32, [vp, i32]),
+        "z2h_sample_feed": (i32, [vp, i32, vp, vp, vp, i32, vp, vp]),
+        "z2h_step_resident": (i32, [vp, i32]),
         "z2h_last_error": (C.c_char_p, [vp]),
         "z2h_destroy": (None, [vp]),
     }
@@ -78,6 +80,7 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
            "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample", "z2h_set_prefill_chunk",
+           "z2h_sample_feed", "z2h_step_resident",
            "z2h_last_error", "z2h_destroy")
 KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
                    "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
@@ -204,6 +207,23 @@ class Context:
         out = np.empty(self.hp["n_codebooks"] * self.hp["audio_vocab"], np.float32)
         self.check(lib().z2h_prefill(self.ctx, slot, _p(ids), ids.shape[0], _p(spk), spk_pos, _p(delta), _p(out)))
         return out
+
+    def sample_feed(self, sp, u, hist=None, hist_len=None):
+        """z2h_sample_feed: sample the last step's columns and leave their next inputs on the device."""
+        n = len(sp)
+        arr = (Sampling * n)(*[Sampling(**d) for d in sp])
+        u = np.ascontiguousarray(u, np.float64)
+        codes = np.empty((n, self.hp["n_codebooks"]), np.int32)
+        cap = 0
+        if hist is not None:
+            hist = np.ascontiguousarray(hist, np.int32)
+            hist_len = np.ascontiguousarray(hist_len, np.int32)
+            cap = hist.shape[-1]
+        self.check(lib().z2h_sample_feed(self.ctx, n, C.cast(arr, C.c_void_p), _p(hist), _p(hist_len), cap, _p(u), _p(codes)))
+        return codes
+
+    def step_resident(self, n: int):
+        self.check(lib().z2h_step_resident(self.ctx, n))
 
     def set_prefill_chunk(self, rows: int):
         self.check(lib().z2h_set_prefill_chunk(self.ctx, rows))
