@@ -129,7 +129,7 @@ int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, con
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits);
 
-/* Rows per prefill chunk (1 .. Z2H_PREFILL_CHUNK_MAX, at most 1024 / max top-k; default the maximum).
+/* Rows per prefill chunk (1 .. Z2H_PREFILL_CHUNK_MAX; default the maximum).
  * A chunk's rows go through each layer together (the projections and expert matmuls see them as one
  * batch; every row appends its K/V before the chunk's attention), so a prompt of n0 rows takes
  * ceil(n0 / rows) passes instead of n0 single-row steps. Any chunk size gives the same results. No

@@ -284,3 +284,22 @@ def test_chunked_prefill_is_chunk_size_independent():
         else:
             want = O.step(om, okv, [slot], [t], ids=ids[t:t + 1])
     assert_close("chunked prefill vs oracle steps", outs[2], want[0])
+
+
+def test_route_lists_in_lds_match_the_sorted_table():
+    """Grouped matmuls list an expert's routes in LDS (small batches) or read k_route_sort's table
+    (large batches, and whenever captures are on): both are the same stable grouping, so the step's
+    logits are identical with capture on and off."""
+    cfg, wl = configs.C2()
+    model = synth.generate_model(cfg, 44)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    rng = np.random.default_rng(8)
+    emb = rng.standard_normal((wl.n_slots, cfg.n_embd)).astype(np.float32)
+    slots, npast = np.arange(wl.n_slots), np.zeros(wl.n_slots, np.int32)
+    ctx.set_capture(True)
+    a = ctx.step(slots, npast, emb=emb)
+    ctx.set_capture(False)
+    b = ctx.step(slots, npast, emb=emb)
+    np.testing.assert_array_equal(a, b)
+    ctx.close()

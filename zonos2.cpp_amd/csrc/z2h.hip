@@ -109,6 +109,7 @@ struct z2h_ctx {
     float * state = nullptr;          // [L][T][rd]
     float * state_ext = nullptr;      // [T][rd] external state for moe_forward
     int32_t * sel = nullptr; float * wsel = nullptr;
+    int32_t * r_off = nullptr, * r_perm = nullptr;   // routes grouped by expert ([E+1] offsets, [T*k] ids)
     float * gu_g = nullptr, * gu_u = nullptr, * eo = nullptr, * logits = nullptr, * tmp_x = nullptr;
     int * d_err = nullptr;
     int32_t * h_pin = nullptr;        // pinned staging for step inputs
@@ -400,7 +401,7 @@ int alloc_scratch(z2h_ctx * ctx) {
     const auto & hp = ctx->hp;
     // rows: a step's columns, or a prefill chunk of up to Z2H_PREFILL_CHUNK_MAX prompt rows (capped so a
     // chunk's routes fit the grouped GEMVs' route lists)
-    const int pmax = std::max(1, std::min(Z2H_PREFILL_CHUNK_MAX, MAX_ROUTES / std::max(1, ctx->kmax)));
+    const int pmax = Z2H_PREFILL_CHUNK_MAX;
     const int T = std::max(ctx->n_slots, pmax), d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     const int ff = hp.n_ff, K = ctx->kmax, E = std::max(1, hp.n_expert), rd = std::max(1, ctx->rd);
     ctx->Tmax = T;
@@ -433,6 +434,7 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->attn_o, (size_t) T * nh * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->state, (size_t) hp.n_layer * T * rd * 4, b)) || (rc = dalloc(ctx, &ctx->state_ext, (size_t) T * rd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->sel, (size_t) T * K * 4, b)) || (rc = dalloc(ctx, &ctx->wsel, (size_t) T * K * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->r_off, (size_t) (E + 1) * 4, b)) || (rc = dalloc(ctx, &ctx->r_perm, (size_t) T * K * 4, b)) ||
         (rc = dalloc(ctx, &ctx->gu_g, (size_t) T * K * std::max(ff, 1) * 4, b)) || (rc = dalloc(ctx, &ctx->gu_u, (size_t) T * K * std::max(ff, 1) * 4, b)) ||
         (rc = dalloc(ctx, &ctx->eo, (size_t) T * K * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->logits, (size_t) T * hp.n_codebooks * hp.audio_vocab * 4, b)) ||
@@ -645,6 +647,17 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         KL(k_router_tail, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }
+    // routes grouped by expert (mul_mat_id's grouping): the grouped matmul blocks list up to LIST_MAX
+    // routes in LDS themselves; larger batches, and captures, take one sort kernel's table
+    const bool sorted = ctx->capture || T * ly.k > LIST_MAX;
+    if (sorted) {
+        prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
+        int32_t * cc = ctx->capture ? (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L) : nullptr;
+        int32_t * co = ctx->capture ? (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L) : nullptr;
+        int32_t * cp = ctx->capture ? (int32_t *) capp(ctx, Z2H_CAP_PERM, L) : nullptr;
+        KL(k_route_sort, dim3(1), dim3(1024), 0, ctx->stream, (const int32_t *) ctx->sel, T * ly.k, ly.E, ctx->r_off, ctx->r_perm, cc, co, cp);
+        HIPX(hipGetLastError());
+    }
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_SEL, L, ctx->sel, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_WEIGHTS, L, ctx->wsel, T))) return rc;
@@ -653,17 +666,14 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         GemvArgs g{};
         g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E; g.mode = MM_SWIGLU;
         g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_g; g.out_ld = hp.n_ff; g.epi = EPI_STORE;
-        if (ctx->capture) {
-            g.cap_counts = (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L);
-            g.cap_offsets = (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L);
-            g.cap_perm = (int32_t *) capp(ctx, Z2H_CAP_PERM, L);
-        }
+        g.r_off = sorted ? ctx->r_off : nullptr; g.r_perm = sorted ? ctx->r_perm : nullptr;
         if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ly.E, Z2H_KF_GEMV_GATEUP))) return rc;
         if ((rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T * ly.k, act_of(ly.down_exps.type), ctx->act_y))) return rc;
         GemvArgs dn{};
         dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
         dn.act = ctx->act_y; dn.act_by_route = 1;
         dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
+        dn.r_off = sorted ? ctx->r_off : nullptr; dn.r_perm = sorted ? ctx->r_perm : nullptr;
         if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ly.E, Z2H_KF_GEMV_DOWN))) return rc;
         return cap_copy(ctx, Z2H_CAP_EXPERT_OUT, L, ctx->eo, T);
     }
@@ -671,11 +681,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     GemvArgs g{};
     g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E;
     g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_u; g.out_ld = hp.n_ff; g.epi = EPI_STORE;
-    if (ctx->capture) {
-        g.cap_counts = (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L);
-        g.cap_offsets = (int32_t *) capp(ctx, Z2H_CAP_OFFSETS, L);
-        g.cap_perm = (int32_t *) capp(ctx, Z2H_CAP_PERM, L);
-    }
+    g.r_off = sorted ? ctx->r_off : nullptr; g.r_perm = sorted ? ctx->r_perm : nullptr;
     if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ly.E, Z2H_KF_GEMV_GATEUP))) return rc;
     // y = up * silu(gate) per route, encoded once for the down matmul
     if ((rc = launch_swiglu(ctx, T * ly.k, act_of(ly.down_exps.type)))) return rc;
@@ -684,6 +690,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
     dn.act = ctx->act_y; dn.act_by_route = 1;
     dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
+    dn.r_off = sorted ? ctx->r_off : nullptr; dn.r_perm = sorted ? ctx->r_perm : nullptr;
     if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ly.E, Z2H_KF_GEMV_DOWN))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_EXPERT_OUT, L, ctx->eo, T))) return rc;
     return Z2H_OK;
@@ -1107,7 +1114,7 @@ int z2h_finalize(z2h_ctx * ctx) {
     if (ctx->finalized) return Z2H_OK;
     if (int rc = z2h_model_finalize(ctx->m)) { ctx->err = ctx->m->err; return rc; }
     const auto & hp = ctx->hp;
-    if ((int64_t) ctx->n_slots * ctx->kmax > MAX_ROUTES) return seterr(ctx, Z2H_ENOTSUP, "n_slots * top_k exceeds the route list");
+    if (hp.n_expert > SORT_EMAX) return seterr(ctx, Z2H_ENOTSUP, "more experts than the route sort handles (256)");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));
     // allow each kernel the rest of gfx950's 160 KiB of LDS (beyond its static LDS) for its dynamic
@@ -1305,8 +1312,7 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
 int z2h_set_prefill_chunk(z2h_ctx * ctx, int rows) {
     if (!ctx) return Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
-    const int pmax = std::max(1, std::min(Z2H_PREFILL_CHUNK_MAX, MAX_ROUTES / std::max(1, ctx->kmax)));
-    if (rows <= 0 || rows > pmax) return seterr(ctx, Z2H_EINVAL, "prefill chunk out of range");
+    if (rows <= 0 || rows > Z2H_PREFILL_CHUNK_MAX) return seterr(ctx, Z2H_EINVAL, "prefill chunk out of range");
     ctx->pch = rows;
     return Z2H_OK;
 }

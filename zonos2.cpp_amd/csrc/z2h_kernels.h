@@ -38,7 +38,6 @@ enum { ACT_NONE = -1, ACT_F16 = 1, ACT_Q8_0 = 8, ACT_Q8_K = 15 };
 constexpr int NT = 16;          // tokens (or routes) per GEMV pass
 constexpr int TILE = 64;        // rows per tile = lanes per wave
 constexpr int ATT_CH = 32;      // attention rows per chunk (<= 64)
-constexpr int MAX_ROUTES = 1024; // top-k routes per step a grouped GEMV can list
 
 template <int WF> struct wfmt;
 template <> struct wfmt<WF_Q4_K> { static constexpr int C = 9;  static constexpr int ACT = ACT_Q8_K; };
@@ -389,8 +388,71 @@ struct GemvArgs {
     // output
     float * out[2]; int out_ld;        // out[m][row-index][rows]; row-index = token or route
     int epi; float cap; const float * route_w;
-    int32_t * cap_counts; int32_t * cap_offsets; int32_t * cap_perm; int E;
+    int E;
+    const int32_t * r_off;             // grouped: [E+1] route offsets by expert (k_route_sort)
+    const int32_t * r_perm;            // grouped: [n_tok*k] flat route ids in expert order
 };
+
+// The grouping of mul_mat_id's routes by expert, as a stable counting sort of the flat top-k ids
+// (route r = token * k + j): counts per expert (LDS atomics), exclusive offsets, then every route's
+// position = offset of its expert + routes of that expert before it. One 1024-thread block; routes
+// are placed 1024 at a time in order, each wave ranking its 64 routes per distinct expert with
+// ballots and the waves' counts prefix-summed in wave order, so the order within an expert is the
+// flat route order. E <= SORT_EMAX.
+constexpr int SORT_EMAX = 256;
+constexpr int LIST_MAX = 1024;   // routes a grouped matmul block lists in LDS itself (without k_route_sort)
+__global__ void __launch_bounds__(1024) k_route_sort(const int32_t * sel, int n_routes, int E, int32_t * off, int32_t * perm,
+                                                     int32_t * cap_counts, int32_t * cap_off, int32_t * cap_perm) {
+    __shared__ int s_cnt[SORT_EMAX], s_off[SORT_EMAX + 1], s_run[SORT_EMAX];
+    __shared__ int s_wc[16][SORT_EMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 1024) { s_cnt[e] = 0; s_run[e] = 0; }
+    __syncthreads();
+    for (int r = tid; r < n_routes; r += 1024) atomicAdd(&s_cnt[sel[r]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) { s_off[e] = acc; acc += s_cnt[e]; }
+        s_off[E] = acc;
+    }
+    __syncthreads();
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int base = 0; base < n_routes; base += 1024) {
+        const int r = base + tid;
+        const bool valid = r < n_routes;
+        const int me = valid ? sel[r] : -1;
+        for (int e = lane; e < E; e += 64) s_wc[wave][e] = 0;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        int rank = 0;
+        uint64_t todo = __ballot(valid);
+        while (todo) {
+            const int leader = __ffsll((unsigned long long) todo) - 1;
+            const int e0 = __shfl(me, leader, 64);
+            const uint64_t m = __ballot(valid && me == e0);
+            if (me == e0) rank = __popcll(m & lt);
+            if (lane == 0) s_wc[wave][e0] = __popcll(m);
+            todo &= ~m;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += 1024) {            // per expert: routes before each wave
+            int acc = s_run[e];
+            for (int w = 0; w < 16; ++w) { const int c = s_wc[w][e]; s_wc[w][e] = acc; acc += c; }
+            s_run[e] = acc;
+        }
+        __syncthreads();
+        if (valid) perm[s_off[me] + s_wc[wave][me] + rank] = r;
+        __syncthreads();
+    }
+    for (int e = tid; e <= E; e += 1024) off[e] = s_off[e];
+    if (cap_counts) {
+        for (int e = tid; e < E; e += 1024) cap_counts[e] = s_cnt[e];
+        for (int e = tid; e <= E; e += 1024) cap_off[e] = s_off[e];
+        __syncthreads();
+        for (int r = tid; r < n_routes; r += 1024) cap_perm[r] = perm[r];
+    }
+}
 
 // Routes of expert e in ascending flat order (the stable counting sort of mul_mat_id's grouping).
 __device__ __forceinline__ int build_route_list(const int32_t * sel, int n_routes, int e, int * list, int * wcount) {
@@ -411,6 +473,14 @@ __device__ __forceinline__ int build_route_list(const int32_t * sel, int n_route
         total += add;
     }
     return total;
+}
+
+// The routes of expert e for a grouped matmul block: from k_route_sort's table when given (r_perm),
+// else listed in LDS by the block (lds, at most LIST_MAX routes). Same stable order either way.
+__device__ __forceinline__ const int32_t * expert_routes(const GemvArgs & a, int e, int * lds, int * wcount, int & n_items) {
+    if (a.r_perm) { n_items = a.r_off[e + 1] - a.r_off[e]; return a.r_perm + a.r_off[e]; }
+    n_items = build_route_list(a.sel, a.n_tok * a.k, e, lds, wcount);
+    return lds;
 }
 
 template <int WF>
@@ -575,7 +645,7 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
     constexpr int AF = wfmt<WF>::ACT;
     constexpr int C = wfmt<WF>::C;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     const int K = a.nsb * 256, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.x, m = blockIdx.z;
@@ -597,24 +667,10 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
     // which rows (tokens / routes) this block serves
     int n_items, item0 = 0;
     int e = 0;
+    const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
         e = blockIdx.y;
-        n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
-        if (a.cap_counts && tile == 0 && m == 0) {                   // grouping capture, one block per expert
-            if (tid == 0) a.cap_counts[e] = n_items;
-            for (int i = tid; i < n_items; i += 256) {
-                int off = 0;
-                for (int r = 0; r < a.n_tok * a.k; ++r) off += a.sel[r] < e;
-                a.cap_perm[off + i] = s_list[i];
-                if (i == 0) a.cap_offsets[e] = off;
-            }
-            if (n_items == 0 && tid == 0) {
-                int off = 0;
-                for (int r = 0; r < a.n_tok * a.k; ++r) off += a.sel[r] < e;
-                a.cap_offsets[e] = off;
-            }
-            if (e == a.E - 1 && tid == 0) a.cap_offsets[a.E] = a.n_tok * a.k;
-        }
+        s_list = expert_routes(a, e, s_lds, s_wcnt, n_items);
         if (n_items == 0) return;
     } else {
         item0 = blockIdx.y * a.tpb;
@@ -696,7 +752,7 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
     constexpr int AF = wfmt<WF>::ACT;
     constexpr int C = wfmt<WF>::C;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     const int K = a.nsb * 256, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.x * 4 + wave, m = blockIdx.z, e = blockIdx.y;
@@ -713,17 +769,8 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
     } else {
         sh = (uint16_t *) p; p += NTE * K * 2;
     }
-    const int n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
-    if (a.cap_counts && blockIdx.x == 0 && m == 0) {                // grouping capture, one block per expert
-        int off = 0;
-        for (int r = 0; r < a.n_tok * a.k; ++r) off += a.sel[r] < e;
-        for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
-        if (tid == 0) {
-            a.cap_counts[e] = n_items;
-            a.cap_offsets[e] = off;
-            if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
-        }
-    }
+    int n_items;
+    const int32_t * s_list = expert_routes(a, e, s_lds, s_wcnt, n_items);
     if (n_items == 0) return;
     const bool has_tile = tile < a.tiles;
     const uint8_t * wbase = a.w[m] + (int64_t) e * a.mat_bytes;
@@ -932,7 +979,7 @@ k_gemv_mfma(GemvArgs a) {
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     __shared__ int s_tok[ROWS];
     const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -944,19 +991,10 @@ k_gemv_mfma(GemvArgs a) {
     float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32))  // Q4_K: [ROWS][K/256]
                                  : (float *) (smem + ROWS * KP);     // Q8_0: [ROWS][K/32]
     int n_items, c0, e = 0;
+    const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
         e = blockIdx.y;
-        n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
-        if (a.cap_counts && blockIdx.x == 0 && blockIdx.z == 0) {
-            int off = 0;
-            for (int rr = 0; rr < a.n_tok * a.k; ++rr) off += a.sel[rr] < e;
-            for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
-            if (tid == 0) {
-                a.cap_counts[e] = n_items;
-                a.cap_offsets[e] = off;
-                if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
-            }
-        }
+        s_list = expert_routes(a, e, s_lds, s_wcnt, n_items);
         c0 = pass * ROWS;
     } else {
         n_items = a.n_tok;
@@ -987,23 +1025,27 @@ k_gemv_mfma(GemvArgs a) {
     __syncthreads();
     if (!has) return;
     float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < U; c += PF) {
+    // units [u0, u1) into acc (DUAL: the gate matrix's, then the up matrix's); unit u sits in ring
+    // slot u % PF (u0 is a multiple of PF: PF divides nsb), and the ring's next load may belong to the
+    // following phase
+    static_assert(PF == 1 || !DUAL, "the dual phases assume PF divides nsb");
+    auto run_units = [&](int u0, int u1, float (&acc)[4]) {
+        for (int c = u0; c < u1; c += PF) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int u = c + j;
-            if (u < U) {
-                float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
-                if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
-                const bool first = !DUAL || u < nsb;
+            for (int j = 0; j < PF; ++j) {
+                const int u = c + j;
+                if (u < u1) {
+                    float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
+                    if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    acc0[i] = first ? acc0[i] + t4[i] : acc0[i];
-                    acc1[i] = first ? acc1[i] : acc1[i] + t4[i];
+                    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + t4[i];
                 }
             }
         }
-    }
+    };
+    run_units(0, nsb, acc0);
+    if (DUAL) run_units(nsb, U, acc1);
     const int q = lane >> 4, row = g16 * 16 + (lane & 15);
     if (row < a.rows) {
 #pragma unroll
@@ -1032,7 +1074,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ int s_list[MAX_ROUTES];
+    __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     __shared__ int s_tok[ROWS];
     __shared__ float s_part[4][8][64];
@@ -1042,19 +1084,10 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     int * sbs2 = (int *) (smem + ROWS * KP);
     float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32)) : (float *) (smem + ROWS * KP);
     int e = 0, m = 0, n_items, c0;
+    const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
         e = blockIdx.y;
-        n_items = build_route_list(a.sel, a.n_tok * a.k, e, s_list, s_wcnt);
-        if (a.cap_counts && blockIdx.x == 0 && blockIdx.z == 0) {   // grouping capture, one block per expert
-            int off = 0;
-            for (int rr = 0; rr < a.n_tok * a.k; ++rr) off += a.sel[rr] < e;
-            for (int i = tid; i < n_items; i += 256) a.cap_perm[off + i] = s_list[i];
-            if (tid == 0) {
-                a.cap_counts[e] = n_items;
-                a.cap_offsets[e] = off;
-                if (e == a.E - 1) a.cap_offsets[a.E] = a.n_tok * a.k;
-            }
-        }
+        s_list = expert_routes(a, e, s_lds, s_wcnt, n_items);
         c0 = blockIdx.z * ROWS;
     } else {
         m = DUAL ? 0 : blockIdx.z;
