@@ -84,6 +84,10 @@ void z2h_model_release(z2h_model * m);
  * z2h_finalize). n_slots decode slots of slot_cap_frames rows each (rounded up to a multiple of 256,
  * as the reference does); the KV cache is zero-filled. */
 int z2h_create_batch(z2h_model * m, int n_slots, int slot_cap_frames, z2h_ctx ** out);
+/* The same with room for max_rows rows per pass (z2h_step_mixed, z2h_moe_forward; at least n_slots
+ * and Z2H_PREFILL_CHUNK_MAX); the step scratch grows with it (about 0.2 MB per row at d_model 2048,
+ * plus attention partials for max_rows x slot_cap / 32 chunks). No reference counterpart. */
+int z2h_create_batch_rows(z2h_model * m, int n_slots, int slot_cap_frames, int max_rows, z2h_ctx ** out);
 
 /* A new model on HIP device `device` and a batch context over it (which then holds the model's only
  * reference) in one call. */
@@ -128,6 +132,17 @@ int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, con
  * row's [n_codebooks][audio_vocab] logits. */
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits);
+
+/* One pass over n_rows rows from any slots, decode columns and prefill-chunk rows mixed (the
+ * reference has no mixed pass; it is its zonos2_batch_step and zonos2_batch_slot_prefill graphs in
+ * one, src/zonos2-graph.cpp:703-837). Row t writes slot_idx[t]'s cache row n_past[t] and attends to
+ * that slot's rows [0, n_past[t]], including rows of this pass: every row's K/V is appended before
+ * the attention. No two rows may share (slot, n_past). ids [n_rows][n_codebooks+1]; emb_map (NULL, or
+ * [n_rows]: -1 = the row sums its ids, e >= 0 = the row takes emb[e], e.g. a speaker prefix row) with
+ * emb [n_emb][n_embd]. out_logits [n_out][n_codebooks][audio_vocab] receives the logits of rows
+ * out_rows[0 .. n_out). n_rows is limited by the context's row capacity (z2h_create_batch_rows). */
+int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
+                   const int32_t * emb_map, const float * emb, int n_emb, int n_out, const int32_t * out_rows, float * out_logits);
 
 /* Rows per prefill chunk (1 .. Z2H_PREFILL_CHUNK_MAX; default the maximum).
  * A chunk's rows go through each layer together (the projections and expert matmuls see them as one

@@ -807,8 +807,12 @@ int orc_kv_read(const orc_kv * kv, int L, int slot, int row0, int n, uint16_t * 
 
 void orc_kv_free(orc_kv * kv) { delete kv; }
 
-int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
-             const int32_t * ids, const float * emb, float * logits, orc_capture * cap) {
+// rows_of_a_slot: several rows may belong to one slot (distinct n_past; all rows' K/V are appended
+// before the attention, so a slot's rows attend to each other causally); emb_map: per row -1 (ids)
+// or the row of emb it takes (NULL: every row takes emb[t] when emb is given).
+static int step_impl(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
+                     const int32_t * ids, const float * emb, const int32_t * emb_map, float * logits, orc_capture * cap,
+                     bool rows_of_a_slot) {
     if (!m || !m->finalized || !kv) return fail("model/kv not ready");
     if (!kv_fits(*m, *kv)) return fail("kv cache shape differs from the model");
     if (T <= 0 || !slot_idx || !n_past || (!ids && !emb) || !logits) return fail("bad step args");
@@ -817,13 +821,15 @@ int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const 
     for (int t = 0; t < T; ++t) {
         if (slot_idx[t] < 0 || slot_idx[t] >= kv->n_slots) return fail("slot out of range");
         if (n_past[t] < 0 || n_past[t] >= kv->S) return fail("n_past out of range");
-        for (int u = 0; u < t; ++u) if (slot_idx[u] == slot_idx[t]) return fail("duplicate slot");
+        for (int u = 0; u < t; ++u)
+            if (slot_idx[u] == slot_idx[t] && (!rows_of_a_slot || n_past[u] == n_past[t])) return fail("duplicate slot row");
     }
     // embedding sum in column order (graph.cpp:248-260), then emb_norm (graph.cpp:300)
     std::vector<float> x((size_t) T * d), res((size_t) T * d), cur((size_t) T * d), tmp(d);
     for (int t = 0; t < T; ++t) {
         float * e = &x[(int64_t) t * d];
-        if (emb) std::memcpy(e, emb + (int64_t) t * d, sizeof(float) * d);
+        const int er = emb ? (emb_map ? emb_map[t] : t) : -1;
+        if (er >= 0) std::memcpy(e, emb + (int64_t) er * d, sizeof(float) * d);
         else {
             for (int kk = 0; kk < W; ++kk) {
                 const tensor & tb = kk < hp.n_codebooks ? m->audio_embd[kk] : m->text_embd;
@@ -894,6 +900,16 @@ int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const 
     if (c > 0.0f)                                               // graph.cpp:359-362
         for (int64_t i = 0; i < (int64_t) T * nout; ++i) logits[i] = std::tanh(logits[i] * (1.0f / c)) * c;
     return 0;
+}
+
+int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
+             const int32_t * ids, const float * emb, float * logits, orc_capture * cap) {
+    return step_impl(m, kv, T, slot_idx, n_past, ids, emb, nullptr, logits, cap, false);
+}
+
+int orc_step_mixed(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
+                   const int32_t * ids, const int32_t * emb_map, const float * emb, float * logits) {
+    return step_impl(m, kv, T, slot_idx, n_past, ids, emb, emb_map, logits, nullptr, true);
 }
 
 int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n0,

@@ -87,6 +87,11 @@ int orc_step(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const 
 // Per-slot prefill of n0 prompt rows (ids [n0][W]); writes K/V rows [0,n0) of `slot` and the
 // last row's logits. spk (optional [spk_dim]) replaces row spk_pos's embedding by
 // spk_proj(spk_lda(spk)) (+ delta [d] if given).
+// Rows from any slots in one pass (several rows of a slot at distinct n_past attend to each other
+// causally: every row's K/V is appended before the attention); emb_map [T] (or NULL): -1 = the row
+// sums its ids, e >= 0 = the row takes emb[e]. logits [T][ncb*av].
+int orc_step_mixed(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx, const int32_t * n_past,
+                   const int32_t * ids, const int32_t * emb_map, const float * emb, float * logits);
 int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n0,
                 const float * spk, int spk_pos, const float * delta, float * last_logits);
 

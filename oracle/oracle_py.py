@@ -66,6 +66,7 @@ def lib() -> C.CDLL:
         "orc_f32_to_f16": (C.c_uint16, [f32]), "orc_f16_to_f32": (f32, [C.c_uint16]),
         "orc_sample": (i32, [vp, i32, f32, i32, f32, f32, f32, i32, i32, i32, vp, i32, C.c_double, i32]),
         "orc_exp_d": (C.c_double, [C.c_double]),
+        "orc_step_mixed": (i32, [vp, vp, i32, vp, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -254,3 +255,16 @@ def sample(logits, sp: dict, cb: int, u: float, hist=None, exp_mode: int = 1) ->
 
 def exp_d(x: float) -> float:
     return float(lib().orc_exp_d(float(x)))
+
+
+def step_mixed(model: "OracleModel", kv: "OracleKV", slot_idx, n_past, ids, emb_map=None, emb=None):
+    """orc_step_mixed: logits [T][ncb*av] of rows from any slots (a slot's rows causal in the pass)."""
+    si = np.ascontiguousarray(slot_idx, np.int32)
+    npast = np.ascontiguousarray(n_past, np.int32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    em = None if emb_map is None else np.ascontiguousarray(emb_map, np.int32)
+    e = None if emb is None else np.ascontiguousarray(emb, np.float32)
+    hp = model.hp
+    out = np.empty((len(si), hp["n_codebooks"] * hp["audio_vocab"]), np.float32)
+    check(lib().orc_step_mixed(model.m, kv.kv, len(si), ptr(si), ptr(npast), ptr(ids), ptr(em), ptr(e), ptr(out)))
+    return out

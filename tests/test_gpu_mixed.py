@@ -1,0 +1,94 @@
+"""Mixed batches (z2h_step_mixed): prefill-chunk rows of several slots and decode columns in one pass,
+against the oracle's mixed step (orc_step_mixed: every row's K/V appended before the attention, a
+slot's rows causal within the pass) at the full bar (cos >= 0.9999, max-abs <= 1e-2 per requested row),
+and bit for bit against the same rows run as separate passes (each row's arithmetic depends only on
+its own inputs and its slot's cache rows)."""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from helpers import assert_close
+from zonos2_amd import configs, synth
+from zonos2_amd.z2h import Context, Model
+
+pytestmark = pytest.mark.gpu
+
+
+def _ids(cfg, n, rng):
+    return np.concatenate([rng.integers(0, cfg.audio_vocab, (n, cfg.n_codebooks)),
+                           rng.integers(0, cfg.text_vocab + 1, (n, 1))], axis=1).astype(np.int32)
+
+
+def _fill(cfg, writers, slot, n, seed):
+    for L in range(cfg.n_layer):
+        k, v = synth.kv_rows(cfg, L, slot, n, seed)
+        for w in writers:
+            w(L, slot, 0, k, v)
+
+
+def _batch(cfg, rng, chunks, decodes):
+    """rows of prefill chunks [(slot, row0, n, speaker?)] then decode columns [(slot, n_past)]"""
+    slots, npast, ids, emap, groups = [], [], [], [], []
+    emb = []
+    for slot, r0, n, spk in chunks:
+        g = []
+        for i in range(n):
+            slots.append(slot); npast.append(r0 + i); g.append(len(slots) - 1)
+            if spk and i == 0:
+                emap.append(len(emb)); emb.append(rng.standard_normal(cfg.n_embd).astype(np.float32))
+            else:
+                emap.append(-1)
+        ids.append(_ids(cfg, n, rng))
+        groups.append(g)
+    for slot, np_ in decodes:
+        slots.append(slot); npast.append(np_); emap.append(-1); groups.append([len(slots) - 1])
+        ids.append(_ids(cfg, 1, rng))
+    return (np.array(slots, np.int32), np.array(npast, np.int32), np.concatenate(ids), np.array(emap, np.int32),
+            np.stack(emb) if emb else np.zeros((1, cfg.n_embd), np.float32), groups)
+
+
+@pytest.mark.parametrize("big", [False, True])
+def test_mixed_batch_vs_oracle_and_separate_passes(big):
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 49)
+    m = Model(cfg.hparams(), model)
+    rng = np.random.default_rng(60 + big)
+    if big:      # > 1024 routes: the grouped matmuls read the device route sort, 16 routes per pass
+        cap, max_rows = 700, 700
+        chunks, decodes = [(0, 0, 300, True), (1, 256, 300, False)], [(2, 17), (3, 300)]
+        pre = {1: 256, 2: 17, 3: 300}
+    else:
+        cap, max_rows = 131, 0
+        chunks, decodes = [(0, 0, 40, True), (1, 64, 36, False)], [(2, 17), (3, 64)]
+        pre = {1: 64, 2: 17, 3: 64}
+    slots, npast, ids, emap, emb, groups = _batch(cfg, rng, chunks, decodes)
+    out_rows = np.array([g[-1] for g in groups] + [5, groups[1][3]], np.int32)
+    print(f"rows {len(slots)}", flush=True)
+    ctx = Context(None, 4, cap, model=m, max_rows=max_rows)
+    om = O.OracleModel(cfg.hparams(), model)
+    okv = O.OracleKV(om, 4, cap)
+    for s, n in pre.items():
+        _fill(cfg, [ctx.kv_write, okv.write], s, n, 70 + s)
+    got = ctx.step_mixed(slots, npast, ids, out_rows, emb_map=emap, emb=emb)
+    want = O.step_mixed(om, okv, slots, npast, ids, emb_map=emap, emb=emb)[out_rows]
+    for i, r in enumerate(out_rows):
+        assert_close(f"mixed row {r}", got[i], want[i])
+    for s, r0, n, _ in chunks:
+        for L in range(cfg.n_layer):
+            gk, gv = ctx.kv_read(L, s, r0, n)
+            ok, ov = okv.read(L, s, r0, n)
+            assert_close(f"K rows slot {s} L{L}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32))
+            assert_close(f"V rows slot {s} L{L}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32))
+    # the same rows as separate passes (one per chunk / decode column) on a second context
+    ctx2 = Context(None, 4, cap, model=m, max_rows=max_rows)
+    for s, n in pre.items():
+        _fill(cfg, [ctx2.kv_write], s, n, 70 + s)
+    sep = {}
+    for g in groups:
+        gi = np.array(g)
+        lo = ctx2.step_mixed(slots[gi], npast[gi], ids[gi], np.arange(len(g)), emb_map=emap[gi], emb=emb)
+        for j, r in enumerate(g):
+            sep[r] = lo[j]
+    for i, r in enumerate(out_rows):
+        np.testing.assert_array_equal(got[i], sep[int(r)])
+    ctx.close(); ctx2.close(); m.close()

@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <set>
 #include <memory>
 #include <string>
 #include <thread>
@@ -100,6 +101,8 @@ struct z2h_ctx {
     int Tmax = 0, Kmax = 0, items_max = 0;   // Tmax: token rows of the scratch (steps and prefill chunks)
     int Tstep = 0;                    // columns a step may list (n_slots); captures are sized for it
     int pch = 0;                      // prefill chunk rows (<= Tmax)
+    int max_rows = 0;                 // requested row capacity (z2h_create_batch_rows)
+    int32_t * d_emb_map = nullptr;    // [Tmax] per-row embedding override
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
@@ -402,7 +405,7 @@ int alloc_scratch(z2h_ctx * ctx) {
     // rows: a step's columns, or a prefill chunk of up to Z2H_PREFILL_CHUNK_MAX prompt rows (capped so a
     // chunk's routes fit the grouped GEMVs' route lists)
     const int pmax = Z2H_PREFILL_CHUNK_MAX;
-    const int T = std::max(ctx->n_slots, pmax), d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
+    const int T = std::max({ctx->n_slots, pmax, ctx->max_rows}), d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     const int ff = hp.n_ff, K = ctx->kmax, E = std::max(1, hp.n_expert), rd = std::max(1, ctx->rd);
     ctx->Tmax = T;
     ctx->Tstep = ctx->n_slots;
@@ -435,6 +438,7 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->state, (size_t) hp.n_layer * T * rd * 4, b)) || (rc = dalloc(ctx, &ctx->state_ext, (size_t) T * rd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->sel, (size_t) T * K * 4, b)) || (rc = dalloc(ctx, &ctx->wsel, (size_t) T * K * 4, b)) ||
         (rc = dalloc(ctx, &ctx->r_off, (size_t) (E + 1) * 4, b)) || (rc = dalloc(ctx, &ctx->r_perm, (size_t) T * K * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->d_emb_map, (size_t) T * 4, b)) ||
         (rc = dalloc(ctx, &ctx->gu_g, (size_t) T * K * std::max(ff, 1) * 4, b)) || (rc = dalloc(ctx, &ctx->gu_u, (size_t) T * K * std::max(ff, 1) * 4, b)) ||
         (rc = dalloc(ctx, &ctx->eo, (size_t) T * K * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->logits, (size_t) T * hp.n_codebooks * hp.audio_vocab * 4, b)) ||
@@ -444,7 +448,7 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->spk_io, (size_t) (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
         return rc;
     (void) E;
-    ctx->h_pin_bytes = (size_t) T * (2 + W) * 4;
+    ctx->h_pin_bytes = (size_t) T * (3 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     const int ncb = std::max(1, (int) hp.n_codebooks);
@@ -510,7 +514,7 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     if (m0.m16) {
         // grouped: ROWS = MT_G routes per pass (an expert serves at most n_tok routes); dense: all
         // MT tokens of a chunk per pass, so each weight tile is read once
-        const int rows = a.grouped ? MT_G : MT;
+        const int rows = a.grouped && !a.r_perm ? MT_G : MT;   // large (sorted) batches: full 16-route MFMA passes
         const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
         const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
@@ -532,10 +536,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
 #define MM16(W_, D_, R_) KL((k_gemv_mfma<W_, D_, R_, R_ == MT_G ? m16fmt<W_>::GPF : 1>), grid, block, lds, ctx->stream, a)
         if (m0.type == Z2H_Q4_K) {
-            if (a.grouped) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
+            if (rows == MT_G) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
         } else {
-            if (a.grouped) { if (dual) MM16(WF_Q8_0, true, MT_G); else MM16(WF_Q8_0, false, MT_G); }
+            if (rows == MT_G) { if (dual) MM16(WF_Q8_0, true, MT_G); else MM16(WF_Q8_0, false, MT_G); }
             else { if (dual) MM16(WF_Q8_0, true, MT); else MM16(WF_Q8_0, false, MT); }
         }
 #undef MM16
@@ -718,10 +722,11 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
 }
 
 // The whole decode step on device-resident inputs in ctx->d_* (T tokens, host copy of n_past).
-// kv_pre: append every token's K/V row before the attention (prefill chunks, whose rows attend to
-// each other); emb_row >= 0: only that token takes d_emb (one row), the others d_ids.
+// kv_pre: append every token's K/V row before the attention (prefill chunks and mixed batches, whose
+// rows of one slot attend to each other); d_emb_map: per token -1 (sum of its ids) or its row of d_emb.
 int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
-             const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false, int emb_row = -1) {
+             const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false,
+             const int32_t * d_emb_map = nullptr) {
     const auto & hp = ctx->hp;
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
@@ -733,7 +738,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     const int n_run = (int) run.size();
     // embeddings + emb_norm + the first block's attn_norm (output_norm when every block is skipped)
     ResNormArgs e{};
-    e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb; e.emb_row = emb_row;
+    e.mode = RN_EMBED; e.ids = d_ids; e.W = ctx->W; e.emb_in = d_emb; e.emb_map = d_emb_map;
     for (int k = 0; k < ctx->W; ++k) { e.tab[k] = ctx->m->tab[k]; e.tab_type[k] = ctx->m->tab_type[k]; e.tab_rows[k] = ctx->m->tab_rows[k]; }
     e.res = ctx->res;
     if (n_run) {
@@ -1064,6 +1069,10 @@ void z2h_model_release(z2h_model * mdl) {
 }
 
 int z2h_create_batch(z2h_model * mdl, int n_slots, int slot_cap_frames, z2h_ctx ** out) {
+    return z2h_create_batch_rows(mdl, n_slots, slot_cap_frames, 0, out);
+}
+
+int z2h_create_batch_rows(z2h_model * mdl, int n_slots, int slot_cap_frames, int max_rows, z2h_ctx ** out) {
     if (!out) return Z2H_EINVAL;
     *out = nullptr;
     if (!mdl || n_slots <= 0 || slot_cap_frames <= 0) return Z2H_EINVAL;
@@ -1073,6 +1082,7 @@ int z2h_create_batch(z2h_model * mdl, int n_slots, int slot_cap_frames, z2h_ctx 
     c->m = mdl; ++mdl->refs;
     c->hp = mdl->hp;
     c->device = mdl->device; c->n_slots = n_slots;
+    c->max_rows = std::max(0, max_rows);
     c->S = ((slot_cap_frames + 255) / 256) * 256;
     c->W = mdl->W; c->rd = mdl->rd; c->kmax = mdl->kmax;
     const auto & hp = c->hp;
@@ -1297,15 +1307,73 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
         std::memcpy(hp_ + 2 * T, ids + (size_t) r0 * W, (size_t) T * W * 4);
         const int er = spk && spk_pos >= r0 && spk_pos < r0 + T ? spk_pos - r0 : -1;
         if (er >= 0) for (int k = 0; k < W; ++k) hp_[2 * T + er * W + k] = 0;      // the row's ids are unused
+        int32_t * map = hp_ + 2 * T + T * W;                         // -1 but for the speaker row
+        for (int t = 0; t < T; ++t) map[t] = t == er ? 0 : -1;
         HIPX(hipMemcpyAsync(ctx->d_slot, hp_, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
         HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + T, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
         HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * W * 4, hipMemcpyHostToDevice, ctx->stream));
-        if (er >= 0) HIPX(hipMemcpyAsync(ctx->d_emb, sp.data(), (size_t) ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (er >= 0) {
+            HIPX(hipMemcpyAsync(ctx->d_emb, sp.data(), (size_t) ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+            HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
+        }
         if (int rc = run_step(ctx, T, hp_ + T, ctx->d_slot, ctx->d_npast, ctx->d_ids, er >= 0 ? ctx->d_emb : nullptr,
-                              ctx->logits, /*kv_pre=*/true, er)) return rc;
+                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr)) return rc;
         if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits + (size_t) (T - 1) * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
         HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }
+    return check_err_flag(ctx);
+}
+
+int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
+                   const int32_t * emb_map, const float * emb, int n_emb, int n_out, const int32_t * out_rows, float * out_logits) {
+    if (!ctx || !slot_idx || !n_past || !ids || (n_out > 0 && (!out_rows || !out_logits)))
+        return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    if (n_rows <= 0 || n_rows > ctx->Tmax || (ctx->capture && n_rows > ctx->Tstep)) return seterr(ctx, Z2H_EINVAL, "n_rows out of range");
+    if (emb_map && (!emb || n_emb <= 0)) return seterr(ctx, Z2H_EINVAL, "emb_map without embedding rows");
+    const int W = ctx->W;
+    std::set<std::pair<int, int>> seen;
+    for (int t = 0; t < n_rows; ++t) {
+        if (slot_idx[t] < 0 || slot_idx[t] >= ctx->n_slots) return seterr(ctx, Z2H_EINVAL, "slot index out of range");
+        if (n_past[t] < 0 || n_past[t] >= ctx->S) return seterr(ctx, Z2H_EINVAL, "n_past out of range");
+        if (!seen.insert({slot_idx[t], n_past[t]}).second) return seterr(ctx, Z2H_EINVAL, "two rows write the same cache row");
+        const int em = emb_map ? emb_map[t] : -1;
+        if (em < -1 || em >= n_emb) return seterr(ctx, Z2H_EINVAL, "emb_map entry out of range");
+        if (em < 0)
+            for (int k = 0; k < W; ++k) {
+                const int id = ids[(size_t) t * W + k];
+                if (id < 0 || id >= ctx->m->tab_rows[k]) return seterr(ctx, Z2H_EINVAL, "token id out of range");
+            }
+    }
+    for (int i = 0; i < n_out; ++i)
+        if (out_rows[i] < 0 || out_rows[i] >= n_rows) return seterr(ctx, Z2H_EINVAL, "out_rows entry out of range");
+    if (emb_map && (size_t) n_emb * ctx->hp.n_embd > (size_t) ctx->Tmax * ctx->hp.n_embd) return seterr(ctx, Z2H_EINVAL, "too many embedding rows");
+    HIPX(hipSetDevice(ctx->device));
+    ctx->resident_T = ctx->resident_last = 0;
+    int32_t * hp_ = ctx->h_pin;
+    std::memcpy(hp_, slot_idx, (size_t) n_rows * 4);
+    std::memcpy(hp_ + n_rows, n_past, (size_t) n_rows * 4);
+    int32_t * hid = hp_ + 2 * n_rows;
+    std::memcpy(hid, ids, (size_t) n_rows * W * 4);
+    int32_t * map = hid + (size_t) n_rows * W;
+    for (int t = 0; t < n_rows; ++t) {
+        map[t] = emb_map ? emb_map[t] : -1;
+        if (map[t] >= 0) for (int k = 0; k < W; ++k) hid[(size_t) t * W + k] = 0;     // unused ids
+    }
+    HIPX(hipMemcpyAsync(ctx->d_slot, hp_, (size_t) n_rows * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPX(hipMemcpyAsync(ctx->d_npast, hp_ + n_rows, (size_t) n_rows * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPX(hipMemcpyAsync(ctx->d_ids, hid, (size_t) n_rows * W * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (emb_map) {
+        HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) n_rows * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) n_emb * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    // every row appends its K/V before the attention; a slot's rows attend causally to each other
+    if (int rc = run_step(ctx, n_rows, hp_ + n_rows, ctx->d_slot, ctx->d_npast, ctx->d_ids, emb_map ? ctx->d_emb : nullptr,
+                          ctx->logits, /*kv_pre=*/true, emb_map ? ctx->d_emb_map : nullptr)) return rc;
+    const size_t row = (size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab;
+    for (int i = 0; i < n_out; ++i)
+        HIPX(hipMemcpyAsync(out_logits + (size_t) i * row, ctx->logits + (size_t) out_rows[i] * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipStreamSynchronize(ctx->stream));
     return check_err_flag(ctx);
 }
 

@@ -215,8 +215,8 @@ constexpr int MAX_TABLES = 16;
 struct ResNormArgs {
     int mode, d;
     const int32_t * ids; int W;
-    const float * emb_in;              // [T][d] injected rows, or one row for token emb_row
-    int emb_row;                       // >= 0: only token emb_row takes emb_in (row 0), others ids
+    const float * emb_in;              // injected rows: [T][d], or rows picked by emb_map
+    const int32_t * emb_map;           // [T]: -1 = token t sums its ids, else its row of emb_in (NULL: row t)
     const uint8_t * tab[MAX_TABLES]; int tab_type[MAX_TABLES]; int64_t tab_rows[MAX_TABLES];
     const float * src; int k;         // ACCUM: [T*k][d] routes; ADD / ENCODE: [T][d]
     float * res;                       // [T][d] (ACCUM may pass null: no residual)
@@ -263,8 +263,9 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     }
     auto add4 = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
     if (a.mode == RN_EMBED) {
-        if (a.emb_in && (a.emb_row < 0 || t == a.emb_row)) {
-            const float * er = a.emb_in + (a.emb_row < 0 ? (int64_t) t * d : 0);
+        const int erow = a.emb_in ? (a.emb_map ? a.emb_map[t] : t) : -1;
+        if (erow >= 0) {
+            const float * er = a.emb_in + (int64_t) erow * d;
 #pragma unroll
             for (int j = 0; j < RN_NV; ++j) {
                 const int i0 = 4 * (tid + 256 * j);

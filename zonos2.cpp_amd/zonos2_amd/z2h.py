@@ -41,6 +41,8 @@ def lib() -> C.CDLL:
         "z2h_model_last_error": (C.c_char_p, [vp]),
         "z2h_model_release": (None, [vp]),
         "z2h_create_batch": (i32, [vp, i32, i32, C.POINTER(vp)]),
+        "z2h_create_batch_rows": (i32, [vp, i32, i32, i32, C.POINTER(vp)]),
+        "z2h_step_mixed": (i32, [vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, vp]),
         "z2h_create": (i32, [C.POINTER(Hparams), i32, i32, i32, C.POINTER(vp)]),
         "z2h_upload_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_int64), vp, C.c_size_t]),
         "z2h_finalize": (i32, [vp]),
@@ -80,7 +82,7 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
            "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample", "z2h_set_prefill_chunk",
-           "z2h_sample_feed", "z2h_step_resident",
+           "z2h_sample_feed", "z2h_step_resident", "z2h_create_batch_rows", "z2h_step_mixed",
            "z2h_last_error", "z2h_destroy")
 KERNEL_FAMILIES = ("resnorm", "gemv_qkv", "qkv_post", "attn", "attn_combine", "gemv_wo", "router_down", "router_tail",
                    "gemv_gateup", "gemv_down", "gemv_dense", "gemv_head", "swiglu")
@@ -150,11 +152,12 @@ class Context:
     """One decode-step context on a device (mirrors zonos2_batch_ctx). Built either from hparams (a
     private model, weights uploaded through upload()) or over a shared Model."""
 
-    def __init__(self, hp: dict | None, n_slots: int, slot_cap: int, device: int = 0, model: Model | None = None):
+    def __init__(self, hp: dict | None, n_slots: int, slot_cap: int, device: int = 0, model: Model | None = None,
+                 max_rows: int = 0):
         out = C.c_void_p()
         if model is not None:
             self.hp = dict(model.hp)
-            rc = lib().z2h_create_batch(model.m, n_slots, slot_cap, C.byref(out))
+            rc = lib().z2h_create_batch_rows(model.m, n_slots, slot_cap, max_rows, C.byref(out))
             if rc != OK:
                 raise Z2HError(rc, lib().z2h_model_last_error(model.m).decode())
         else:
@@ -224,6 +227,20 @@ class Context:
 
     def step_resident(self, n: int):
         self.check(lib().z2h_step_resident(self.ctx, n))
+
+    def step_mixed(self, slot_idx, n_past, ids, out_rows, emb_map=None, emb=None):
+        """z2h_step_mixed: rows from any slots (prefill chunks and decode columns); returns the logits
+        of out_rows [n_out][n_codebooks * audio_vocab]."""
+        si = np.ascontiguousarray(slot_idx, np.int32)
+        npast = np.ascontiguousarray(n_past, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        orow = np.ascontiguousarray(out_rows, np.int32)
+        em = None if emb_map is None else np.ascontiguousarray(emb_map, np.int32)
+        e = None if emb is None else np.ascontiguousarray(emb, np.float32)
+        out = np.empty((len(orow), self.hp["n_codebooks"] * self.hp["audio_vocab"]), np.float32)
+        self.check(lib().z2h_step_mixed(self.ctx, len(si), _p(si), _p(npast), _p(ids), _p(em), _p(e),
+                                        0 if e is None else e.shape[0], len(orow), _p(orow), _p(out)))
+        return out
 
     def set_prefill_chunk(self, rows: int):
         self.check(lib().z2h_set_prefill_chunk(self.ctx, rows))
