@@ -105,7 +105,7 @@ struct z2h_ctx {
     int32_t * d_emb_map = nullptr;    // [Tmax] per-row embedding override
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
-    float * res = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
+    float * res = nullptr, * res2 = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
     ActBuf act{}, act_y{};
     float * attn_o = nullptr;         // [T][nh*hd] gated attention output
@@ -420,7 +420,8 @@ int alloc_scratch(z2h_ctx * ctx) {
     const int W = ctx->W;
     if ((rc = dalloc(ctx, &ctx->d_slot, T * 4, b)) || (rc = dalloc(ctx, &ctx->d_npast, T * 4, b)) ||
         (rc = dalloc(ctx, &ctx->d_ids, (size_t) T * W * 4, b)) || (rc = dalloc(ctx, &ctx->d_emb, (size_t) T * d * 4, b)) ||
-        (rc = dalloc(ctx, &ctx->res, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->cur, (size_t) T * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->res, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->res2, (size_t) T * d * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->cur, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->tmp_x, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->qkvg, (size_t) T * R * 4, b)) ||
         (rc = dalloc(ctx, &ctx->wo_out, (size_t) T * d * 4, b)) ||
@@ -612,10 +613,8 @@ int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
     return Z2H_OK;
 }
 
-int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in) {
+RouterArgs router_args(z2h_ctx * ctx, const Layer & ly, int L, int T, const float * state_in) {
     const auto & hp = ctx->hp;
-    int rc;
-    // router (exact contract)
     RouterArgs r{};
     r.x = ctx->cur; r.T = T; r.d = hp.n_embd; r.rd = ctx->rd; r.E = ly.E; r.k = ly.k;
     r.w_down = ly.r_down; r.b_down = ly.r_down_b; r.eda = ly.r_eda; r.state_in = state_in;
@@ -626,11 +625,52 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     r.sel = ctx->sel; r.wsel = ctx->wsel;
     r.cap_logits = (float *) capp(ctx, Z2H_CAP_ROUTER_LOGITS, L);
     r.cap_probs = (float *) capp(ctx, Z2H_CAP_PROBS, L);
-    {
+    return r;
+}
+
+// router-down elements per lane: the next power of two >= ceil(d / 64); unguarded when d fills every lane
+int router_ni(int d) { return d <= 64 ? 1 : 1 << (32 - __builtin_clz((unsigned) ((d + 63) / 64 - 1))); }
+
+// An MoE layer's FFN entry as one launch (k_ffn_entry): res_out = res_in + src, x = ffn_norm(res_out)
+// into ctx->cur and the expert activations, router-down state of layer L.
+int launch_ffn_entry(z2h_ctx * ctx, const Layer & ly, int L, int T, const float * state_in,
+                     const float * src, const float * res_in, float * res_out) {
+    prof_scope ps(ctx, Z2H_KF_ROUTER_DOWN);
+    const auto & hp = ctx->hp;
+    const RouterArgs r = router_args(ctx, ly, L, T, state_in);
+    ResNormArgs f{};
+    f.mode = RN_ADD; f.d = hp.n_embd; f.src = src; f.res_in = res_in; f.res = res_out; f.norm_w = ly.ffn_norm;
+    f.eps = hp.rms_eps; f.cur_out = ctx->cur; f.act = ctx->act; f.act_fmt = act_of(ly.up_exps.type); f.err = ctx->d_err;
+    const dim3 grid((ctx->rd + 3) / 4, T);
+    const size_t lds = (size_t) kpad(hp.n_embd) * 4;
+    const int ni = router_ni(hp.n_embd);
+    const bool exact = hp.n_embd == 64 * ni;
+#define FEN(N_) do { if (exact) KL((k_ffn_entry<N_, false>), grid, dim3(256), lds, ctx->stream, f, r); \
+                     else KL((k_ffn_entry<N_, true>), grid, dim3(256), lds, ctx->stream, f, r); } while (0)
+    switch (ni) {
+        case 1: FEN(1); break;
+        case 2: FEN(2); break;
+        case 4: FEN(4); break;
+        case 8: FEN(8); break;
+        case 16: FEN(16); break;
+        case 32: FEN(32); break;
+        default: FEN(64); break;
+    }
+#undef FEN
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+// down_done: the router-down state of layer L is already in place (k_ffn_entry)
+int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in, bool down_done = false) {
+    const auto & hp = ctx->hp;
+    int rc;
+    // router (exact contract)
+    const RouterArgs r = router_args(ctx, ly, L, T, state_in);
+    if (!down_done) {
         prof_scope ps(ctx, Z2H_KF_ROUTER_DOWN);
         const dim3 grid((ctx->rd + 3) / 4, T);
-        // elements per lane: the next power of two >= ceil(d / 64); unguarded when d fills every lane
-        const int ni = hp.n_embd <= 64 ? 1 : 1 << (32 - __builtin_clz((unsigned) ((hp.n_embd + 63) / 64 - 1)));
+        const int ni = router_ni(hp.n_embd);
         const bool exact = hp.n_embd == 64 * ni;
 #define RDN(N_) do { if (exact) KL((k_router_down<N_, false>), grid, dim3(256), 0, ctx->stream, r); \
                      else KL((k_router_down<N_, true>), grid, dim3(256), 0, ctx->stream, r); } while (0)
@@ -676,6 +716,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         GemvArgs dn{};
         dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
         dn.act = ctx->act_y; dn.act_by_route = 1;
+
         dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
         dn.r_off = sorted ? ctx->r_off : nullptr; dn.r_perm = sorted ? ctx->r_perm : nullptr;
         if ((rc = launch_gemv(ctx, ly.down_exps, nullptr, dn, ly.E, Z2H_KF_GEMV_DOWN))) return rc;
@@ -803,20 +844,26 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         // W_o
         if ((rc = launch_gemv(ctx, ly.wo, nullptr, gemv_dense(ctx, T, ctx->wo_out, d, EPI_STORE), 1, Z2H_KF_GEMV_WO))) return rc;
         if ((rc = cap_copy(ctx, Z2H_CAP_ATTN_OUT, L, ctx->wo_out, T))) return rc;
-        // res += attn; ffn_norm; encode for the FFN
-        ResNormArgs f{};
-        f.mode = RN_ADD; f.src = ctx->wo_out; f.res = ctx->res; f.norm_w = ly.ffn_norm; f.cur_out = ctx->cur;
-        f.act = ctx->act; f.act_fmt = act_of(ly.moe ? ly.up_exps.type : ly.ffn_up.type);
-        if ((rc = launch_resnorm(ctx, T, f))) return rc;
-        if ((rc = cap_copy(ctx, Z2H_CAP_FFN_IN, L, ctx->cur, T))) return rc;
+        // res += attn; ffn_norm; encode for the FFN (MoE layers: with the router down projection, the
+        // new residual in res2 until the FFN output folds it back into res)
         if (ly.moe) {
             const float * st = prev_moe >= 0 ? ctx->state + (size_t) prev_moe * ctx->Tmax * ctx->rd : nullptr;
-            if ((rc = expert_block(ctx, ly, L, T, st))) return rc;
+            if ((rc = launch_ffn_entry(ctx, ly, L, T, st, ctx->wo_out, ctx->res, ctx->res2))) return rc;
+            if ((rc = cap_copy(ctx, Z2H_CAP_FFN_IN, L, ctx->cur, T))) return rc;
+            if ((rc = expert_block(ctx, ly, L, T, st, true))) return rc;
             prev_moe = L;
-        } else if ((rc = dense_block(ctx, ly, T))) return rc;
+        } else {
+            ResNormArgs f{};
+            f.mode = RN_ADD; f.src = ctx->wo_out; f.res = ctx->res; f.norm_w = ly.ffn_norm; f.cur_out = ctx->cur;
+            f.act = ctx->act; f.act_fmt = act_of(ly.ffn_up.type);
+            if ((rc = launch_resnorm(ctx, T, f))) return rc;
+            if ((rc = cap_copy(ctx, Z2H_CAP_FFN_IN, L, ctx->cur, T))) return rc;
+            if ((rc = dense_block(ctx, ly, T))) return rc;
+        }
         // fold the FFN output into the residual; next layer's attn_norm (or output_norm)
         ResNormArgs n{};
         n.mode = RN_ACCUM; n.src = ctx->eo; n.k = ly.moe ? ly.k : 1; n.res = ctx->res;
+        n.res_in = ly.moe ? ctx->res2 : nullptr;
         n.cap_x = (float *) capp(ctx, Z2H_CAP_FFN_OUT, L);
         const bool last = i + 1 == n_run;
         const int nx = last ? -1 : run[i + 1];

@@ -37,7 +37,7 @@ enum { ACT_NONE = -1, ACT_F16 = 1, ACT_Q8_0 = 8, ACT_Q8_K = 15 };
 
 constexpr int NT = 16;          // tokens (or routes) per GEMV pass
 constexpr int TILE = 64;        // rows per tile = lanes per wave
-constexpr int ATT_CH = 32;      // attention rows per chunk (<= 64)
+constexpr int ATT_CH = 64;      // attention rows per chunk (<= 64)
 
 template <int WF> struct wfmt;
 template <> struct wfmt<WF_Q4_K> { static constexpr int C = 9;  static constexpr int ACT = ACT_Q8_K; };
@@ -62,30 +62,34 @@ __device__ __forceinline__ void q8k_block(const float * x, int8_t * q, float * d
     const float v[4] = {x[lane * 4], x[lane * 4 + 1], x[lane * 4 + 2], x[lane * 4 + 3]};
     q8k_block_v(v, q, d, bs, lane);
 }
-__device__ __forceinline__ void q8k_block_v(const float (&v)[4], int8_t * q, float * d, int16_t * bs, int lane) {
+// The Q8_K values of the wave's 256-block (qi, 4 per lane) and its scale d (the same in every lane).
+__device__ __forceinline__ float q8k_quant(const float (&v)[4], int (&qi)[4]) {
     // largest |x| by a DPP max; its first occurrence (lowest element index lane*4+i) from ballots
     const float lmax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     const float amax = wave_max_f(lmax);
-    int qi[4];
     if (amax == 0.0f) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qi[i] = 0;
-        if (lane == 0) *d = 0.0f;
-    } else {
-        int best = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint64_t m = __ballot(fabsf(v[i]) == amax);
-            if (m) best = min(best, (int) (__ffsll((unsigned long long) m) - 1) * 4 + i);
-        }
-        const int bi = best & 3;
-        const float vb = bi == 0 ? v[0] : bi == 1 ? v[1] : bi == 2 ? v[2] : v[3];
-        const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vb), best >> 2));
-        const float iscale = -127.0f / bval;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qi[i] = min(127, (int) rintf(iscale * v[i]));
-        if (lane == 0) *d = 1.0f / iscale;
+        return 0.0f;
     }
+    int best = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t m = __ballot(fabsf(v[i]) == amax);
+        if (m) best = min(best, (int) (__ffsll((unsigned long long) m) - 1) * 4 + i);
+    }
+    const int bi = best & 3;
+    const float vb = bi == 0 ? v[0] : bi == 1 ? v[1] : bi == 2 ? v[2] : v[3];
+    const float bval = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vb), best >> 2));
+    const float iscale = -127.0f / bval;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qi[i] = min(127, (int) rintf(iscale * v[i]));
+    return 1.0f / iscale;
+}
+__device__ __forceinline__ void q8k_block_v(const float (&v)[4], int8_t * q, float * d, int16_t * bs, int lane) {
+    int qi[4];
+    const float dd = q8k_quant(v, qi);
+    if (lane == 0) *d = dd;
     const uint32_t packed = (uint32_t) (qi[0] & 255) | ((uint32_t) (qi[1] & 255) << 8) |
                             ((uint32_t) (qi[2] & 255) << 16) | ((uint32_t) (qi[3] & 255) << 24);
     *(uint32_t *) (q + lane * 4) = packed;
@@ -220,6 +224,7 @@ struct ResNormArgs {
     const uint8_t * tab[MAX_TABLES]; int tab_type[MAX_TABLES]; int64_t tab_rows[MAX_TABLES];
     const float * src; int k;         // ACCUM: [T*k][d] routes; ADD / ENCODE: [T][d]
     float * res;                       // [T][d] (ACCUM may pass null: no residual)
+    const float * res_in;              // ACCUM: residual read from here instead of res (null: res)
     const float * norm_w; float eps;
     float * cur_out;                   // [T][d] fp32 normalised row (nullable)
     ActBuf act; int act_fmt;
@@ -317,7 +322,8 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             float4 r[8];
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) if (jj < a.k) r[jj] = *(const float4 *) (src + (int64_t) jj * d + i0);
-            const float4 r0 = res ? *(const float4 *) (res + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float * rin = a.res_in ? a.res_in + (int64_t) t * d : res;
+            const float4 r0 = res ? *(const float4 *) (rin + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
             float4 x = r[0];
 #pragma unroll
             for (int jj = 1; jj < 8; ++jj) if (jj < a.k) x = add4(x, r[jj]);
@@ -1335,9 +1341,9 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         // arithmetic (rows past the chunk re-read its last row; the new row, still absent from the
         // cache, is overwritten below)
         constexpr int N4 = ATT_CH * RW;                              // uint4 per matrix
-        static_assert(N4 <= 512, "two 16-byte items per thread and matrix at most");
+        static_assert(N4 <= 1024, "four 16-byte items per thread and matrix at most");
         // (named registers: an array here is not promoted out of scratch)
-        uint4 k0, v0, k1 = {}, v1 = {};
+        uint4 k0, v0, k1 = {}, v1 = {}, k2 = {}, v2 = {}, k3 = {}, v3 = {};
         auto kv_at = [&](int i, uint4 & kk, uint4 & vv) {           // threads past N4 repeat the last item
             i = min(i, N4 - 1);
             const int r = min(i / RW, nr - 1), q4 = i % RW;
@@ -1346,6 +1352,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         };
         kv_at(tid, k0, v0);
         if constexpr (N4 > 256) kv_at(tid + 256, k1, v1);
+        if constexpr (N4 > 512) { kv_at(tid + 512, k2, v2); kv_at(tid + 768, k3, v3); }
         // ---- queries of the group (one wave per head), and the new k / v row (wave 3)
         uint32_t nk = 0, nv = 0;
         {
@@ -1386,13 +1393,14 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             *(uint4 *) &s_k[(tid / RW) * KST + 8 * (tid % RW)] = k0;
             *(uint4 *) &s_v[(tid / RW) * HD + 8 * (tid % RW)] = v0;
         }
-        if constexpr (N4 > 256) {
-            const int i = tid + 256;
+        auto kv_put = [&](int i, const uint4 & kk, const uint4 & vv) {
             if (i < N4) {
-                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = k1;
-                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = v1;
+                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = kk;
+                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = vv;
             }
-        }
+        };
+        if constexpr (N4 > 256) kv_put(tid + 256, k1, v1);
+        if constexpr (N4 > 512) { kv_put(tid + 512, k2, v2); kv_put(tid + 768, k3, v3); }
         __syncthreads();                                             // the chunk copy is in LDS
         if (mk && lane < NP) {                                       // replace the stale new row
             *(uint32_t *) &s_k[(nr - 1) * KST + 2 * lane] = nk;
@@ -1617,6 +1625,66 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     float v = wave_tree_f(acc) + b;
     if (a.eda && a.state_in) v = v + st;
     if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+}
+
+// An MoE layer's FFN entry in one launch: residual add, ffn_norm, the activation encoding for the
+// expert matmuls and the router down projection. Grid (ceil(rd/4), T), 256 threads. Every block of
+// token t forms x = rms_w(res_in + src) with k_resnorm's RN_ADD arithmetic (same element ownership,
+// double partial order and scale) into LDS; the blocks with blockIdx.x == 0 also store the new
+// residual to res_out (never in place: the token's other blocks still read res_in), x to cur_out and
+// its encoding. Wave w then forms router output o = 4 * blockIdx.x + w from the LDS row with
+// k_router_down's fma chain, so rh is bit-identical to the two-kernel path. The wave's router weights
+// are requested before the row loads.
+template <int NI, bool GUARD>
+__global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) {
+    extern __shared__ float xs[];      // [kpad(d)]
+    __shared__ double red[4];
+    const int t = blockIdx.y, d = f.d, tid = threadIdx.x, lane = tid & 63;
+    const int o = blockIdx.x * 4 + (tid >> 6);
+    const bool lead = blockIdx.x == 0, has_o = o < r.rd;
+    const float * __restrict__ w = r.w_down + (int64_t) (has_o ? o : 0) * d + lane;
+    float wv[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) wv[j] = !GUARD || lane + 64 * j < d ? w[64 * j] : 0.0f;
+    const float b = has_o ? r.b_down[o] : 0.0f;
+    const bool eda = r.eda && r.state_in;
+    const float st = has_o && eda ? r.state_in[(int64_t) t * r.rd + o] * r.eda[o] : 0.0f;
+    const float * __restrict__ src = f.src + (int64_t) t * d;
+    const float * __restrict__ rin = f.res_in + (int64_t) t * d;
+    float4 nw[RN_NV], xv[RN_NV];
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j) {
+        const int i0 = 4 * (tid + 256 * j);
+        if (i0 >= d) continue;
+        nw[j] = *(const float4 *) (f.norm_w + i0);
+        const float4 x = *(const float4 *) (src + i0), r0 = *(const float4 *) (rin + i0);
+        xv[j] = make_float4(x.x + r0.x, x.y + r0.y, x.z + r0.z, x.w + r0.w);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j)
+        if (4 * (tid + 256 * j) < d) ss += (double) (xv[j].x * xv[j].x) + (double) (xv[j].y * xv[j].y) + (double) (xv[j].z * xv[j].z) + (double) (xv[j].w * xv[j].w);
+    const double tot = block_sum_d(ss, red);
+    const float scale = 1.0f / sqrtf((float) (tot / (double) d) + f.eps);
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j) {
+        const int i0 = 4 * (tid + 256 * j);
+        if (i0 >= d) continue;
+        if (lead) *(float4 *) (f.res + (int64_t) t * d + i0) = xv[j];
+        xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
+        if (lead && f.cur_out) *(float4 *) (f.cur_out + (int64_t) t * d + i0) = xv[j];
+        *(float4 *) (xs + i0) = xv[j];
+    }
+    __syncthreads();
+    if (lead && f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
+    if (!has_o) return;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+        if (!GUARD || lane + 64 * j < d) acc = __builtin_fmaf(wv[j], xs[lane + 64 * j], acc);
+    float v = wave_tree_f(acc) + b;
+    if (eda) v = v + st;
+    if (lane == 0) r.rh[(int64_t) t * r.rd + o] = v;
 }
 
 // Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k, one
