@@ -608,7 +608,13 @@ int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
     prof_scope ps(ctx, Z2H_KF_RESNORM);
     if (!a.d) a.d = ctx->hp.n_embd;
     a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
-    KL(k_resnorm, dim3(T), dim3(256), (size_t) kpad(a.d) * 4, ctx->stream, a);
+    const size_t lds = (size_t) kpad(a.d) * 4;
+    switch (a.mode) {
+        case RN_EMBED: KL(k_resnorm<RN_EMBED>, dim3(T), dim3(256), lds, ctx->stream, a); break;
+        case RN_ACCUM: KL(k_resnorm<RN_ACCUM>, dim3(T), dim3(256), lds, ctx->stream, a); break;
+        case RN_ADD: KL(k_resnorm<RN_ADD>, dim3(T), dim3(256), lds, ctx->stream, a); break;
+        default: KL(k_resnorm<RN_ENCODE>, dim3(T), dim3(256), lds, ctx->stream, a); break;
+    }
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -1185,7 +1191,7 @@ int z2h_finalize(z2h_ctx * ctx) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
-    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm) LDS_ATTR(k_swiglu_encode)
+    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     (void) hp;
     ctx->graph_gen = ctx->m->gen;

@@ -252,8 +252,12 @@ __device__ __forceinline__ float4 table_elem4(const uint8_t * row, int type, int
 
 // One block per token; thread tid owns elements 4*(tid + 256*j) .. +3 (d % 4 == 0, d <= 4096). Every
 // global read the block needs (norm weight, routes, residual, embedding rows) is issued before the
-// first reduction.
+// first reduction and before the first store (a store between loads would order them: the
+// compiler cannot tell the residual row from the sources), and every global store comes after the
+// last barrier (a barrier waits for the block's outstanding stores). One instantiation per mode
+// keeps each kernel's code to its own path.
 constexpr int RN_NV = 4;
+template <int MODE>
 __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     extern __shared__ float sm_rn[];
     float * xs = sm_rn;                // [d]
@@ -261,13 +265,15 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     const int t = blockIdx.x, d = a.d, tid = threadIdx.x;
     float * res = a.res ? a.res + (int64_t) t * d : nullptr;
     float4 nw[RN_NV], xv[RN_NV];
+    float4 res_out[RN_NV], cap_out[RN_NV];          // stored at the end
+    bool st_res = false, st_cap = false;
 #pragma unroll
     for (int j = 0; j < RN_NV; ++j) {
         const int i0 = 4 * (tid + 256 * j);
         if (a.norm_w && i0 < d) nw[j] = *(const float4 *) (a.norm_w + i0);
     }
     auto add4 = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
-    if (a.mode == RN_EMBED) {
+    if constexpr (MODE == RN_EMBED) {
         const int erow = a.emb_in ? (a.emb_map ? a.emb_map[t] : t) : -1;
         if (erow >= 0) {
             const float * er = a.emb_in + (int64_t) erow * d;
@@ -310,37 +316,51 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             const int i0 = 4 * (tid + 256 * j);
             if (i0 >= d) continue;
             xv[j] = make_float4(xv[j].x * scale, xv[j].y * scale, xv[j].z * scale, xv[j].w * scale);
-            *(float4 *) (res + i0) = xv[j];
+            res_out[j] = xv[j];
         }
-    } else if (a.mode == RN_ACCUM) {
+        st_res = true;
+    } else if constexpr (MODE == RN_ACCUM) {
         // sum of the token's k routes in route order, + residual
         const float * __restrict__ src = a.src + ((int64_t) t * a.k) * d;
+        const float * rin = a.res_in ? a.res_in + (int64_t) t * d : res;
+        float4 r[RN_NV][8], r0[RN_NV];
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
             const int i0 = 4 * (tid + 256 * j);
             if (i0 >= d) continue;
-            float4 r[8];
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) if (jj < a.k) r[jj] = *(const float4 *) (src + (int64_t) jj * d + i0);
-            const float * rin = a.res_in ? a.res_in + (int64_t) t * d : res;
-            const float4 r0 = res ? *(const float4 *) (rin + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
-            float4 x = r[0];
+            for (int jj = 0; jj < 8; ++jj) if (jj < a.k) r[j][jj] = *(const float4 *) (src + (int64_t) jj * d + i0);
+            r0[j] = res ? *(const float4 *) (rin + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
 #pragma unroll
-            for (int jj = 1; jj < 8; ++jj) if (jj < a.k) x = add4(x, r[jj]);
-            if (a.cap_x) *(float4 *) (a.cap_x + (int64_t) t * d + i0) = x;
-            if (res) { x = add4(x, r0); *(float4 *) (res + i0) = x; }
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 >= d) continue;
+            float4 x = r[j][0];
+#pragma unroll
+            for (int jj = 1; jj < 8; ++jj) if (jj < a.k) x = add4(x, r[j][jj]);
+            cap_out[j] = x;
+            if (res) { x = add4(x, r0[j]); res_out[j] = x; }
             xv[j] = x;
         }
-    } else if (a.mode == RN_ADD) {
+        st_cap = a.cap_x != nullptr;
+        st_res = res != nullptr;
+    } else if constexpr (MODE == RN_ADD) {
         const float * __restrict__ src = a.src + (int64_t) t * d;
+        float4 x[RN_NV], r0[RN_NV];
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 < d) { x[j] = *(const float4 *) (src + i0); r0[j] = *(const float4 *) (res + i0); }
+        }
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
             const int i0 = 4 * (tid + 256 * j);
             if (i0 >= d) continue;
-            const float4 x = *(const float4 *) (src + i0), r0 = *(const float4 *) (res + i0);
-            xv[j] = add4(x, r0);
-            *(float4 *) (res + i0) = xv[j];
+            xv[j] = add4(x[j], r0[j]);
+            res_out[j] = xv[j];
         }
+        st_res = true;
     } else {
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
@@ -360,18 +380,26 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             const int i0 = 4 * (tid + 256 * j);
             if (i0 >= d) continue;
             xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
-            if (a.cur_out) *(float4 *) (a.cur_out + (int64_t) t * d + i0) = xv[j];
         }
     }
-    if (a.act_fmt == ACT_NONE) return;
-    // the encoders read the row from LDS (a 256-block spans the elements of 64 threads)
+    if (a.act_fmt != ACT_NONE) {
+        // the encoders read the row from LDS (a 256-block spans the elements of 64 threads)
+#pragma unroll
+        for (int j = 0; j < RN_NV; ++j) {
+            const int i0 = 4 * (tid + 256 * j);
+            if (i0 < d) *(float4 *) (xs + i0) = xv[j];
+        }
+        __syncthreads();
+        encode_row_rt(a.act_fmt, xs, d, a.act, t);
+    }
 #pragma unroll
     for (int j = 0; j < RN_NV; ++j) {
         const int i0 = 4 * (tid + 256 * j);
-        if (i0 < d) *(float4 *) (xs + i0) = xv[j];
+        if (i0 >= d) continue;
+        if (st_res) *(float4 *) (res + i0) = res_out[j];
+        if (st_cap) *(float4 *) (a.cap_x + (int64_t) t * d + i0) = cap_out[j];
+        if (a.norm_w && a.cur_out) *(float4 *) (a.cur_out + (int64_t) t * d + i0) = xv[j];
     }
-    __syncthreads();
-    encode_row_rt(a.act_fmt, xs, d, a.act, t);
 }
 
 // ------------------------------------------------------------------ k_gemv
@@ -1295,8 +1323,8 @@ __device__ __forceinline__ void norm_rope(float x0, float x1, float mul, float e
 // KV head g). The block requests the chunk's K and V rows with coalesced 16-byte loads and, while
 // they are in flight, forms the group's queries from the fused projection output (per-head RMSNorm,
 // |temp|, interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, f16);
-// the chunk that holds the new row also forms k and v, appends them to the f16 cache and to the
-// LDS copy. Then every thread scores one (row, head) pair (f16 dot products, fp32 accumulation), one
+// the chunk that holds the new row also forms k and v, puts them in the LDS copy and, with the
+// partials after the last barrier (a barrier waits for earlier stores), in the f16 cache. Then every thread scores one (row, head) pair (f16 dot products, fp32 accumulation), one
 // wave per head reduces the chunk's softmax partial (max, sum of exp; lane = row), and every thread accumulates
 // one (head, dim pair) of the unnormalised P.V over the chunk's rows. k_attn_combine merges chunks.
 template <int HD, int GRP>
@@ -1380,8 +1408,6 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
                     const float v0 = xq[HPW + 1][0], v1 = xq[HPW + 1][1];
                     nk = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
                     nv = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
-                    *(uint32_t *) (a.kc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nk;
-                    *(uint32_t *) (a.vc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nv;
                     if (a.cap_k) {
                         a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane] = k0; a.cap_k[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = k1;
                         a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane] = v0; a.cap_v[((int64_t) t * nkv + g) * HD + 2 * lane + 1] = v1;
@@ -1421,17 +1447,17 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
         }
         __syncthreads();
-        // ---- per-head chunk softmax partial (lane = row)
-        for (int h = wave; h < GRP; h += 4) {
+        // ---- per-head chunk softmax partial (lane = row); (max, sum) stored with the outputs
+        float2 ml[(GRP + 3) / 4];
+#pragma unroll
+        for (int i = 0; i < (GRP + 3) / 4; ++i) {
+            const int h = wave + 4 * i;
+            if (h >= GRP) break;
             const float sv = lane < ATT_CH ? s_p[min(lane, ATT_CH - 1)][h] : -__builtin_inff();
             const float mx = wave_max_f(sv);
             const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
-            const float l = wave_tree_f(pe);
+            ml[i] = make_float2(mx, wave_tree_f(pe));
             if (lane < ATT_CH) s_p[lane][h] = pe;
-            if (lane == 0) {
-                a.part_ml[((int64_t) item * GRP + h) * 2 + 0] = mx;
-                a.part_ml[((int64_t) item * GRP + h) * 2 + 1] = l;
-            }
         }
         __syncthreads();
         // ---- P.V: one (head, dim pair) per thread, rows in order
@@ -1447,7 +1473,16 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             }
             *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
         }
-        __syncthreads();                                             // LDS reuse by the next item
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < (GRP + 3) / 4; ++i)
+                if (wave + 4 * i < GRP) *(float2 *) (a.part_ml + ((int64_t) item * GRP + wave + 4 * i) * 2) = ml[i];
+        }
+        if (mk && lane < NP) {                                       // the new row into the cache
+            *(uint32_t *) (a.kc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nk;
+            *(uint32_t *) (a.vc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nv;
+        }
+        if (item + (int) gridDim.x < n_items) __syncthreads();      // LDS reuse by the next item
     }
 }
 
@@ -1630,11 +1665,12 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
 // An MoE layer's FFN entry in one launch: residual add, ffn_norm, the activation encoding for the
 // expert matmuls and the router down projection. Grid (ceil(rd/4), T), 256 threads. Every block of
 // token t forms x = rms_w(res_in + src) with k_resnorm's RN_ADD arithmetic (same element ownership,
-// double partial order and scale) into LDS; the blocks with blockIdx.x == 0 also store the new
-// residual to res_out (never in place: the token's other blocks still read res_in), x to cur_out and
-// its encoding. Wave w then forms router output o = 4 * blockIdx.x + w from the LDS row with
-// k_router_down's fma chain, so rh is bit-identical to the two-kernel path. The wave's router weights
-// are requested before the row loads.
+// double partial order and scale) into LDS. Wave w then forms router output o = 4 * blockIdx.x + w
+// from the LDS row with k_router_down's fma chain, so rh is bit-identical to the two-kernel path; the
+// blocks with blockIdx.x == 0 then store the new residual to res_out (never in place: the token's
+// other blocks still read res_in), x to cur_out and its encoding, all after the block's only barrier
+// (a barrier waits for the stores issued before it). The wave's router weights are requested
+// before the row loads.
 template <int NI, bool GUARD>
 __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) {
     extern __shared__ float xs[];      // [kpad(d)]
@@ -1666,25 +1702,34 @@ __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) 
         if (4 * (tid + 256 * j) < d) ss += (double) (xv[j].x * xv[j].x) + (double) (xv[j].y * xv[j].y) + (double) (xv[j].z * xv[j].z) + (double) (xv[j].w * xv[j].w);
     const double tot = block_sum_d(ss, red);
     const float scale = 1.0f / sqrtf((float) (tot / (double) d) + f.eps);
+    float4 hv[RN_NV];                  // the new residual (stored after the barrier)
 #pragma unroll
     for (int j = 0; j < RN_NV; ++j) {
         const int i0 = 4 * (tid + 256 * j);
         if (i0 >= d) continue;
-        if (lead) *(float4 *) (f.res + (int64_t) t * d + i0) = xv[j];
+        hv[j] = xv[j];
         xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
-        if (lead && f.cur_out) *(float4 *) (f.cur_out + (int64_t) t * d + i0) = xv[j];
         *(float4 *) (xs + i0) = xv[j];
     }
     __syncthreads();
-    if (lead && f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
-    if (!has_o) return;
-    float acc = 0.0f;
+    if (has_o) {
+        float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NI; ++j)
-        if (!GUARD || lane + 64 * j < d) acc = __builtin_fmaf(wv[j], xs[lane + 64 * j], acc);
-    float v = wave_tree_f(acc) + b;
-    if (eda) v = v + st;
-    if (lane == 0) r.rh[(int64_t) t * r.rd + o] = v;
+        for (int j = 0; j < NI; ++j)
+            if (!GUARD || lane + 64 * j < d) acc = __builtin_fmaf(wv[j], xs[lane + 64 * j], acc);
+        float v = wave_tree_f(acc) + b;
+        if (eda) v = v + st;
+        if (lane == 0) r.rh[(int64_t) t * r.rd + o] = v;
+    }
+    if (!lead) return;
+    if (f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
+#pragma unroll
+    for (int j = 0; j < RN_NV; ++j) {
+        const int i0 = 4 * (tid + 256 * j);
+        if (i0 >= d) continue;
+        *(float4 *) (f.res + (int64_t) t * d + i0) = hv[j];
+        if (f.cur_out) *(float4 *) (f.cur_out + (int64_t) t * d + i0) = xv[j];
+    }
 }
 
 // Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k, one
