@@ -105,10 +105,10 @@ __device__ __forceinline__ float z_sigmoid(float x) { return 1.0f / (1.0f + z_ex
 
 // Reductions over the 64 lanes with the tree of an xor butterfly (offsets 32, 16, 8, 4, 2, 1): at each
 // level a node adds the two nodes of the level below that differ in one lane bit. Only lane 0's
-// chain of the tree is formed (lane i < off adds lane i + off), the two cross-row levels by lane
-// shuffles and the four in-row levels by DPP row shifts; lane 0's value is then broadcast. Every
-// addition is the one the butterfly makes (a + b and b + a are the same IEEE value), so the result
-// equals the butterfly's bit for bit.
+// chain of the tree is formed (lane i < off adds lane i + off), the two cross-row levels by gfx950's
+// lane-swap instructions and the four in-row levels by DPP row shifts, none of which goes through
+// LDS; lane 0's value is then broadcast. Every addition is the one the butterfly makes (a + b and
+// b + a are the same IEEE value), so the result equals the butterfly's bit for bit.
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
 template <int CTRL>
@@ -120,6 +120,28 @@ __device__ __forceinline__ double dpp_d(double v) {
     return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
 }
 constexpr int DPP_ROW_SHL = 0x100;     // lane i reads lane i + n of its 16-lane row
+// Lane i < 32 receives lane i + 32 (v_permlane32_swap trades rows 2-3 of its first operand for rows
+// 0-1 of its second; with both operands v the second's rows 0-1 become v's rows 2-3).
+__device__ __forceinline__ int up32_i(int v) {
+    return (int) __builtin_amdgcn_permlane32_swap((unsigned) v, (unsigned) v, false, false)[1];
+}
+// Lane i of rows 0 and 2 receives lane i + 16 (v_permlane16_swap: rows 1 and 3 of the first operand
+// for rows 0 and 2 of the second).
+__device__ __forceinline__ int up16_i(int v) {
+    return (int) __builtin_amdgcn_permlane16_swap((unsigned) v, (unsigned) v, false, false)[1];
+}
+__device__ __forceinline__ float up32_f(float v) { return __builtin_bit_cast(float, up32_i(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ float up16_f(float v) { return __builtin_bit_cast(float, up16_i(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ double up32_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t) up32_i((int) (uint32_t) u), hi = (uint32_t) up32_i((int) (uint32_t) (u >> 32));
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
+}
+__device__ __forceinline__ double up16_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t) up16_i((int) (uint32_t) u), hi = (uint32_t) up16_i((int) (uint32_t) (u >> 32));
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
+}
 constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
 __device__ __forceinline__ float lane0_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)); }
@@ -131,8 +153,8 @@ __device__ __forceinline__ double lane0_d(double v) {
 }
 
 __device__ __forceinline__ float wave_tree_f(float v) {
-    v = v + __shfl_down(v, 32, WAVE);
-    v = v + __shfl_down(v, 16, WAVE);
+    v = v + up32_f(v);
+    v = v + up16_f(v);
     v = v + dpp_f<DPP_ROW_SHL + 8>(v);
     v = v + dpp_f<DPP_ROW_SHL + 4>(v);
     v = v + dpp_f<DPP_ROW_SHL + 2>(v);
@@ -140,8 +162,8 @@ __device__ __forceinline__ float wave_tree_f(float v) {
     return lane0_f(v);
 }
 __device__ __forceinline__ double wave_tree_d(double v) {
-    v = v + __shfl_down(v, 32, WAVE);
-    v = v + __shfl_down(v, 16, WAVE);
+    v = v + up32_d(v);
+    v = v + up16_d(v);
     v = v + dpp_d<DPP_ROW_SHL + 8>(v);
     v = v + dpp_d<DPP_ROW_SHL + 4>(v);
     v = v + dpp_d<DPP_ROW_SHL + 2>(v);
@@ -149,8 +171,8 @@ __device__ __forceinline__ double wave_tree_d(double v) {
     return lane0_d(v);
 }
 __device__ __forceinline__ float wave_max_f(float v) {
-    v = fmaxf(v, __shfl_down(v, 32, WAVE));
-    v = fmaxf(v, __shfl_down(v, 16, WAVE));
+    v = fmaxf(v, up32_f(v));
+    v = fmaxf(v, up16_f(v));
     v = fmaxf(v, dpp_f<DPP_ROW_SHL + 8>(v));
     v = fmaxf(v, dpp_f<DPP_ROW_SHL + 4>(v));
     v = fmaxf(v, dpp_f<DPP_ROW_SHL + 2>(v));
@@ -158,8 +180,8 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return lane0_f(v);
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-    v += __shfl_down(v, 32, WAVE);
-    v += __shfl_down(v, 16, WAVE);
+    v += up32_i(v);
+    v += up16_i(v);
     v += dpp_i<DPP_ROW_SHL + 8>(v);
     v += dpp_i<DPP_ROW_SHL + 4>(v);
     v += dpp_i<DPP_ROW_SHL + 2>(v);

@@ -1250,13 +1250,18 @@ struct AttnArgs {
 // an inclusive scan of the per-token chunk counts locates an item, so the cost is one load per 64
 // tokens instead of a chain of dependent loads per token.
 __device__ __forceinline__ int wave_scan_incl(int v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int u = __shfl_up(v, off, 64);
-        if (lane >= off) v += u;
-    }
+    // DPP only: row shifts right by 1, 2, 4, 8 (lanes without a source add 0), then lane 15 of each
+    // row into the next row and lane 31 into the upper half
+    (void) lane;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);     // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);     // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);     // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);     // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);     // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);     // row_bcast:31 into rows 2, 3
     return v;
 }
+__device__ __forceinline__ int lane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 // item -> token t (with n_past np and slot), chunk c, kv head g; n_items = all items of the step
 __device__ __forceinline__ bool attn_locate(const int32_t * n_past, const int32_t * slot_idx, int T, int nkv, int item,
                                             int & n_items, int & t, int & np, int & slot, int & c, int & g) {
@@ -1273,12 +1278,12 @@ __device__ __forceinline__ bool attn_locate(const int32_t * n_past, const int32_
         if (hit) {
             const int l = __ffsll((unsigned long long) hit) - 1;
             t = t0 + l;
-            np = __shfl(npu, l, 64);
-            slot = __shfl(su, l, 64);
-            c = want - base - __shfl(excl, l, 64);
+            np = lane_i(npu, l);
+            slot = lane_i(su, l);
+            c = want - base - lane_i(excl, l);
             found = true;
         }
-        base += __shfl(incl, 63, 64);
+        base += lane_i(incl, 63);
     }
     n_items = base * nkv;
     return found;
@@ -1293,10 +1298,10 @@ __device__ __forceinline__ void attn_chunks_of(const int32_t * n_past, int T, in
         const int nc = u < T ? (n_past[u] + ATT_CH) / ATT_CH : 0;
         const int incl = wave_scan_incl(nc, lane);
         if (t < t0 + 64) {
-            before = base + __shfl(incl - nc, t - t0, 64);
-            nc_t = __shfl(nc, t - t0, 64);
+            before = base + lane_i(incl - nc, t - t0);
+            nc_t = lane_i(nc, t - t0);
         }
-        base += __shfl(incl, 63, 64);
+        base += lane_i(incl, 63);
     }
 }
 
