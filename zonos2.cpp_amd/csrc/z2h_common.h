@@ -189,6 +189,15 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return __builtin_amdgcn_readlane(v, 0);
 }
 
+// Block barrier that orders LDS only. __syncthreads() also waits for every global access the wave
+// has in flight, which would turn a weight prefetch issued before a staging barrier into a stall;
+// blocks that exchange data only through LDS use this one, and their loads stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

@@ -159,9 +159,9 @@ __device__ __forceinline__ void copy16(int n, Src src, Dst dst) {
 __device__ __forceinline__ double block_sum_d(double v, double * red) {
     v = wave_tree_d(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();                               // earlier readers of red are done
+    lds_sync();                               // earlier readers of red are done
     if (lane == 0) red[wave] = v;
-    __syncthreads();
+    lds_sync();
     return red[0] + red[1] + red[2] + red[3];
 }
 
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             const int i0 = 4 * (tid + 256 * j);
             if (i0 < d) *(float4 *) (xs + i0) = xv[j];
         }
-        __syncthreads();
+        lds_sync();
         encode_row_rt(a.act_fmt, xs, d, a.act, t);
     }
 #pragma unroll
@@ -499,12 +499,12 @@ __device__ __forceinline__ int build_route_list(const int32_t * sel, int n_route
         const unsigned long long m = __ballot(hit);
         const int before = __popcll(m & ((1ull << lane) - 1ull));
         if (lane == 0) wcount[wave] = __popcll(m);
-        __syncthreads();
+        lds_sync();
         int off = total;
         for (int w = 0; w < wave; ++w) off += wcount[w];
         if (hit) list[off + before] = r;
         const int add = wcount[0] + wcount[1] + wcount[2] + wcount[3];
-        __syncthreads();
+        lds_sync();
         total += add;
     }
     return total;
@@ -727,12 +727,12 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
 
     for (int c0 = 0; c0 < n_items; c0 += NT) {
         const int nt = min(NT, n_items - c0);
-        __syncthreads();
+        lds_sync();
         // ---- stage the activation rows of this chunk into LDS
         stage_acts<AF>(a, nt, [&](int tt) { const int it = a.grouped ? s_list[c0 + tt] : item0 + c0 + tt;
                                              return a.grouped && !a.act_by_route ? it / a.k : it; },
                        K, sq, sd32, sd256, sbs, sh);
-        __syncthreads();
+        lds_sync();
         // ---- each wave: its share of the 256-column units, lane = row of the tile; partial sums
         // accumulate in the wave's LDS slice s_red[wave][tt][lane] in unit order
         float * sacc = s_red + (wave * NT) * TILE + lane;
@@ -751,7 +751,7 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
             const uint16_t * dp = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb) * TILE + lane : nullptr;
             gemv_unit<WF>(r, dp, sb, a.nsb, K, sq, sd32, sd256, sbs, sh, nt, sacc);
         }
-        __syncthreads();
+        lds_sync();
         // ---- reduce the 4 waves (in wave order) and store
         for (int o = tid; o < nt * TILE; o += 256) {
             const int tt = o / TILE, r = o % TILE;
@@ -820,11 +820,11 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
             load_unit<WF>(wt, u0);
             if (a.nsb > 1) load_unit<WF>(wt + (size_t) C * TILE, u1);
         }
-        __syncthreads();
+        lds_sync();
         stage_acts<AF>(a, nt, [&](int tt) { const int it = s_list[c0 + tt]; return a.act_by_route ? it : it / a.k; },
                        K, sq, sd32, sd256, sbs, sh);
         for (int tt = 0; tt < nt; ++tt) sacc[tt * TILE] = 0.0f;
-        __syncthreads();
+        lds_sync();
         if (has_tile) {
             for (int sb = 0; sb < a.nsb; sb += 2) {
                 const uint16_t * dp0 = WF == WF_Q6_K ? dbase + ((size_t) tile * a.nsb + sb) * TILE + lane : nullptr;
@@ -966,22 +966,23 @@ __device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok,
         u32x4 v[8];
         uint32_t sv[4];
         float dv = 0.0f;
+        // (indices past the end re-read the last item, so the loads issue without branches)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int i = it * 2048 + tid + 256 * j;
-            if (i < nq) v[j] = *(const u32x4 *) (act.q + (int64_t) tok(i / per) * K + (i % per) * 16);
+            const int i = min(it * 2048 + tid + 256 * j, nq - 1);
+            v[j] = *(const u32x4 *) (act.q + (int64_t) tok(i / per) * K + (i % per) * 16);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int i = it * 1024 + tid + 256 * j;
-            sv[j] = 0;
-            if (i < nsd) {
-                if constexpr (AF == ACT_Q8_K) sv[j] = *(const uint32_t *) (act.bs + (int64_t) tok(i / ns) * (K / 16) + 2 * (i % ns));
-                else sv[j] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tok(i / ns) * ns + i % ns]);
-            }
+            const int i = min(it * 1024 + tid + 256 * j, nsd - 1);
+            if constexpr (AF == ACT_Q8_K) sv[j] = *(const uint32_t *) (act.bs + (int64_t) tok(i / ns) * (K / 16) + 2 * (i % ns));
+            else sv[j] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tok(i / ns) * ns + i % ns]);
         }
         const int id = it * 256 + tid;
-        if (AF == ACT_Q8_K && id < ndd) dv = act.d256[(int64_t) tok(id / nd) * nd + id % nd];
+        if constexpr (AF == ACT_Q8_K) {
+            const int ic = min(id, ndd - 1);
+            dv = act.d256[(int64_t) tok(ic / nd) * nd + ic % nd];
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int i = it * 2048 + tid + 256 * j;
@@ -1055,9 +1056,9 @@ k_gemv_mfma(GemvArgs a) {
         }
         s_tok[tid] = tok;
     }
-    __syncthreads();
+    lds_sync();
     m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
-    __syncthreads();
+    lds_sync();
     if (!has) return;
     float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // units [u0, u1) into acc (DUAL: the gate matrix's, then the up matrix's); unit u sits in ring
@@ -1149,9 +1150,9 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         }
         s_tok[tid] = tok;
     }
-    __syncthreads();
+    lds_sync();
     m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
-    __syncthreads();
+    lds_sync();
     float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < SPLIT_UMAX; ++j) {
@@ -1169,7 +1170,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) { s_part[wave][i][lane] = acc0[i]; s_part[wave][4 + i][lane] = acc1[i]; }
-    __syncthreads();
+    lds_sync();
     if (wave != 0) return;
     const int q = lane >> 4, row = g16 * 16 + (lane & 15);
     if (row >= a.rows) return;
@@ -1432,12 +1433,12 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         };
         if constexpr (N4 > 256) kv_put(tid + 256, k1, v1);
         if constexpr (N4 > 512) { kv_put(tid + 512, k2, v2); kv_put(tid + 768, k3, v3); }
-        __syncthreads();                                             // the chunk copy is in LDS
+        lds_sync();                                             // the chunk copy is in LDS
         if (mk && lane < NP) {                                       // replace the stale new row
             *(uint32_t *) &s_k[(nr - 1) * KST + 2 * lane] = nk;
             *(uint32_t *) &s_v[(nr - 1) * HD + 2 * lane] = nv;
         }
-        __syncthreads();
+        lds_sync();
         // ---- scores: one (row, head) per thread
         for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
             const int r = sidx / GRP, h = sidx % GRP;
@@ -1451,7 +1452,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             }
             s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
         }
-        __syncthreads();
+        lds_sync();
         // ---- per-head chunk softmax partial (lane = row); (max, sum) stored with the outputs
         float2 ml[(GRP + 3) / 4];
 #pragma unroll
@@ -1464,7 +1465,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             ml[i] = make_float2(mx, wave_tree_f(pe));
             if (lane < ATT_CH) s_p[lane][h] = pe;
         }
-        __syncthreads();
+        lds_sync();
         // ---- P.V: one (head, dim pair) per thread, rows in order
         for (int o = tid; o < GRP * NP; o += 256) {
             const int h = o / NP, dp = o % NP;
@@ -1487,7 +1488,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             *(uint32_t *) (a.kc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nk;
             *(uint32_t *) (a.vc + band + (int64_t) (nr - 1) * HD + 2 * lane) = nv;
         }
-        if (item + (int) gridDim.x < n_items) __syncthreads();      // LDS reuse by the next item
+        if (item + (int) gridDim.x < n_items) lds_sync();      // LDS reuse by the next item
     }
 }
 
@@ -1567,7 +1568,7 @@ __global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int n
     }
     den = wave_tree_f(den);
     if (part == 0 && lane == 0) sden[hl] = den;
-    __syncthreads();
+    lds_sync();
     const int np2 = hd / 2;
     for (int pi = lane; pi < np2; pi += 64) {
         float o0 = 0.0f, o1 = 0.0f;
@@ -1589,7 +1590,7 @@ __global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int n
         pw[wave * hd + 2 * pi] = o0;
         pw[wave * hd + 2 * pi + 1] = o1;
     }
-    __syncthreads();
+    lds_sync();
     const float * gate = a.qkvg + (int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd;
     for (int i = tid; i < hpb * hd; i += 512) {
         const int l = i / hd, dim = i - l * hd;
@@ -1599,7 +1600,7 @@ __global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int n
         if (a.cap_gate && dim == 0) a.cap_gate[(int64_t) t * nh + h0 + l] = gsig;
         ob[i] = s * (gsig / sden[l]);
     }
-    __syncthreads();
+    lds_sync();
     const int base = h0 * hd, span = hpb * hd;
     for (int i = tid; i < span; i += 512) a.o_out[(int64_t) t * nh * hd + base + i] = ob[i];
     if (a.act_fmt == ACT_NONE || tid >= 256) return;
@@ -1716,7 +1717,7 @@ __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) 
         xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
         *(float4 *) (xs + i0) = xv[j];
     }
-    __syncthreads();
+    lds_sync();
     if (has_o) {
         float acc = 0.0f;
 #pragma unroll
@@ -1857,13 +1858,13 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
             if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
         }
     }
-    __syncthreads();                               // s_x holds the normalised state
+    lds_sync();                               // s_x holds the normalised state
     rt_layer<0, NM>(w0, s_x, rd, s_y, b0, b0, false, false);
-    __syncthreads();
+    lds_sync();
     rt_layer<0, NM>(w2, s_y, rd, s_x, b2, b2, false, false);
-    __syncthreads();
+    lds_sync();
     rt_layer<1, NM>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
-    __syncthreads();
+    lds_sync();
     if (wave != 0) return;
     // softmax (own exp, double tree sum) + selection scores
     float lg[4], pr[4], sc[4];
