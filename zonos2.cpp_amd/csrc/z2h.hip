@@ -99,6 +99,7 @@ struct z2h_ctx {
 
     // scratch (sized for n_slots tokens)
     int Tmax = 0, Kmax = 0, items_max = 0;   // Tmax: token rows of the scratch (steps and prefill chunks)
+    int attn_slots = 2048;            // attention blocks resident at once (compute units x blocks per unit)
     int Tstep = 0;                    // columns a step may list (n_slots); captures are sized for it
     int pch = 0;                      // prefill chunk rows (<= Tmax)
     int max_rows = 0;                 // requested row capacity (z2h_create_batch_rows)
@@ -800,7 +801,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     if (n_run && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, run[0], ctx->res, T))) return rc;
     (void) h_npast;
     // persistent attention grid: the item count comes from the device n_past table
-    const int attn_grid = std::min(ctx->items_max, 2048);    // ~7 resident blocks per CU; more items loop
+    // persistent attention grid: as many blocks as fit on the chip at once (a block past that would
+    // wait for a slot only to find no item left); blocks loop over the items beyond it
+    const int attn_grid = std::min(ctx->items_max, ctx->attn_slots);
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int i = 0; i < n_run; ++i) {
@@ -1193,6 +1196,24 @@ int z2h_finalize(z2h_ctx * ctx) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
+    {
+        int n_cu = 0, per_cu = 0;
+        HIPX(hipSetDevice(ctx->device));
+        HIPX(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, ctx->device));
+        const void * fn = nullptr;
+        const int grp = hp.n_head / std::max(1, hp.n_head_kv);
+#define ATT_FN(H_) fn = grp == 1 ? (const void *) &k_attn_chunk<H_, 1> : grp == 2 ? (const void *) &k_attn_chunk<H_, 2> : \
+                        grp == 4 ? (const void *) &k_attn_chunk<H_, 4> : (const void *) &k_attn_chunk<H_, 8>
+        switch (hp.head_dim) {
+            case 16: ATT_FN(16); break;
+            case 32: ATT_FN(32); break;
+            case 64: ATT_FN(64); break;
+            default: ATT_FN(128); break;
+        }
+#undef ATT_FN
+        HIPX(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0));
+        if (n_cu > 0 && per_cu > 0) ctx->attn_slots = n_cu * per_cu;
+    }
     (void) hp;
     ctx->graph_gen = ctx->m->gen;
     ctx->finalized = true;
