@@ -92,7 +92,7 @@ def main() -> int:
     import numpy as np
     import torch
     from zonos2_amd import configs, synth
-    from zonos2_amd.z2h import Context
+    from zonos2_amd.z2h import Context, Model
 
     if args.config == "c3":
         cfg, wl = configs.C3()
@@ -105,8 +105,8 @@ def main() -> int:
     model = synth.generate_model(cfg, seed=42)
     log(f"generated {cfg.name}: {sum(t.data.nbytes for t in model.values()) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
     t0 = time.time()
-    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap, device=0)
-    ctx.upload(model)
+    mdl = Model(cfg.hparams(), model)              # device weights, shared by the step and mixed contexts
+    ctx = Context(None, wl.n_slots, wl.slot_cap, model=mdl)
     kv_cache = {}
     for L in range(cfg.n_layer):
         for s, n in enumerate(wl.kv_lens):
@@ -231,6 +231,8 @@ def main() -> int:
     samp_us = (time.perf_counter() - t0) / 20 * 1e6
     log(f"device sampling: {samp_us:.1f} us per frame of {T} columns (host round trip included)")
 
+    mixed = mixed_pass(np, Context, synth, cfg, mdl) if args.config == "c3" else None
+
     line = {
         "metric": "batched-decode tok/s (Q4_K MoE step, 16 ragged reqs); % of HBM peak GB/s",
         "value": round(T / (ms / 1000.0), 1),
@@ -260,6 +262,7 @@ def main() -> int:
         "prefill": {"rows": n_pf, "chunk_rows": 256, "ms": round(pf_ms, 2), "rows_per_s": round(n_pf / pf_ms * 1000.0, 1)},
         "sampler": {"columns": T, "settings": "temperature 1.15, top-k 106, min-p 0.18, repetition 1.2 over 50",
                     "us_per_frame_step": round(samp_us, 1)},
+        "mixed": mixed,
     }
     if args.config != "c3":
         line["metric"] = "batched-decode tok/s (MoE step); % of HBM peak GB/s"
@@ -272,7 +275,73 @@ def main() -> int:
         torch.cuda.synchronize()
         log("calibration copy: 256 MiB read + 256 MiB written")
     ctx.close()
+    mdl.close()
     return 0
+
+
+INT8_MFMA_PEAK_TOPS = 5000.0
+
+
+def mixed_pass(np, Context, synth, cfg, mdl):
+    """One mixed pass of chunked prefill and decode rows on the same weights: 8 prefill chunks of
+    256 prompt rows, each after a speaker row (a 2048-d N(0,1) embedding row in place of the summed
+    token embeddings), at a 256-aligned offset inside a prompt of U[300, 1200] rows whose earlier rows
+    are pre-filled N(0,1) in the KV cache, plus 32 decode columns with KV lengths U[32, 1200]:
+    2088 rows through every layer in one z2h_step_mixed call (host API: ids up, 40 logit rows down).
+    Median of 3 after one warm-up; algorithmic FLOPs count the expert, projection and attention-score
+    products (2 per multiply-add)."""
+    rng = np.random.default_rng(55)
+    n_pre, n_dec, chunk = 8, 32, 256
+    plen = rng.integers(300, 1201, n_pre)
+    r0 = [int(rng.integers(0, (int(p) - chunk) // 256 + 1)) * 256 for p in plen]
+    dlen = [int(x) for x in rng.integers(32, 1201, n_dec)]
+    cap = max(max(r + chunk + 1 for r in r0), max(dlen) + 1)
+    slots, npast, emap, groups = [], [], [], []
+    for i, r in enumerate(r0):
+        g = []
+        for j in range(chunk + 1):                 # the speaker row, then the chunk's prompt rows
+            slots.append(i); npast.append(r + j); emap.append(i if j == 0 else -1); g.append(len(slots) - 1)
+        groups.append(g)
+    for i, n in enumerate(dlen):
+        slots.append(n_pre + i); npast.append(n); emap.append(-1); groups.append([len(slots) - 1])
+    R = len(slots)
+    W = cfg.n_codebooks + 1
+    ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (R, cfg.n_codebooks)),
+                          rng.integers(0, cfg.text_vocab + 1, (R, 1))], axis=1).astype(np.int32)
+    assert ids.shape[1] == W
+    emb = rng.standard_normal((n_pre, cfg.n_embd)).astype(np.float32)
+    out_rows = np.array([g[-1] for g in groups], np.int32)
+    mctx = Context(None, n_pre + n_dec, cap, model=mdl, max_rows=R)
+    for L in range(cfg.n_layer):
+        for i, r in enumerate(r0):
+            if r:
+                k, v = synth.kv_rows(cfg, L, i, r, 11)
+                mctx.kv_write(L, i, 0, k, v)
+        for i, n in enumerate(dlen):
+            k, v = synth.kv_rows(cfg, L, n_pre + i, n, 11)
+            mctx.kv_write(L, n_pre + i, 0, k, v)
+    args = (np.array(slots, np.int32), np.array(npast, np.int32), ids, out_rows)
+    mctx.step_mixed(*args, emb_map=np.array(emap, np.int32), emb=emb)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        mctx.step_mixed(*args, emb_map=np.array(emap, np.int32), emb=emb)
+        ts.append(time.perf_counter() - t0)
+    ms = float(np.median(ts)) * 1000.0
+    mctx.close()
+    d, ff, k = cfg.n_embd, cfg.n_ff, cfg.top_k
+    R_qkvg = (cfg.n_head + 2 * cfg.n_head_kv) * cfg.head_dim + cfg.n_head
+    per_row = 2 * (k * 3 * ff * d + R_qkvg * d + d * cfg.n_head * cfg.head_dim)
+    ctx_rows = sum(n + 1 for n in npast)
+    flops = cfg.n_layer * (R * per_row + 2 * 2 * ctx_rows * cfg.n_head * cfg.head_dim)
+    tops = flops / (ms / 1000.0) / 1e12
+    log(f"mixed pass: {R} rows ({n_pre} prefill chunks + {n_dec} decode) in {ms:.1f} ms, "
+        f"{R / ms * 1000.0:.0f} rows/s, {tops:.1f} TOP/s algorithmic ({tops / INT8_MFMA_PEAK_TOPS:.2%} of int8 MFMA peak)")
+    return {"rows": R, "prefill_chunks": n_pre, "chunk_rows": chunk, "decode_rows": n_dec, "ms": round(ms, 2),
+            "rows_per_s": round(R / ms * 1000.0, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s (int8)",
+                         "frac": round(tops / INT8_MFMA_PEAK_TOPS, 5)},
+            "weights": "q4_k", "speaker_rows": "N(0,1) embedding rows in place of the summed token embeddings"}
 
 
 if __name__ == "__main__":
