@@ -252,6 +252,33 @@ def test_layer_skip_vs_oracle():
     ctx.close()
 
 
+def test_tiled_prefill_attention_equals_decode_steps():
+    """Prefill and mixed passes attend through tiles (up to 16 rows of one slot at consecutive
+    positions share each K/V chunk read); every row keeps the decode kernel's arithmetic. A 100-row
+    prompt prefilled in one chunk (tiles of 16 and a ragged 4, two 64-row chunks) and the same prompt
+    stepped row by row leave bit-identical K/V rows and last-row logits."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 52)
+    n0, slot = 100, 1
+    ids = _prompt(cfg, n0, 13)
+    a = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    a.upload(model)
+    print("prefill 100 rows", flush=True)
+    last = a.prefill(slot, ids)
+    b = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    b.upload(model)
+    print("100 decode steps", flush=True)
+    for t in range(n0):
+        lg = b.step([slot], [t], ids=ids[t:t + 1])
+    np.testing.assert_array_equal(last, lg[0])
+    for L in range(cfg.n_layer):
+        ka, va = a.kv_read(L, slot, 0, n0)
+        kb, vb = b.kv_read(L, slot, 0, n0)
+        np.testing.assert_array_equal(ka, kb)
+        np.testing.assert_array_equal(va, vb)
+    a.close(); b.close()
+
+
 def test_chunked_prefill_is_chunk_size_independent():
     """Chunked prefill (every row of a chunk appends its K/V before the chunk's attention) gives the
     same bits for any chunk size: one row at a time, 7-row chunks (ragged last chunk, the speaker

@@ -116,6 +116,8 @@ struct z2h_ctx {
     int32_t * r_off = nullptr, * r_perm = nullptr;   // routes grouped by expert ([E+1] offsets, [T*k] ids)
     float * gu_g = nullptr, * gu_u = nullptr, * eo = nullptr, * logits = nullptr, * tmp_x = nullptr;
     int * d_err = nullptr;
+    int4 * d_tiles = nullptr;         // [items_max] attention tile entries of a kv_pre pass (k_attn_tile)
+    int4 * h_tiles = nullptr;         // pinned staging for them
     int32_t * h_pin = nullptr;        // pinned staging for step inputs
     size_t h_pin_bytes = 0;
 
@@ -150,6 +152,7 @@ int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; re
 int seterr(z2h_model * c, int code, const std::string & m) { if (c) c->err = m; return code; }
 int upload_mat_t64(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
+int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles);
 int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T);
 
 constexpr int PROF_MAX = 16384;
@@ -450,6 +453,9 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->spk_io, (size_t) (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
         return rc;
     (void) E;
+    if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) ctx->items_max * sizeof(int4), b))) return rc;
+    if (hipHostMalloc((void **) &ctx->h_tiles, (size_t) ctx->items_max * sizeof(int4), hipHostMallocDefault) != hipSuccess)
+        return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     ctx->h_pin_bytes = (size_t) T * (3 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
@@ -774,7 +780,7 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
 // rows of one slot attend to each other); d_emb_map: per token -1 (sum of its ids) or its row of d_emb.
 int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
              const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false,
-             const int32_t * d_emb_map = nullptr) {
+             const int32_t * d_emb_map = nullptr, const int32_t * h_slot = nullptr) {
     const auto & hp = ctx->hp;
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
@@ -804,6 +810,25 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     // persistent attention grid: as many blocks as fit on the chip at once (a block past that would
     // wait for a slot only to find no item left); blocks loop over the items beyond it
     const int attn_grid = std::min(ctx->items_max, ctx->attn_slots);
+    // kv_pre passes (host copies of the rows' slots and positions at hand): tiles of up to ATT_TILE
+    // rows of one slot at consecutive positions share each K/V chunk read (k_attn_tile)
+    int n_tiles = 0;
+    if (kv_pre && h_slot && h_npast) {
+        int before = 0;
+        for (int t = 0; t < T;) {
+            int m = 1;
+            while (t + m < T && m < ATT_TILE && h_slot[t + m] == h_slot[t] && h_npast[t + m] == h_npast[t] + m) ++m;
+            const int nc_last = (h_npast[t + m - 1] + ATT_CH) / ATT_CH;
+            for (int c = 0; c < nc_last; ++c)
+                for (int g = 0; g < nkv; ++g) {
+                    if (n_tiles >= ctx->items_max) return seterr(ctx, Z2H_EINVAL, "attention tile table overflow");
+                    ctx->h_tiles[n_tiles++] = make_int4(t, m | (g << 16), c, before);
+                }
+            for (int j = 0; j < m; ++j) before += (h_npast[t + j] + ATT_CH) / ATT_CH;
+            t += m;
+        }
+        HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) n_tiles * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
+    }
     const int R = (nh + 2 * nkv) * hd + nh;
     int prev_moe = -1;
     for (int i = 0; i < n_run; ++i) {
@@ -836,7 +861,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
             // QK-norm / RoPE / KV append fused in; item count from the device n_past table
             prof_scope ps(ctx, Z2H_KF_ATTN);
             if (kv_pre && (rc = launch_kv_append(ctx, a, T))) return rc;
-            if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
+            if (n_tiles > 0) {
+                if ((rc = launch_attn_tile(ctx, a, n_tiles))) return rc;
+            } else if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
         }
         {
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
@@ -906,6 +933,22 @@ int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T) {
         case 64: KL(k_kv_append<64>, grid, dim3(64), 0, ctx->stream, a); break;
         default: KL(k_kv_append<128>, grid, dim3(64), 0, ctx->stream, a); break;
     }
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
+int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles) {
+    const int grp = a.nh / a.nkv;
+#define ATT(H_, G_) KL((k_attn_tile<H_, G_>), dim3(n_tiles), dim3(256), 0, ctx->stream, a, (const int4 *) ctx->d_tiles)
+#define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
+    switch (a.hd) {
+        case 16: ATT_G(16) break;
+        case 32: ATT_G(32) break;
+        case 64: ATT_G(64) break;
+        default: ATT_G(128) break;
+    }
+#undef ATT_G
+#undef ATT
     HIPX(hipGetLastError());
     return Z2H_OK;
 }
@@ -1391,7 +1434,7 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
             HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
         }
         if (int rc = run_step(ctx, T, hp_ + T, ctx->d_slot, ctx->d_npast, ctx->d_ids, er >= 0 ? ctx->d_emb : nullptr,
-                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr)) return rc;
+                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr, hp_)) return rc;
         if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits + (size_t) (T - 1) * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
         HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }
@@ -1443,7 +1486,7 @@ int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const in
     }
     // every row appends its K/V before the attention; a slot's rows attend causally to each other
     if (int rc = run_step(ctx, n_rows, hp_ + n_rows, ctx->d_slot, ctx->d_npast, ctx->d_ids, emb_map ? ctx->d_emb : nullptr,
-                          ctx->logits, /*kv_pre=*/true, emb_map ? ctx->d_emb_map : nullptr)) return rc;
+                          ctx->logits, /*kv_pre=*/true, emb_map ? ctx->d_emb_map : nullptr, hp_)) return rc;
     const size_t row = (size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab;
     for (int i = 0; i < n_out; ++i)
         HIPX(hipMemcpyAsync(out_logits + (size_t) i * row, ctx->logits + (size_t) out_rows[i] * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -1713,6 +1756,7 @@ void z2h_destroy(z2h_ctx * ctx) {
     for (auto & e : ctx->ev) (void) hipEventDestroy(e);
     for (void * p : ctx->allocs) (void) hipFree(p);
     if (ctx->h_pin) (void) hipHostFree(ctx->h_pin);
+    if (ctx->h_tiles) (void) hipHostFree(ctx->h_tiles);
     if (ctx->h_samp) (void) hipHostFree(ctx->h_samp);
     if (ctx->stream) (void) hipStreamDestroy(ctx->stream);
     z2h_model * mdl = ctx->m;

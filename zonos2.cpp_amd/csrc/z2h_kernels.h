@@ -1492,6 +1492,131 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     }
 }
 
+// Attention for passes whose rows already appended their K/V (prefill chunks, mixed batches): a block
+// per (tile, chunk c, KV head g), where a tile is a run of up to ATT_TILE rows of one slot at
+// consecutive positions (tiles[blockIdx.x]: x = first row t0, y = rows m | g << 16, z = c, w = the
+// chunks of all rows before t0). The chunk's K/V rows are read once into LDS for all of the tile's
+// rows; each row whose band reaches chunk c then goes through k_attn_chunk's item arithmetic
+// (queries, scores, chunk softmax, P.V) line for line and writes its partial at its own item index,
+// so every row's result is the decode kernel's bit for bit and k_attn_combine merges them unchanged.
+constexpr int ATT_TILE = 16;
+template <int HD, int GRP>
+__global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __restrict__ tiles) {
+    constexpr int NP = HD / 2, RW = HD / 8, KST = HD + 8;
+    constexpr int N4 = ATT_CH * RW;
+    static_assert(N4 <= 1024, "four 16-byte items per thread and matrix at most");
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];
+    __shared__ float s_p[ATT_CH][GRP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
+    const int4 e = tiles[blockIdx.x];
+    const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16, c = e.z;
+    const int slot = a.slot_idx[t0], p0 = a.n_past[t0];
+    const int r0 = c * ATT_CH, nrmax = min(ATT_CH, p0 + m - r0);
+    const int64_t band = (((int64_t) slot * nkv + g) * a.S + r0) * HD;
+    {
+        // the chunk's rows once (rows past the tile's last one re-read it)
+        uint4 kk[4], vv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = min(tid + 256 * j, N4 - 1), r = min(i / RW, nrmax - 1), q4 = i % RW;
+            kk[j] = *(const uint4 *) (a.kc + band + (int64_t) r * HD + 8 * q4);
+            vv[j] = *(const uint4 *) (a.vc + band + (int64_t) r * HD + 8 * q4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            if (i < N4) {
+                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = kk[j];
+                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = vv[j];
+            }
+        }
+    }
+    constexpr int HPW = (GRP + 3) / 4;
+    int before = e.w;
+    for (int i = 0; i < m; ++i) {
+        const int t = t0 + i, np = p0 + i, nc = (np + ATT_CH) / ATT_CH;
+        const int64_t item = (int64_t) (before + c) * nkv + g;
+        before += nc;
+        if (c >= nc) continue;                                       // row t's band ends before chunk c
+        const int nr = min(ATT_CH, np + 1 - r0);
+        // ---- the row's queries of the group (one wave per head), as k_attn_chunk forms them
+        {
+            const float * row = a.qkvg + (int64_t) t * a.R;
+            float xq[HPW][2];
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) {
+                const int h = wave + 4 * j;
+                const float * src = row + (int64_t) (g * GRP + min(h, GRP - 1)) * HD;
+                xq[j][0] = lane < NP ? src[2 * lane] : 0.0f;
+                xq[j][1] = lane < NP ? src[2 * lane + 1] : 0.0f;
+            }
+            float cs, sn;
+            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) {
+                const int h = wave + 4 * j;
+                if (h >= GRP) break;
+                const int qh = g * GRP + h;
+                float y0, y1;
+                norm_rope<HD>(xq[j][0], xq[j][1], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
+                if (lane < NP) {
+                    s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                    if (a.cap_q && c == 0) {
+                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
+                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
+                    }
+                }
+            }
+        }
+        lds_sync();                                                  // s_q (and, first time, the chunk)
+        for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
+            const int r = sidx / GRP, h = sidx % GRP;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < RW; ++j) {
+                const uint4 kk = *(const uint4 *) &s_k[r * KST + 8 * j];
+                const uint4 qq = *(const uint4 *) &s_q[h][4 * j];
+                acc = fdot2(kk.x, qq.x, acc); acc = fdot2(kk.y, qq.y, acc);
+                acc = fdot2(kk.z, qq.z, acc); acc = fdot2(kk.w, qq.w, acc);
+            }
+            s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
+        }
+        lds_sync();
+        float2 ml[HPW];
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) {
+            const int h = wave + 4 * j;
+            if (h >= GRP) break;
+            const float sv = lane < ATT_CH ? s_p[min(lane, ATT_CH - 1)][h] : -__builtin_inff();
+            const float mx = wave_max_f(sv);
+            const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
+            ml[j] = make_float2(mx, wave_tree_f(pe));
+            if (lane < ATT_CH) s_p[lane][h] = pe;
+        }
+        lds_sync();
+        for (int o = tid; o < GRP * NP; o += 256) {
+            const int h = o / NP, dp = o % NP;
+            float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 16
+            for (int r = 0; r < ATT_CH; ++r) {
+                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * dp];
+                const float pp = s_p[r][h];
+                o0 = __builtin_fmaf(pp, h2f(vv & 0xffffu), o0);
+                o1 = __builtin_fmaf(pp, h2f(vv >> 16), o1);
+            }
+            *(float2 *) (a.part_o + (item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < HPW; ++j)
+                if (wave + 4 * j < GRP) *(float2 *) (a.part_ml + (item * GRP + wave + 4 * j) * 2) = ml[j];
+        }
+        lds_sync();                                                  // s_q / s_p reuse by the next row
+    }
+}
+
 // K/V append for every token of a prefill chunk before its attention reads them: one wave per
 // (token, KV head) forms the new k (per-head RMSNorm, RoPE at n_past) and v rows in f16 exactly as the
 // attention kernel does for its new row, and stores them at row n_past of the slot's band.
