@@ -1954,11 +1954,8 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
         rh[j] = i < rd ? a.rh[(int64_t) t * rd + i] : 0.0f;
         nw[j] = i < rd ? a.norm_w[i] : 0.0f;
     }
-    const int ldw = rd + 4;
-    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
-    rt_load<NM>(a.w0t, ldw, rd, w0);
-    rt_load<NM>(a.w2t, ldw, rd, w2);
-    rt_load<NM>(a.w4t, ldw, E, w4);
+    // the small vectors before the three matrices: loads complete in issue order, so a layer that
+    // needs its bias waits only for the loads issued before it
     float b0[4], b2[4], blg[4], bmk[4];
     rt_bias(a.b0, rd, b0);
     rt_bias(a.b2, rd, b2);
@@ -1970,6 +1967,14 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
         sb[j] = i < E ? a.sc_bias[i] : 0.0f;
         mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
     }
+    const int ldw = rd + 4;
+    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w0t, ldw, rd, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w2t, ldw, rd, w2);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w4t, ldw, E, w4);
     // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
     if (wave == 0) {
         double part = 0.0;
