@@ -1496,9 +1496,11 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
 // per (tile, chunk c, KV head g), where a tile is a run of up to ATT_TILE rows of one slot at
 // consecutive positions (tiles[blockIdx.x]: x = first row t0, y = rows m | g << 16, z = c, w = the
 // chunks of all rows before t0). The chunk's K/V rows are read once into LDS for all of the tile's
-// rows; each row whose band reaches chunk c then goes through k_attn_chunk's item arithmetic
-// (queries, scores, chunk softmax, P.V) line for line and writes its partial at its own item index,
-// so every row's result is the decode kernel's bit for bit and k_attn_combine merges them unchanged.
+// rows; then each wave takes whole rows (rows w, w + 4, ...) and computes k_attn_chunk's item
+// arithmetic for them without block barriers: the same per-(row, head) score dots, the same chunk
+// softmax with lane = chunk row, the same per-(head, dim pair) P.V sums over rows in order. Each row
+// writes its partial at its own item index, so every row's result is the decode kernel's bit for bit
+// and k_attn_combine merges them unchanged.
 constexpr int ATT_TILE = 16;
 template <int HD, int GRP>
 __global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __restrict__ tiles) {
@@ -1507,8 +1509,8 @@ __global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __re
     static_assert(N4 <= 1024, "four 16-byte items per thread and matrix at most");
     __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
-    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];
-    __shared__ float s_p[ATT_CH][GRP];
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[4][GRP][NP];   // per wave
+    __shared__ float s_p[4][ATT_CH][GRP];                               // per wave
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
     const int4 e = tiles[blockIdx.x];
     const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16, c = e.z;
@@ -1533,36 +1535,30 @@ __global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __re
             }
         }
     }
-    constexpr int HPW = (GRP + 3) / 4;
+    lds_sync();
+    uint32_t (*wq)[NP] = s_q[wave];
+    float (*wp)[GRP] = s_p[wave];
     int before = e.w;
     for (int i = 0; i < m; ++i) {
-        const int t = t0 + i, np = p0 + i, nc = (np + ATT_CH) / ATT_CH;
+        const int np = p0 + i, nc = (np + ATT_CH) / ATT_CH;
         const int64_t item = (int64_t) (before + c) * nkv + g;
         before += nc;
-        if (c >= nc) continue;                                       // row t's band ends before chunk c
-        const int nr = min(ATT_CH, np + 1 - r0);
-        // ---- the row's queries of the group (one wave per head), as k_attn_chunk forms them
+        if ((i & 3) != wave || c >= nc) continue;                    // row i is wave i % 4's; its band may end before c
+        const int t = t0 + i, nr = min(ATT_CH, np + 1 - r0);
+        // ---- the row's queries of the group, one head at a time (lane = dim pair)
         {
             const float * row = a.qkvg + (int64_t) t * a.R;
-            float xq[HPW][2];
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) {
-                const int h = wave + 4 * j;
-                const float * src = row + (int64_t) (g * GRP + min(h, GRP - 1)) * HD;
-                xq[j][0] = lane < NP ? src[2 * lane] : 0.0f;
-                xq[j][1] = lane < NP ? src[2 * lane + 1] : 0.0f;
-            }
             float cs, sn;
             rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
 #pragma unroll
-            for (int j = 0; j < HPW; ++j) {
-                const int h = wave + 4 * j;
-                if (h >= GRP) break;
+            for (int h = 0; h < GRP; ++h) {
                 const int qh = g * GRP + h;
+                const float * src = row + (int64_t) qh * HD;
+                const float x0 = lane < NP ? src[2 * lane] : 0.0f, x1 = lane < NP ? src[2 * lane + 1] : 0.0f;
                 float y0, y1;
-                norm_rope<HD>(xq[j][0], xq[j][1], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
+                norm_rope<HD>(x0, x1, a.temp[qh], a.qk_eps, cs, sn, y0, y1);
                 if (lane < NP) {
-                    s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                    wq[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
                     if (a.cap_q && c == 0) {
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
@@ -1570,50 +1566,38 @@ __global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __re
                 }
             }
         }
-        lds_sync();                                                  // s_q (and, first time, the chunk)
-        for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
-            const int r = sidx / GRP, h = sidx % GRP;
+        // ---- scores (lane = chunk row), then the chunk softmax of each head
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < RW; ++j) {
-                const uint4 kk = *(const uint4 *) &s_k[r * KST + 8 * j];
-                const uint4 qq = *(const uint4 *) &s_q[h][4 * j];
+                const uint4 kk = *(const uint4 *) &s_k[lane * KST + 8 * j];
+                const uint4 qq = *(const uint4 *) &wq[h][4 * j];
                 acc = fdot2(kk.x, qq.x, acc); acc = fdot2(kk.y, qq.y, acc);
                 acc = fdot2(kk.z, qq.z, acc); acc = fdot2(kk.w, qq.w, acc);
             }
-            s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
-        }
-        lds_sync();
-        float2 ml[HPW];
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-            const int h = wave + 4 * j;
-            if (h >= GRP) break;
-            const float sv = lane < ATT_CH ? s_p[min(lane, ATT_CH - 1)][h] : -__builtin_inff();
+            const float sv = lane < nr ? acc * a.scale : -__builtin_inff();
             const float mx = wave_max_f(sv);
             const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
-            ml[j] = make_float2(mx, wave_tree_f(pe));
-            if (lane < ATT_CH) s_p[lane][h] = pe;
+            const float l = wave_tree_f(pe);
+            wp[lane][h] = pe;
+            if (lane == 0) *(float2 *) (a.part_ml + (item * GRP + h) * 2) = make_float2(mx, l);
         }
-        lds_sync();
-        for (int o = tid; o < GRP * NP; o += 256) {
-            const int h = o / NP, dp = o % NP;
+        // ---- P.V: lane = dim pair, rows in order
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            if (lane >= NP) break;
             float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll 16
             for (int r = 0; r < ATT_CH; ++r) {
-                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * dp];
-                const float pp = s_p[r][h];
+                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * lane];
+                const float pp = wp[r][h];
                 o0 = __builtin_fmaf(pp, h2f(vv & 0xffffu), o0);
                 o1 = __builtin_fmaf(pp, h2f(vv >> 16), o1);
             }
-            *(float2 *) (a.part_o + (item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
+            *(float2 *) (a.part_o + (item * GRP + h) * HD + 2 * lane) = make_float2(o0, o1);
         }
-        if (lane == 0) {
-#pragma unroll
-            for (int j = 0; j < HPW; ++j)
-                if (wave + 4 * j < GRP) *(float2 *) (a.part_ml + (item * GRP + wave + 4 * j) * 2) = ml[j];
-        }
-        lds_sync();                                                  // s_q / s_p reuse by the next row
     }
 }
 
