@@ -62,16 +62,15 @@ __device__ __forceinline__ void q8k_block(const float * x, int8_t * q, float * d
     const float v[4] = {x[lane * 4], x[lane * 4 + 1], x[lane * 4 + 2], x[lane * 4 + 3]};
     q8k_block_v(v, q, d, bs, lane);
 }
-// The Q8_K values of the wave's 256-block (qi, 4 per lane) and its scale d (the same in every lane).
-__device__ __forceinline__ float q8k_quant(const float (&v)[4], int (&qi)[4]) {
-    // largest |x| by a DPP max; its first occurrence (lowest element index lane*4+i) from ballots
-    const float lmax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    const float amax = wave_max_f(lmax);
+// The Q8_K values of the wave's 256-block (qi, 4 per lane) and its scale d (the same in every lane),
+// given the block's largest |x| (amax, from a wave max).
+__device__ __forceinline__ float q8k_quant_m(const float (&v)[4], float amax, int (&qi)[4]) {
     if (amax == 0.0f) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qi[i] = 0;
         return 0.0f;
     }
+    // the first occurrence (lowest element index lane*4+i) of the largest |x| from ballots
     int best = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -86,6 +85,12 @@ __device__ __forceinline__ float q8k_quant(const float (&v)[4], int (&qi)[4]) {
     for (int i = 0; i < 4; ++i) qi[i] = min(127, (int) rintf(iscale * v[i]));
     return 1.0f / iscale;
 }
+__device__ __forceinline__ float q8k_lmax(const float (&v)[4]) {
+    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+}
+__device__ __forceinline__ float q8k_quant(const float (&v)[4], int (&qi)[4]) {
+    return q8k_quant_m(v, wave_max_f(q8k_lmax(v)), qi);
+}
 __device__ __forceinline__ void q8k_block_v(const float (&v)[4], int8_t * q, float * d, int16_t * bs, int lane) {
     int qi[4];
     const float dd = q8k_quant(v, qi);
@@ -99,6 +104,22 @@ __device__ __forceinline__ void q8k_block_v(const float (&v)[4], int8_t * q, flo
     if ((lane & 3) == 0) bs[lane >> 2] = (int16_t) s;
 }
 
+// Two independent 256-blocks by one wave: q8k_block_v on each, written as one straight-line
+// sequence so the two max / ballot / scale chains interleave.
+__device__ __forceinline__ void q8k_block_v2(const float (&va)[4], const float (&vb)[4], int8_t * qa, int8_t * qb,
+                                             float * da, float * db, int16_t * bsa, int16_t * bsb, int lane) {
+    int qia[4], qib[4];
+    const float ma = wave_max_f(q8k_lmax(va)), mb = wave_max_f(q8k_lmax(vb));
+    const float dda = q8k_quant_m(va, ma, qia), ddb = q8k_quant_m(vb, mb, qib);
+    if (lane == 0) { *da = dda; *db = ddb; }
+    *(uint32_t *) (qa + lane * 4) = (uint32_t) (qia[0] & 255) | ((uint32_t) (qia[1] & 255) << 8) | ((uint32_t) (qia[2] & 255) << 16) | ((uint32_t) (qia[3] & 255) << 24);
+    *(uint32_t *) (qb + lane * 4) = (uint32_t) (qib[0] & 255) | ((uint32_t) (qib[1] & 255) << 8) | ((uint32_t) (qib[2] & 255) << 16) | ((uint32_t) (qib[3] & 255) << 24);
+    int sa = qia[0] + qia[1] + qia[2] + qia[3], sb = qib[0] + qib[1] + qib[2] + qib[3];
+    sa += dpp_i<DPP_QUAD_XOR1>(sa); sb += dpp_i<DPP_QUAD_XOR1>(sb);
+    sa += dpp_i<DPP_QUAD_XOR2>(sa); sb += dpp_i<DPP_QUAD_XOR2>(sb);
+    if ((lane & 3) == 0) { bsa[lane >> 2] = (int16_t) sa; bsb[lane >> 2] = (int16_t) sb; }
+}
+
 // Encode one row x[K] (any memory) by a 256-thread block into the given destination planes.
 // x must hold Kp = round_up(K, 256) readable entries for Q8_K (callers keep K % 256 == 0 there);
 // for Q8_0 / F16 the entries in [K, Kp) are encoded as zeros.
@@ -108,8 +129,18 @@ __device__ __forceinline__ void encode_row(const float * x, int K, int8_t * q, f
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Kp = (K + 255) & ~255;
     if constexpr (AF == ACT_Q8_K) {
-        for (int b = wave; b < K / 256; b += 4)
-            q8k_block(x + 256 * b, q + 256 * b, d256 + b, bs + 16 * b, lane);
+        // two blocks per wave and pass (b and b + 4), so their reductions overlap
+        const int nb = K / 256;
+        for (int b = wave; b < nb; b += 8) {
+            const float v0[4] = {x[256 * b + lane * 4], x[256 * b + lane * 4 + 1], x[256 * b + lane * 4 + 2], x[256 * b + lane * 4 + 3]};
+            if (b + 4 < nb) {
+                const int b1 = b + 4;
+                const float v1[4] = {x[256 * b1 + lane * 4], x[256 * b1 + lane * 4 + 1], x[256 * b1 + lane * 4 + 2], x[256 * b1 + lane * 4 + 3]};
+                q8k_block_v2(v0, v1, q + 256 * b, q + 256 * b1, d256 + b, d256 + b1, bs + 16 * b, bs + 16 * b1, lane);
+            } else {
+                q8k_block_v(v0, q + 256 * b, d256 + b, bs + 16 * b, lane);
+            }
+        }
     } else if constexpr (AF == ACT_Q8_0) {
         for (int i = tid; i < Kp; i += 256) {         // 64 lanes = two 32-blocks
             const float v = i < K ? x[i] : 0.0f;
@@ -1644,6 +1675,9 @@ __global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int n
     float * sw = pw + 8 * hd;                                        // [hpb][ncs] chunk weights
     float * sden = sw + hpb * ncs;                                   // [hpb]
     int item0, nc;
+    // the gate logit of the thread's output head, requested before the chunk bookkeeping
+    const float * gate = a.qkvg + (int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd;
+    const float gate_x = tid < hpb * hd ? gate[h0 + tid / hd] : 0.0f;
     attn_chunks_of(a.n_past, a.T, t, item0, nc);
     const float2 * __restrict__ ml2 = (const float2 *) a.part_ml;
     const float2 * __restrict__ po2 = (const float2 *) a.part_o;
@@ -1700,12 +1734,11 @@ __global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int n
         pw[wave * hd + 2 * pi + 1] = o1;
     }
     lds_sync();
-    const float * gate = a.qkvg + (int64_t) t * a.R + (int64_t) (nh + 2 * nkv) * hd;
     for (int i = tid; i < hpb * hd; i += 512) {
         const int l = i / hd, dim = i - l * hd;
         float s = 0.0f;
         for (int p = 0; p < wph; ++p) s += pw[(l * wph + p) * hd + dim];
-        const float gsig = z_sigmoid(gate[h0 + l]);
+        const float gsig = z_sigmoid(i == tid ? gate_x : gate[h0 + l]);
         if (a.cap_gate && dim == 0) a.cap_gate[(int64_t) t * nh + h0 + l] = gsig;
         ob[i] = s * (gsig / sden[l]);
     }
