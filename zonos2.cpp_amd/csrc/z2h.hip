@@ -555,9 +555,9 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         return Z2H_OK;
     }
     if (a.grouped) {
-        // grouped expert matmuls: row-streaming kernel, 4 tiles per block
+        // grouped expert matmuls: row-streaming kernel, 4 tiles per block, NTE routes per block
         const size_t lds = gemv_rows_lds_bytes(af, m0.nsb * 256);
-        dim3 grid((m0.tiles + 3) / 4, grid_y, m1 ? 2 : 1), block(256);
+        dim3 grid((m0.tiles + 3) / 4, grid_y, (m1 ? 2 : 1) * ((a.n_tok + NTE - 1) / NTE)), block(256);
         switch (m0.type) {
             case Z2H_Q4_K: KL(k_gemv_rows<WF_Q4_K>, grid, block, lds, ctx->stream, a); break;
             case Z2H_Q6_K: KL(k_gemv_rows<WF_Q6_K>, grid, block, lds, ctx->stream, a); break;

@@ -821,7 +821,9 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
     __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     const int K = a.nsb * 256, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = blockIdx.x * 4 + wave, m = blockIdx.z, e = blockIdx.y;
+    // grid z = matrix + n_mats * pass: pass p takes the expert's routes [p * NTE, p * NTE + NTE), so a
+    // popular expert's routes spread over blocks instead of looping in one
+    const int tile = blockIdx.x * 4 + wave, m = blockIdx.z % a.n_mats, pass = blockIdx.z / a.n_mats, e = blockIdx.y;
     float * s_acc = (float *) smem;                                  // [4][NTE][64]
     char * p = smem + 4 * NTE * TILE * 4;
     int8_t * sq = nullptr; float * sd32 = nullptr; float * sd256 = nullptr; int16_t * sbs = nullptr; uint16_t * sh = nullptr;
@@ -844,7 +846,9 @@ __global__ void __launch_bounds__(256) k_gemv_rows(GemvArgs a) {
     const uint4 * wt = (const uint4 *) wbase + (size_t) (has_tile ? tile : 0) * a.nsb * C * TILE + lane;
     float * sacc = s_acc + (wave * NTE) * TILE + lane;
 
-    for (int c0 = 0; c0 < n_items; c0 += NTE) {
+    {
+        const int c0 = pass * NTE;
+        if (c0 >= n_items) return;
         const int nt = min(NTE, n_items - c0);
         uint4 u0[C], u1[C];
         if (has_tile) {
