@@ -244,7 +244,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights x q8_k activations (int8 dot, fp32 accumulate); f16 KV; fp32 router",
+        "dtype": dtype_of(cfg.bulk),
         "data": "synthetic (random-init weights, N(0,1) f16 KV, uniform token ids)",
         "config": {"workload": f"{cfg.name}: {cfg.n_layer}-layer MoE backbone decode step, {T} ragged requests "
                                f"(KV {min(wl.kv_lens)}..{max(wl.kv_lens)}), d_model {cfg.n_embd}, "
@@ -252,7 +252,7 @@ def main() -> int:
                    "requests": T, "kv_lens": wl.kv_lens, "parallelism": "single GPU"},
         "step_hbm": {"bytes": B, "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
-        "roofline": {"kernel": "k_gemv_mfma<Q4_K, DUAL> grouped expert gate/up + SwiGLU", "bound": "hbm",
+        "roofline": {"kernel": gateup_kernel_of(cfg.bulk), "bound": "hbm",
                      "achieved": round(dom_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(args.config),
                      "avg_launch_us": round(gu_ms / max(1, gu_n) * 1000.0, 2),
@@ -280,6 +280,27 @@ def main() -> int:
 
 
 INT8_MFMA_PEAK_TOPS = 5000.0
+
+
+def dtype_of(bulk):
+    """The arithmetic of the expert and projection matmuls for a weight type."""
+    from zonos2_amd.configs import TYPE_NAMES
+    w = TYPE_NAMES[bulk].lower()
+    if w in ("q4_k", "q8_0"):
+        act = "q8_k" if w == "q4_k" else "q8_0"
+        return f"{w} weights x {act} activations (int8 MFMA dot, fp32 accumulate); f16 KV; fp32 router"
+    if w == "q6_k":
+        return "q6_k weights x q8_k activations (int8 dot4, fp32 accumulate); f16 KV; fp32 router"
+    return f"{w} weights x f16 activations (fp32 accumulate); f16 KV; fp32 router"
+
+
+def gateup_kernel_of(bulk):
+    from zonos2_amd.configs import TYPE_NAMES
+    w = TYPE_NAMES[bulk]
+    if w in ("Q4_K", "Q8_0"):
+        return f"k_gemv_mfma<{w}, DUAL> grouped expert gate/up + SwiGLU"
+    return f"k_gemv_rows<{w}> grouped expert gate and up"
+
 
 
 def mixed_pass(np, Context, synth, cfg, mdl):
