@@ -179,15 +179,6 @@ __device__ __forceinline__ float wave_max_f(float v) {
     v = fmaxf(v, dpp_f<DPP_ROW_SHL + 1>(v));
     return lane0_f(v);
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-    v += up32_i(v);
-    v += up16_i(v);
-    v += dpp_i<DPP_ROW_SHL + 8>(v);
-    v += dpp_i<DPP_ROW_SHL + 4>(v);
-    v += dpp_i<DPP_ROW_SHL + 2>(v);
-    v += dpp_i<DPP_ROW_SHL + 1>(v);
-    return __builtin_amdgcn_readlane(v, 0);
-}
 
 // Block barrier that orders LDS only. __syncthreads() also waits for every global access the wave
 // has in flight, which would turn a weight prefetch issued before a staging barrier into a stall;

@@ -57,13 +57,8 @@ struct ActBuf {
 // ------------------------------------------------------------------ activation encoders
 // Q8_K of one 256-block by one wave (4 elements per lane). The element of largest |x| (first
 // occurrence) fixes iscale = -127/x; q = min(127, rint(iscale*x)); d = 1/iscale; sums of 16.
-__device__ __forceinline__ void q8k_block_v(const float (&vin)[4], int8_t * q, float * d, int16_t * bs, int lane);
-__device__ __forceinline__ void q8k_block(const float * x, int8_t * q, float * d, int16_t * bs, int lane) {
-    const float v[4] = {x[lane * 4], x[lane * 4 + 1], x[lane * 4 + 2], x[lane * 4 + 3]};
-    q8k_block_v(v, q, d, bs, lane);
-}
-// The Q8_K values of the wave's 256-block (qi, 4 per lane) and its scale d (the same in every lane),
-// given the block's largest |x| (amax, from a wave max).
+// q8k_quant_m: the block's values (qi, 4 per lane) and its scale d (the same in every lane), given
+// the block's largest |x| (amax, from a wave max).
 __device__ __forceinline__ float q8k_quant_m(const float (&v)[4], float amax, int (&qi)[4]) {
     if (amax == 0.0f) {
 #pragma unroll
