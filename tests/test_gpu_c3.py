@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle_py as O
-from helpers import assert_close, cos, fill_kv, oracle_pair
+from helpers import assert_close, cos, explain_topk_flips, fill_kv, oracle_pair
 from zonos2_amd import configs, synth
 from zonos2_amd.z2h import Context
 
@@ -78,9 +78,15 @@ def test_c3_layers_teacher_forced(c3):
     cap_ = cfg.logit_softcap
     assert_close("head + softcap", got, cap_ * np.tanh(mout / cap_))
     # end to end, routing decisions feed back through 24 layers: a top-k near-tie that rounds the
-    # other way in one layer changes every later layer's input, so only a sanity bound applies here
-    want = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)
-    print(f"worst per-layer cos {worst:.7f}; end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}")
+    # other way in one layer changes every later layer's input. Every layer where the two runs route
+    # a token differently must be a near-tie: the oracle's margin between the swapped experts below
+    # the score movement the measured hidden-state difference causes there.
+    want, ocap = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids, capture=True)
+    gcap = {L: {"ffn_in": rd(L, "ffn_in").reshape(T, d), "sel": rd(L, "sel").reshape(T, k)} for L in range(cfg.n_layer)}
+    orc = {L: {"ffn_in": ocap["ffn_in"][L]} for L in range(cfg.n_layer)}
+    flips = explain_topk_flips(om, model, cfg, T, gcap, orc, "C3")
+    print(f"worst per-layer cos {worst:.7f}; end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}; "
+          f"{len(flips)} layers with a top-k near-tie flip")
     assert cos(got, want) >= 0.99
 
 

@@ -114,3 +114,15 @@ def test_decode_bench_harness_with_gpu_sampling(root):
     for extra in (["--gpu-sample"], ["--gpu-sample", "--sampled"], ["--sampled"]):
         r = _cli("--model", str(root / FIXTURE), "--decode-bench", "--slots", "4", "--steps", "16", "--prompt-len", "8", *extra)
         assert r.returncode == 0 and "decode-bench: slots=4 steps=16" in r.stdout, r.stdout + r.stderr
+
+
+def test_batch_api_refuses_a_step_past_slot_capacity(root):
+    """zonos2_batch_step with device sampling (zonos2_batch_sample feeding the device-resident
+    tables): requests whose 250-row prompt + frames outgrow a 256-row slot (six resident steps fill
+    rows 250..255) must have the step at row 256
+    refused before any launch (the batch API falls back to z2h_step, which rejects the full slot)
+    instead of writing past the band. The harness reports the refusal and exits with status 3."""
+    r = _cli("--model", str(root / FIXTURE), "--batch-test", "--greedy", "--gpu-sample", "--slots", "3", "--requests", "3",
+             "--dup", "--max-frames", "64", "--prompt-len", "250", "--slot-cap", "256")
+    assert r.returncode == 3, r.stdout + r.stderr
+    assert "batch-test: step refused: slot" in r.stdout and "at n_past 256 (slot capacity 256)" in r.stdout

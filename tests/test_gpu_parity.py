@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle_py as O
-from helpers import COS_MIN, MAXABS, assert_close, fill_kv, oracle_pair, min_topk_margin
+from helpers import COS_MIN, MAXABS, assert_close, fill_kv, oracle_pair, min_topk_margin, router_bias
 from zonos2_amd import configs, synth
 from zonos2_amd.z2h import Context, Model
 
@@ -24,7 +24,7 @@ def _build(cfg, wl, seed=42):
     return model, ctx, om, okv
 
 
-def _check_routing(cfg, ctx, om, T):
+def _check_routing(cfg, ctx, om, T, model=None):
     """Teacher-forced: the oracle router on the device's router input must match bit for bit."""
     prev = None
     E, rd = cfg.n_expert, cfg.router_dim
@@ -51,7 +51,8 @@ def _check_routing(cfg, ctx, om, T):
         eo, out = O.experts(om, L, x, sel, w)
         geo = ctx.read_capture(L, "expert_out", T).reshape(-1, cfg.n_embd)[:T * k]
         assert_close(f"layer {L} expert_out", geo, eo)
-        print(f"layer {L}: routing bit-exact, min top-k margin {min_topk_margin(ref['probs'], np.zeros(E), k):.3e}")
+        rb = router_bias(model, L) if model is not None else np.zeros(E, np.float32)
+        print(f"layer {L}: routing bit-exact, min top-k margin (probs + router_bias) {min_topk_margin(ref['probs'], rb, k):.3e}")
         prev = rh
 
 
@@ -69,7 +70,7 @@ def test_c1_step_vs_oracle():
             assert_close(f"layer {L} {name}", g, cap[name][L])
     assert_close("out_norm", ctx.read_capture(0, "out_norm", T).reshape(T, -1), cap["out_norm"])
     assert_close("logits", got, want)
-    _check_routing(cfg, ctx, om, T)
+    _check_routing(cfg, ctx, om, T, model)
     # the new K/V rows written by the step
     for L in range(cfg.n_layer):
         for s, n in enumerate(wl.kv_lens):
@@ -121,6 +122,49 @@ def test_c2_moe_layer_vs_oracle():
     assert np.array_equal(ctx.read_capture(0, "perm", T), perm)
     eo, out = O.experts(om, 0, x, ref["sel"], ref["w"])
     assert_close("moe out", got, out)
+
+
+def test_router_ties_go_to_the_lower_expert_index():
+    """Exact ties in the selection scores through the device router: with router_mlp4 zero every
+    router logit is 0, so the softmax gives exactly 1/E (1/7 under a one-expert mask) to every kept
+    expert, and router_bias decides the order with tied values. north_star's contract: scores
+    descending, ties to the lower expert index. The device's top-k ids, weights and grouping must be
+    the oracle's, and the ids the closed-form answer."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 45)
+    E, k, d = cfg.n_expert, cfg.top_k, cfg.n_embd
+    bias = np.array([0.0, 0.5, 0.5, 0.0, 0.5, 0.0, 0.25, 0.5], np.float32)
+    for L in range(cfg.n_layer):
+        if cfg.expert_used[L] == 0:
+            continue
+        model[f"blk.{L}.router_mlp4.weight"].data[...] = 0
+        model[f"blk.{L}.router_bias"].data[...] = bias.view(model[f"blk.{L}.router_bias"].data.dtype)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    om = O.OracleModel(cfg.hparams(), model)
+    T = wl.n_slots
+    x = synth.gen_normal_f32((T, d), 3, "inputs.ties")
+    L = next(L for L in range(cfg.n_layer) if cfg.expert_used[L])
+    ctx.set_capture(True)
+    for keep, want_sel in ((None, [1, 2]), (np.array([1, 0, 1, 1, 1, 1, 1, 1], np.uint8), [2, 4])):
+        ctx.set_expert_mask(L, keep)
+        om.set_expert_mask(L, keep)
+        got = ctx.moe_forward(L, x)
+        sel = ctx.read_capture(L, "sel", T).reshape(T, ctx.kmax)[:, :k]
+        w = ctx.read_capture(L, "weights", T).reshape(T, ctx.kmax)[:, :k]
+        ref = O.router(om, L, x, None)
+        p = np.float32(1.0) / np.float32(E if keep is None else int(keep.sum()))
+        kept = ref["probs"][:, keep.astype(bool)] if keep is not None else ref["probs"]
+        assert np.all(kept == kept[0, 0]), "probabilities not tied"
+        assert np.array_equal(sel, np.tile(np.array(want_sel, np.int32), (T, 1))), f"device top-k {sel[0]} != {want_sel}"
+        assert np.array_equal(sel, ref["sel"])
+        assert np.array_equal(w.view(np.uint32), ref["w"].view(np.uint32))
+        assert abs(float(ref["probs"][0, want_sel[0]]) - float(p)) < 1e-6
+        counts, offsets, perm = O.group(sel, E)
+        assert np.array_equal(ctx.read_capture(L, "perm", T)[:T * k], perm)
+        eo, out = O.experts(om, L, x, sel, w)
+        assert_close("tied-route moe out", got, out)
+    ctx.close()
 
 
 def test_graph_replay_matches_eager():
@@ -177,7 +221,7 @@ def test_shared_model_contexts_and_mask_invalidation():
     sel = a.read_capture(L, "sel", T).reshape(T, a.kmax)[:, :cfg.expert_used[L]]
     assert np.all(sel % 2 == 0), "a masked expert was routed"
     om.set_expert_mask(L, keep)
-    _check_routing(cfg, a, om, T)                   # masked routing bit-exact against the oracle
+    _check_routing(cfg, a, om, T, model)            # masked routing bit-exact against the oracle
     a.set_capture(False)
     a.set_expert_mask(L, None)
     assert np.array_equal(b.step(inp.slot_idx, inp.n_past, emb=inp.emb), want)

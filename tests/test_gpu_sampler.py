@@ -9,7 +9,7 @@ import pytest
 
 import oracle_py as O
 from zonos2_amd import configs, synth
-from zonos2_amd.z2h import Context
+from zonos2_amd.z2h import Context, Z2HError, lib
 
 pytestmark = pytest.mark.gpu
 
@@ -115,3 +115,41 @@ def test_resident_decode_loop_matches_host_loop():
     with pytest.raises(Exception):
         a.step_resident(n)                                           # the tables were consumed
     a.close(); b.close()
+
+
+def test_resident_steps_stop_at_slot_capacity():
+    """The device-resident loop (z2h_sample_feed advances n_past on the GPU) must refuse a step whose
+    fed row would be the slot's row S (past its band, i.e. row 0 of the next KV head's band or past the
+    cache), before any launch, as z2h_step refuses it: the last valid row S - 1 steps, row S raises,
+    and no band's row 0 changes."""
+    cfg, wl = configs.C1()
+    model = synth.generate_model(cfg, 46)
+    n, ncb = wl.n_slots, cfg.n_codebooks
+    c = Context(cfg.hparams(), n, wl.slot_cap)
+    c.upload(model)
+    S = lib().z2h_slot_cap(c.ctx)
+    rng = np.random.default_rng(5)
+    for L in range(cfg.n_layer):
+        for s in range(n):
+            k, v = synth.kv_rows(cfg, L, s, S - 3, 9)
+            c.kv_write(L, s, 0, k, v)
+    row0 = [[c.kv_read(L, s, 0, 1) for s in range(n)] for L in range(cfg.n_layer)]
+    slots = np.arange(n, dtype=np.int32)
+    npast = np.full(n, S - 3, np.int32)
+    ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (n, ncb)), np.full((n, 1), cfg.text_vocab)], axis=1).astype(np.int32)
+    sp = [SETTINGS[i % 4] for i in range(n)]
+    c.step(slots, npast, ids=ids)                                  # row S - 3
+    for f in range(2):                                             # rows S - 2, S - 1
+        c.sample_feed(sp, rng.random((n, ncb)))
+        c.step_resident(n)
+    c.sample_feed(sp, rng.random((n, ncb)))                        # the tables now hold row S
+    with pytest.raises(Z2HError) as e:
+        c.step_resident(n)
+    assert "slot full" in str(e.value)
+    for L in range(cfg.n_layer):
+        for s in range(n):
+            k0, v0 = c.kv_read(L, s, 0, 1)
+            assert np.array_equal(k0, row0[L][s][0]) and np.array_equal(v0, row0[L][s][1]), f"row 0 of layer {L} slot {s} changed"
+    # the context stays usable: a host step at valid rows runs
+    c.step(slots, np.full(n, 5, np.int32), ids=ids)
+    c.close()

@@ -127,6 +127,7 @@ struct z2h_ctx {
     uint8_t * h_samp = nullptr;
     int resident_T = 0;               // columns whose next-step inputs z2h_sample_feed left in d_ids / d_npast
     int resident_last = 0;            // width of the last step whose inputs and logits are in d_* / logits
+    std::vector<int32_t> last_np;     // host copy of the device table's n_past per column (last step, + 1 per feed)
 
     // HIP graphs of the whole step, one per (batch width, embedding-injection) pair
     bool use_graphs = true;
@@ -1328,6 +1329,7 @@ int z2h_step(z2h_ctx * ctx, int T, const int32_t * slot_idx, const int32_t * n_p
     if (ids) HIPX(hipMemcpyAsync(ctx->d_ids, hp_ + 2 * T, (size_t) T * ctx->W * 4, hipMemcpyHostToDevice, ctx->stream));
     if (emb) HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
     ctx->resident_T = ctx->resident_last = 0;
+    ctx->last_np.assign(n_past, n_past + T);
     if (int rc = step_internal(ctx, T, n_past, ids != nullptr)) return rc;
     const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
     if (out_logits) HIPX(hipMemcpyAsync(out_logits, ctx->logits, nout * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -1345,6 +1347,7 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
     if (stream) ctx->stream = (hipStream_t) stream;
     int rc = Z2H_OK;
     ctx->resident_T = ctx->resident_last = 0;
+    ctx->last_np.assign(h_npast, h_npast + T);
     if (ctx->use_graphs && !ctx->capture && !ctx->prof) {
         // inputs into the context's fixed buffers, replay, logits out
         const size_t nout = (size_t) T * ctx->hp.n_codebooks * ctx->hp.audio_vocab;
@@ -1721,7 +1724,10 @@ static int sample_impl(z2h_ctx * ctx, int n_active, const float * d_logits, cons
     HIPX(hipMemcpyAsync(hc_out, ctx->d_codes, (size_t) n_active * ncb * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
     std::memcpy(codes, hc_out, (size_t) n_active * ncb * 4);
-    if (feed) ctx->resident_T = n_active;
+    if (feed) {
+        ctx->resident_T = n_active;
+        for (int i = 0; i < n_active; ++i) ctx->last_np[i] += 1;     // what k_feed wrote
+    }
     return Z2H_OK;
 }
 
@@ -1732,7 +1738,8 @@ int z2h_sample(z2h_ctx * ctx, int n_active, const float * d_logits, const z2h_sa
 
 int z2h_sample_feed(z2h_ctx * ctx, int n_active, const z2h_sampling * sp, const int32_t * hist, const int32_t * hist_len,
                     int hist_cap, const double * u, int32_t * codes) {
-    if (ctx && (ctx->resident_last != n_active)) return seterr(ctx, Z2H_ESTATE, "z2h_sample_feed: the last step had another width or no device tables");
+    if (ctx && (ctx->resident_last != n_active || (int) ctx->last_np.size() != n_active))
+        return seterr(ctx, Z2H_ESTATE, "z2h_sample_feed: the last step had another width or no device tables");
     return sample_impl(ctx, n_active, nullptr, sp, hist, hist_len, hist_cap, u, codes, true);
 }
 
@@ -1741,6 +1748,13 @@ int z2h_step_resident(z2h_ctx * ctx, int n_active) {
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
     if (n_active <= 0 || n_active != ctx->resident_T)
         return seterr(ctx, Z2H_ESTATE, "z2h_step_resident: no fed device tables of this width (z2h_sample_feed)");
+    // the fed rows must fit the slots' bands, as z2h_step checks (a full slot refuses the step before
+    // any launch; the device tables keep the refused n_past, so only a new z2h_step resumes)
+    for (int i = 0; i < n_active; ++i)
+        if ((int) ctx->last_np.size() != n_active || ctx->last_np[i] < 0 || ctx->last_np[i] >= ctx->S) {
+            ctx->resident_T = 0;
+            return seterr(ctx, Z2H_EINVAL, "z2h_step_resident: n_past out of range (slot full)");
+        }
     HIPX(hipSetDevice(ctx->device));
     ctx->resident_T = 0;
     if (int rc = step_internal(ctx, n_active, nullptr, true)) return rc;

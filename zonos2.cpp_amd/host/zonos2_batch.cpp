@@ -272,8 +272,10 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
     // the same columns as the last step, each one row further, fed by the device sampler: run from
     // the device-resident tables
     bool resident = bc.resident && bc.device_sampling && n == bc.last_n && (int) bc.fed_ids.size() == n * W;
+    // (a slot whose band is full takes the host path, which refuses the step before any launch)
     for (int i = 0; resident && i < n; ++i)
         resident = run[i]->index == bc.h_slot_prev[i] && run[i]->n_past == bc.h_npast_prev[i] + 1 &&
+                   run[i]->n_past < bc.slot_cap &&
                    std::equal(run[i]->next_ids.begin(), run[i]->next_ids.begin() + W, bc.fed_ids.begin() + (size_t) i * W);
     bc.resident = false;
     if (resident) {

@@ -13,10 +13,13 @@
 // this library); --requests R gives R prompts, request i reusing prompt i % 2 when --dup is set.
 // --gpu-sample samples the batched run's frames on the GPU from the step's logits
 // (zonos2_batch_sample) instead of the host sampler; --sampled makes --decode-bench use the default
-// sampling settings instead of greedy feedback.
+// sampling settings instead of greedy feedback. --slot-cap N gives the batch-test's shared context
+// slots of N frames, so requests that outgrow it must have their next step refused (exit status 3,
+// "batch-test: step refused: ..."), the no-write behaviour of a full band.
 #include "zonos2.h"
 #include "zonos2-sampler.h"
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -34,13 +37,14 @@ struct Args {
     bool gpu_sample = false;          // sample on the GPU from the step's logits (zonos2_batch_sample)
     bool sampled = false;             // decode-bench: default sampling settings instead of greedy
     int slots = 0, steps = 64, max_frames = 48, prompt_len = 32, requests = 3;
+    int slot_cap = 0;                 // batch-test: slot capacity of the shared context (0: fits every request)
     uint32_t seed = 1;
 };
 
 int usage() {
     fprintf(stderr, "usage: zonos2-batch --model F.gguf (--info | --decode-bench | --batch-test)\n"
                     "       [--slots N] [--steps K] [--max-frames M] [--prompt-len N0] [--requests R]\n"
-                    "       [--greedy] [--dup] [--seed S] [--gpu-sample] [--sampled]\n");
+                    "       [--greedy] [--dup] [--seed S] [--gpu-sample] [--sampled] [--slot-cap N]\n");
     return 2;
 }
 
@@ -80,175 +84,183 @@ int run_info(const Args & a) {
     return 0;
 }
 
-int run_decode_bench(zonos2_model & m, const Args & a) {
-    const int ncb = (int) m.hp.n_codebooks, av = (int) m.hp.audio_vocab;
-    const int n_slots = std::max(1, a.slots), n_steps = a.steps, n0 = a.prompt_len;
-    const std::vector<float> idf = make_prompt(m, n0, a.seed);
+// One request of a harness run: its prompt, sampler, slot record and the frames it produced.
+struct Request {
+    std::vector<float> prompt;        // [n0][W] ids as floats (the prefill API's form)
+    int n0 = 0, prompt_id = 0;
+    std::unique_ptr<zonos2_sampler> smp;
+    zonos2_slot slot;
+    std::vector<float> logits;        // [ncb][av]: the prefill's, then (host sampling) the last step's
+    std::vector<int32_t> codes;
+};
+
+// A batch context and the requests living in it. Frames are produced by advance(): one batched step
+// over the listed requests, then one frame each, sampled on the host from the step's logits or on the
+// GPU (zonos2_batch_sample). A slot whose step is refused (its band is full) stops the run.
+struct Harness {
+    zonos2_model & m;
     zonos2_batch_ctx bc;
-    if (!zonos2_batch_init(bc, m, n_slots, n0 + n_steps + 16)) { fprintf(stderr, "decode-bench: batch init failed\n"); return 1; }
-    zonos2_sampling sp; sp.greedy = !a.sampled; sp.seed = a.seed;
-    std::vector<zonos2_sampler> smp(n_slots, zonos2_sampler(sp, ncb, av));
-    std::vector<zonos2_slot> slots(n_slots);
-    std::vector<std::vector<float>> lo(n_slots, std::vector<float>((size_t) av * ncb));
-    std::vector<int32_t> sink;
-    std::vector<zonos2_slot *> active(n_slots);
-    for (int i = 0; i < n_slots; ++i) {
-        slots[i] = zonos2_slot{}; slots[i].index = i; slots[i].active = true; slots[i].n_past = n0;
-        if (!zonos2_batch_slot_prefill(bc, i, idf.data(), n0, nullptr, 0, lo[i].data())) {
-            fprintf(stderr, "decode-bench: prefill slot %d failed\n", i); zonos2_batch_free(bc); return 1;
-        }
-        active[i] = &slots[i];
+    bool gpu = false, ready = false;
+    int frame_cap = 0;                // frames after which a request is cut (sampler max_frames)
+    std::string refused;              // why a step was refused, if one was
+    Harness(zonos2_model & model, int n_slots, int slot_cap, bool gpu_sampling, int frames) : m(model), gpu(gpu_sampling), frame_cap(frames) {
+        ready = zonos2_batch_init(bc, m, n_slots, slot_cap);
+        bc.device_sampling = gpu;
     }
-    // a frame = sampling (host: from the copied logits; --gpu-sample: on the GPU from the step's
-    // logits) + one batched step
-    std::vector<zonos2_sampler *> smp_p(n_slots);
-    std::vector<std::vector<int32_t> *> sink_p(n_slots, &sink);
-    for (int i = 0; i < n_slots; ++i) smp_p[i] = &smp[i];
-    for (int i = 0; i < n_slots; ++i) zonos2_slot_sample(m, slots[i], smp[i], lo[i].data(), sink, n_steps + n0 + 32, {});
-    bc.device_sampling = a.gpu_sample;
-    bool ok = true;
-    auto step_once = [&]() {
-        for (int i = 0; i < n_slots; ++i) slots[i].done = false;
-        zonos2_batch_step(bc, active);
-        if (a.gpu_sample) {
-            ok = ok && zonos2_batch_sample(bc, active, smp_p, sink_p, n_steps + n0 + 32, {});
-        } else {
-            for (int i = 0; i < n_slots; ++i) {
-                std::memcpy(lo[i].data(), zonos2_batch_slot_logits(bc, i), (size_t) av * ncb * sizeof(float));
-                zonos2_slot_sample(m, slots[i], smp[i], lo[i].data(), sink, n_steps + n0 + 32, {});
+    ~Harness() { if (ready) zonos2_batch_free(bc); }
+    int ncb() const { return (int) m.hp.n_codebooks; }
+    int av() const { return (int) m.hp.audio_vocab; }
+
+    // prefill the request into slot `index` and take its first frame from the prefill logits
+    bool admit(Request & r, int index, const zonos2_sampling & sp) {
+        r.smp = std::make_unique<zonos2_sampler>(sp, ncb(), av());
+        r.slot = zonos2_slot{};
+        r.slot.index = index; r.slot.active = true; r.slot.n_past = r.n0;
+        r.logits.assign((size_t) av() * ncb(), 0.0f);
+        if (!zonos2_batch_slot_prefill(bc, index, r.prompt.data(), r.n0, nullptr, 0, r.logits.data())) return false;
+        zonos2_slot_sample(m, r.slot, *r.smp, r.logits.data(), r.codes, frame_cap, {});
+        return true;
+    }
+
+    // one step over `reqs` (their slots' done flags as the caller left them) and one frame each
+    bool advance(const std::vector<Request *> & reqs) {
+        std::vector<zonos2_slot *> cols;
+        std::vector<int> before;
+        for (Request * r : reqs) { cols.push_back(&r->slot); before.push_back(r->slot.n_past); }
+        zonos2_batch_step(bc, cols);
+        for (size_t i = 0; i < reqs.size(); ++i)
+            if (reqs[i]->slot.n_past == before[i]) {
+                refused = "slot " + std::to_string(reqs[i]->slot.index) + " at n_past " + std::to_string(before[i]) +
+                          " (slot capacity " + std::to_string(bc.slot_cap) + ")";
+                return false;
             }
+        if (gpu) {
+            std::vector<zonos2_sampler *> smps;
+            std::vector<std::vector<int32_t> *> outs;
+            for (Request * r : reqs) { smps.push_back(r->smp.get()); outs.push_back(&r->codes); }
+            return zonos2_batch_sample(bc, cols, smps, outs, frame_cap, {});
         }
-        sink.clear();
+        for (Request * r : reqs) {
+            const float * src = zonos2_batch_slot_logits(bc, r->slot.index);
+            r->logits.assign(src, src + (size_t) av() * ncb());
+            zonos2_slot_sample(m, r->slot, *r->smp, r->logits.data(), r->codes, frame_cap, {});
+        }
+        return true;
+    }
+
+    // frames until every request is done (or a step is refused)
+    bool drain(std::vector<Request *> reqs) {
+        for (;;) {
+            std::vector<Request *> live;
+            for (Request * r : reqs) if (r->slot.active && !r->slot.done) live.push_back(r);
+            if (live.empty()) return true;
+            if (!advance(live)) return false;
+        }
+    }
+};
+
+// decode-bench: n_slots copies of one prompt, 8 untimed frames, then --steps timed frames with the
+// done flags cleared every frame (EOS is ignored, as in the reference's probe)
+int run_decode_bench(zonos2_model & m, const Args & a) {
+    const int n_slots = std::max(1, a.slots), n0 = a.prompt_len;
+    Harness h(m, n_slots, n0 + a.steps + 16, a.gpu_sample, a.steps + n0 + 32);
+    if (!h.ready) { fprintf(stderr, "decode-bench: batch init failed\n"); return 1; }
+    zonos2_sampling sp; sp.greedy = !a.sampled; sp.seed = a.seed;
+    std::vector<Request> reqs(n_slots);
+    std::vector<Request *> all;
+    for (int i = 0; i < n_slots; ++i) {
+        reqs[i].n0 = n0;
+        reqs[i].prompt = make_prompt(m, n0, a.seed);
+        if (!h.admit(reqs[i], i, sp)) { fprintf(stderr, "decode-bench: prefill slot %d failed\n", i); return 1; }
+        all.push_back(&reqs[i]);
+    }
+    auto frames = [&](int n) {
+        for (int f = 0; f < n; ++f) {
+            for (Request * r : all) { r->slot.done = false; r->codes.clear(); }
+            if (!h.advance(all)) return false;
+        }
+        return true;
     };
-    for (int w = 0; w < 8; ++w) step_once();
+    if (!frames(8)) return 1;
     const auto t0 = std::chrono::steady_clock::now();
-    for (int s = 0; s < n_steps; ++s) step_once();
+    if (!frames(a.steps)) return 1;
     const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    const double fps = (double) n_slots * n_steps / dt;
-    if (!ok) { zonos2_batch_free(bc); return 1; }
+    const double fps = (double) n_slots * a.steps / dt;
     printf("decode-bench: slots=%d steps=%d  %.3fs  %.0f frames/s  %.1fx real-time  (%.1f frames/s/slot)  [%s, sampling on the %s]\n",
-           n_slots, n_steps, dt, fps, fps / (44100.0 / 512.0), fps / n_slots, sp.greedy ? "greedy" : "sampled",
+           n_slots, a.steps, dt, fps, fps / (44100.0 / 512.0), fps / n_slots, sp.greedy ? "greedy" : "sampled",
            a.gpu_sample ? "GPU" : "host");
-    zonos2_batch_free(bc);
     return 0;
 }
 
-// one request decoded in a context of its own (the single-sequence path)
-std::vector<int32_t> decode_alone(zonos2_model & m, const std::vector<float> & idf, int n0, int max_frames,
-                                  const zonos2_sampling & sp, int & eos) {
-    const int ncb = (int) m.hp.n_codebooks, av = (int) m.hp.audio_vocab;
-    std::vector<int32_t> codes;
-    zonos2_batch_ctx bc;
-    if (!zonos2_batch_init(bc, m, 1, n0 + max_frames)) return codes;
-    zonos2_sampler smp(sp, ncb, av);
-    zonos2_slot s; s.index = 0; s.active = true; s.n_past = n0;
-    std::vector<float> lo((size_t) av * ncb);
-    if (!zonos2_batch_slot_prefill(bc, 0, idf.data(), n0, nullptr, 0, lo.data())) { zonos2_batch_free(bc); return codes; }
-    std::vector<zonos2_slot *> one{&s};
-    for (;;) {
-        zonos2_slot_sample(m, s, smp, lo.data(), codes, max_frames, {});
-        if (s.done) break;
-        zonos2_batch_step(bc, one);
-        std::memcpy(lo.data(), zonos2_batch_slot_logits(bc, 0), lo.size() * sizeof(float));
-    }
-    eos = s.eos_frame;
-    zonos2_batch_free(bc);
-    return codes;
-}
-
+// batch-test: every request decoded alone in a one-slot context (host sampling), then all of them in
+// one shared context of max(--slots, requests) slots (idle slots stay unlisted); frames compared.
 int run_batch_test(zonos2_model & m, const Args & a) {
-    const int ncb = (int) m.hp.n_codebooks, av = (int) m.hp.audio_vocab;
+    const int ncb = (int) m.hp.n_codebooks;
     const int n_req = std::max(1, a.requests), n_slots = std::max(n_req, a.slots);
-    zonos2_sampling sp;
-    sp.greedy = a.greedy;
-    sp.seed = a.seed;
-    struct Job {
-        std::vector<float> idf;
-        int n0 = 0, prompt_id = 0, eos_frame = -1;
-        std::unique_ptr<zonos2_sampler> smp;
-        zonos2_slot slot;
-        std::vector<float> logits;
-        std::vector<int32_t> codes;
+    zonos2_sampling sp; sp.greedy = a.greedy; sp.seed = a.seed;
+    auto make = [&](std::vector<Request> & v) {
+        v.resize(n_req);
+        for (int i = 0; i < n_req; ++i) {
+            v[i].prompt_id = a.dup ? i % 2 : i;
+            v[i].n0 = a.prompt_len + (a.dup ? 0 : 3 * i);              // ragged unless duplicated
+            v[i].prompt = make_prompt(m, v[i].n0, a.seed + 101u * (uint32_t) v[i].prompt_id);
+        }
     };
-    std::vector<Job> jobs(n_req);
+    std::vector<Request> alone, batched;
+    make(alone);
+    make(batched);
     int max_n0 = 0;
-    for (int i = 0; i < n_req; ++i) {
-        jobs[i].prompt_id = a.dup ? i % 2 : i;
-        jobs[i].n0 = a.prompt_len + (a.dup ? 0 : 3 * i);            // ragged unless duplicated
-        jobs[i].idf = make_prompt(m, jobs[i].n0, a.seed + 101u * (uint32_t) jobs[i].prompt_id);
-        max_n0 = std::max(max_n0, jobs[i].n0);
-    }
-    std::vector<std::vector<int32_t>> ref(n_req);
-    std::vector<int> ref_eos(n_req, -1);
-    for (int i = 0; i < n_req; ++i) ref[i] = decode_alone(m, jobs[i].idf, jobs[i].n0, a.max_frames, sp, ref_eos[i]);
-
-    zonos2_batch_ctx bc;
-    if (!zonos2_batch_init(bc, m, n_slots, max_n0 + a.max_frames)) { fprintf(stderr, "batch-test: batch init failed\n"); return 1; }
-    for (int i = 0; i < n_req; ++i) {
-        Job & j = jobs[i];
-        j.smp = std::make_unique<zonos2_sampler>(sp, ncb, av);
-        j.slot = zonos2_slot{}; j.slot.index = i; j.slot.active = true; j.slot.n_past = j.n0;
-        j.logits.assign((size_t) av * ncb, 0.0f);
-        if (!zonos2_batch_slot_prefill(bc, i, j.idf.data(), j.n0, nullptr, 0, j.logits.data())) {
-            j.slot.done = true;
-            fprintf(stderr, "batch-test: prefill slot %d failed\n", i);
+    for (const Request & r : batched) max_n0 = std::max(max_n0, r.n0);
+    if (a.slot_cap <= 0)
+        for (Request & r : alone) {
+            Harness one(m, 1, r.n0 + a.max_frames, false, a.max_frames);
+            if (!one.ready || !one.admit(r, 0, sp) || !one.drain({&r})) r.codes.clear();
         }
+    Harness h(m, n_slots, a.slot_cap > 0 ? a.slot_cap : max_n0 + a.max_frames, a.gpu_sample, a.max_frames);
+    if (!h.ready) { fprintf(stderr, "batch-test: batch init failed\n"); return 1; }
+    std::vector<Request *> live;
+    for (int i = 0; i < n_req; ++i) {
+        if (h.admit(batched[i], i, sp)) live.push_back(&batched[i]);
+        else fprintf(stderr, "batch-test: prefill slot %d failed\n", i);
     }
-    // the first frame comes from the prefill logits on the host; later frames are sampled on the host
-    // from the step's logits, or on the GPU (--gpu-sample) straight after the step
-    bc.device_sampling = a.gpu_sample;
-    for (Job & j : jobs) {
-        if (!j.slot.active || j.slot.done) continue;
-        zonos2_slot_sample(m, j.slot, *j.smp, j.logits.data(), j.codes, a.max_frames, {});
-        j.eos_frame = j.slot.eos_frame;
-    }
-    for (;;) {
-        std::vector<zonos2_slot *> list;
-        for (Job & j : jobs) if (j.slot.active && !j.slot.done) list.push_back(&j.slot);
-        if (list.empty()) break;
-        zonos2_batch_step(bc, list);
-        if (a.gpu_sample) {
-            std::vector<zonos2_sampler *> smps;
-            std::vector<std::vector<int32_t> *> outs;
-            for (zonos2_slot * s : list) { smps.push_back(jobs[s->index].smp.get()); outs.push_back(&jobs[s->index].codes); }
-            if (!zonos2_batch_sample(bc, list, smps, outs, a.max_frames, {})) { zonos2_batch_free(bc); return 1; }
-        } else {
-            for (zonos2_slot * s : list) {
-                Job & j = jobs[s->index];
-                std::memcpy(j.logits.data(), zonos2_batch_slot_logits(bc, s->index), (size_t) av * ncb * sizeof(float));
-                zonos2_slot_sample(m, j.slot, *j.smp, j.logits.data(), j.codes, a.max_frames, {});
-            }
+    if (!h.drain(live)) {
+        if (!h.refused.empty()) {
+            printf("batch-test: step refused: %s\n", h.refused.c_str());
+            return 3;
         }
-        for (zonos2_slot * s : list) jobs[s->index].eos_frame = s->eos_frame;
+        fprintf(stderr, "batch-test: batched run failed\n");
+        return 1;
     }
+    if (a.slot_cap > 0) { printf("batch-test: no slot reached its capacity\n"); return 0; }
     printf("\n=== batch-test: %d requests in %d slots, %s%s, max=%d ===\n", n_req, n_slots, sp.greedy ? "greedy" : "sampling",
            a.gpu_sample ? " on the GPU" : "", a.max_frames);
-    int fails = 0, exact_all = 1;
+    auto frame_eq = [&](const std::vector<int32_t> & x, const std::vector<int32_t> & y, int f) {
+        return std::equal(x.begin() + (size_t) f * ncb, x.begin() + (size_t) (f + 1) * ncb, y.begin() + (size_t) f * ncb);
+    };
+    int fails = 0;
+    bool all_exact = true;
     for (int i = 0; i < n_req; ++i) {
-        const auto & b = jobs[i].codes;
-        const auto & r = ref[i];
-        const int nb = (int) b.size() / ncb, nr = (int) r.size() / ncb, cmp = std::min(nb, nr);
-        int first_div = -1, agree = 0;
-        for (int f = 0; f < cmp; ++f) {
-            bool eq = true;
-            for (int cb = 0; cb < ncb; ++cb) if (b[(size_t) f * ncb + cb] != r[(size_t) f * ncb + cb]) { eq = false; break; }
-            if (eq) ++agree; else if (first_div < 0) first_div = f;
+        const Request & b = batched[i], & r = alone[i];
+        const int nb = (int) b.codes.size() / ncb, nr = (int) r.codes.size() / ncb, common = std::min(nb, nr);
+        int same = 0, diverge = -1;
+        for (int f = 0; f < common; ++f) {
+            if (frame_eq(b.codes, r.codes, f)) ++same;
+            else if (diverge < 0) diverge = f;
         }
-        const bool exact = nb == nr && agree == cmp && nr > 0;
-        exact_all &= exact ? 1 : 0;
+        const bool exact = nr > 0 && nb == nr && same == common;
+        all_exact = all_exact && exact;
         printf("  req %d (prompt %d, n0=%d): batch=%d(eos=%d) ref=%d(eos=%d)  agree=%d/%d first_div=%d %s\n",
-               i, jobs[i].prompt_id, jobs[i].n0, nb, jobs[i].eos_frame, nr, ref_eos[i], agree, cmp, first_div, exact ? "EXACT" : "");
-        if (n_slots == 1 && sp.greedy && !exact) ++fails;            // F.1
+               i, b.prompt_id, b.n0, nb, b.slot.eos_frame, nr, r.slot.eos_frame, same, common, diverge, exact ? "EXACT" : "");
+        if (n_slots == 1 && sp.greedy && !exact) ++fails;             // one slot, greedy: must be exact
     }
     for (int i = 0; i < n_req; ++i)
-        for (int k = i + 1; k < n_req; ++k)
-            if (jobs[i].prompt_id == jobs[k].prompt_id && jobs[i].n0 == jobs[k].n0) {
-                const bool same = jobs[i].codes == jobs[k].codes;
-                printf("  F.2 slots %d,%d identical prompt -> %s\n", i, k, same ? "MATCH" : "MISMATCH");
-                if (!same) ++fails;
-            }
-    printf("  batch == alone for every request: %s\n", exact_all ? "yes" : "no");
-    zonos2_batch_free(bc);
+        for (int k = i + 1; k < n_req; ++k) {
+            if (batched[i].prompt_id != batched[k].prompt_id || batched[i].n0 != batched[k].n0) continue;
+            const bool match = batched[i].codes == batched[k].codes;  // identical prompts: identical frames
+            printf("  F.2 slots %d,%d identical prompt -> %s\n", i, k, match ? "MATCH" : "MISMATCH");
+            fails += match ? 0 : 1;
+        }
+    printf("  batch == alone for every request: %s\n", all_exact ? "yes" : "no");
     printf("batch-test: %s\n", fails ? "FAIL" : "OK");
     return fails ? 1 : 0;
 }
@@ -275,6 +287,7 @@ int main(int argc, char ** argv) {
         else if (s == "--prompt-len" && (v = next())) a.prompt_len = std::atoi(v);
         else if (s == "--requests" && (v = next())) a.requests = std::atoi(v);
         else if (s == "--seed" && (v = next())) a.seed = (uint32_t) std::strtoul(v, nullptr, 10);
+        else if (s == "--slot-cap" && (v = next())) a.slot_cap = std::atoi(v);
         else return usage();
     }
     if (a.model.empty() || (a.info + a.bench + a.test) != 1) return usage();
