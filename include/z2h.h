@@ -127,9 +127,10 @@ int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, con
                     float * d_logits, void * stream);
 
 /* Prefill n0 prompt rows into `slot` (rows [0, n0)), causal within the prompt as in the reference's
- * per-slot prefill; ids [n0][n_codebooks+1]. spk (optional, [spk_dim]) replaces row spk_pos's
- * embedding by spk_proj(spk_lda(spk)) (+ delta [n_embd] if non-NULL). last_logits receives the final
- * row's [n_codebooks][audio_vocab] logits. */
+ * per-slot prefill: the rows attend each other's fp32 K/V (src/zonos2-graph.cpp:155-169) while their
+ * f16 rows are written to the slot's cache for the decode steps; ids [n0][n_codebooks+1]. spk
+ * (optional, [spk_dim]) replaces row spk_pos's embedding by spk_proj(spk_lda(spk)) (+ delta [n_embd]
+ * if non-NULL). last_logits receives the final row's [n_codebooks][audio_vocab] logits. */
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits);
 

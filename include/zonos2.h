@@ -12,6 +12,9 @@
 //   zonos2_model_load / free    src/zonos2.h:124-125, src/zonos2.cpp:15-195
 //   zonos2_router_dim           src/zonos2.h:128, src/zonos2.cpp:241-246
 //   zonos2_set_expert_mask      src/zonos2.h:130-136, src/zonos2.cpp:203-239
+//   zonos2_prompt_options       src/zonos2.h:178-188 (+ zonos2_build_prompt 190-194, defined by the reference's
+//                               src/zonos2-prompt.cpp compiled against this header)
+//   zonos2_backend_name         stands for ggml_backend_name(model.backend), src/server.cpp:1601
 //   zonos2_sampling / sampler   src/zonos2.h:197-210, src/zonos2-sampler.h
 //   zonos2_frame_cb             src/zonos2.h:212-215
 //   zonos2_batch_ctx / slot     src/zonos2.h:217-274
@@ -99,6 +102,28 @@ int zonos2_router_dim(const zonos2_model & model);
 // others get -inf router logits and selection scores); layers absent from `keep` are unmasked and
 // {} clears every mask. Applies to every batch context of the model from its next step.
 bool zonos2_set_expert_mask(zonos2_model & model, const std::map<int, std::vector<int>> & keep);
+
+// Options of the text prompt builder (src/zonos2.h:178-188, same fields and defaults). The builder
+// itself, zonos2_build_prompt (src/zonos2-prompt.cpp), reads only model.hp (its cond_* layout,
+// n_codebooks, text_vocab, audio_pad_id) and is not part of this library: a caller that builds
+// prompts compiles the reference's src/zonos2-prompt.cpp against this header.
+struct zonos2_prompt_options {
+    bool             prepend_silence        = true;  // append 17 sheared-silence frames
+    int              speaking_rate_bucket   = -1;    // -1 = no speaking-rate row
+    std::vector<int> quality_buckets;                // per-feature bucket (-1 = skip); empty => default
+    bool             add_speaker_slot        = false; // prepend a speaker slot (+ markers) for cloning
+    bool             clean_speaker_background = true;
+    bool             accurate_mode           = true;
+};
+
+// Row-major input_ids [n_rows][n_codebooks + 1] of `text` (src/zonos2.h:190-194); spk_pos is the
+// speaker slot's row when one was prepended, else -1. Defined by src/zonos2-prompt.cpp.
+std::vector<int32_t> zonos2_build_prompt(const zonos2_model & model, const std::string & text,
+                                         const zonos2_prompt_options & opt, int & n_rows, int & spk_pos);
+
+// Name of the device the model's weights live on, for the messages and placement choices a caller
+// made from ggml_backend_name(model.backend) (src/server.cpp:1601); "" before a successful load.
+const char * zonos2_backend_name(const zonos2_model & model);
 
 struct zonos2_sampling {
     float    temperature   = 1.15f;

@@ -237,9 +237,9 @@ def _prompt(cfg, n0, seed):
 
 def test_prefill_with_speaker_vs_oracle():
     """zonos2_batch_slot_prefill with a speaker row (graph.cpp:262-297, 703-760): the device prefill
-    (speaker projections on the device, then causal rows over the f16 band) against the oracle's
-    row-by-row decode of the same prompt with the oracle's speaker row (full bar), and against the
-    oracle's one-shot prefill, whose in-prompt K/V stay fp32 (f16 rounding bar)."""
+    (speaker projections on the device, the prompt's own rows attended with fp32 K/V as the
+    reference's one-graph prefill does, graph.cpp:155-169) against the oracle's prefill at the full
+    bar: last-row logits and the f16 K/V rows left in the cache."""
     cfg, wl = configs.C1()
     model = synth.generate_model(cfg, 47)
     ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
@@ -251,23 +251,22 @@ def test_prefill_with_speaker_vs_oracle():
     delta = synth.gen_normal_f32((cfg.n_embd,), 4, "delta") * 0.1
     got = ctx.prefill(slot, ids, spk=spk, spk_pos=pos, delta=delta)
     okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
-    want_pf = O.prefill(om, okv, slot, ids, spk=spk, spk_pos=pos, delta=delta)
-    assert_close("prefill(spk) vs oracle prefill", got, want_pf, cos_min=0.9999, maxabs=5e-2)
-    # the oracle's speaker row, injected into row-by-row oracle steps
-    kv2 = O.OracleKV(om, wl.n_slots, wl.slot_cap)
-    sp = None
-    for t in range(n0):
-        if t == pos:
-            sp = _speaker_row_f32(model, spk, delta)   # the oracle's W_lda / W_proj products
-            want = O.step(om, kv2, [slot], [t], emb=sp[None, :])
-        else:
-            want = O.step(om, kv2, [slot], [t], ids=ids[t:t + 1])
-    assert_close("prefill(spk) vs oracle steps", got, want[0])
+    want = O.prefill(om, okv, slot, ids, spk=spk, spk_pos=pos, delta=delta)
+    assert_close("prefill(spk) vs oracle prefill", got, want)
     for L in range(cfg.n_layer):
         gk, gv = ctx.kv_read(L, slot, 0, n0)
-        ok, ov = kv2.read(L, slot, 0, n0)
+        ok, ov = okv.read(L, slot, 0, n0)
         assert_close(f"prefill K rows L{L}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32))
         assert_close(f"prefill V rows L{L}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32))
+    # the same prompt as row-by-row decode steps attends the f16 cache instead (the reference's decode
+    # path): close, but not the prefill's numbers
+    kv2 = O.OracleKV(om, wl.n_slots, wl.slot_cap)
+    for t in range(n0):
+        if t == pos:
+            dec = O.step(om, kv2, [slot], [t], emb=_speaker_row_f32(model, spk, delta)[None, :])
+        else:
+            dec = O.step(om, kv2, [slot], [t], ids=ids[t:t + 1])
+    assert_close("oracle prefill vs oracle steps", want, dec[0], cos_min=0.999, maxabs=1e-1)
     ctx.close()
 
 
@@ -296,38 +295,38 @@ def test_layer_skip_vs_oracle():
     ctx.close()
 
 
-def test_tiled_prefill_attention_equals_decode_steps():
-    """Prefill and mixed passes attend through tiles (up to 16 rows of one slot at consecutive
-    positions share each K/V chunk read); every row keeps the decode kernel's arithmetic. A 100-row
-    prompt prefilled in one chunk (tiles of 16 and a ragged 4, two 64-row chunks) and the same prompt
-    stepped row by row leave bit-identical K/V rows and last-row logits."""
+def test_tiled_attention_equals_decode_steps():
+    """Mixed passes attend through tiles (up to 16 rows of one slot at consecutive positions share
+    each K/V chunk read) over the f16 cache, keeping the decode kernel's arithmetic for every row. A
+    100-row run of one slot in one mixed pass (tiles of 16 and a ragged 4, two 64-row chunks) and the
+    same rows stepped one by one leave bit-identical K/V rows and logits."""
     cfg, wl = configs.C1()
     model = synth.generate_model(cfg, 52)
     n0, slot = 100, 1
     ids = _prompt(cfg, n0, 13)
-    a = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
-    a.upload(model)
-    print("prefill 100 rows", flush=True)
-    last = a.prefill(slot, ids)
-    b = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
-    b.upload(model)
+    m = Model(cfg.hparams(), model)
+    a = Context(None, wl.n_slots, wl.slot_cap, model=m, max_rows=n0)
+    print("one mixed pass of 100 rows", flush=True)
+    rows = np.arange(n0, dtype=np.int32)
+    got = a.step_mixed(np.full(n0, slot, np.int32), rows, ids, rows)
+    b = Context(None, wl.n_slots, wl.slot_cap, model=m)
     print("100 decode steps", flush=True)
     for t in range(n0):
         lg = b.step([slot], [t], ids=ids[t:t + 1])
-    np.testing.assert_array_equal(last, lg[0])
+        np.testing.assert_array_equal(got[t], lg[0])
     for L in range(cfg.n_layer):
         ka, va = a.kv_read(L, slot, 0, n0)
         kb, vb = b.kv_read(L, slot, 0, n0)
         np.testing.assert_array_equal(ka, kb)
         np.testing.assert_array_equal(va, vb)
-    a.close(); b.close()
+    a.close(); b.close(); m.close()
 
 
 def test_chunked_prefill_is_chunk_size_independent():
-    """Chunked prefill (every row of a chunk appends its K/V before the chunk's attention) gives the
-    same bits for any chunk size: one row at a time, 7-row chunks (ragged last chunk, the speaker
-    row inside a chunk) and the whole prompt in one chunk; the last-row logits also match the oracle's
-    row-by-row decode (full bar)."""
+    """Chunked prefill (every row of a chunk appends its K/V before the chunk's attention, which reads
+    the prompt's fp32 rows) gives the same bits for any chunk size: one row at a time, 7-row chunks
+    (ragged last chunk, the speaker row inside a chunk) and the whole prompt in one chunk; the last-row
+    logits also match the oracle's one-graph prefill (full bar)."""
     cfg, wl = configs.C1()
     model = synth.generate_model(cfg, 48)
     om = O.OracleModel(cfg.hparams(), model)
@@ -349,12 +348,8 @@ def test_chunked_prefill_is_chunk_size_independent():
             np.testing.assert_array_equal(kvs[i][L][0], kvs[0][L][0])
             np.testing.assert_array_equal(kvs[i][L][1], kvs[0][L][1])
     okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
-    for t in range(n0):
-        if t == pos:
-            want = O.step(om, okv, [slot], [t], emb=_speaker_row_f32(model, spk, np.zeros(cfg.n_embd, np.float32))[None, :])
-        else:
-            want = O.step(om, okv, [slot], [t], ids=ids[t:t + 1])
-    assert_close("chunked prefill vs oracle steps", outs[2], want[0])
+    want = O.prefill(om, okv, slot, ids, spk=spk, spk_pos=pos)
+    assert_close("chunked prefill vs oracle prefill", outs[2], want)
 
 
 def test_route_lists_in_lds_match_the_sorted_table():

@@ -108,6 +108,7 @@ struct z2h_ctx {
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * res2 = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
+    float * pf_kv = nullptr;          // z2h_prefill: the prompt's fp32 K/V rows [L][2][nkv][S][hd] (one slot at a time)
     ActBuf act{}, act_y{};
     float * attn_o = nullptr;         // [T][nh*hd] gated attention output
     float * state = nullptr;          // [L][T][rd]
@@ -432,6 +433,7 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->wo_out, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->part_o, (size_t) ctx->items_max * grp * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->part_ml, (size_t) ctx->items_max * grp * 2 * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->pf_kv, (size_t) hp.n_layer * 2 * nkv * ctx->S * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->act.q, (size_t) T * KM, b)) || (rc = dalloc(ctx, &ctx->act.d32, (size_t) T * (KM / 32) * 4, b)) ||
         (rc = dalloc(ctx, &ctx->act.d256, (size_t) T * (KM / 256) * 4, b)) || (rc = dalloc(ctx, &ctx->act.bs, (size_t) T * (KM / 16) * 2, b)) ||
         (rc = dalloc(ctx, &ctx->act.h, (size_t) T * KM * 2, b)) ||
@@ -779,9 +781,11 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
 // The whole decode step on device-resident inputs in ctx->d_* (T tokens, host copy of n_past).
 // kv_pre: append every token's K/V row before the attention (prefill chunks and mixed batches, whose
 // rows of one slot attend to each other); d_emb_map: per token -1 (sum of its ids) or its row of d_emb.
+// f32_prompt (per-slot prefill): the rows also keep their fp32 K/V in ctx->pf_kv and attend over those
+// (the reference's in-prompt attention, src/zonos2-graph.cpp:155-169) instead of the f16 cache rows.
 int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
              const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false,
-             const int32_t * d_emb_map = nullptr, const int32_t * h_slot = nullptr) {
+             const int32_t * d_emb_map = nullptr, const int32_t * h_slot = nullptr, bool f32_prompt = false) {
     const auto & hp = ctx->hp;
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
@@ -848,6 +852,10 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         a.cap_gate = (float *) capp(ctx, Z2H_CAP_GATE, L);
         a.part_o = ctx->part_o; a.part_ml = ctx->part_ml;
         a.o_out = ctx->attn_o;
+        if (f32_prompt) {
+            a.kf = ctx->pf_kv + (size_t) (2 * L) * nkv * ctx->S * hd;
+            a.vf = a.kf + (size_t) nkv * ctx->S * hd;
+        }
         a.act = ctx->act;
         const int wo_act = act_of(ly.wo.type);
         // heads per combine block: the fewest (1, 2, 4 or 8, dividing the group) whose outputs cover
@@ -940,6 +948,21 @@ int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T) {
 
 int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles) {
     const int grp = a.nh / a.nkv;
+    if (a.kf) {
+        const size_t lds = attn_tile_f32_lds(a.hd, grp);
+#define ATF(H_, G_) KL((k_attn_tile_f32<H_, G_>), dim3(n_tiles), dim3(256), lds, ctx->stream, a, (const int4 *) ctx->d_tiles)
+#define ATF_G(H_) switch (grp) { case 1: ATF(H_, 1); break; case 2: ATF(H_, 2); break; case 4: ATF(H_, 4); break; default: ATF(H_, 8); }
+        switch (a.hd) {
+            case 16: ATF_G(16) break;
+            case 32: ATF_G(32) break;
+            case 64: ATF_G(64) break;
+            default: ATF_G(128) break;
+        }
+#undef ATF_G
+#undef ATF
+        HIPX(hipGetLastError());
+        return Z2H_OK;
+    }
 #define ATT(H_, G_) KL((k_attn_tile<H_, G_>), dim3(n_tiles), dim3(256), 0, ctx->stream, a, (const int4 *) ctx->d_tiles)
 #define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
     switch (a.hd) {
@@ -1238,6 +1261,9 @@ int z2h_finalize(z2h_ctx * ctx) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
+#define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>))
+    LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
+#undef LDS_TF
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     {
@@ -1413,10 +1439,11 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
         sp.resize(ctx->hp.n_embd);
         if (int rc = speaker_row(ctx, spk, delta, sp.data())) return rc;
     }
-    // causal prefill in chunks of rows [r0, r0 + T): every row of a chunk appends its K/V before the
-    // chunk's attention, then row r attends rows [0, r] of the band. Each row's arithmetic is the
-    // decode step's for a column at n_past = r, so any chunk size gives the same bits. With capture on,
-    // chunks stay within the step width the capture buffers hold.
+    // causal prefill in chunks of rows [r0, r0 + T): every row of a chunk appends its K/V (f16 into the
+    // cache, fp32 into the prompt rows) before the chunk's attention, then row r attends the prompt's
+    // fp32 rows [0, r], as the reference's one-graph prefill attends its fp32 K/V (graph.cpp:155-169).
+    // A row's arithmetic does not depend on the chunk it is in, so any chunk size gives the same bits.
+    // With capture on, chunks stay within the step width the capture buffers hold.
     const int chunk = std::max(1, std::min(ctx->pch, ctx->capture ? ctx->Tstep : ctx->Tmax));
     const size_t row = (size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab;
     for (int r0 = 0; r0 < n0; r0 += chunk) {
@@ -1437,7 +1464,7 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
             HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
         }
         if (int rc = run_step(ctx, T, hp_ + T, ctx->d_slot, ctx->d_npast, ctx->d_ids, er >= 0 ? ctx->d_emb : nullptr,
-                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr, hp_)) return rc;
+                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr, hp_, /*f32_prompt=*/true)) return rc;
         if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits + (size_t) (T - 1) * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
         HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }

@@ -1275,6 +1275,7 @@ struct AttnArgs {
     float * part_ml;         // [items][grp][2]
     float * o_out;           // [T][nh*hd] (combine: gated output, fp32)
     ActBuf act; int act_fmt; // encoding of o_out for W_o
+    float * kf, * vf;        // per-slot prefill: this layer's fp32 prompt K/V [nkv][S][hd] (null: f16 cache only)
 };
 
 // Wave-parallel item bookkeeping: lane u of each 64-token group loads n_past[u] (and slot_idx[u]) and
@@ -1651,7 +1652,113 @@ __global__ void __launch_bounds__(64) k_kv_append(AttnArgs a) {
         const int64_t at = (((int64_t) slot * nkv + g) * a.S + np) * HD + 2 * lane;
         *(uint32_t *) (a.kc + at) = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
         *(uint32_t *) (a.vc + at) = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
+        if (a.kf) {                                                  // the prompt's fp32 rows
+            const int64_t af = ((int64_t) g * a.S + np) * HD + 2 * lane;
+            *(float2 *) (a.kf + af) = make_float2(k0, k1);
+            *(float2 *) (a.vf + af) = make_float2(v0, v1);
+        }
     }
+}
+
+// Per-slot prefill attention with the reference's in-prompt semantics (src/zonos2-graph.cpp:155-169:
+// the prompt's K and V stay fp32 for its own causal attention, softmax(K^T q / sqrt(hd)) then V.P):
+// k_attn_tile's tiling, item numbering and partial layout, with the chunk's K/V rows read from the
+// fp32 prompt rows (a.kf / a.vf, [nkv][S][hd], written by k_kv_append) and fp32 queries; scores and
+// P.V are fp32 fma chains over dims / rows in order. k_attn_combine merges the partials unchanged.
+// LDS (dynamic): K [64][HD + 4], V [64][HD], per-wave queries [4][GRP][HD] and weights [4][64][GRP].
+template <int HD, int GRP>
+__global__ void __launch_bounds__(256) k_attn_tile_f32(AttnArgs a, const int4 * __restrict__ tiles) {
+    constexpr int NP = HD / 2, KST = HD + 4, N4 = ATT_CH * HD / 4;
+    extern __shared__ __attribute__((aligned(16))) float sm_at[];
+    float * s_k = sm_at;                                             // [ATT_CH][KST]
+    float * s_v = s_k + ATT_CH * KST;                                // [ATT_CH][HD]
+    float * s_q = s_v + ATT_CH * HD;                                 // [4][GRP][HD]
+    float * s_p = s_q + 4 * GRP * HD;                                // [4][ATT_CH][GRP]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
+    const int4 e = tiles[blockIdx.x];
+    const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16, c = e.z;
+    const int p0 = a.n_past[t0];
+    const int r0 = c * ATT_CH, nrmax = min(ATT_CH, p0 + m - r0);
+    const float * kb = a.kf + ((int64_t) g * a.S + r0) * HD, * vb = a.vf + ((int64_t) g * a.S + r0) * HD;
+    {
+        // the chunk's rows once (rows past the tile's last one re-read it), every load before a store
+        constexpr int PER = (N4 + 255) / 256;
+        float4 kk[PER], vv[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = min(tid + 256 * j, N4 - 1), r = min(i / (HD / 4), nrmax - 1), d4 = i % (HD / 4);
+            kk[j] = *(const float4 *) (kb + (int64_t) r * HD + 4 * d4);
+            vv[j] = *(const float4 *) (vb + (int64_t) r * HD + 4 * d4);
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid + 256 * j;
+            if (i < N4) {
+                *(float4 *) &s_k[(i / (HD / 4)) * KST + 4 * (i % (HD / 4))] = kk[j];
+                *(float4 *) &s_v[(i / (HD / 4)) * HD + 4 * (i % (HD / 4))] = vv[j];
+            }
+        }
+    }
+    lds_sync();
+    float * wq = s_q + wave * GRP * HD;
+    float * wp = s_p + wave * ATT_CH * GRP;
+    int before = e.w;
+    for (int i = 0; i < m; ++i) {
+        const int np = p0 + i, nc = (np + ATT_CH) / ATT_CH;
+        const int64_t item = (int64_t) (before + c) * nkv + g;
+        before += nc;
+        if ((i & 3) != wave || c >= nc) continue;                    // row i is wave i % 4's; its band may end before c
+        const int t = t0 + i, nr = min(ATT_CH, np + 1 - r0);
+        {
+            const float * row = a.qkvg + (int64_t) t * a.R;
+            float cs, sn;
+            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
+#pragma unroll
+            for (int h = 0; h < GRP; ++h) {
+                const int qh = g * GRP + h;
+                const float * src = row + (int64_t) qh * HD;
+                const float x0 = lane < NP ? src[2 * lane] : 0.0f, x1 = lane < NP ? src[2 * lane + 1] : 0.0f;
+                float y0, y1;
+                norm_rope<HD>(x0, x1, a.temp[qh], a.qk_eps, cs, sn, y0, y1);
+                if (lane < NP) *(float2 *) &wq[h * HD + 2 * lane] = make_float2(y0, y1);
+            }
+        }
+        // scores (lane = chunk row), then the chunk softmax of each head
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int d4 = 0; d4 < HD / 4; ++d4) {
+                const float4 kk = *(const float4 *) &s_k[lane * KST + 4 * d4];
+                const float4 qq = *(const float4 *) &wq[h * HD + 4 * d4];
+                acc = __builtin_fmaf(qq.x, kk.x, acc); acc = __builtin_fmaf(qq.y, kk.y, acc);
+                acc = __builtin_fmaf(qq.z, kk.z, acc); acc = __builtin_fmaf(qq.w, kk.w, acc);
+            }
+            const float sv = lane < nr ? acc * a.scale : -__builtin_inff();
+            const float mx = wave_max_f(sv);
+            const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
+            const float l = wave_tree_f(pe);
+            wp[lane * GRP + h] = pe;
+            if (lane == 0) *(float2 *) (a.part_ml + (item * GRP + h) * 2) = make_float2(mx, l);
+        }
+        // P.V: lane = dim pair, rows in order
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            if (lane >= NP) break;
+            float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 16
+            for (int r = 0; r < ATT_CH; ++r) {
+                const float2 vv = *(const float2 *) &s_v[r * HD + 2 * lane];
+                const float pp = wp[r * GRP + h];
+                o0 = __builtin_fmaf(pp, vv.x, o0);
+                o1 = __builtin_fmaf(pp, vv.y, o1);
+            }
+            *(float2 *) (a.part_o + (item * GRP + h) * HD + 2 * lane) = make_float2(o0, o1);
+        }
+    }
+}
+__host__ __device__ inline size_t attn_tile_f32_lds(int hd, int grp) {
+    return (size_t) 4 * (ATT_CH * (hd + 4) + ATT_CH * hd + 4 * grp * hd + 4 * ATT_CH * grp);
 }
 
 // Merge the chunks of HPB query heads of one token and apply the per-head sigmoid gate. grid

@@ -303,6 +303,10 @@ void zonos2_batch_step(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *> &
     for (zonos2_slot * sp : run) sp->n_past += 1;
 }
 
+const char * zonos2_backend_name(const zonos2_model & model) {
+    return model.is_gpu && model.dev ? "ROCm HIP (MI355X, gfx950)" : "";
+}
+
 const float * zonos2_batch_slot_logits(const zonos2_batch_ctx & bc, int index) {
     return bc.h_logits.data() + (size_t) index * bc.av * bc.ncb;
 }
