@@ -160,6 +160,22 @@ int z2h_moe_forward(z2h_ctx * ctx, int layer, int n_tokens, const float * x, con
 int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int n_tokens, const float * d_x, const float * d_state_in,
                            float * d_out, void * stream);
 
+/* One MoE layer (as z2h_moe_forward_device) on a model alone, allocating nothing: no context, and no
+ * hipMalloc / hipFree or other allocating call. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it). Every intermediate buffer (activation encodings, routing, route lists, SwiGLU
+ * rows, per-route outputs, the router state unless d_state_out is given) is carved from a static
+ * device array of 16 MiB per GPU, held until the process ends; a call whose buffers would not fit
+ * (n_tokens x top-k routes at the model's widths) is refused with Z2H_EINVAL before any launch, as
+ * is n_tokens * top-k > 1024. Calls on one GPU share that array: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialized by the caller. Enqueued on `stream` (NULL: the
+ * null stream) without synchronizing. d_x [n_tokens][n_embd] (the layer's ffn_in), d_state_in
+ * ([n_tokens][router_dim] or NULL), d_state_out (NULL, or [n_tokens][router_dim] receiving this
+ * layer's router state), d_out [n_tokens][n_embd]. Results are bit-identical to z2h_moe_forward_device.
+ * Errors: z2h_model_last_error. */
+int z2h_model_moe_forward_noalloc(z2h_model * m, int layer, int n_tokens, const float * d_x, const float * d_state_in,
+                                  float * d_state_out, float * d_out, void * stream);
+
 /* Runtime expert mask for one MoE layer: keep[e] != 0 keeps expert e routable (logits and selection
  * scores of the others get -inf); keep == NULL clears the layer's mask. */
 int z2h_set_expert_mask(z2h_ctx * ctx, int layer, const uint8_t * keep);

@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <set>
 #include <memory>
 #include <string>
@@ -113,6 +114,7 @@ struct z2h_ctx {
     float * attn_o = nullptr;         // [T][nh*hd] gated attention output
     float * state = nullptr;          // [L][T][rd]
     float * state_ext = nullptr;      // [T][rd] external state for moe_forward
+    float * state_one = nullptr;      // when set: the router state of the one layer run (no per-layer table)
     int32_t * sel = nullptr; float * wsel = nullptr;
     int32_t * r_off = nullptr, * r_perm = nullptr;   // routes grouped by expert ([E+1] offsets, [T*k] ids)
     float * gu_g = nullptr, * gu_u = nullptr, * eo = nullptr, * logits = nullptr, * tmp_x = nullptr;
@@ -634,7 +636,7 @@ RouterArgs router_args(z2h_ctx * ctx, const Layer & ly, int L, int T, const floa
     RouterArgs r{};
     r.x = ctx->cur; r.T = T; r.d = hp.n_embd; r.rd = ctx->rd; r.E = ly.E; r.k = ly.k;
     r.w_down = ly.r_down; r.b_down = ly.r_down_b; r.eda = ly.r_eda; r.state_in = state_in;
-    r.rh = ctx->state + (size_t) L * ctx->Tmax * ctx->rd;
+    r.rh = ctx->state_one ? ctx->state_one : ctx->state + (size_t) L * ctx->Tmax * ctx->rd;
     r.norm_w = ly.r_norm; r.eps = hp.rms_eps;
     r.w0t = ly.r_m0t; r.b0 = ly.r_m0_b; r.w2t = ly.r_m2t; r.b2 = ly.r_m2_b; r.w4t = ly.r_m4t;
     r.logit_bias = ly.logit_bias; r.mask = ly.mask; r.sc_bias = ly.r_bias;
@@ -1045,6 +1047,38 @@ int step_internal(z2h_ctx * ctx, int T, const int32_t * h_npast, bool use_ids) {
     return Z2H_OK;
 }
 
+} // namespace
+
+// ---------------------------------------------------------------- the no-allocation MoE layer's scratch
+// z2h_model_moe_forward_noalloc carves every intermediate buffer of one MoE layer from this array
+// instead of a context's allocations. Each GPU the library runs on holds its own copy for the life of
+// the process; host code never names it (its name is a host-side stand-in): it uses the per-device
+// address that hipGetSymbolAddress returns, taken once per device with that device current.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) 16 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void * g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// the device address of `scratch` on `device` (looked up on the first call for that device)
+int scratch_address(int device, void ** out, std::string & err) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) { err = "device index out of range"; return Z2H_EINVAL; }
+    if (!g_scratch_ptr[device]) {
+        int keep = 0;
+        if (hipGetDevice(&keep) != hipSuccess) { err = "hipGetDevice failed"; return Z2H_EDEVICE; }
+        if (hipSetDevice(device) != hipSuccess) { err = "hipSetDevice failed"; return Z2H_EDEVICE; }
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        (void) hipSetDevice(keep);
+        if (e != hipSuccess || !p) { err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e); return Z2H_EDEVICE; }
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return Z2H_OK;
+}
 } // namespace
 
 // ====================================================================== C ABI
@@ -1565,6 +1599,58 @@ int z2h_moe_forward(z2h_ctx * ctx, int layer, int T, const float * x, const floa
     if (int rc = z2h_moe_forward_device(ctx, layer, T, ctx->tmp_x, state_in ? ctx->state_ext : nullptr, ctx->wo_out, nullptr)) return rc;
     HIPX(hipMemcpyAsync(out, ctx->wo_out, (size_t) T * ctx->hp.n_embd * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
+    return Z2H_OK;
+}
+
+int z2h_model_moe_forward_noalloc(z2h_model * mdl, int layer, int T, const float * d_x, const float * d_state_in,
+                                  float * d_state_out, float * d_out, void * stream) {
+    if (!mdl || !d_x || !d_out) return mdl ? seterr(mdl, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (!mdl->finalized) return seterr(mdl, Z2H_ESTATE, "model not finalized");
+    const auto & hp = mdl->hp;
+    if (layer < 0 || layer >= hp.n_layer || !mdl->layers[layer].moe) return seterr(mdl, Z2H_EINVAL, "layer is not MoE");
+    Layer & ly = mdl->layers[layer];
+    if (T <= 0 || T * ly.k > LIST_MAX) return seterr(mdl, Z2H_EINVAL, "n_tokens out of range (1 .. 1024 / top-k)");
+    // the buffers z2h_moe_forward_device takes from a context, carved 256-byte aligned from `scratch`
+    const int d = hp.n_embd, ff = hp.n_ff, K = ly.k, E = std::max(1, ly.E), rd = std::max(1, mdl->rd);
+    const int Kd = kpad(d), Kf = kpad(std::max(ff, 1)), R = T * K;
+    struct Piece { void ** at; size_t bytes; };
+    z2h_ctx c;
+    std::vector<Piece> plan;                          // (host vector: no device allocation)
+    plan.reserve(20);
+    auto want = [&](auto ** p, size_t n) { plan.push_back({(void **) p, n}); };
+    want(&c.act.q, (size_t) T * Kd); want(&c.act.d32, (size_t) T * (Kd / 32) * 4); want(&c.act.d256, (size_t) T * (Kd / 256) * 4);
+    want(&c.act.bs, (size_t) T * (Kd / 16) * 2); want(&c.act.h, (size_t) T * Kd * 2);
+    want(&c.act_y.q, (size_t) R * Kf); want(&c.act_y.d32, (size_t) R * (Kf / 32) * 4); want(&c.act_y.d256, (size_t) R * (Kf / 256) * 4);
+    want(&c.act_y.bs, (size_t) R * (Kf / 16) * 2); want(&c.act_y.h, (size_t) R * Kf * 2);
+    want(&c.sel, (size_t) R * 4); want(&c.wsel, (size_t) R * 4);
+    want(&c.r_off, (size_t) (E + 1) * 4); want(&c.r_perm, (size_t) R * 4);
+    want(&c.gu_g, (size_t) R * ff * 4); want(&c.gu_u, (size_t) R * ff * 4); want(&c.eo, (size_t) R * d * 4);
+    if (!d_state_out) want(&c.state_one, (size_t) T * rd * 4);
+    size_t total = 0;
+    for (const Piece & pc : plan) total += (pc.bytes + 255) & ~(size_t) 255;
+    if (total > NOALLOC_SCRATCH_BYTES)
+        return seterr(mdl, Z2H_EINVAL, "z2h_model_moe_forward_noalloc: " + std::to_string(T) + " tokens need " + std::to_string(total) +
+                                       " bytes of scratch; the static scratch holds " + std::to_string(NOALLOC_SCRATCH_BYTES));
+    void * base = nullptr;
+    std::string err;
+    if (int rc = scratch_address(mdl->device, &base, err)) return seterr(mdl, rc, err);
+    if (hipSetDevice(mdl->device) != hipSuccess) return seterr(mdl, Z2H_EDEVICE, "hipSetDevice failed");
+    size_t off = 0;
+    for (const Piece & pc : plan) { *pc.at = (uint8_t *) base + off; off += (pc.bytes + 255) & ~(size_t) 255; }
+    if (d_state_out) c.state_one = d_state_out;
+    c.m = mdl; c.hp = hp; c.device = mdl->device; c.stream = (hipStream_t) stream;
+    c.W = mdl->W; c.rd = mdl->rd; c.kmax = mdl->kmax; c.Tmax = c.Tstep = T; c.finalized = true;
+    c.cur = const_cast<float *>(d_x);                 // read only: the router input and the encoder's source
+    // the kernels of z2h_moe_forward_device: encode, router + grouped experts, k-sum (no memset, no copy)
+    int rc;
+    ResNormArgs e{};
+    e.mode = RN_ENCODE; e.src = c.cur; e.act = c.act; e.act_fmt = act_of(ly.up_exps.type);
+    if (!(rc = launch_resnorm(&c, T, e)) && !(rc = expert_block(&c, ly, layer, T, d_state_in))) {
+        ResNormArgs n{};
+        n.mode = RN_ACCUM; n.src = c.eo; n.k = ly.k; n.res = nullptr; n.cap_x = d_out; n.act_fmt = ACT_NONE;
+        rc = launch_resnorm(&c, T, n);
+    }
+    if (rc) return seterr(mdl, rc, c.err);
     return Z2H_OK;
 }
 

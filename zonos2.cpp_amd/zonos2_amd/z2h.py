@@ -54,6 +54,7 @@ def lib() -> C.CDLL:
         "z2h_prefill": (i32, [vp, i32, vp, i32, vp, i32, vp, vp]),
         "z2h_moe_forward": (i32, [vp, i32, i32, vp, vp, vp]),
         "z2h_moe_forward_device": (i32, [vp, i32, i32, vp, vp, vp, vp]),
+        "z2h_model_moe_forward_noalloc": (i32, [vp, i32, i32, vp, vp, vp, vp, vp]),
         "z2h_set_expert_mask": (i32, [vp, i32, vp]),
         "z2h_set_logit_bias": (i32, [vp, i32, vp]),
         "z2h_set_capture": (i32, [vp, i32]),
@@ -80,6 +81,7 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_model_set_logit_bias", "z2h_model_set_layer_skip", "z2h_set_layer_skip", "z2h_model_last_error", "z2h_model_release", "z2h_create_batch",
            "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
+           "z2h_model_moe_forward_noalloc",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
            "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample", "z2h_set_prefill_chunk",
            "z2h_sample_feed", "z2h_step_resident", "z2h_create_batch_rows", "z2h_step_mixed",
@@ -138,6 +140,11 @@ class Model:
     def set_expert_mask(self, layer, keep):
         k = None if keep is None else np.ascontiguousarray(keep, dtype=np.uint8)
         self.check(lib().z2h_model_set_expert_mask(self.m, layer, _p(k)))
+
+    def moe_forward_noalloc(self, layer, n_tokens, d_x, d_state_in, d_state_out, d_out, stream=None):
+        """z2h_model_moe_forward_noalloc on device pointers (ints), enqueued on `stream`."""
+        self.check(lib().z2h_model_moe_forward_noalloc(self.m, layer, n_tokens, d_x, d_state_in or None,
+                                                       d_state_out or None, d_out, stream))
 
     def close(self):
         if getattr(self, "m", None):
