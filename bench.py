@@ -80,7 +80,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c3", "c4-q6_k", "c4-q8_0"])
-    ap.add_argument("--cpu-steps", type=int, default=2, help="timed oracle steps for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=5, help="timed oracle steps for the CPU baseline after 2 warm-ups (0: skip)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the timed region, copy 256 MiB device to device once (a kernel of known traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -147,13 +147,17 @@ def main() -> int:
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     ev0.record(stream)
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        evs[i].record(stream)
         one()
+    evs[args.steps].record(stream)
     ev1.record(stream)
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / args.steps
-    log(f"step: {ms:.3f} ms over {args.steps} steps")
+    med_ms = float(np.median([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]))
+    log(f"step: {ms:.3f} ms mean over {args.steps} steps (median {med_ms:.3f} ms)")
     got = d_logits.cpu().numpy()
     assert np.array_equal(got, logits_gpu), "device-resident step differs from the host-API step"
 
@@ -172,7 +176,7 @@ def main() -> int:
     # + the encoded activations read + the fp32 gate/up rows written
     gu_w = sum(model[f"blk.{L}.ffn_gate_exps.weight"].data.nbytes // cfg.n_expert * 2 * len(used[L]) for L in range(cfg.n_layer))
     act_b = cfg.n_layer * T * (cfg.n_embd + cfg.n_embd // 256 * 4 + cfg.n_embd // 16 * 2)
-    gu_out = cfg.n_layer * T * cfg.top_k * cfg.n_ff * 4 * 2
+    gu_out = cfg.n_layer * T * cfg.top_k * cfg.n_ff * 4                 # one fp32 SwiGLU row per route
     gu_ms, gu_n = prof["gemv_gateup"]
     dom_gbps = (gu_w + act_b + gu_out) * args.steps / (gu_ms / 1000.0) / 1e9 if gu_ms > 0 else 0.0
     step_gbps = B / (ms / 1000.0) / 1e9
@@ -180,15 +184,16 @@ def main() -> int:
     cpu = None
     if args.cpu_steps > 0:
         import oracle_py as O
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads, nproc, cpu_model = cpu_share()
         O.lib().orc_set_threads(threads)
         om = O.OracleModel(cfg.hparams(), model, logit_bias=bias)
         okv = O.OracleKV(om, wl.n_slots, wl.slot_cap)
         for (L, s), (k, v) in kv_cache.items():
             okv.write(L, s, 0, k, v)
         t0 = time.time()
-        ref, cap = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids, capture=True)
+        ref, cap = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids, capture=True)   # warm-up 1 (+ parity capture)
         t_first = time.time() - t0
+        O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids)                             # warm-up 2
         times = []
         for _ in range(args.cpu_steps):
             t0 = time.time()
@@ -201,8 +206,9 @@ def main() -> int:
         log(f"oracle: {t_cpu:.2f}s/step on {threads} threads (first {t_first:.2f}s); logits cos {cosv:.7f}, "
             f"max|d| {np.abs(a - b).max():.2e}; layers whose top-k ids differ end-to-end: {mism}/{cfg.n_layer}")
         cpu = {"value": round(T / t_cpu, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{1 + args.cpu_steps} full decode steps of the same workload (median of {args.cpu_steps} "
-                         f"after 1 warm-up), C++ restatement of the ggml CPU path",
+               "sample": f"{2 + args.cpu_steps} full decode steps of the same workload (median of {args.cpu_steps} "
+                         f"after 2 warm-ups), C++ restatement of the ggml CPU path",
+               "nproc": nproc, "cpu_model": cpu_model, "threads": threads,
                "logits_cos_vs_gpu": round(cosv, 7)}
 
     # the next rows of the path, outside the decode step: chunked prefill of one 1024-row prompt (it
@@ -241,6 +247,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "median_ms_per_step": round(med_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -279,6 +286,27 @@ def main() -> int:
     return 0
 
 
+def cpu_share():
+    """Threads for the CPU baseline: the cores this process may run on, capped by OMP_NUM_THREADS
+    when it is set (the machine's share for one GPU); also nproc and the CPU model, for the record."""
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = nproc
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(avail, cap) if cap > 0 else avail)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, nproc, model
+
+
 INT8_MFMA_PEAK_TOPS = 5000.0
 
 
@@ -292,6 +320,11 @@ def dtype_of(bulk):
     if w == "q6_k":
         return "q6_k weights x q8_k activations (int8 dot4, fp32 accumulate); f16 KV; fp32 router"
     return f"{w} weights x f16 activations (fp32 accumulate); f16 KV; fp32 router"
+
+
+def type_name(t):
+    from zonos2_amd.configs import TYPE_NAMES
+    return TYPE_NAMES[t]
 
 
 def gateup_kernel_of(bulk):
@@ -330,7 +363,7 @@ def mixed_pass(np, Context, synth, cfg, mdl):
     ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (R, cfg.n_codebooks)),
                           rng.integers(0, cfg.text_vocab + 1, (R, 1))], axis=1).astype(np.int32)
     assert ids.shape[1] == W
-    emb = rng.standard_normal((n_pre, cfg.n_embd)).astype(np.float32)
+    spk = rng.standard_normal((n_pre, cfg.spk_dim)).astype(np.float32)   # speaker vectors, projected per pass
     out_rows = np.array([g[-1] for g in groups], np.int32)
     mctx = Context(None, n_pre + n_dec, cap, model=mdl, max_rows=R)
     for L in range(cfg.n_layer):
@@ -342,11 +375,17 @@ def mixed_pass(np, Context, synth, cfg, mdl):
             k, v = synth.kv_rows(cfg, L, n_pre + i, n, 11)
             mctx.kv_write(L, n_pre + i, 0, k, v)
     args = (np.array(slots, np.int32), np.array(npast, np.int32), ids, out_rows)
-    mctx.step_mixed(*args, emb_map=np.array(emap, np.int32), emb=emb)
+    emap_a = np.array(emap, np.int32)
+
+    def one_pass():
+        emb = mctx.speaker_embed(spk)                  # spk_lda -> spk_proj on the device (graph.cpp:262-297)
+        return mctx.step_mixed(*args, emb_map=emap_a, emb=emb)
+
+    one_pass()
     ts = []
     for _ in range(3):
         t0 = time.perf_counter()
-        mctx.step_mixed(*args, emb_map=np.array(emap, np.int32), emb=emb)
+        one_pass()
         ts.append(time.perf_counter() - t0)
     ms = float(np.median(ts)) * 1000.0
     mctx.close()
@@ -362,7 +401,7 @@ def mixed_pass(np, Context, synth, cfg, mdl):
             "rows_per_s": round(R / ms * 1000.0, 1),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s (int8)",
                          "frac": round(tops / INT8_MFMA_PEAK_TOPS, 5)},
-            "weights": "q4_k", "speaker_rows": "N(0,1) embedding rows in place of the summed token embeddings"}
+            "weights": type_name(cfg.bulk).lower(), "speaker_rows": "2048-d N(0,1) speaker vectors through spk_lda -> spk_proj on the device (z2h_speaker_embed), in the timed pass"}
 
 
 if __name__ == "__main__":

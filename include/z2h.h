@@ -21,6 +21,7 @@
  *   z2h_finalize          as z2h_model_finalize, then the context's scratch
  *   z2h_step              zonos2_batch_step            src/zonos2-graph.cpp:762-837 (+ slot_logits 839-841)
  *   z2h_prefill           zonos2_batch_slot_prefill    src/zonos2-graph.cpp:703-760
+ *   z2h_speaker_embed     the speaker column of build_graph, src/zonos2-graph.cpp:262-297
  *   z2h_moe_forward       build_moe                    src/zonos2-graph.cpp:191-239 (one MoE layer)
  *   z2h_set_expert_mask   zonos2_set_expert_mask       src/zonos2.cpp:203-239, src/zonos2.h:136
  *   z2h_destroy           zonos2_batch_free            src/zonos2-graph.cpp:692-701 (+ drops the model reference)
@@ -133,6 +134,14 @@ int z2h_step_device(z2h_ctx * ctx, int n_active, const int32_t * d_slot_idx, con
  * if non-NULL). last_logits receives the final row's [n_codebooks][audio_vocab] logits. */
 int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const float * spk, int spk_pos,
                 const float * delta, float * last_logits);
+
+/* The speaker rows of n speaker vectors (spk [n][spk_dim]; n <= Z2H_SPEAKER_MAX): spk_proj(spk_lda(spk)
+ * + b_lda) + b_proj (+ delta [n][n_embd] if non-NULL), into out [n][n_embd] (host memory) - the
+ * column the reference writes over a prompt row before emb_norm (src/zonos2-graph.cpp:262-297), for
+ * callers that place speaker rows in a mixed pass themselves (emb_map / emb of z2h_step_mixed);
+ * z2h_prefill computes its speaker row the same way. Synchronizes the context's stream. */
+#define Z2H_SPEAKER_MAX 64
+int z2h_speaker_embed(z2h_ctx * ctx, int n, const float * spk, const float * delta, float * out);
 
 /* One pass over n_rows rows from any slots, decode columns and prefill-chunk rows mixed (the
  * reference has no mixed pass; it is its zonos2_batch_step and zonos2_batch_slot_prefill graphs in

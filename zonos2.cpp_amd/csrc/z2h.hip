@@ -455,7 +455,7 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->d_err, 16, b)))
         return rc;
     if (hp.spk_dim > 0 && hp.spk_lda_dim > 0 &&
-        (rc = dalloc(ctx, &ctx->spk_io, (size_t) (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
+        (rc = dalloc(ctx, &ctx->spk_io, (size_t) Z2H_SPEAKER_MAX * (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
         return rc;
     (void) E;
     if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) ctx->items_max * sizeof(int4), b))) return rc;
@@ -1428,28 +1428,35 @@ int z2h_step_device(z2h_ctx * ctx, int T, const int32_t * d_slot, const int32_t 
     return rc;
 }
 
-// Speaker row (graph.cpp:262-297): sp = W_proj (W_lda spk + b_lda) + b_proj (+ delta) -> host [n_embd]
-static int speaker_row(z2h_ctx * ctx, const float * spk, const float * delta, float * out) {
+// Speaker rows (graph.cpp:262-297): sp = W_proj (W_lda spk + b_lda) + b_proj (+ delta), for n <=
+// Z2H_SPEAKER_MAX speaker vectors at once (each GEMV takes the n rows as one batch) -> host [n][n_embd]
+static int speaker_rows(z2h_ctx * ctx, int n, const float * spk, const float * delta, float * out) {
     z2h_model * m = ctx->m;
     const auto & hp = ctx->hp;
     if (!m->spk_lda.ok() || !m->spk_proj.ok() || !m->spk_lda_b || !m->spk_proj_b || !ctx->spk_io)
         return seterr(ctx, Z2H_ESTATE, "speaker tensors (spk_lda / spk_proj) not uploaded");
+    if (n <= 0 || n > Z2H_SPEAKER_MAX) return seterr(ctx, Z2H_EINVAL, "speaker rows out of range (1 .. Z2H_SPEAKER_MAX)");
     const int sd = hp.spk_dim, ld = hp.spk_lda_dim, d = hp.n_embd;
     if (m->spk_lda.K != sd || m->spk_lda.rows != ld || m->spk_proj.K != ld || m->spk_proj.rows != d)
         return seterr(ctx, Z2H_EINVAL, "speaker tensor shapes do not match spk_dim / spk_lda_dim");
-    float * x = ctx->spk_io, * sl = x + kpad(sd), * sp = sl + kpad(ld), * dl = sp + kpad(d);
+    float * x = ctx->spk_io, * sl = x + (size_t) n * kpad(sd), * sp = sl + (size_t) n * kpad(ld), * dl = sp + (size_t) n * kpad(d);
     int rc;
-    HIPX(hipMemcpyAsync(x, spk, (size_t) sd * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (delta) HIPX(hipMemcpyAsync(dl, delta, (size_t) d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_encode(ctx, x, sd, sd, 1, act_of(m->spk_lda.type), ctx->act))) return rc;
-    if ((rc = launch_gemv(ctx, m->spk_lda, nullptr, gemv_dense(ctx, 1, sl, ld, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
-    KL(k_bias_add, dim3((ld + 255) / 256), dim3(256), 0, ctx->stream, sl, (const float *) m->spk_lda_b, (const float *) nullptr, ld);
-    HIPX(hipGetLastError());
-    if ((rc = launch_encode(ctx, sl, ld, ld, 1, act_of(m->spk_proj.type), ctx->act))) return rc;
-    if ((rc = launch_gemv(ctx, m->spk_proj, nullptr, gemv_dense(ctx, 1, sp, d, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
-    KL(k_bias_add, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, sp, (const float *) m->spk_proj_b, (const float *) (delta ? dl : nullptr), d);
-    HIPX(hipGetLastError());
-    HIPX(hipMemcpyAsync(out, sp, (size_t) d * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPX(hipMemcpyAsync(x, spk, (size_t) n * sd * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (delta) HIPX(hipMemcpyAsync(dl, delta, (size_t) n * d * 4, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_encode(ctx, x, sd, sd, n, act_of(m->spk_lda.type), ctx->act))) return rc;
+    if ((rc = launch_gemv(ctx, m->spk_lda, nullptr, gemv_dense(ctx, n, sl, ld, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
+    for (int r = 0; r < n; ++r) {
+        KL(k_bias_add, dim3((ld + 255) / 256), dim3(256), 0, ctx->stream, sl + (size_t) r * ld, (const float *) m->spk_lda_b, (const float *) nullptr, ld);
+        HIPX(hipGetLastError());
+    }
+    if ((rc = launch_encode(ctx, sl, ld, ld, n, act_of(m->spk_proj.type), ctx->act))) return rc;
+    if ((rc = launch_gemv(ctx, m->spk_proj, nullptr, gemv_dense(ctx, n, sp, d, EPI_STORE), 1, Z2H_KF_GEMV_DENSE))) return rc;
+    for (int r = 0; r < n; ++r) {
+        KL(k_bias_add, dim3((d + 255) / 256), dim3(256), 0, ctx->stream, sp + (size_t) r * d, (const float *) m->spk_proj_b,
+           (const float *) (delta ? dl + (size_t) r * d : nullptr), d);
+        HIPX(hipGetLastError());
+    }
+    HIPX(hipMemcpyAsync(out, sp, (size_t) n * d * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
     return Z2H_OK;
 }
@@ -1471,7 +1478,7 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
     std::vector<float> sp;
     if (spk) {
         sp.resize(ctx->hp.n_embd);
-        if (int rc = speaker_row(ctx, spk, delta, sp.data())) return rc;
+        if (int rc = speaker_rows(ctx, 1, spk, delta, sp.data())) return rc;
     }
     // causal prefill in chunks of rows [r0, r0 + T): every row of a chunk appends its K/V (f16 into the
     // cache, fp32 into the prompt rows) before the chunk's attention, then row r attends the prompt's
@@ -1503,6 +1510,13 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
         HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }
     return check_err_flag(ctx);
+}
+
+int z2h_speaker_embed(z2h_ctx * ctx, int n, const float * spk, const float * delta, float * out) {
+    if (!ctx || !spk || !out) return ctx ? seterr(ctx, Z2H_EINVAL, "null argument") : Z2H_EINVAL;
+    if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
+    HIPX(hipSetDevice(ctx->device));
+    return speaker_rows(ctx, n, spk, delta, out);
 }
 
 int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,

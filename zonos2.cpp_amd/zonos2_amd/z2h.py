@@ -52,6 +52,7 @@ def lib() -> C.CDLL:
         "z2h_step": (i32, [vp, i32, vp, vp, vp, vp, vp]),
         "z2h_step_device": (i32, [vp, i32, vp, vp, vp, vp, vp, vp, vp]),
         "z2h_prefill": (i32, [vp, i32, vp, i32, vp, i32, vp, vp]),
+        "z2h_speaker_embed": (i32, [vp, i32, vp, vp, vp]),
         "z2h_moe_forward": (i32, [vp, i32, i32, vp, vp, vp]),
         "z2h_moe_forward_device": (i32, [vp, i32, i32, vp, vp, vp, vp]),
         "z2h_model_moe_forward_noalloc": (i32, [vp, i32, i32, vp, vp, vp, vp, vp]),
@@ -81,7 +82,7 @@ EXPORTS = ("z2h_model_create", "z2h_model_upload_tensor", "z2h_model_finalize", 
            "z2h_model_set_logit_bias", "z2h_model_set_layer_skip", "z2h_set_layer_skip", "z2h_model_last_error", "z2h_model_release", "z2h_create_batch",
            "z2h_create", "z2h_upload_tensor", "z2h_finalize", "z2h_slot_cap", "z2h_kv_write", "z2h_kv_read",
            "z2h_step", "z2h_step_device", "z2h_prefill", "z2h_moe_forward", "z2h_moe_forward_device",
-           "z2h_model_moe_forward_noalloc",
+           "z2h_model_moe_forward_noalloc", "z2h_speaker_embed",
            "z2h_set_expert_mask", "z2h_set_logit_bias", "z2h_set_capture", "z2h_capture_bytes",
            "z2h_read_capture", "z2h_device_bytes", "z2h_set_graphs", "z2h_profile_begin", "z2h_profile_end", "z2h_sample", "z2h_set_prefill_chunk",
            "z2h_sample_feed", "z2h_step_resident", "z2h_create_batch_rows", "z2h_step_mixed",
@@ -234,6 +235,14 @@ class Context:
 
     def step_resident(self, n: int):
         self.check(lib().z2h_step_resident(self.ctx, n))
+
+    def speaker_embed(self, spk, delta=None):
+        """z2h_speaker_embed: speaker rows [n][n_embd] of speaker vectors spk [n][spk_dim]."""
+        spk = np.ascontiguousarray(np.atleast_2d(spk), np.float32)
+        d = None if delta is None else np.ascontiguousarray(np.atleast_2d(delta), np.float32)
+        out = np.empty((spk.shape[0], self.hp["n_embd"]), np.float32)
+        self.check(lib().z2h_speaker_embed(self.ctx, spk.shape[0], _p(spk), _p(d), _p(out)))
+        return out
 
     def step_mixed(self, slot_idx, n_past, ids, out_rows, emb_map=None, emb=None):
         """z2h_step_mixed: rows from any slots (prefill chunks and decode columns); returns the logits
