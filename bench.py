@@ -81,6 +81,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c3", "c4-q6_k", "c4-q8_0"])
     ap.add_argument("--cpu-steps", type=int, default=5, help="timed oracle steps for the CPU baseline after 2 warm-ups (0: skip)")
+    ap.add_argument("--no-mixed-f16", dest="mixed_f16", action="store_false",
+                    help="skip the mixed pass on the F16-weight model")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the timed region, copy 256 MiB device to device once (a kernel of known traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -238,6 +240,20 @@ def main() -> int:
     log(f"device sampling: {samp_us:.1f} us per frame of {T} columns (host round trip included)")
 
     mixed = mixed_pass(np, Context, synth, cfg, mdl) if args.config == "c3" else None
+    mixed_f16 = None
+    if args.config == "c3" and args.mixed_f16:
+        # the same mixed pass on the 24-layer model with F16 weights (about 15 GB)
+        ctx.close()
+        mdl.close()
+        fcfg = configs.zonos2_24l(configs.F16)
+        t0 = time.time()
+        fmodel = synth.generate_model(fcfg, seed=43)
+        fmdl = Model(fcfg.hparams(), fmodel)
+        del fmodel
+        log(f"F16 model generated + uploaded in {time.time() - t0:.1f}s")
+        mixed_f16 = mixed_pass(np, Context, synth, fcfg, fmdl)
+        fmdl.close()
+        ctx = mdl = None
 
     line = {
         "metric": "batched-decode tok/s (Q4_K MoE step, 16 ragged reqs); % of HBM peak GB/s",
@@ -270,6 +286,7 @@ def main() -> int:
         "sampler": {"columns": T, "settings": "temperature 1.15, top-k 106, min-p 0.18, repetition 1.2 over 50",
                     "us_per_frame_step": round(samp_us, 1)},
         "mixed": mixed,
+        "mixed_f16": mixed_f16,
     }
     if args.config != "c3":
         line["metric"] = "batched-decode tok/s (MoE step); % of HBM peak GB/s"
@@ -281,8 +298,9 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         log("calibration copy: 256 MiB read + 256 MiB written")
-    ctx.close()
-    mdl.close()
+    if ctx is not None:
+        ctx.close()
+        mdl.close()
     return 0
 
 
@@ -308,6 +326,12 @@ def cpu_share():
 
 
 INT8_MFMA_PEAK_TOPS = 5000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def configs_f16():
+    from zonos2_amd.configs import F16
+    return F16
 
 
 def dtype_of(bulk):
@@ -395,12 +419,14 @@ def mixed_pass(np, Context, synth, cfg, mdl):
     ctx_rows = sum(n + 1 for n in npast)
     flops = cfg.n_layer * (R * per_row + 2 * 2 * ctx_rows * cfg.n_head * cfg.head_dim)
     tops = flops / (ms / 1000.0) / 1e12
-    log(f"mixed pass: {R} rows ({n_pre} prefill chunks + {n_dec} decode) in {ms:.1f} ms, "
-        f"{R / ms * 1000.0:.0f} rows/s, {tops:.1f} TOP/s algorithmic ({tops / INT8_MFMA_PEAK_TOPS:.2%} of int8 MFMA peak)")
+    f16 = cfg.bulk == configs_f16()
+    peak, peak_unit = (F16_MFMA_PEAK_TFLOPS, "TFLOP/s (fp16)") if f16 else (INT8_MFMA_PEAK_TOPS, "TOP/s (int8)")
+    log(f"mixed pass ({type_name(cfg.bulk)}): {R} rows ({n_pre} prefill chunks + {n_dec} decode) in {ms:.1f} ms, "
+        f"{R / ms * 1000.0:.0f} rows/s, {tops:.1f} {peak_unit} algorithmic ({tops / peak:.2%} of the MFMA peak)")
     return {"rows": R, "prefill_chunks": n_pre, "chunk_rows": chunk, "decode_rows": n_dec, "ms": round(ms, 2),
             "rows_per_s": round(R / ms * 1000.0, 1),
-            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s (int8)",
-                         "frac": round(tops / INT8_MFMA_PEAK_TOPS, 5)},
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": peak, "unit": peak_unit,
+                         "frac": round(tops / peak, 5)},
             "weights": type_name(cfg.bulk).lower(), "speaker_rows": "2048-d N(0,1) speaker vectors through spk_lda -> spk_proj on the device (z2h_speaker_embed), in the timed pass"}
 
 
