@@ -150,7 +150,8 @@ int z2h_speaker_embed(z2h_ctx * ctx, int n, const float * spk, const float * del
  * the attention. No two rows may share (slot, n_past). ids [n_rows][n_codebooks+1]; emb_map (NULL, or
  * [n_rows]: -1 = the row sums its ids, e >= 0 = the row takes emb[e], e.g. a speaker prefix row) with
  * emb [n_emb][n_embd]. out_logits [n_out][n_codebooks][audio_vocab] receives the logits of rows
- * out_rows[0 .. n_out). n_rows is limited by the context's row capacity (z2h_create_batch_rows). */
+ * out_rows[0 .. n_out) (the output head runs on those rows only). n_rows and n_out are limited by
+ * the context's row capacity (z2h_create_batch_rows). */
 int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
                    const int32_t * emb_map, const float * emb, int n_emb, int n_out, const int32_t * out_rows, float * out_logits);
 

@@ -104,3 +104,41 @@ def explain_topk_flips(om, model, cfg, T, gpu_cap, orc_cap, label=""):
             assert 0.0 <= margin <= 2 * move, f"{label} L{L}: top-k flip at margin {margin:.3e} > bound {2 * move:.3e}"
         prev_g, prev_o = rg["rh"], ro["rh"]
     return rows
+
+
+def check_layers_teacher_forced(ctx, om, okv, model, cfg, T, slot_idx, n_past, got, label=""):
+    """Per-layer parity of a captured step: every layer's attention from the device's attn_in (the
+    oracle appends its own K/V rows to okv), the router bit-exact from ffn_in, the dense FFN or the
+    experts on the device's routing from ffn_in, the residual folds bit-exact, and the head from
+    out_norm, each held to the full bar. Returns the worst per-layer cosine."""
+    d, E = cfg.n_embd, cfg.n_expert
+    rd = lambda L, n: ctx.read_capture(L, n, T)
+    si, npast = np.ascontiguousarray(slot_idx, np.int32), np.ascontiguousarray(n_past, np.int32)
+    prev, worst = None, 1.0
+    for L in range(cfg.n_layer):
+        res_in, attn_in = rd(L, "res_in").reshape(T, d), rd(L, "attn_in").reshape(T, d)
+        ffn_in, attn_out, ffn_out = rd(L, "ffn_in").reshape(T, d), rd(L, "attn_out").reshape(T, d), rd(L, "ffn_out").reshape(T, d)
+        ao = np.empty((T, cfg.n_head * cfg.head_dim), np.float32)
+        oo = np.empty((T, d), np.float32)
+        O.check(O.lib().orc_attention(om.m, okv.kv, L, T, O.ptr(si), O.ptr(npast), O.ptr(attn_in), O.ptr(ao), O.ptr(oo)))
+        worst = min(worst, assert_close(f"{label} L{L} attn_out", attn_out, oo)[0])
+        k = cfg.expert_used[L]
+        if k:
+            r = O.router(om, L, ffn_in, prev)
+            sel = rd(L, "sel").ravel()[:T * k].reshape(T, k)
+            assert np.array_equal(sel, r["sel"]), f"{label} L{L} top-k ids"
+            assert np.array_equal(rd(L, "probs").reshape(T, E).view(np.uint32), r["probs"].view(np.uint32)), f"{label} L{L} probs"
+            w = rd(L, "weights").ravel()[:T * k].reshape(T, k)
+            _, out = O.experts(om, L, ffn_in, sel, w)
+            prev = r["rh"]
+        else:
+            out = np.empty((T, d), np.float32)
+            O.check(O.lib().orc_dense_ffn(om.m, L, T, O.ptr(np.ascontiguousarray(ffn_in)), O.ptr(out)))
+        worst = min(worst, assert_close(f"{label} L{L} ffn_out", ffn_out, out)[0])
+        if L + 1 < cfg.n_layer:
+            assert np.array_equal(rd(L + 1, "res_in").reshape(T, d), ffn_out + (attn_out + res_in)), f"{label} L{L} residual fold"
+    hn = ctx.read_capture(0, "out_norm", T).reshape(T, d)
+    hw = model["output.weight"]
+    mout = O.matmul(hw.type, hw.data, hw.ne[0], hw.ne[1], hn).astype(np.float64)
+    assert_close(f"{label} head + softcap", got, cfg.logit_softcap * np.tanh(mout / cfg.logit_softcap))
+    return worst

@@ -9,6 +9,7 @@
 // and after the last layer k_resnorm(output_norm) -> k_gemv(head, softcap).
 #include "z2h.h"
 #include "z2h_kernels.h"
+#include "z2h_gemm.h"
 #include <hip/hip_ext.h>
 #include "z2_formats.h"
 
@@ -105,6 +106,7 @@ struct z2h_ctx {
     int pch = 0;                      // prefill chunk rows (<= Tmax)
     int max_rows = 0;                 // requested row capacity (z2h_create_batch_rows)
     int32_t * d_emb_map = nullptr;    // [Tmax] per-row embedding override
+    int32_t * d_head_rows = nullptr;  // [Tmax] rows of a mixed pass that get logits
     int32_t * d_slot = nullptr, * d_npast = nullptr, * d_ids = nullptr; float * d_emb = nullptr;
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * res2 = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
@@ -426,6 +428,9 @@ int alloc_scratch(z2h_ctx * ctx) {
     int rc = 0;
     const int KM = ctx->Kmax;
     const int W = ctx->W;
+    // act_y rows per token: the token's routes' FFN activations, or (the head's gathered rows) one
+    // activation row of any matmul
+    const size_t ypr = std::max((size_t) std::max(K, 1) * kpad(std::max(ff, 1)), (size_t) KM);
     if ((rc = dalloc(ctx, &ctx->d_slot, T * 4, b)) || (rc = dalloc(ctx, &ctx->d_npast, T * 4, b)) ||
         (rc = dalloc(ctx, &ctx->d_ids, (size_t) T * W * 4, b)) || (rc = dalloc(ctx, &ctx->d_emb, (size_t) T * d * 4, b)) ||
         (rc = dalloc(ctx, &ctx->res, (size_t) T * d * 4, b)) || (rc = dalloc(ctx, &ctx->res2, (size_t) T * d * 4, b)) ||
@@ -439,11 +444,12 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->act.q, (size_t) T * KM, b)) || (rc = dalloc(ctx, &ctx->act.d32, (size_t) T * (KM / 32) * 4, b)) ||
         (rc = dalloc(ctx, &ctx->act.d256, (size_t) T * (KM / 256) * 4, b)) || (rc = dalloc(ctx, &ctx->act.bs, (size_t) T * (KM / 16) * 2, b)) ||
         (rc = dalloc(ctx, &ctx->act.h, (size_t) T * KM * 2, b)) ||
-        (rc = dalloc(ctx, &ctx->act_y.q, (size_t) T * K * kpad(std::max(ff, 1)), b)) ||
-        (rc = dalloc(ctx, &ctx->act_y.d32, (size_t) T * K * (kpad(std::max(ff, 1)) / 32) * 4, b)) ||
-        (rc = dalloc(ctx, &ctx->act_y.d256, (size_t) T * K * (kpad(std::max(ff, 1)) / 256) * 4, b)) ||
-        (rc = dalloc(ctx, &ctx->act_y.bs, (size_t) T * K * (kpad(std::max(ff, 1)) / 16) * 2, b)) ||
-        (rc = dalloc(ctx, &ctx->act_y.h, (size_t) T * K * kpad(std::max(ff, 1)) * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.q, (size_t) T * ypr, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.d32, (size_t) T * (ypr / 32) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.d256, (size_t) T * (ypr / 256) * 4, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.bs, (size_t) T * (ypr / 16) * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->act_y.h, (size_t) T * ypr * 2, b)) ||
+        (rc = dalloc(ctx, &ctx->d_head_rows, (size_t) T * 4, b)) ||
         (rc = dalloc(ctx, &ctx->attn_o, (size_t) T * nh * hd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->state, (size_t) hp.n_layer * T * rd * 4, b)) || (rc = dalloc(ctx, &ctx->state_ext, (size_t) T * rd * 4, b)) ||
         (rc = dalloc(ctx, &ctx->sel, (size_t) T * K * 4, b)) || (rc = dalloc(ctx, &ctx->wsel, (size_t) T * K * 4, b)) ||
@@ -461,7 +467,7 @@ int alloc_scratch(z2h_ctx * ctx) {
     if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) ctx->items_max * sizeof(int4), b))) return rc;
     if (hipHostMalloc((void **) &ctx->h_tiles, (size_t) ctx->items_max * sizeof(int4), hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
-    ctx->h_pin_bytes = (size_t) T * (3 + W) * 4;
+    ctx->h_pin_bytes = (size_t) T * (4 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     const int ncb = std::max(1, (int) hp.n_codebooks);
@@ -508,7 +514,64 @@ int cap_copy(z2h_ctx * ctx, int what, int L, const void * src, int T) {
 }
 
 // ---------------------------------------------------------------- launch helpers
+// Passes of more than 64 token rows (prefill chunks, mixed passes) run their Q4_K (m16) matmuls as
+// GEMMs (k_gemm_q4k), decode steps the GEMVs: both fold a row's superblocks in the same order with
+// the same operations. Every F16 (t64) matmul runs on k_gemm_f16, in its wide or narrow shape (same
+// bits per row either way).
+constexpr int GEMM_MIN_ROWS = 65;
+bool use_gemm(const DevMat & m, int n_tok) {
+    if (!m.m16 && m.type == Z2H_F16) return true;
+    return n_tok >= GEMM_MIN_ROWS && m.m16 && m.type == Z2H_Q4_K;
+}
+// gate and up fused with SwiGLU in one GEMM launch: same type, layout and shape
+bool gemm_dual_ok(const DevMat & g, const DevMat & u) {
+    return g.type == u.type && g.m16 == u.m16 && g.nsb == u.nsb && g.tiles == u.tiles && g.rows == u.rows && g.mat_bytes == u.mat_bytes;
+}
+
+int launch_gemm(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & g, int fam) {
+    const bool dual = g.mode == MM_SWIGLU;
+    if (dual && (!m1 || !gemm_dual_ok(m0, *m1))) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
+    if (!dual && m1) {
+        // two matrices, two outputs: one launch each
+        GemvArgs g0 = g, g1 = g;
+        g1.out[0] = g.out[1];
+        if (int rc = launch_gemm(ctx, m0, nullptr, g0, fam)) return rc;
+        return launch_gemm(ctx, *m1, nullptr, g1, fam);
+    }
+    if (g.grouped && (!g.r_off || !g.r_perm)) return seterr(ctx, Z2H_EINVAL, "grouped GEMM without the route grouping");
+    prof_scope ps(ctx, fam);
+    GemmArgs a{};
+    a.w[0] = m0.w; a.w[1] = dual ? m1->w : m0.w; a.mat_bytes = m0.mat_bytes;
+    a.nsb = m0.nsb; a.rows = m0.rows; a.tiles = m0.tiles;
+    a.grouped = g.grouped; a.n_tok = g.n_tok; a.k = g.k; a.E = g.E; a.act_by_route = g.act_by_route;
+    a.r_off = g.r_off; a.r_perm = g.r_perm; a.act = g.act;
+    a.out = g.out[0]; a.out_ld = g.out_ld; a.epi = g.epi; a.cap = g.cap; a.route_w = g.route_w;
+    if (m0.type == Z2H_Q4_K) {
+        const dim3 grid(dual ? (m0.tiles + 3) / 4 : (m0.tiles + 7) / 8, gemm_slots(a.grouped, a.n_tok, a.k, a.E, GM_T));
+        if (dual) KL(k_gemm_q4k<true>, grid, dim3(256), gemm_q4k_lds(), ctx->stream, a);
+        else KL(k_gemm_q4k<false>, grid, dim3(256), gemm_q4k_lds(), ctx->stream, a);
+    } else {
+        // wide tiles (64 token rows) for wide dense passes and experts averaging 32+ routes, else
+        // narrow ones (16 token rows, 16 output rows per wave)
+        const bool wide = a.grouped ? a.n_tok * a.k >= 32 * a.E : a.n_tok >= GEMM_MIN_ROWS;
+        const int rpb = wide ? (dual ? 128 : 256) : 64;
+        const dim3 grid((m0.rows + rpb - 1) / rpb, gemm_slots(a.grouped, a.n_tok, a.k, a.E, wide ? 64 : 16));
+        const size_t lds = gemm_f16_lds(wide ? 4 : 1);
+        if (wide) {
+            if (dual) KL((k_gemm_f16<true, 4, 4>), grid, dim3(256), lds, ctx->stream, a);
+            else KL((k_gemm_f16<false, 4, 4>), grid, dim3(256), lds, ctx->stream, a);
+        } else {
+            if (dual) KL((k_gemm_f16<true, 2, 1>), grid, dim3(256), lds, ctx->stream, a);
+            else KL((k_gemm_f16<false, 1, 1>), grid, dim3(256), lds, ctx->stream, a);
+        }
+    }
+    HIPX(hipGetLastError());
+    return Z2H_OK;
+}
+
 int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & base, int grid_y, int fam) {
+    if (use_gemm(m0, base.n_tok) && (!m1 || gemm_dual_ok(m0, *m1)) && (!base.grouped || (base.r_off && base.r_perm)))
+        return launch_gemm(ctx, m0, m1, base, fam);
     prof_scope ps(ctx, fam);
     GemvArgs a = base;
     a.w[0] = m0.w; a.w[1] = m1 ? m1->w : m0.w;
@@ -586,9 +649,11 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     return Z2H_OK;
 }
 
-// SwiGLU fused into the gate/up matmul (both in the 16-row MFMA layout, same shape)
-bool fused_ffn(const DevMat & g, const DevMat & u) {
-    return g.m16 && u.m16 && g.type == u.type && g.nsb == u.nsb && g.tiles == u.tiles;
+// SwiGLU fused into the gate/up matmul: both in the 16-row MFMA layout with the same shape, or a
+// pass of T rows that takes the GEMMs
+bool fused_ffn(const DevMat & g, const DevMat & u, int T) {
+    return (g.m16 && u.m16 && g.type == u.type && g.nsb == u.nsb && g.tiles == u.tiles) ||
+           (use_gemm(g, T) && gemm_dual_ok(g, u));
 }
 
 int launch_encode(z2h_ctx * ctx, const float * x, int ld, int K, int n_rows, int act_fmt, const ActBuf & act) {
@@ -711,7 +776,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     }
     // routes grouped by expert (mul_mat_id's grouping): the grouped matmul blocks list up to LIST_MAX
     // routes in LDS themselves; larger batches, and captures, take one sort kernel's table
-    const bool sorted = ctx->capture || T * ly.k > LIST_MAX;
+    const bool sorted = ctx->capture || T * ly.k > LIST_MAX || use_gemm(ly.gate_exps, T) || use_gemm(ly.down_exps, T);
     if (sorted) {
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
         int32_t * cc = ctx->capture ? (int32_t *) capp(ctx, Z2H_CAP_COUNTS, L) : nullptr;
@@ -723,7 +788,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     if ((rc = cap_copy(ctx, Z2H_CAP_ROUTER_STATE, L, r.rh, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_SEL, L, ctx->sel, T))) return rc;
     if ((rc = cap_copy(ctx, Z2H_CAP_WEIGHTS, L, ctx->wsel, T))) return rc;
-    if (fused_ffn(ly.gate_exps, ly.up_exps)) {
+    if (fused_ffn(ly.gate_exps, ly.up_exps, T)) {
         // gate + up + SwiGLU in one grouped launch -> y [route][ff] fp32, encoded once for down
         GemvArgs g{};
         g.grouped = 1; g.n_tok = T; g.sel = ctx->sel; g.k = ly.k; g.act = ctx->act; g.E = ly.E; g.mode = MM_SWIGLU;
@@ -762,7 +827,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
 int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
     const auto & hp = ctx->hp;
     int rc;
-    if (fused_ffn(ly.ffn_gate, ly.ffn_up)) {
+    if (fused_ffn(ly.ffn_gate, ly.ffn_up, T)) {
         GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
         g.mode = MM_SWIGLU;
         if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, 1, Z2H_KF_GEMV_DENSE))) return rc;
@@ -785,9 +850,13 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
 // rows of one slot attend to each other); d_emb_map: per token -1 (sum of its ids) or its row of d_emb.
 // f32_prompt (per-slot prefill): the rows also keep their fp32 K/V in ctx->pf_kv and attend over those
 // (the reference's in-prompt attention, src/zonos2-graph.cpp:155-169) instead of the f16 cache rows.
+// head_rows: which rows get logits (rows [0, n_head) of d_logits): every row, none, the last row, or
+// the n_head rows listed in d_head_rows.
+enum { HEAD_ALL = 0, HEAD_NONE = 1, HEAD_LAST = 2, HEAD_ROWS = 3 };
 int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_slot, const int32_t * d_npast,
              const int32_t * d_ids, const float * d_emb, float * d_logits, bool kv_pre = false,
-             const int32_t * d_emb_map = nullptr, const int32_t * h_slot = nullptr, bool f32_prompt = false) {
+             const int32_t * d_emb_map = nullptr, const int32_t * h_slot = nullptr, bool f32_prompt = false,
+             int head_rows = HEAD_ALL, const int32_t * d_head_rows = nullptr, int n_head = 0) {
     const auto & hp = ctx->hp;
     const int d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     int rc;
@@ -920,18 +989,55 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         if ((rc = launch_resnorm(ctx, T, n))) return rc;
         if (!last && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, nx, ctx->res, T))) return rc;
     }
-    // output head + softcap
+    // output head + softcap on the rows that want logits
+    if (head_rows == HEAD_NONE) return Z2H_OK;
     const int nout = hp.n_codebooks * hp.audio_vocab;
-    return launch_gemv(ctx, ctx->m->head, nullptr, gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE),
-                       1, Z2H_KF_GEMV_HEAD);
+    GemvArgs h = gemv_dense(ctx, T, d_logits, nout, hp.logit_softcap > 0.0f ? EPI_SOFTCAP : EPI_STORE);
+    const int haf = act_of(ctx->m->head.type), Kp = kpad(d);
+    if (head_rows == HEAD_LAST) {
+        // the encoded row T - 1 as a one-row buffer
+        const int64_t r = T - 1;
+        h.n_tok = 1;
+        h.act.q = ctx->act.q + r * Kp; h.act.d32 = ctx->act.d32 + r * (Kp / 32); h.act.d256 = ctx->act.d256 + r * (Kp / 256);
+        h.act.bs = ctx->act.bs + r * (Kp / 16); h.act.h = ctx->act.h + r * Kp;
+    } else if (head_rows == HEAD_ROWS) {
+        if (n_head <= 0) return Z2H_OK;
+        prof_scope ps(ctx, Z2H_KF_GEMV_HEAD);
+        KL(k_gather_act, dim3(n_head), dim3(256), 0, ctx->stream, ctx->act, ctx->act_y, Kp, haf, d_head_rows);
+        HIPX(hipGetLastError());
+        h.n_tok = n_head;
+        h.act = ctx->act_y;
+    }
+    return launch_gemv(ctx, ctx->m->head, nullptr, h, 1, Z2H_KF_GEMV_HEAD);
 }
 
 // Raise a kernel's dynamic-LDS limit to what gfx950's 160 KiB leaves beside its static LDS.
-int allow_lds(const void * fn, z2h_ctx * ctx) {
+int allow_lds(const void * fn, std::string & err) {
     hipFuncAttributes fa{};
-    HIPX(hipFuncGetAttributes(&fa, fn));
-    const int dyn = 160 * 1024 - (int) fa.sharedSizeBytes;
-    HIPX(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e == hipSuccess) e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - (int) fa.sharedSizeBytes);
+    if (e != hipSuccess) { err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e); return Z2H_EDEVICE; }
+    return Z2H_OK;
+}
+
+// every kernel with a dynamic LDS carve-up may use the rest of the 160 KiB beside its static LDS
+int set_lds_limits(std::string & err) {
+#define LDS_ATTR(K_) if (int rc_ = allow_lds((const void *) &(K_), err)) return rc_;
+    LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
+    LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
+    LDS_ATTR((k_gemv_split<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT>))
+    LDS_ATTR((k_gemv_split<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT, 1>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
+    LDS_ATTR(k_gemm_q4k<true>) LDS_ATTR(k_gemm_q4k<false>)
+    LDS_ATTR((k_gemm_f16<true, 4, 4>)) LDS_ATTR((k_gemm_f16<false, 4, 4>)) LDS_ATTR((k_gemm_f16<true, 2, 1>)) LDS_ATTR((k_gemm_f16<false, 1, 1>))
+#define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>))
+    LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
+#undef LDS_TF
+    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
+#undef LDS_ATTR
     return Z2H_OK;
 }
 
@@ -1208,6 +1314,11 @@ int z2h_model_finalize(z2h_model * mdl) {
         } else if (!ly.ffn_up.ok() || !ly.ffn_gate.ok() || !ly.ffn_down.ok()) missing += b + "ffn_{up,gate,down} ";
     }
     if (!missing.empty()) return seterr(mdl, Z2H_EINVAL, "missing tensors: " + missing);
+    {
+        std::string err;
+        if (hipSetDevice(mdl->device) != hipSuccess) return seterr(mdl, Z2H_EDEVICE, "hipSetDevice failed");
+        if (int rc = set_lds_limits(err)) return seterr(mdl, rc, err);
+    }
     if (mdl->rd > 0) {
         if (mdl->rd != 32 && mdl->rd != 64 && mdl->rd != 128) return seterr(mdl, Z2H_ENOTSUP, "router_dim must be 32, 64 or 128");
         if (mdl->kmax > 8) return seterr(mdl, Z2H_ENOTSUP, "top-k above 8");
@@ -1284,22 +1395,10 @@ int z2h_finalize(z2h_ctx * ctx) {
     if (hp.n_expert > SORT_EMAX) return seterr(ctx, Z2H_ENOTSUP, "more experts than the route sort handles (256)");
     if (int rc = alloc_scratch(ctx)) return rc;
     HIPX(hipMemset(ctx->d_err, 0, 16));
-    // allow each kernel the rest of gfx950's 160 KiB of LDS (beyond its static LDS) for its dynamic
-    // carve-up
-#define LDS_ATTR(K_) if (int rc_ = allow_lds((const void *) &(K_), ctx)) return rc_;
-    LDS_ATTR(k_gemv<WF_Q4_K>) LDS_ATTR(k_gemv<WF_Q6_K>) LDS_ATTR(k_gemv<WF_Q8_0>) LDS_ATTR(k_gemv<WF_F16>)
-    LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
-    LDS_ATTR((k_gemv_split<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT>))
-    LDS_ATTR((k_gemv_split<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT, 1>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
-    LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
-#define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>))
-    LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
-#undef LDS_TF
-    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
-#undef LDS_ATTR
+    {
+        std::string err;
+        if (int rc = set_lds_limits(err)) return seterr(ctx, rc, err);
+    }
     {
         int n_cu = 0, per_cu = 0;
         HIPX(hipSetDevice(ctx->device));
@@ -1505,8 +1604,9 @@ int z2h_prefill(z2h_ctx * ctx, int slot, const int32_t * ids, int n0, const floa
             HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) T * 4, hipMemcpyHostToDevice, ctx->stream));
         }
         if (int rc = run_step(ctx, T, hp_ + T, ctx->d_slot, ctx->d_npast, ctx->d_ids, er >= 0 ? ctx->d_emb : nullptr,
-                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr, hp_, /*f32_prompt=*/true)) return rc;
-        if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits + (size_t) (T - 1) * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
+                              ctx->logits, /*kv_pre=*/true, er >= 0 ? ctx->d_emb_map : nullptr, hp_, /*f32_prompt=*/true,
+                              last ? HEAD_LAST : HEAD_NONE)) return rc;
+        if (last) HIPX(hipMemcpyAsync(last_logits, ctx->logits, row * 4, hipMemcpyDeviceToHost, ctx->stream));
         HIPX(hipStreamSynchronize(ctx->stream));               // the pinned inputs are reused by the next chunk
     }
     return check_err_flag(ctx);
@@ -1540,6 +1640,7 @@ int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const in
                 if (id < 0 || id >= ctx->m->tab_rows[k]) return seterr(ctx, Z2H_EINVAL, "token id out of range");
             }
     }
+    if (n_out < 0 || n_out > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "n_out out of range");
     for (int i = 0; i < n_out; ++i)
         if (out_rows[i] < 0 || out_rows[i] >= n_rows) return seterr(ctx, Z2H_EINVAL, "out_rows entry out of range");
     if (emb_map && (size_t) n_emb * ctx->hp.n_embd > (size_t) ctx->Tmax * ctx->hp.n_embd) return seterr(ctx, Z2H_EINVAL, "too many embedding rows");
@@ -1562,12 +1663,17 @@ int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const in
         HIPX(hipMemcpyAsync(ctx->d_emb_map, map, (size_t) n_rows * 4, hipMemcpyHostToDevice, ctx->stream));
         HIPX(hipMemcpyAsync(ctx->d_emb, emb, (size_t) n_emb * ctx->hp.n_embd * 4, hipMemcpyHostToDevice, ctx->stream));
     }
-    // every row appends its K/V before the attention; a slot's rows attend causally to each other
+    // the requested rows' indices (pinned, after the ids and the embedding map)
+    int32_t * hrows = map + n_rows;
+    std::memcpy(hrows, out_rows, (size_t) n_out * 4);
+    if (n_out > 0) HIPX(hipMemcpyAsync(ctx->d_head_rows, hrows, (size_t) n_out * 4, hipMemcpyHostToDevice, ctx->stream));
+    // every row appends its K/V before the attention; a slot's rows attend causally to each other; the
+    // head runs on the requested rows only
     if (int rc = run_step(ctx, n_rows, hp_ + n_rows, ctx->d_slot, ctx->d_npast, ctx->d_ids, emb_map ? ctx->d_emb : nullptr,
-                          ctx->logits, /*kv_pre=*/true, emb_map ? ctx->d_emb_map : nullptr, hp_)) return rc;
+                          ctx->logits, /*kv_pre=*/true, emb_map ? ctx->d_emb_map : nullptr, hp_, false,
+                          HEAD_ROWS, ctx->d_head_rows, n_out)) return rc;
     const size_t row = (size_t) ctx->hp.n_codebooks * ctx->hp.audio_vocab;
-    for (int i = 0; i < n_out; ++i)
-        HIPX(hipMemcpyAsync(out_logits + (size_t) i * row, ctx->logits + (size_t) out_rows[i] * row, row * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (n_out > 0) HIPX(hipMemcpyAsync(out_logits, ctx->logits, (size_t) n_out * row * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPX(hipStreamSynchronize(ctx->stream));
     return check_err_flag(ctx);
 }

@@ -916,10 +916,20 @@ __device__ __forceinline__ void m16_load(const uint4 * __restrict__ unit, int la
 
 // One 256-column unit of a wave's 16 rows against the staged token rows. Token rows beyond the last
 // valid one (ntm1) read that row instead (their results are discarded), so LDS holds only the valid
-// rows.
+// rows. The unit's value x per (token, row) is folded into the row's sum by m16_fold: Q4_K x =
+// fma(d, isum, -dmin * msum) and sum = fma(dx, x, sum) with the token's block scale dx (xd); Q8_0
+// x = the unit's 8 scaled block products (xd = 1) and sum = sum + x. Every Q4_K matmul (the GEMVs
+// here and k_gemm_q4k) folds the units of a row in superblock order with these operations, so a
+// token's result does not depend on the batch it is in.
+template <int WF>
+__device__ __forceinline__ void m16_fold(float & acc, float x, float xd) {
+    if constexpr (WF == WF_Q4_K) acc = __builtin_fmaf(xd, x, acc);
+    else acc = acc + x;
+}
 template <int WF>
 __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], const uint4 & hd, int sb, int K, int lane,
-                                         const int8_t * sq, const int * sbs2, const float * sdx, int nsb, int ntm1, float (&acc)[4]) {
+                                         const int8_t * sq, const int * sbs2, const float * sdx, int nsb, int ntm1, float (&acc)[4],
+                                         float (&xd)[4]) {
     // every operand load and all MFMAs of the unit are issued before the scale arithmetic, so the 8
     // independent products pipeline instead of each waiting for its predecessor's scaling
     const int q = lane >> 4, r = min(lane & 15, ntm1), KP = K + 16;
@@ -963,7 +973,10 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
             for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scj, C[j][i]);   // |products| < 2^22
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += (d * dx[i]) * (float) sumi[i] - (dmin * dx[i]) * S[i];
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = __builtin_fmaf(d, (float) sumi[i], -(dmin * S[i]));
+            xd[i] = dx[i];
+        }
     } else {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -973,6 +986,8 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
         }
         uint16_t dh[8];
         __builtin_memcpy(dh, &hd, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xd[i] = 1.0f;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const float dw = h2f(dh[b]);
@@ -1101,11 +1116,11 @@ k_gemv_mfma(GemvArgs a) {
             for (int j = 0; j < PF; ++j) {
                 const int u = c + j;
                 if (u < u1) {
-                    float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
+                    float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
+                    m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
                     if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + t4[i];
+                    for (int i = 0; i < 4; ++i) m16_fold<WF>(acc[i], t4[i], xd[i]);
                 }
             }
         }
@@ -1130,7 +1145,8 @@ k_gemv_mfma(GemvArgs a) {
 
 // m16 GEMV with the K units split over the block's 4 waves: one 16-row group per block (grid x), wave
 // w takes units w, w+4, ... (all requested up front, so a wave has all its weight bytes in flight at
-// once), partial sums are added in LDS in wave order. Dense: grid (groups, token chunks of ROWS, mats);
+// once); every unit's values go to LDS and wave 0 folds them in superblock order (m16_fold), the
+// order of every other Q4_K matmul. Dense: grid (groups, token chunks of ROWS, mats);
 // grouped (expert matmuls): grid (groups, experts, passes of ROWS routes), the expert's routes listed
 // first so blocks of untouched experts read no weights. Each 16-row group gives 4x more, shorter
 // waves than a wave streaming the whole K, which keeps enough bytes in flight to cover HBM latency.
@@ -1143,7 +1159,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     __shared__ int s_lds[LIST_MAX];
     __shared__ int s_wcnt[4];
     __shared__ int s_tok[ROWS];
-    __shared__ float s_part[4][8][64];
+    __shared__ float s_x[4 * SPLIT_UMAX][4][64];                    // [unit][token of the lane][lane]
     const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g16 = blockIdx.x;
     int8_t * sq = (int8_t *) smem;
@@ -1183,23 +1199,16 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     lds_sync();
     m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
     lds_sync();
-    float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < SPLIT_UMAX; ++j) {
         const int u = wave + 4 * j;
         if (u < U) {
-            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4);
-            const bool first = !DUAL || u < nsb;
+            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
+            m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc0[i] = first ? acc0[i] + t4[i] : acc0[i];
-                acc1[i] = first ? acc1[i] : acc1[i] + t4[i];
-            }
+            for (int i = 0; i < 4; ++i) s_x[u][i][lane] = t4[i];
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { s_part[wave][i][lane] = acc0[i]; s_part[wave][4 + i][lane] = acc1[i]; }
     lds_sync();
     if (wave != 0) return;
     const int q = lane >> 4, row = g16 * 16 + (lane & 15);
@@ -1209,14 +1218,36 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         const int t = 4 * q + i;
         if (t >= nt) continue;
         const int it = a.grouped ? s_list[c0 + t] : c0 + t;
-        const float g = ((s_part[0][i][lane] + s_part[1][i][lane]) + s_part[2][i][lane]) + s_part[3][i][lane];
+        // the units in superblock order (the block scale of the token's superblock sb: Q8_K only)
+        float g = 0.0f, up = 0.0f;
+        for (int sb = 0; sb < nsb; ++sb) {
+            const float xd = AF == ACT_Q8_K ? sdx[t * nsb + sb] : 1.0f;
+            m16_fold<WF>(g, s_x[sb][i][lane], xd);
+            if (DUAL) m16_fold<WF>(up, s_x[nsb + sb][i][lane], xd);
+        }
         float y = g;
-        if (DUAL) {
-            const float u = ((s_part[0][4 + i][lane] + s_part[1][4 + i][lane]) + s_part[2][4 + i][lane]) + s_part[3][4 + i][lane];
-            y = u * z_silu(g);
-        } else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+        if (DUAL) y = up * z_silu(g);
+        else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
         else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
         a.out[m][(int64_t) it * a.out_ld + row] = y;
+    }
+}
+
+// Row rows[i] of an encoded activation buffer (row stride Kp) copied to row i of dst: the rows of a
+// pass that get logits, gathered for the output head. One block per row.
+__global__ void __launch_bounds__(256) k_gather_act(ActBuf src, ActBuf dst, int Kp, int af, const int32_t * rows) {
+    const int i = blockIdx.x, tid = threadIdx.x;
+    const int64_t r = rows[i];
+    if (af == ACT_F16) {
+        for (int j = tid; j < Kp / 8; j += 256) ((uint4 *) (dst.h + (int64_t) i * Kp))[j] = ((const uint4 *) (src.h + r * Kp))[j];
+        return;
+    }
+    for (int j = tid; j < Kp / 16; j += 256) ((uint4 *) (dst.q + (int64_t) i * Kp))[j] = ((const uint4 *) (src.q + r * Kp))[j];
+    if (af == ACT_Q8_0) {
+        for (int j = tid; j < Kp / 32; j += 256) dst.d32[(int64_t) i * (Kp / 32) + j] = src.d32[r * (Kp / 32) + j];
+    } else {
+        for (int j = tid; j < Kp / 256; j += 256) dst.d256[(int64_t) i * (Kp / 256) + j] = src.d256[r * (Kp / 256) + j];
+        for (int j = tid; j < Kp / 16; j += 256) dst.bs[(int64_t) i * (Kp / 16) + j] = src.bs[r * (Kp / 16) + j];
     }
 }
 
