@@ -724,10 +724,30 @@ int launch_ffn_entry(z2h_ctx * ctx, const Layer & ly, int L, int T, const float 
     ResNormArgs f{};
     f.mode = RN_ADD; f.d = hp.n_embd; f.src = src; f.res_in = res_in; f.res = res_out; f.norm_w = ly.ffn_norm;
     f.eps = hp.rms_eps; f.cur_out = ctx->cur; f.act = ctx->act; f.act_fmt = act_of(ly.up_exps.type); f.err = ctx->d_err;
-    const dim3 grid((ctx->rd + 3) / 4, T);
-    const size_t lds = (size_t) kpad(hp.n_embd) * 4;
     const int ni = router_ni(hp.n_embd);
     const bool exact = hp.n_embd == 64 * ni;
+    if (T >= GEMM_MIN_ROWS && ni % 4 == 0 && ctx->rd % 32 == 0) {
+        // wide passes: the norm once per token (k_resnorm, the same arithmetic), then the router down
+        // projection with each weight row reused across RD_T tokens
+        f.res = res_out; f.res_in = res_in;
+        if (int rc = launch_resnorm(ctx, T, f)) return rc;
+        const dim3 g2(ctx->rd / 32, (T + RD_T - 1) / RD_T);
+        const size_t l2 = router_down_t_lds(ni);
+#define RDT(N_) do { if (exact) KL((k_router_down_t<N_, false>), g2, dim3(256), l2, ctx->stream, r); \
+                     else KL((k_router_down_t<N_, true>), g2, dim3(256), l2, ctx->stream, r); } while (0)
+        switch (ni) {
+            case 4: RDT(4); break;
+            case 8: RDT(8); break;
+            case 16: RDT(16); break;
+            case 32: RDT(32); break;
+            default: RDT(64); break;
+        }
+#undef RDT
+        HIPX(hipGetLastError());
+        return Z2H_OK;
+    }
+    const dim3 grid((ctx->rd + 3) / 4, T);
+    const size_t lds = (size_t) kpad(hp.n_embd) * 4;
 #define FEN(N_) do { if (exact) KL((k_ffn_entry<N_, false>), grid, dim3(256), lds, ctx->stream, f, r); \
                      else KL((k_ffn_entry<N_, true>), grid, dim3(256), lds, ctx->stream, f, r); } while (0)
     switch (ni) {
@@ -1031,6 +1051,10 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
+    LDS_ATTR((k_router_down_t<4, false>)) LDS_ATTR((k_router_down_t<8, false>)) LDS_ATTR((k_router_down_t<16, false>))
+    LDS_ATTR((k_router_down_t<32, false>)) LDS_ATTR((k_router_down_t<64, false>))
+    LDS_ATTR((k_router_down_t<4, true>)) LDS_ATTR((k_router_down_t<8, true>)) LDS_ATTR((k_router_down_t<16, true>))
+    LDS_ATTR((k_router_down_t<32, true>)) LDS_ATTR((k_router_down_t<64, true>))
     LDS_ATTR(k_gemm_q4k<true>) LDS_ATTR(k_gemm_q4k<false>)
     LDS_ATTR((k_gemm_f16<true, 4, 4>)) LDS_ATTR((k_gemm_f16<false, 4, 4>)) LDS_ATTR((k_gemm_f16<true, 2, 1>)) LDS_ATTR((k_gemm_f16<false, 1, 1>))
 #define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>))

@@ -250,7 +250,7 @@ struct ResNormArgs {
     const uint8_t * tab[MAX_TABLES]; int tab_type[MAX_TABLES]; int64_t tab_rows[MAX_TABLES];
     const float * src; int k;         // ACCUM: [T*k][d] routes; ADD / ENCODE: [T][d]
     float * res;                       // [T][d] (ACCUM may pass null: no residual)
-    const float * res_in;              // ACCUM: residual read from here instead of res (null: res)
+    const float * res_in;              // ACCUM / ADD: residual read from here instead of res (null: res)
     const float * norm_w; float eps;
     float * cur_out;                   // [T][d] fp32 normalised row (nullable)
     ActBuf act; int act_fmt;
@@ -372,12 +372,14 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
         st_cap = a.cap_x != nullptr;
         st_res = res != nullptr;
     } else if constexpr (MODE == RN_ADD) {
+        // res = res_in (or res itself) + src
         const float * __restrict__ src = a.src + (int64_t) t * d;
+        const float * rin = a.res_in ? a.res_in + (int64_t) t * d : res;
         float4 x[RN_NV], r0[RN_NV];
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
             const int i0 = 4 * (tid + 256 * j);
-            if (i0 < d) { x[j] = *(const float4 *) (src + i0); r0[j] = *(const float4 *) (res + i0); }
+            if (i0 < d) { x[j] = *(const float4 *) (src + i0); r0[j] = *(const float4 *) (rin + i0); }
         }
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
@@ -1945,6 +1947,61 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
     float v = wave_tree_f(acc) + b;
     if (a.eda && a.state_in) v = v + st;
     if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+}
+
+// k_router_down for wide passes: the same per-(token, output) fma chain, wave tree, bias and state
+// term, with each output's weight row held in registers across RD_T tokens whose normalised rows sit
+// in LDS lane-major ([token][lane][j] = x[lane + 64 j], rows padded to NI + 4 floats so the lanes'
+// 16-byte reads fall in distinct banks). Grid (rd / 32, ceil(T / RD_T)), 256 threads: wave w of block
+// (og, tb) forms outputs 32 og + 8 w + u (u < 8) for tokens [RD_T tb, RD_T tb + RD_T). NI % 4 == 0.
+constexpr int RD_T = 8;
+__host__ __device__ inline size_t router_down_t_lds(int ni) { return (size_t) RD_T * 64 * (ni + 4) * 4; }
+template <int NI, bool GUARD>
+__global__ void __launch_bounds__(256) k_router_down_t(RouterArgs a) {
+    static_assert(NI % 4 == 0, "16-byte LDS reads");
+    constexpr int S = NI + 4;
+    extern __shared__ __attribute__((aligned(16))) float xs_t[];     // [RD_T][64][S]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t0 = blockIdx.y * RD_T;
+    const int nt = min(RD_T, a.T - t0);
+    // the rows (tokens past T repeat the last one), element i -> [lane i % 64][j = i / 64]
+    for (int idx = tid; idx < RD_T * (a.d / 4); idx += 256) {
+        const int tt = idx / (a.d / 4), i0 = 4 * (idx % (a.d / 4));
+        const float4 v = *(const float4 *) (a.x + (int64_t) (t0 + min(tt, nt - 1)) * a.d + i0);
+        float * dst = xs_t + ((size_t) tt * 64) * S + (i0 >> 6);
+        const int l0 = i0 & 63;
+        dst[(l0 + 0) * S] = v.x; dst[(l0 + 1) * S] = v.y; dst[(l0 + 2) * S] = v.z; dst[(l0 + 3) * S] = v.w;
+    }
+    lds_sync();                        // (slots past d are never read: GUARD skips them)
+    const bool eda = a.eda && a.state_in;
+    for (int u = 0; u < 8; ++u) {
+        const int o = blockIdx.x * 32 + wave * 8 + u;
+        if (o >= a.rd) break;
+        const float * __restrict__ w = a.w_down + (int64_t) o * a.d + lane;
+        float wv[NI];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) wv[j] = !GUARD || lane + 64 * j < a.d ? w[64 * j] : 0.0f;
+        const float b = a.b_down[o];
+        const float ev = eda ? a.eda[o] : 0.0f;
+        for (int tt = 0; tt < nt; ++tt) {
+            const int t = t0 + tt;
+            const float st = eda ? a.state_in[(int64_t) t * a.rd + o] * ev : 0.0f;
+            const float * xr = xs_t + ((size_t) tt * 64 + lane) * S;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < NI / 4; ++j4) {
+                const float4 xv = *(const float4 *) (xr + 4 * j4);
+                const float xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * j4 + jj;
+                    if (!GUARD || lane + 64 * j < a.d) acc = __builtin_fmaf(wv[j], xx[jj], acc);
+                }
+            }
+            float v = wave_tree_f(acc) + b;
+            if (eda) v = v + st;
+            if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+        }
+    }
 }
 
 // An MoE layer's FFN entry in one launch: residual add, ffn_norm, the activation encoding for the
