@@ -10,6 +10,7 @@
 #include "z2h.h"
 #include "z2h_kernels.h"
 #include "z2h_gemm.h"
+#include "z2h_attn.h"
 #include <hip/hip_ext.h>
 #include "z2_formats.h"
 
@@ -157,6 +158,7 @@ namespace {
 int seterr(z2h_ctx * c, int code, const std::string & m) { if (c) c->err = m; return code; }
 int seterr(z2h_model * c, int code, const std::string & m) { if (c) c->err = m; return code; }
 int upload_mat_t64(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm);
+int launch_attn_fa(z2h_ctx * ctx, const AttnArgs & a, int grid);
 int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid);
 int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles);
 int launch_kv_append(z2h_ctx * ctx, const AttnArgs & a, int T);
@@ -464,8 +466,8 @@ int alloc_scratch(z2h_ctx * ctx) {
         (rc = dalloc(ctx, &ctx->spk_io, (size_t) Z2H_SPEAKER_MAX * (kpad(hp.spk_dim) + kpad(hp.spk_lda_dim) + 2 * kpad(d)) * 4, b)))
         return rc;
     (void) E;
-    if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) ctx->items_max * sizeof(int4), b))) return rc;
-    if (hipHostMalloc((void **) &ctx->h_tiles, (size_t) ctx->items_max * sizeof(int4), hipHostMallocDefault) != hipSuccess)
+    if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) 2 * ctx->items_max * sizeof(int4), b))) return rc;
+    if (hipHostMalloc((void **) &ctx->h_tiles, (size_t) 2 * ctx->items_max * sizeof(int4), hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     ctx->h_pin_bytes = (size_t) T * (4 + W) * 4;
     if (hipHostMalloc((void **) &ctx->h_pin, ctx->h_pin_bytes, hipHostMallocDefault) != hipSuccess)
@@ -902,14 +904,36 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     if ((rc = launch_resnorm(ctx, T, e))) return rc;
     if (n_run && (rc = cap_copy(ctx, Z2H_CAP_RES_IN, run[0], ctx->res, T))) return rc;
     (void) h_npast;
-    // persistent attention grid: the item count comes from the device n_past table
-    // persistent attention grid: as many blocks as fit on the chip at once (a block past that would
-    // wait for a slot only to find no item left); blocks loop over the items beyond it
+    // decode steps: a persistent attention grid (the item count comes from the device n_past table),
+    // as many blocks as fit on the chip at once; blocks loop over the items beyond it
+    const int grp = nh / nkv;
     const int attn_grid = std::min(ctx->items_max, ctx->attn_slots);
-    // kv_pre passes (host copies of the rows' slots and positions at hand): tiles of up to ATT_TILE
-    // rows of one slot at consecutive positions share each K/V chunk read (k_attn_tile)
+    // wide passes (host copies of the rows' slots and positions at hand): work items (tile, KV head,
+    // segment), a tile being up to FA_ROWS rows of one slot at consecutive positions (k_attn_fa)
+    int n_fa = 0;
+    if (kv_pre && !f32_prompt && h_slot && h_npast) {
+        const int rows_max = std::max(1, std::min(FA_ROWS, 64 / grp));
+        int segs = 0;
+        for (int t = 0; t < T;) {
+            int m = 1;
+            while (t + m < T && m < rows_max && h_slot[t + m] == h_slot[t] && h_npast[t + m] == h_npast[t] + m) ++m;
+            const int ns = fa_nseg(h_npast[t] + m - 1);
+            for (int s = 0; s < ns; ++s)
+                for (int g = 0; g < nkv; ++g) {
+                    if (n_fa >= ctx->items_max) return seterr(ctx, Z2H_EINVAL, "attention tile table overflow");
+                    ctx->h_tiles[2 * n_fa] = make_int4(t, m | (g << 16), s, segs);
+                    ctx->h_tiles[2 * n_fa + 1] = make_int4(h_npast[t], h_slot[t], 0, 0);
+                    ++n_fa;
+                }
+            for (int j = 0; j < m; ++j) segs += fa_nseg(h_npast[t + j]);
+            t += m;
+        }
+        HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) 2 * n_fa * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
+    }
+    // per-slot prefill (f32_prompt): tiles of up to ATT_TILE rows of one slot at consecutive positions
+    // share each 64-row chunk of the prompt's fp32 K/V (k_attn_tile_f32, then k_attn_combine)
     int n_tiles = 0;
-    if (kv_pre && h_slot && h_npast) {
+    if (kv_pre && f32_prompt && h_slot && h_npast) {
         int before = 0;
         for (int t = 0; t < T;) {
             int m = 1;
@@ -949,27 +973,39 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         }
         a.act = ctx->act;
         const int wo_act = act_of(ly.wo.type);
-        // heads per combine block: the fewest (1, 2, 4 or 8, dividing the group) whose outputs cover
-        // whole encoding blocks, so the block encodes its slice for W_o; else a separate encode pass
-        int hpb = 0;
-        for (int h = 1; h <= 8 && !hpb; h *= 2)
-            if ((nh / nkv) % h == 0 && (h * hd) % 256 == 0) hpb = h;
-        const bool in_block = hpb != 0;
-        if (!hpb) hpb = 1;
-        a.act_fmt = in_block ? wo_act : ACT_NONE;
-        {
-            // QK-norm / RoPE / KV append fused in; item count from the device n_past table
-            prof_scope ps(ctx, Z2H_KF_ATTN);
-            if (kv_pre && (rc = launch_kv_append(ctx, a, T))) return rc;
-            if (n_tiles > 0) {
-                if ((rc = launch_attn_tile(ctx, a, n_tiles))) return rc;
-            } else if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
-        }
-        {
+        bool in_block;
+        if (!kv_pre || f32_prompt) {
+            // heads per combine block: the fewest (1, 2, 4 or 8, dividing the group) whose outputs
+            // cover whole encoding blocks, so the block encodes its slice for W_o; else a separate
+            // encode pass
+            int hpb = 0;
+            for (int h = 1; h <= 8 && !hpb; h *= 2)
+                if (grp % h == 0 && (h * hd) % 256 == 0) hpb = h;
+            in_block = hpb != 0;
+            if (!hpb) hpb = 1;
+            a.act_fmt = in_block ? wo_act : ACT_NONE;
+            {
+                // decode steps: QK-norm / RoPE / KV append fused in, items from the device n_past table;
+                // per-slot prefill: the appended fp32 prompt rows
+                prof_scope ps(ctx, Z2H_KF_ATTN);
+                if (kv_pre) {
+                    if ((rc = launch_kv_append(ctx, a, T))) return rc;
+                    if ((rc = launch_attn_tile(ctx, a, n_tiles))) return rc;
+                } else if ((rc = launch_attn(ctx, a, attn_grid))) return rc;
+            }
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
             const int nc_max = (ctx->S + ATT_CH - 1) / ATT_CH;
             KL(k_attn_combine, dim3(nh / hpb, T), dim3(512), attn_combine_lds(hpb, hd, nc_max), ctx->stream, a, hpb, nc_max);
             HIPX(hipGetLastError());
+        } else {
+            // wide passes: k_attn_fa / k_attn_merge finish (and encode) a KV group's heads of a row in
+            // one block
+            in_block = (grp * hd) % 256 == 0;
+            a.act_fmt = in_block ? wo_act : ACT_NONE;
+            prof_scope ps(ctx, Z2H_KF_ATTN);
+            if ((rc = launch_kv_append(ctx, a, T))) return rc;
+            a.tiles = (const int4 *) ctx->d_tiles;
+            if (n_fa > 0 && (rc = launch_attn_fa(ctx, a, n_fa))) return rc;
         }
         if (!in_block) {
             ResNormArgs en{};
@@ -1057,7 +1093,9 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_router_down_t<32, true>)) LDS_ATTR((k_router_down_t<64, true>))
     LDS_ATTR(k_gemm_q4k<true>) LDS_ATTR(k_gemm_q4k<false>)
     LDS_ATTR((k_gemm_f16<true, 4, 4>)) LDS_ATTR((k_gemm_f16<false, 4, 4>)) LDS_ATTR((k_gemm_f16<true, 2, 1>)) LDS_ATTR((k_gemm_f16<false, 1, 1>))
-#define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>))
+#define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>)) \
+                   LDS_ATTR((k_attn_fa<H_, 1>)) LDS_ATTR((k_attn_fa<H_, 2>)) LDS_ATTR((k_attn_fa<H_, 4>)) LDS_ATTR((k_attn_fa<H_, 8>)) \
+                   LDS_ATTR((k_attn_merge<H_, 1>)) LDS_ATTR((k_attn_merge<H_, 2>)) LDS_ATTR((k_attn_merge<H_, 4>)) LDS_ATTR((k_attn_merge<H_, 8>))
     LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
 #undef LDS_TF
     LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
@@ -1095,7 +1133,12 @@ int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles) {
         HIPX(hipGetLastError());
         return Z2H_OK;
     }
-#define ATT(H_, G_) KL((k_attn_tile<H_, G_>), dim3(n_tiles), dim3(256), 0, ctx->stream, a, (const int4 *) ctx->d_tiles)
+    return seterr(ctx, Z2H_EINVAL, "chunk tiles without the prompt's fp32 K/V");
+}
+
+int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
+    const int grp = a.nh / a.nkv;
+#define ATT(H_, G_) KL((k_attn_chunk<H_, G_>), dim3(grid), dim3(256), 0, ctx->stream, a)
 #define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
     switch (a.hd) {
         case 16: ATT_G(16) break;
@@ -1109,9 +1152,13 @@ int launch_attn_tile(z2h_ctx * ctx, const AttnArgs & a, int n_tiles) {
     return Z2H_OK;
 }
 
-int launch_attn(z2h_ctx * ctx, const AttnArgs & a, int grid) {
+// k_attn_fa on `grid` blocks, then k_attn_merge over (row, KV head) for the rows of several segments
+int launch_attn_fa(z2h_ctx * ctx, const AttnArgs & a, int grid) {
     const int grp = a.nh / a.nkv;
-#define ATT(H_, G_) KL((k_attn_chunk<H_, G_>), dim3(grid), dim3(256), 0, ctx->stream, a)
+    const size_t lds = attn_fa_lds(a.hd);
+    const size_t mlds = attn_merge_lds(a.hd, grp, (ctx->S + FA_SEG - 1) / FA_SEG);
+#define ATT(H_, G_) do { KL((k_attn_fa<H_, G_>), dim3(grid), dim3(256), lds, ctx->stream, a); \
+                         KL((k_attn_merge<H_, G_>), dim3(a.T * a.nkv), dim3(256), mlds, ctx->stream, a); } while (0)
 #define ATT_G(H_) switch (grp) { case 1: ATT(H_, 1); break; case 2: ATT(H_, 2); break; case 4: ATT(H_, 4); break; default: ATT(H_, 8); }
     switch (a.hd) {
         case 16: ATT_G(16) break;

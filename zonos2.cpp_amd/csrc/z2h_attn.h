@@ -1,0 +1,408 @@
+// z2h_attn.h — ragged GQA attention on MFMA for decode steps and wide passes (prefill chunks, mixed
+// batches): src/zonos2-graph.cpp:113-175 (QK-norm, |temp|, interleaved RoPE, f16 KV append,
+// softmax(K^T q / sqrt(hd)) V over the slot's band [0, n_past], sigmoid gate).
+//
+// Work item = (tile, KV head g, segment s): a tile is one row (decode) or a run of up to FA_ROWS rows
+// of one slot at consecutive positions (wide passes); segment s is keys [128 s, 128 s + 128) of the
+// band. The block loads the segment's K rows and V columns once for all rows of the tile, forms the
+// rows' queries (one wave per row: per-head RMSNorm, |temp|, RoPE, f16) and computes, per row-head
+// rh = row * GRP + head:
+//   S^T = K Q^T            v_mfma_f32_16x16x32_f16 (M = 16 keys, N = 16 row-heads, K = 32 dims)
+//   softmax over the segment's keys (causal mask per row), fp32, exp = z_expf
+//   O^T = V^T P^T          the same MFMA with P split in two f16 parts (p = hi + lo, lo = p - hi)
+// With S^T as the MFMA output, lane (rh, q) holds keys {16 mt + 4 q + i}, which is exactly the
+// lane's share of the next product's P^T operand (the k-slot order only has to agree between the
+// two operands); V is transposed on its way into LDS.
+// A row whose band fits one segment is finished in the block (normalised, gated, encoded for W_o);
+// the others leave one partial (max, sum, O) per segment, which k_attn_merge folds in order. A row's
+// arithmetic does not depend on the tile it is in, so a decode step and a wide pass give the same
+// bits.
+#pragma once
+#include "z2h_gemm.h"
+
+namespace z2d {
+
+constexpr int FA_SEG = 128;            // keys per segment
+constexpr int FA_ROWS = 16;            // rows per wide tile (and rows * GRP <= 64)
+
+__host__ __device__ inline int fa_nseg(int pos) { return (pos + FA_SEG) / FA_SEG; }   // segments of keys [0, pos]
+
+// K rows [FA_SEG][hdp + 8], then V columns [hd][FA_SEG + 8] (the queries [64][hdp + 8] before them)
+__host__ __device__ inline size_t attn_fa_lds(int hd) {
+    const int hdp = hd < 32 ? 32 : hd;
+    const size_t vt = (size_t) hd * (FA_SEG + 8), q = (size_t) 64 * (hdp + 8);
+    return (size_t) FA_SEG * (hdp + 8) * 2 + (vt > q ? vt : q) * 2;
+}
+
+// decode items: item = (segment of token t, KV head g) over all tokens in order; sb = segments of the
+// tokens before t
+__device__ __forceinline__ bool fa_locate(const int32_t * n_past, const int32_t * slot_idx, int T, int nkv, int item,
+                                          int & n_items, int & t, int & s, int & g, int & sb, int & np, int & slot) {
+    const int lane = threadIdx.x & 63, want = item / nkv;
+    g = item % nkv;
+    int base = 0;
+    bool found = false;
+    for (int t0 = 0; t0 < T; t0 += 64) {
+        const int u = t0 + lane;
+        const int npu = u < T ? n_past[u] : 0, su = u < T ? slot_idx[u] : 0;
+        const int ns = u < T ? fa_nseg(npu) : 0;
+        const int incl = wave_scan_incl(ns, lane), excl = incl - ns;
+        const uint64_t hit = __ballot(!found && want >= base + excl && want < base + incl);
+        if (hit) {
+            const int l = __ffsll((unsigned long long) hit) - 1;
+            t = t0 + l;
+            sb = base + lane_i(excl, l);
+            s = want - sb;
+            np = lane_i(npu, l);
+            slot = lane_i(su, l);
+            found = true;
+        }
+        base += lane_i(incl, 63);
+    }
+    n_items = base * nkv;
+    return found;
+}
+
+// The block's output rows [m][GRP * HD] in s_out: stored to o_out (the group's slice of each row) and
+// encoded for W_o (Q8_K per 256-block by one wave, as encode_row; Q8_0 / F16 through encode_row).
+template <int HD, int GRP>
+__device__ __forceinline__ void fa_store_rows(const AttnArgs & a, const float * s_out, int t0, int m, int g) {
+    constexpr int SPAN = GRP * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int base = g * SPAN, W = a.nh * HD;
+    for (int i = tid; i < m * (SPAN / 4); i += 256) {
+        const int r = i / (SPAN / 4), c = 4 * (i % (SPAN / 4));
+        *(float4 *) (a.o_out + (int64_t) (t0 + r) * W + base + c) = *(const float4 *) (s_out + r * SPAN + c);
+    }
+    if (a.act_fmt == ACT_NONE) return;
+    const int Kp = kpad(W);
+    if (a.act_fmt == ACT_Q8_K) {
+        constexpr int NB = SPAN / 256;
+        for (int b = wave; b < m * NB; b += 4) {
+            const int r = b / NB, bb = b % NB, t = t0 + r;
+            const float4 v4 = *(const float4 *) (s_out + r * SPAN + 256 * bb + 4 * lane);
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            q8k_block_v(v, a.act.q + (int64_t) t * Kp + base + 256 * bb, a.act.d256 + (int64_t) t * (Kp / 256) + base / 256 + bb,
+                        a.act.bs + (int64_t) t * (Kp / 16) + base / 16 + 16 * bb, lane);
+        }
+        return;
+    }
+    for (int r = 0; r < m; ++r) {
+        const int t = t0 + r;
+        if (a.act_fmt == ACT_Q8_0)
+            encode_row<ACT_Q8_0>(s_out + r * SPAN, SPAN, a.act.q + (int64_t) t * Kp + base, a.act.d32 + (int64_t) t * (Kp / 32) + base / 32,
+                                 nullptr, nullptr, nullptr);
+        else
+            encode_row<ACT_F16>(s_out + r * SPAN, SPAN, nullptr, nullptr, nullptr, nullptr, a.act.h + (int64_t) t * Kp + base);
+    }
+}
+
+// grid: wide passes one block per item, a.tiles[2 item] = (first row t0, rows m | g << 16, segment,
+// segments of all rows before t0) and a.tiles[2 item + 1] = (n_past of t0, its slot); decode steps a
+// persistent grid over the items fa_locate finds.
+// 256 threads; dynamic LDS attn_fa_lds(HD). Decode items form the new row's k / v (the last segment)
+// and append them to the cache; wide passes have appended theirs (k_kv_append).
+template <int HD, int GRP>
+__global__ void __launch_bounds__(256, 2) k_attn_fa(AttnArgs a) {
+    constexpr int HDP = HD < 32 ? 32 : HD;             // dims padded to the 32-wide k-steps of Q.K
+    constexpr int KP = HDP + 8, VP = FA_SEG + 8;       // LDS pitches (halves)
+    constexpr int NP = HD / 2;                         // dim pairs of a head (lane = pair)
+    constexpr int DT = HD / 16;                        // 16-dim tiles of O
+    constexpr int KS = HDP / 32;                       // k-steps of Q.K
+    constexpr int MT = FA_SEG / 16;                    // 16-key tiles of a segment
+    constexpr int PS = FA_SEG / 32;                    // 32-key steps of P.V
+    constexpr int U4 = FA_SEG * HD / 8 / 256;          // 16-byte K (and V) items per thread
+    static_assert(HD >= 16 && HD <= 128 && FA_SEG * HD / 8 % 256 == 0, "head size");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    uint16_t * s_k = (uint16_t *) smem;                // [FA_SEG][KP]
+    uint16_t * s_vt = s_k + FA_SEG * KP;               // [HD][VP]
+    uint16_t * s_q = s_vt;                             // [64][KP] (before s_vt is filled)
+    float * s_out = (float *) smem;                    // [rows][GRP * HD] (after the products)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
+    const int nkv = a.nkv;
+    const bool wide = a.tiles != nullptr;
+    for (int item = blockIdx.x;; item += gridDim.x) {
+        int t0, m, g, s, sb0, p0, slot;
+        if (wide) {
+            if (item >= (int) gridDim.x) break;
+            const int4 e = a.tiles[2 * item], e2 = a.tiles[2 * item + 1];
+            t0 = e.x; m = e.y & 0xffff; g = e.y >> 16; s = e.z; sb0 = e.w; p0 = e2.x; slot = e2.y;
+        } else {
+            int n_items;
+            if (!fa_locate(a.n_past, a.slot_idx, a.T, nkv, item, n_items, t0, s, g, sb0, p0, slot)) break;
+            m = 1;
+        }
+        const int plast = p0 + m - 1, nseg_t = fa_nseg(plast), k0 = s * FA_SEG;
+        const int cmax = wide ? plast : p0 - 1;                       // last key row taken from the cache
+        const int64_t band = ((int64_t) slot * nkv + g) * a.S * HD;
+        const bool mk = !wide && s == nseg_t - 1;                     // decode: the segment holds the new row
+        const int P = m * GRP, RT = P <= 16 ? 1 : P <= 32 ? 2 : 4;
+        // ---- the wave's query inputs first, then the segment's K rows and V columns, so the query
+        // arithmetic waits only for its own loads. Row-head slot k of the wave: with one row, rh =
+        // wave + 4k (one wave per head); else row wave + 4 (k / GRP), head k % GRP (one wave per row).
+        // (slots 8..15 only occur in wide tiles; their loads follow the K / V requests)
+        constexpr int QK = 16, QK0 = 8;
+        float qx0[QK], qx1[QK];
+        auto q_load = [&](int k) {
+            const int i = m == 1 ? (wave + 4 * k) / GRP : wave + 4 * (k / GRP), h = m == 1 ? (wave + 4 * k) % GRP : k % GRP;
+            const bool ok = i < m && i * GRP + h < 16 * RT;
+            const float * row = a.qkvg + (int64_t) (t0 + (ok ? i : 0)) * a.R + (int64_t) (g * GRP + h) * HD;
+            qx0[k] = ok && lane < NP ? row[2 * lane] : 0.0f;
+            qx1[k] = ok && lane < NP ? row[2 * lane + 1] : 0.0f;
+        };
+#pragma unroll
+        for (int k = 0; k < QK0; ++k) q_load(k);
+        float nx[4] = {0.0f, 0.0f, 0.0f, 0.0f};                     // the decode row's new k and v (wave 3)
+        if (mk && wave == 3 && lane < NP) {
+            const float * row = a.qkvg + (int64_t) t0 * a.R;
+            nx[0] = row[(int64_t) (a.nh + g) * HD + 2 * lane]; nx[1] = row[(int64_t) (a.nh + g) * HD + 2 * lane + 1];
+            nx[2] = row[(int64_t) (a.nh + nkv + g) * HD + 2 * lane]; nx[3] = row[(int64_t) (a.nh + nkv + g) * HD + 2 * lane + 1];
+        }
+        // K rows and V columns: every load issued (entries past cmax read the band's start and are
+        // stored as zeros); K goes to LDS at once, V once the queries have left its region
+        uint4 kr[U4], vr[U4];
+#pragma unroll
+        for (int j = 0; j < U4; ++j) {
+            const int i = tid + 256 * j;
+            const int r = i / (HD / 8), c = i % (HD / 8);             // K: key row r, dims 8c..
+            kr[j] = *(const uint4 *) (a.kc + band + (k0 + r <= cmax ? (int64_t) (k0 + r) * HD + 8 * c : 0));
+        }
+#pragma unroll
+        for (int j = 0; j < U4; ++j) {
+            const int i = tid + 256 * j;
+            const int r = i % FA_SEG, c = i / FA_SEG;                // V: key row r (lanes), dims 8c..
+            vr[j] = *(const uint4 *) (a.vc + band + (k0 + r <= cmax ? (int64_t) (k0 + r) * HD + 8 * c : 0));
+        }
+#pragma unroll
+        for (int k = QK0; k < QK; ++k) q_load(k);
+        // K straight to LDS (its region is not shared with the queries)
+#pragma unroll
+        for (int j = 0; j < U4; ++j) {
+            const int i = tid + 256 * j;
+            const int r = i / (HD / 8), c = i % (HD / 8);
+            *(uint4 *) &s_k[r * KP + 8 * c] = k0 + r <= cmax ? kr[j] : make_uint4(0, 0, 0, 0);
+        }
+        if (HD < HDP)                                                 // zero dims [HD, HDP) of the K rows
+            for (int i = tid; i < FA_SEG * (HDP - HD) / 8; i += 256) {
+                const int r = i / ((HDP - HD) / 8), c = i % ((HDP - HD) / 8);
+                *(uint4 *) &s_k[r * KP + HD + 8 * c] = make_uint4(0, 0, 0, 0);
+            }
+        // ---- queries of row-heads rh < 16 RT (past P: zeros), and the decode row's new k / v
+        uint32_t nk = 0, nv = 0;
+        {
+            float cs = 1.0f, sn = 0.0f;
+#pragma unroll
+            for (int k = 0; k < QK; ++k) {
+                const int i = m == 1 ? (wave + 4 * k) / GRP : wave + 4 * (k / GRP), h = m == 1 ? (wave + 4 * k) % GRP : k % GRP;
+                const int rh = i * GRP + h;
+                if (rh >= 16 * RT) continue;
+                // one RoPE angle per row: the first row-head slot of each row (every slot with one row)
+                if (i < m && (m == 1 ? k == 0 : h == 0)) rope_cs(p0 + i, min(lane, NP - 1), a.theta_scale, cs, sn);
+                uint32_t qv = 0;
+                if (i < m) {
+                    const int qh = g * GRP + h;
+                    float y0, y1;
+                    norm_rope<HD>(qx0[k], qx1[k], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
+                    if (lane < NP) {
+                        qv = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                        if (a.cap_q && s == 0) {
+                            a.cap_q[((int64_t) (t0 + i) * a.nh + qh) * HD + 2 * lane] = y0;
+                            a.cap_q[((int64_t) (t0 + i) * a.nh + qh) * HD + 2 * lane + 1] = y1;
+                        }
+                    }
+                }
+                if (lane < HDP / 2) *(uint32_t *) &s_q[rh * KP + 2 * lane] = qv;
+            }
+        }
+        if (mk && wave == 3) {
+            float cs, sn, k0f, k1f;
+            rope_cs(p0, min(lane, NP - 1), a.theta_scale, cs, sn);
+            norm_rope<HD>(nx[0], nx[1], 1.0f, a.qk_eps, cs, sn, k0f, k1f);
+            if (lane < NP) {
+                nk = (uint32_t) f2h(k0f) | ((uint32_t) f2h(k1f) << 16);
+                nv = (uint32_t) f2h(nx[2]) | ((uint32_t) f2h(nx[3]) << 16);
+                if (a.cap_k) {
+                    a.cap_k[((int64_t) t0 * nkv + g) * HD + 2 * lane] = k0f; a.cap_k[((int64_t) t0 * nkv + g) * HD + 2 * lane + 1] = k1f;
+                    a.cap_v[((int64_t) t0 * nkv + g) * HD + 2 * lane] = nx[2]; a.cap_v[((int64_t) t0 * nkv + g) * HD + 2 * lane + 1] = nx[3];
+                }
+            }
+        }
+        lds_sync();                                                   // queries and K rows in LDS
+        const int rt = wave % RT, split = wave / RT, nsplit = 4 / RT;
+        v8h_t qf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const v8h_t *) &s_q[(16 * rt + c16) * KP + 32 * ks + 8 * q4];
+        if (mk && wave == 3 && lane < NP) {
+            // the new row (key p0) into the LDS copy of K and into the cache
+            *(uint32_t *) &s_k[(p0 - k0) * KP + 2 * lane] = nk;
+            *(uint32_t *) (a.kc + band + (int64_t) p0 * HD + 2 * lane) = nk;
+            *(uint32_t *) (a.vc + band + (int64_t) p0 * HD + 2 * lane) = nv;
+        }
+        lds_sync();                                                   // s_q is free; s_k complete
+        // ---- S^T = K Q^T for the wave's 16 row-heads, scaled and masked (key > the row's position)
+        const int rh = 16 * rt + c16;
+        const bool rh_ok = rh < P;
+        const int prow = p0 + min(rh / GRP, m - 1);
+        float sc[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const v8h_t *) &s_k[(16 * mt + c16) * KP + 32 * ks + 8 * q4], qf[ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kp = k0 + 16 * mt + 4 * q4 + i;
+                sc[mt][i] = kp <= prow ? acc[i] * a.scale : -__builtin_inff();
+            }
+        }
+        // ---- softmax over the segment (the rh's keys sit in lanes c16, c16 + 16, + 32, + 48)
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mt][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float lsum = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = sc[mt][i] == -__builtin_inff() ? 0.0f : z_expf(sc[mt][i] - mx);
+                sc[mt][i] = p;
+                lsum = lsum + p;
+            }
+        lsum = lsum + __shfl_xor(lsum, 16);
+        lsum = lsum + __shfl_xor(lsum, 32);
+        v8h_t ph[PS], pl[PS];
+#pragma unroll
+        for (int ps = 0; ps < PS; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = sc[2 * ps + (j >> 2)][j & 3];
+                const _Float16 hi = (_Float16) p;
+                ph[ps][j] = hi;
+                pl[ps][j] = (_Float16) (p - (float) hi);
+            }
+        // ---- the V rows transposed into LDS (keys past cmax zeroed; the decode row's new v after them):
+        // the lanes of a store are consecutive keys of one dim
+#pragma unroll
+        for (int j = 0; j < U4; ++j) {
+            const int i = tid + 256 * j;
+            const int r = i % FA_SEG, c = i / FA_SEG;
+            const uint4 v = k0 + r <= cmax ? vr[j] : make_uint4(0, 0, 0, 0);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_vt[(8 * c + e) * VP + r] = (uint16_t) (w[e >> 1] >> (16 * (e & 1)));
+        }
+        lds_sync();
+        if (mk) {
+            if (wave == 3 && lane < NP) {
+                s_vt[(2 * lane) * VP + p0 - k0] = (uint16_t) (nv & 0xffffu);
+                s_vt[(2 * lane + 1) * VP + p0 - k0] = (uint16_t) (nv >> 16);
+            }
+            lds_sync();
+        }
+        // ---- O^T = V^T P^T over the wave's dim tiles dt = split, split + nsplit, ... A row whose band
+        // is one segment is finished here (normalised, gated, encoded); the others leave partials
+        // (segment max, sum, unnormalised O) for k_attn_merge
+        const int i_row = min(rh / GRP, m - 1), hh = rh % GRP, qh = g * GRP + hh, t_row = t0 + i_row;
+        const int ns_row = fa_nseg(p0 + i_row);
+        const bool fin = ns_row == 1;                                 // (then s == 0)
+        float gsig = 0.0f;
+        if (rh_ok && fin) gsig = z_sigmoid(a.qkvg[(int64_t) t_row * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qh]);
+        int sb_row = sb0;
+        for (int j = 0; j < i_row; ++j) sb_row += fa_nseg(p0 + j);
+        const bool has_seg = s < ns_row;
+        const int64_t pidx = ((int64_t) (sb_row + s) * nkv + g) * GRP + hh;
+        if (!fin && rh_ok && has_seg && q4 == 0 && split == 0) *(float2 *) (a.part_ml + pidx * 2) = make_float2(mx, lsum);
+#pragma unroll
+        for (int u = 0; u < DT; ++u) {
+            const int dt = split + nsplit * u;
+            if (dt >= DT) break;
+            v4f_t o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ps = 0; ps < PS; ++ps) {
+                const uint16_t * vp = &s_vt[(16 * dt + c16) * VP + 32 * ps + 4 * q4];
+                const uint2 lo = *(const uint2 *) vp, hi = *(const uint2 *) (vp + 16);
+                const v8h_t vf = __builtin_bit_cast(v8h_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ps], o, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[ps], o, 0, 0, 0);
+            }
+            const int dim = 16 * dt + 4 * q4;
+            if (!rh_ok) continue;
+            if (fin) {
+                const float f = gsig / lsum;
+                *(float4 *) (s_out + i_row * (GRP * HD) + hh * HD + dim) = make_float4(o[0] * f, o[1] * f, o[2] * f, o[3] * f);
+            } else if (has_seg) {
+                *(float4 *) (a.part_o + pidx * HD + dim) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
+        // rows [0, m1) of the tile are one-segment rows (positions below FA_SEG), finished by segment 0
+        const int m1 = s == 0 ? max(0, min(m, FA_SEG - p0)) : 0;
+        if (m1 > 0) {
+            if (a.cap_gate && rh_ok && fin && q4 == 0 && split == 0) a.cap_gate[(int64_t) t_row * a.nh + qh] = gsig;
+            lds_sync();                                               // s_out rows complete
+            fa_store_rows<HD, GRP>(a, s_out, t0, m1, g);
+        }
+        lds_sync();                                                   // LDS reuse by the next item
+    }
+}
+
+// The segments of rows whose band spans several: block (row t, KV head g), its GRP heads. Every
+// partial of the row is requested at once into LDS, then each (head, 4 dims) folds the segments in
+// order: M = max m_s, w_s = exp(m_s - M), L = sum w_s l_s, O = sum w_s O_s (fmaf chains), out =
+// O * (sigmoid(gate) / L); the row's group slice is stored and encoded for W_o as k_attn_fa does.
+// Dynamic LDS attn_merge_lds(hd, grp, max segments).
+__host__ __device__ inline size_t attn_merge_lds(int hd, int grp, int nsmax) {
+    return (size_t) 4 * ((size_t) nsmax * grp * (hd + 2) + (size_t) grp * hd);
+}
+template <int HD, int GRP>
+__global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float sm_mg[];
+    const int t = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv, tid = threadIdx.x, nkv = a.nkv;
+    const int lane = tid & 63;
+    const int ns = fa_nseg(a.n_past[t]);
+    if (ns == 1) return;                                              // finished by k_attn_fa
+    // segments of the rows before t (every wave scans; lanes are rows)
+    int sb = 0;
+    for (int u0 = 0; u0 < t; u0 += 64) {
+        const int u = u0 + lane;
+        sb += lane_i(wave_scan_incl(u < t ? fa_nseg(a.n_past[u]) : 0, lane), 63);
+    }
+    float * s_o = sm_mg;                                              // [ns][GRP][HD]
+    float * s_ml = s_o + (size_t) ns * GRP * HD;                      // [ns][GRP][2]
+    float * s_out = s_ml + (size_t) ns * GRP * 2;                     // [GRP][HD]
+    const int64_t pst = (int64_t) nkv * GRP, p_0 = ((int64_t) sb * nkv + g) * GRP;
+    // partial (segment ss, head h) = p_0 + ss * pst + h
+    for (int i = tid; i < ns * GRP * (HD / 4); i += 256) {
+        const int ss = i / (GRP * (HD / 4)), h = (i / (HD / 4)) % GRP, d4 = 4 * (i % (HD / 4));
+        *(float4 *) (s_o + (ss * GRP + h) * HD + d4) = *(const float4 *) (a.part_o + (p_0 + ss * pst + h) * HD + d4);
+    }
+    for (int i = tid; i < ns * GRP; i += 256)
+        *(float2 *) (s_ml + 2 * i) = *(const float2 *) (a.part_ml + (p_0 + (i / GRP) * pst + i % GRP) * 2);
+    lds_sync();
+    for (int u = tid; u < GRP * (HD / 4); u += 256) {
+        const int h = u / (HD / 4), d4 = 4 * (u % (HD / 4)), qh = g * GRP + h;
+        const float gs = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qh]);
+        float M = -__builtin_inff();
+        for (int ss = 0; ss < ns; ++ss) M = fmaxf(M, s_ml[(ss * GRP + h) * 2]);
+        float L = 0.0f;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int ss = 0; ss < ns; ++ss) {
+            const float2 ml = *(const float2 *) (s_ml + (ss * GRP + h) * 2);
+            const float w = ml.x == -__builtin_inff() ? 0.0f : z_expf(ml.x - M);
+            const float4 po = *(const float4 *) (s_o + (ss * GRP + h) * HD + d4);
+            L = __builtin_fmaf(w, ml.y, L);
+            o = make_float4(__builtin_fmaf(w, po.x, o.x), __builtin_fmaf(w, po.y, o.y), __builtin_fmaf(w, po.z, o.z), __builtin_fmaf(w, po.w, o.w));
+        }
+        const float f = gs / L;
+        if (a.cap_gate && d4 == 0) a.cap_gate[(int64_t) t * a.nh + qh] = gs;
+        *(float4 *) (s_out + h * HD + d4) = make_float4(o.x * f, o.y * f, o.z * f, o.w * f);
+    }
+    lds_sync();
+    fa_store_rows<HD, GRP>(a, s_out, t, 1, g);
+}
+
+} // namespace z2d

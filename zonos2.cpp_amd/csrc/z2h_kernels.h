@@ -11,13 +11,16 @@
 //                    weight
 //   k_gemv / k_gemv_rows   the same on the 64-row tiled layout (Q6_K, F16)
 //   k_swiglu_encode / k_encode_rows   up * silu(gate) (183, 225) / fp32 rows encoded for the next matmul
-//   k_attn_chunk     QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137) and ragged GQA
-//                    decode attention over the slot's band in 32-row chunks (139-153)
+//   k_attn_chunk     decode steps: QK-RMSNorm, |temp|, interleaved RoPE, f16 KV append (113-137) and
+//                    ragged GQA decode attention over the slot's band in 64-row chunks (139-153)
 //   k_attn_combine   chunk merge, per-head sigmoid gate (107, 173), encoding for W_o
+//   k_attn_fa / k_attn_merge   (z2h_attn.h) wide passes: the same attention on MFMA over 128-key
+//                    segments for tiles of rows of one slot, segments merged in order
+//   k_attn_tile_f32  the per-slot prefill's in-prompt fp32 attention (155-169), with k_attn_combine
 //   k_router_down    EDA router down-projection + state threading (199-203)
 //   k_router_tail    router norm, erf-GELU MLP, softmax, bias, mask, top-k, weights (206-220)
 //   k_kv_move / k_bias_add   KV row staging for host reads and writes / speaker-projection biases
-//   k_kv_append      K/V rows of every token of a prefill chunk, before the chunk's attention
+//   k_kv_append      K/V rows of every token of a wide pass, before the pass's attention
 //   k_sample         frame sampler (src/zonos2-sampler.cpp:16-77) on the step's logits
 //
 // Weight layouts in HBM: "m16" for Q4_K and Q8_0 (see k_gemv_mfma) and "row-tiled" (t64) for Q6_K
@@ -1309,6 +1312,7 @@ struct AttnArgs {
     float * o_out;           // [T][nh*hd] (combine: gated output, fp32)
     ActBuf act; int act_fmt; // encoding of o_out for W_o
     float * kf, * vf;        // per-slot prefill: this layer's fp32 prompt K/V [nkv][S][hd] (null: f16 cache only)
+    const int4 * tiles;      // k_attn_fa: wide-pass work items (null: decode items located from n_past)
 };
 
 // Wave-parallel item bookkeeping: lane u of each 64-token group loads n_past[u] (and slot_idx[u]) and
@@ -1556,114 +1560,9 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     }
 }
 
-// Attention for passes whose rows already appended their K/V (prefill chunks, mixed batches): a block
-// per (tile, chunk c, KV head g), where a tile is a run of up to ATT_TILE rows of one slot at
-// consecutive positions (tiles[blockIdx.x]: x = first row t0, y = rows m | g << 16, z = c, w = the
-// chunks of all rows before t0). The chunk's K/V rows are read once into LDS for all of the tile's
-// rows; then each wave takes whole rows (rows w, w + 4, ...) and computes k_attn_chunk's item
-// arithmetic for them without block barriers: the same per-(row, head) score dots, the same chunk
-// softmax with lane = chunk row, the same per-(head, dim pair) P.V sums over rows in order. Each row
-// writes its partial at its own item index, so every row's result is the decode kernel's bit for bit
-// and k_attn_combine merges them unchanged.
+// Tiles of the per-slot prefill's fp32 attention (k_attn_tile_f32): up to ATT_TILE rows of one slot
+// at consecutive positions per 64-row chunk.
 constexpr int ATT_TILE = 16;
-template <int HD, int GRP>
-__global__ void __launch_bounds__(256) k_attn_tile(AttnArgs a, const int4 * __restrict__ tiles) {
-    constexpr int NP = HD / 2, RW = HD / 8, KST = HD + 8;
-    constexpr int N4 = ATT_CH * RW;
-    static_assert(N4 <= 1024, "four 16-byte items per thread and matrix at most");
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
-    __shared__ __attribute__((aligned(16))) uint32_t s_q[4][GRP][NP];   // per wave
-    __shared__ float s_p[4][ATT_CH][GRP];                               // per wave
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
-    const int4 e = tiles[blockIdx.x];
-    const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16, c = e.z;
-    const int slot = a.slot_idx[t0], p0 = a.n_past[t0];
-    const int r0 = c * ATT_CH, nrmax = min(ATT_CH, p0 + m - r0);
-    const int64_t band = (((int64_t) slot * nkv + g) * a.S + r0) * HD;
-    {
-        // the chunk's rows once (rows past the tile's last one re-read it)
-        uint4 kk[4], vv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = min(tid + 256 * j, N4 - 1), r = min(i / RW, nrmax - 1), q4 = i % RW;
-            kk[j] = *(const uint4 *) (a.kc + band + (int64_t) r * HD + 8 * q4);
-            vv[j] = *(const uint4 *) (a.vc + band + (int64_t) r * HD + 8 * q4);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            if (i < N4) {
-                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = kk[j];
-                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = vv[j];
-            }
-        }
-    }
-    lds_sync();
-    uint32_t (*wq)[NP] = s_q[wave];
-    float (*wp)[GRP] = s_p[wave];
-    int before = e.w;
-    for (int i = 0; i < m; ++i) {
-        const int np = p0 + i, nc = (np + ATT_CH) / ATT_CH;
-        const int64_t item = (int64_t) (before + c) * nkv + g;
-        before += nc;
-        if ((i & 3) != wave || c >= nc) continue;                    // row i is wave i % 4's; its band may end before c
-        const int t = t0 + i, nr = min(ATT_CH, np + 1 - r0);
-        // ---- the row's queries of the group, one head at a time (lane = dim pair)
-        {
-            const float * row = a.qkvg + (int64_t) t * a.R;
-            float cs, sn;
-            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
-#pragma unroll
-            for (int h = 0; h < GRP; ++h) {
-                const int qh = g * GRP + h;
-                const float * src = row + (int64_t) qh * HD;
-                const float x0 = lane < NP ? src[2 * lane] : 0.0f, x1 = lane < NP ? src[2 * lane + 1] : 0.0f;
-                float y0, y1;
-                norm_rope<HD>(x0, x1, a.temp[qh], a.qk_eps, cs, sn, y0, y1);
-                if (lane < NP) {
-                    wq[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
-                    if (a.cap_q && c == 0) {
-                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
-                        a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
-                    }
-                }
-            }
-        }
-        // ---- scores (lane = chunk row), then the chunk softmax of each head
-#pragma unroll
-        for (int h = 0; h < GRP; ++h) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < RW; ++j) {
-                const uint4 kk = *(const uint4 *) &s_k[lane * KST + 8 * j];
-                const uint4 qq = *(const uint4 *) &wq[h][4 * j];
-                acc = fdot2(kk.x, qq.x, acc); acc = fdot2(kk.y, qq.y, acc);
-                acc = fdot2(kk.z, qq.z, acc); acc = fdot2(kk.w, qq.w, acc);
-            }
-            const float sv = lane < nr ? acc * a.scale : -__builtin_inff();
-            const float mx = wave_max_f(sv);
-            const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
-            const float l = wave_tree_f(pe);
-            wp[lane][h] = pe;
-            if (lane == 0) *(float2 *) (a.part_ml + (item * GRP + h) * 2) = make_float2(mx, l);
-        }
-        // ---- P.V: lane = dim pair, rows in order
-#pragma unroll
-        for (int h = 0; h < GRP; ++h) {
-            if (lane >= NP) break;
-            float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 16
-            for (int r = 0; r < ATT_CH; ++r) {
-                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * lane];
-                const float pp = wp[r][h];
-                o0 = __builtin_fmaf(pp, h2f(vv & 0xffffu), o0);
-                o1 = __builtin_fmaf(pp, h2f(vv >> 16), o1);
-            }
-            *(float2 *) (a.part_o + (item * GRP + h) * HD + 2 * lane) = make_float2(o0, o1);
-        }
-    }
-}
 
 // K/V append for every token of a prefill chunk before its attention reads them: one wave per
 // (token, KV head) forms the new k (per-head RMSNorm, RoPE at n_past) and v rows in f16 exactly as the
