@@ -103,6 +103,7 @@ struct z2h_ctx {
     // scratch (sized for n_slots tokens)
     int Tmax = 0, Kmax = 0, items_max = 0;   // Tmax: token rows of the scratch (steps and prefill chunks)
     int attn_slots = 2048;            // attention blocks resident at once (compute units x blocks per unit)
+    int n_cu = 256;                   // compute units of the device
     int Tstep = 0;                    // columns a step may list (n_slots); captures are sized for it
     int pch = 0;                      // prefill chunk rows (<= Tmax)
     int max_rows = 0;                 // requested row capacity (z2h_create_batch_rows)
@@ -793,7 +794,10 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
     }
     {
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
-        KL(k_router_tail, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        // wide passes: up to one block per compute unit, each looping over its tokens with the MLP
+        // matrices loaded once
+        if (T >= GEMM_MIN_ROWS) KL(k_router_tail<true>, dim3(std::min(T, ctx->n_cu)), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        else KL(k_router_tail<false>, dim3(T), dim3(256), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }
     // routes grouped by expert (mul_mat_id's grouping): the grouped matmul blocks list up to LIST_MAX
@@ -1098,7 +1102,7 @@ int set_lds_limits(std::string & err) {
                    LDS_ATTR((k_attn_merge<H_, 1>)) LDS_ATTR((k_attn_merge<H_, 2>)) LDS_ATTR((k_attn_merge<H_, 4>)) LDS_ATTR((k_attn_merge<H_, 8>))
     LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
 #undef LDS_TF
-    LDS_ATTR(k_router_tail) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
+    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     return Z2H_OK;
 }
@@ -1487,6 +1491,7 @@ int z2h_finalize(z2h_ctx * ctx) {
 #undef ATT_FN
         HIPX(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0));
         if (n_cu > 0 && per_cu > 0) ctx->attn_slots = n_cu * per_cu;
+        if (n_cu > 0) ctx->n_cu = n_cu;
     }
     (void) hp;
     ctx->graph_gen = ctx->m->gen;

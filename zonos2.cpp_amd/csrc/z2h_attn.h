@@ -77,8 +77,9 @@ __device__ __forceinline__ void fa_store_rows(const AttnArgs & a, const float * 
     if (a.act_fmt == ACT_NONE) return;
     const int Kp = kpad(W);
     if (a.act_fmt == ACT_Q8_K) {
-        constexpr int NB = SPAN / 256;
-        for (int b = wave; b < m * NB; b += 4) {
+        // (the host encodes in the block only when the span covers whole 256-blocks)
+        constexpr int NB = SPAN / 256 > 0 ? SPAN / 256 : 1;
+        for (int b = wave; b < m * (SPAN / 256); b += 4) {
             const int r = b / NB, bb = b % NB, t = t0 + r;
             const float4 v4 = *(const float4 *) (s_out + r * SPAN + 256 * bb + 4 * lane);
             const float v[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -375,10 +376,23 @@ __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
     float * s_ml = s_o + (size_t) ns * GRP * HD;                      // [ns][GRP][2]
     float * s_out = s_ml + (size_t) ns * GRP * 2;                     // [GRP][HD]
     const int64_t pst = (int64_t) nkv * GRP, p_0 = ((int64_t) sb * nkv + g) * GRP;
-    // partial (segment ss, head h) = p_0 + ss * pst + h
-    for (int i = tid; i < ns * GRP * (HD / 4); i += 256) {
-        const int ss = i / (GRP * (HD / 4)), h = (i / (HD / 4)) % GRP, d4 = 4 * (i % (HD / 4));
-        *(float4 *) (s_o + (ss * GRP + h) * HD + d4) = *(const float4 *) (a.part_o + (p_0 + ss * pst + h) * HD + d4);
+    // partial (segment ss, head h) = p_0 + ss * pst + h; MB loads per thread in flight before their stores
+    constexpr int MB = 8;
+    for (int base = 0; base < ns * GRP * (HD / 4); base += 256 * MB) {
+        float4 v[MB];
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+            const int i = min(base + tid + 256 * u, ns * GRP * (HD / 4) - 1);
+            const int ss = i / (GRP * (HD / 4)), h = (i / (HD / 4)) % GRP, d4 = 4 * (i % (HD / 4));
+            v[u] = *(const float4 *) (a.part_o + (p_0 + ss * pst + h) * HD + d4);
+        }
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+            const int i = base + tid + 256 * u;
+            if (i >= ns * GRP * (HD / 4)) break;
+            const int ss = i / (GRP * (HD / 4)), h = (i / (HD / 4)) % GRP, d4 = 4 * (i % (HD / 4));
+            *(float4 *) (s_o + (ss * GRP + h) * HD + d4) = v[u];
+        }
     }
     for (int i = tid; i < ns * GRP; i += 256)
         *(float2 *) (s_ml + 2 * i) = *(const float2 *) (a.part_ml + (p_0 + (i / GRP) * pst + i % GRP) * 2);

@@ -1004,60 +1004,61 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
 
 // Stage the encoded activation rows of nt tokens (LDS row tt = token tok(tt)) for the m16 kernels:
 // int8 values [rows][K+16], Q8_K sums of 32 [rows][K/32] and scales [rows][K/256], or Q8_0 scales
-// [rows][K/32]. Every global load of a batch is issued before its first LDS store.
-template <int AF, class TokFn>
-__device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2, float * sdx) {
+// [rows][K/32]. Rows go in batches of RB with thread tid on 16-byte column item c0 + tid of each row
+// (no index division); every global load of a batch is issued before its first LDS store, and
+// indices past the end re-read the last item, so the loads issue without branches. mid() runs once,
+// after the first batch's loads are issued: the caller's weight loads go there, behind the staging
+// loads, so the stores wait only for the staging data (loads complete in issue order).
+template <int AF, int RB, class TokFn, class MidFn>
+__device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2, float * sdx,
+                                          MidFn mid) {
     const int tid = threadIdx.x, KP = K + 16;
-    const int per = K / 16, nq = nt * per;                 // 16-byte items of the int8 rows
-    const int ns = K / 32, nsd = nt * ns;                  // sums of 32 (Q8_K) / scales (Q8_0)
-    const int nd = K / 256, ndd = nt * nd;                 // Q8_K block scales
-    const int iters = max(max((nq + 2047) / 2048, (nsd + 1023) / 1024), (ndd + 255) / 256);
-    for (int it = 0; it < iters; ++it) {
-        u32x4 v[8];
-        uint32_t sv[4];
-        float dv = 0.0f;
-        // (indices past the end re-read the last item, so the loads issue without branches)
+    const int per = K / 16, ns = K / 32, nd = K / 256;
+    bool first = true;
+    for (int r0 = 0; r0 < nt; r0 += RB) {
+        int tr[RB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = min(it * 2048 + tid + 256 * j, nq - 1);
-            v[j] = *(const u32x4 *) (act.q + (int64_t) tok(i / per) * K + (i % per) * 16);
-        }
+        for (int rr = 0; rr < RB; ++rr) tr[rr] = tok(min(r0 + rr, nt - 1));
+        for (int c0 = 0; c0 < per; c0 += 256) {
+            const int c = c0 + tid, cq = min(c, per - 1), cs = min(c, ns - 1), cd = min(c, nd - 1);
+            u32x4 v[RB];
+            uint32_t sv[RB];
+            float dv[RB];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = min(it * 1024 + tid + 256 * j, nsd - 1);
-            if constexpr (AF == ACT_Q8_K) sv[j] = *(const uint32_t *) (act.bs + (int64_t) tok(i / ns) * (K / 16) + 2 * (i % ns));
-            else sv[j] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tok(i / ns) * ns + i % ns]);
-        }
-        const int id = it * 256 + tid;
-        if constexpr (AF == ACT_Q8_K) {
-            const int ic = min(id, ndd - 1);
-            dv = act.d256[(int64_t) tok(ic / nd) * nd + ic % nd];
-        }
+            for (int rr = 0; rr < RB; ++rr) {
+                v[rr] = *(const u32x4 *) (act.q + (int64_t) tr[rr] * K + cq * 16);
+                if constexpr (AF == ACT_Q8_K) {
+                    sv[rr] = *(const uint32_t *) (act.bs + (int64_t) tr[rr] * (K / 16) + 2 * cs);
+                    dv[rr] = act.d256[(int64_t) tr[rr] * nd + cd];
+                } else {
+                    sv[rr] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tr[rr] * ns + cs]);
+                }
+            }
+            if (first) { mid(); first = false; }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = it * 2048 + tid + 256 * j;
-            if (i < nq) *(u32x4 *) (sq + (i / per) * KP + (i % per) * 16) = v[j];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = it * 1024 + tid + 256 * j;
-            if (i < nsd) {
-                if constexpr (AF == ACT_Q8_K) sbs2[i] = (int) (int16_t) (sv[j] & 0xffffu) + (int) (int16_t) (sv[j] >> 16);
-                else sdx[i] = __builtin_bit_cast(float, sv[j]);
+            for (int rr = 0; rr < RB; ++rr) {
+                const int row = r0 + rr;
+                if (row >= nt) break;
+                if (c < per) *(u32x4 *) (sq + row * KP + c * 16) = v[rr];
+                if (c < ns) {
+                    if constexpr (AF == ACT_Q8_K) sbs2[row * ns + c] = (int) (int16_t) (sv[rr] & 0xffffu) + (int) (int16_t) (sv[rr] >> 16);
+                    else sdx[row * ns + c] = __builtin_bit_cast(float, sv[rr]);
+                }
+                if (AF == ACT_Q8_K && c < nd) sdx[row * nd + c] = dv[rr];
             }
         }
-        if (AF == ACT_Q8_K && id < ndd) sdx[id] = dv;
     }
 }
 
 // grid: x = 16-row group quads, y = expert (grouped) or token chunk of ROWS (dense), z = matrix +
 // n_mats * route pass (grouped: routes [ROWS*pass, ROWS*pass+ROWS) of the expert, so hot experts
 // spread over blocks). DUAL: each wave computes the same 16 rows of two matrices (w[0] = gate,
-// w[1] = up) and stores up * silu(gate) (SwiGLU). The wave's weight units (both matrices for DUAL)
-// stream through a PF-deep register ring; the first PF are requested before the activations are
-// staged. PF = 1 caps registers for 5 (Q4_K) / 4 (Q8_0) waves per SIMD; deeper rings (fewer waves
-// per SIMD) keep more bytes in flight per wave where few blocks are resident (the expert matmuls:
-// the touched experts x row-group quads come to under two blocks per CU).
+// w[1] = up) and stores up * silu(gate) (SwiGLU). The wave's weight units (the gate matrix's, then
+// the up matrix's for DUAL) stream through a PF-deep register ring; the first PF are requested right
+// behind the first activation staging loads. PF = 1 caps registers for 5 (Q4_K) / 4 (Q8_0) waves per
+// SIMD; deeper rings (fewer waves per SIMD) keep more bytes in flight per wave where few blocks are
+// resident (the expert matmuls: the touched experts x row-group quads come to under three blocks per
+// CU).
 template <int WF, bool DUAL, int ROWS, int PF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE,
                                                                           PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE)))
@@ -1094,10 +1095,6 @@ k_gemv_mfma(GemvArgs a) {
     const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB) : ub0;
     auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
     uint4 pq[PF][QS], ph[PF];
-#pragma unroll
-    for (int j = 0; j < PF; ++j)
-        if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
-
     if (tid < ROWS) {
         int tok = 0;
         if (tid < nt) {
@@ -1107,31 +1104,33 @@ k_gemv_mfma(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
+    m16_stage<AF, (PF > 1 ? 4 : 2)>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+#pragma unroll
+        for (int j = 0; j < PF; ++j)
+            if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
+    });
     lds_sync();
     if (!has) return;
     float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // units [u0, u1) into acc (DUAL: the gate matrix's, then the up matrix's); unit u sits in ring
-    // slot u % PF (u0 is a multiple of PF: PF divides nsb), and the ring's next load may belong to the
-    // following phase
-    static_assert(PF == 1 || !DUAL, "the dual phases assume PF divides nsb");
-    auto run_units = [&](int u0, int u1, float (&acc)[4]) {
-        for (int c = u0; c < u1; c += PF) {
+    // unit u (the gate matrix's units, then the up matrix's for DUAL) sits in ring slot u % PF
+    for (int c = 0; c < U; c += PF) {
 #pragma unroll
-            for (int j = 0; j < PF; ++j) {
-                const int u = c + j;
-                if (u < u1) {
-                    float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
-                    m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
-                    if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
+        for (int j = 0; j < PF; ++j) {
+            const int u = c + j;
+            if (u < U) {
+                float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
+                m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
+                if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
+                if (!DUAL || u < nsb) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) m16_fold<WF>(acc[i], t4[i], xd[i]);
+                    for (int i = 0; i < 4; ++i) m16_fold<WF>(acc0[i], t4[i], xd[i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) m16_fold<WF>(acc1[i], t4[i], xd[i]);
                 }
             }
         }
-    };
-    run_units(0, nsb, acc0);
-    if (DUAL) run_units(nsb, U, acc1);
+    }
     const int q = lane >> 4, row = g16 * 16 + (lane & 15);
     if (row < a.rows) {
 #pragma unroll
@@ -1149,8 +1148,8 @@ k_gemv_mfma(GemvArgs a) {
 }
 
 // m16 GEMV with the K units split over the block's 4 waves: one 16-row group per block (grid x), wave
-// w takes units w, w+4, ... (all requested up front, so a wave has all its weight bytes in flight at
-// once); every unit's values go to LDS and wave 0 folds them in superblock order (m16_fold), the
+// w takes units w, w+4, ... (all requested behind the first activation staging loads, so a wave has
+// all its weight bytes in flight at once); every unit's values go to LDS and wave 0 folds them in superblock order (m16_fold), the
 // order of every other Q4_K matmul. Dense: grid (groups, token chunks of ROWS, mats);
 // grouped (expert matmuls): grid (groups, experts, passes of ROWS routes), the expert's routes listed
 // first so blocks of untouched experts read no weights. Each 16-row group gives 4x more, shorter
@@ -1189,9 +1188,6 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + eoff) : ub0;
     auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
     uint4 pq[SPLIT_UMAX][QS], ph[SPLIT_UMAX];
-#pragma unroll
-    for (int j = 0; j < SPLIT_UMAX; ++j)
-        if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
     if (tid < ROWS) {
         const int tt = min(tid, nt - 1);
         int tok = c0 + tt;
@@ -1202,7 +1198,11 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx);
+    m16_stage<AF, 4>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+#pragma unroll
+        for (int j = 0; j < SPLIT_UMAX; ++j)
+            if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
+    });
     lds_sync();
 #pragma unroll
     for (int j = 0; j < SPLIT_UMAX; ++j) {
@@ -1849,43 +1849,65 @@ __global__ void __launch_bounds__(256) k_router_down(RouterArgs a) {
 }
 
 // k_router_down for wide passes: the same per-(token, output) fma chain, wave tree, bias and state
-// term, with each output's weight row held in registers across RD_T tokens whose normalised rows sit
-// in LDS lane-major ([token][lane][j] = x[lane + 64 j], rows padded to NI + 4 floats so the lanes'
-// 16-byte reads fall in distinct banks). Grid (rd / 32, ceil(T / RD_T)), 256 threads: wave w of block
-// (og, tb) forms outputs 32 og + 8 w + u (u < 8) for tokens [RD_T tb, RD_T tb + RD_T). NI % 4 == 0.
+// term. A block takes RD_T tokens, whose rows sit in LDS lane-major ([token][lane][j] = x[lane + 64 j],
+// rows padded to NI + 4 floats so the lanes' 16-byte reads fall in distinct banks), and 32 outputs:
+// wave w forms outputs 32 og + 8 w + [0, 8) in groups of OB, each group's weight rows held in
+// registers across the RD_T tokens, so every LDS read of a token's row serves OB independent chains.
+// Grid (rd / 32, ceil(T / RD_T)), 256 threads; tokens past T repeat the last row and are not stored.
 constexpr int RD_T = 8;
 __host__ __device__ inline size_t router_down_t_lds(int ni) { return (size_t) RD_T * 64 * (ni + 4) * 4; }
 template <int NI, bool GUARD>
 __global__ void __launch_bounds__(256) k_router_down_t(RouterArgs a) {
     static_assert(NI % 4 == 0, "16-byte LDS reads");
-    constexpr int S = NI + 4;
+    constexpr int S = NI + 4, OB = NI >= 64 ? 2 : 4, PER = RD_T * (NI / 4) * 64 / 256;
     extern __shared__ __attribute__((aligned(16))) float xs_t[];     // [RD_T][64][S]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t0 = blockIdx.y * RD_T;
-    const int nt = min(RD_T, a.T - t0);
-    // the rows (tokens past T repeat the last one), element i -> [lane i % 64][j = i / 64]
-    for (int idx = tid; idx < RD_T * (a.d / 4); idx += 256) {
-        const int tt = idx / (a.d / 4), i0 = 4 * (idx % (a.d / 4));
-        const float4 v = *(const float4 *) (a.x + (int64_t) (t0 + min(tt, nt - 1)) * a.d + i0);
-        float * dst = xs_t + ((size_t) tt * 64) * S + (i0 >> 6);
-        const int l0 = i0 & 63;
-        dst[(l0 + 0) * S] = v.x; dst[(l0 + 1) * S] = v.y; dst[(l0 + 2) * S] = v.z; dst[(l0 + 3) * S] = v.w;
-    }
-    lds_sync();                        // (slots past d are never read: GUARD skips them)
-    const bool eda = a.eda && a.state_in;
-    for (int u = 0; u < 8; ++u) {
-        const int o = blockIdx.x * 32 + wave * 8 + u;
-        if (o >= a.rd) break;
-        const float * __restrict__ w = a.w_down + (int64_t) o * a.d + lane;
-        float wv[NI];
+    const int nt = min(RD_T, a.T - t0), d = GUARD ? a.d : 64 * NI;
+    // staging item (tt, j4, ln): x[lane ln + 64 (4 j4 + c)], c < 4, as one 16-byte LDS store; every
+    // load is issued before the first store
+    {
+        float4 v[PER];
 #pragma unroll
-        for (int j = 0; j < NI; ++j) wv[j] = !GUARD || lane + 64 * j < a.d ? w[64 * j] : 0.0f;
-        const float b = a.b_down[o];
-        const float ev = eda ? a.eda[o] : 0.0f;
-        for (int tt = 0; tt < nt; ++tt) {
-            const int t = t0 + tt;
-            const float st = eda ? a.state_in[(int64_t) t * a.rd + o] * ev : 0.0f;
-            const float * xr = xs_t + ((size_t) tt * 64 + lane) * S;
-            float acc = 0.0f;
+        for (int u = 0; u < PER; ++u) {
+            const int idx = tid + 256 * u, ln = idx & 63, j4 = (idx >> 6) % (NI / 4), tt = (idx >> 6) / (NI / 4);
+            const float * src = a.x + (int64_t) (t0 + min(tt, nt - 1)) * d + ln + 256 * j4;
+            float e[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) e[c] = !GUARD || ln + 64 * (4 * j4 + c) < d ? src[64 * c] : 0.0f;
+            v[u] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int idx = tid + 256 * u, ln = idx & 63, j4 = (idx >> 6) % (NI / 4), tt = (idx >> 6) / (NI / 4);
+            *(float4 *) (xs_t + (tt * 64 + ln) * S + 4 * j4) = v[u];
+        }
+    }
+    lds_sync();
+    const bool eda = a.eda && a.state_in;
+#pragma unroll 1
+    for (int g = 0; g < 8 / OB; ++g) {
+        const int o0 = blockIdx.x * 32 + wave * 8 + g * OB;
+        float wv[OB][NI], b[OB];
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob) {
+            const float * __restrict__ w = a.w_down + (int64_t) (o0 + ob) * d + lane;
+#pragma unroll
+            for (int j = 0; j < NI; ++j) wv[ob][j] = !GUARD || lane + 64 * j < d ? w[64 * j] : 0.0f;
+            b[ob] = a.b_down[o0 + ob];
+        }
+        // the state terms of the group's (token, output) pairs, lane tt * OB + ob, read back by readlane
+        float st_l = 0.0f;
+        if (eda && lane < RD_T * OB) {
+            const int o = o0 + lane % OB;
+            st_l = a.state_in[(int64_t) (t0 + min(lane / OB, nt - 1)) * a.rd + o] * a.eda[o];
+        }
+#pragma unroll 2
+        for (int tt = 0; tt < RD_T; ++tt) {
+            const int t = t0 + min(tt, nt - 1);
+            const float * xr = xs_t + (tt * 64 + lane) * S;
+            float acc[OB];
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) acc[ob] = 0.0f;
 #pragma unroll
             for (int j4 = 0; j4 < NI / 4; ++j4) {
                 const float4 xv = *(const float4 *) (xr + 4 * j4);
@@ -1893,12 +1915,19 @@ __global__ void __launch_bounds__(256) k_router_down_t(RouterArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
                     const int j = 4 * j4 + jj;
-                    if (!GUARD || lane + 64 * j < a.d) acc = __builtin_fmaf(wv[j], xx[jj], acc);
+                    if (!GUARD || lane + 64 * j < d) {
+#pragma unroll
+                        for (int ob = 0; ob < OB; ++ob) acc[ob] = __builtin_fmaf(wv[ob][j], xx[jj], acc[ob]);
+                    }
                 }
             }
-            float v = wave_tree_f(acc) + b;
-            if (eda) v = v + st;
-            if (lane == 0) a.rh[(int64_t) t * a.rd + o] = v;
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) {
+                const float st = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, st_l), tt * OB + ob));
+                float v = wave_tree_f(acc[ob]) + b[ob];
+                if (eda) v = v + st;
+                if (lane == 0 && tt < nt) a.rh[(int64_t) t * a.rd + o0 + ob] = v;
+            }
         }
     }
 }
@@ -2047,66 +2076,11 @@ __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const fl
     }
 }
 
-// One token's router tail for router_dim = 8 * NM (<= 128 outputs per layer). Every global load of
-// the block is issued at entry, the state row first: the norm waits only for it, and the three MLP
-// matrices, the biases and the mask arrive while it runs.
-template <int NM>
-__device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
-    const int rd = a.rd, E = a.E;
-    float * s_x = sm_rt;                        // [rd]
-    float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
-    float * s_l = s_y + max(rd, 64);            // [E]
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float rh[4], nw[4], sb[4], mk[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = lane + 64 * j;
-        rh[j] = i < rd ? a.rh[(int64_t) t * rd + i] : 0.0f;
-        nw[j] = i < rd ? a.norm_w[i] : 0.0f;
-    }
-    // the small vectors before the three matrices: loads complete in issue order, so a layer that
-    // needs its bias waits only for the loads issued before it
-    float b0[4], b2[4], blg[4], bmk[4];
-    rt_bias(a.b0, rd, b0);
-    rt_bias(a.b2, rd, b2);
-    rt_bias(a.logit_bias, E, blg);
-    rt_bias(a.mask, E, bmk);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = lane + 64 * j;
-        sb[j] = i < E ? a.sc_bias[i] : 0.0f;
-        mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
-    }
-    const int ldw = rd + 4;
-    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
-    __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w0t, ldw, rd, w0);
-    __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w2t, ldw, rd, w2);
-    __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w4t, ldw, E, w4);
-    // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
-    if (wave == 0) {
-        double part = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
-        const double ss = wave_tree_d(part);
-        const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = lane + 64 * j;
-            if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
-        }
-    }
-    lds_sync();                               // s_x holds the normalised state
-    rt_layer<0, NM>(w0, s_x, rd, s_y, b0, b0, false, false);
-    lds_sync();
-    rt_layer<0, NM>(w2, s_y, rd, s_x, b2, b2, false, false);
-    lds_sync();
-    rt_layer<1, NM>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
-    lds_sync();
-    if (wave != 0) return;
-    // softmax (own exp, double tree sum) + selection scores
+// softmax (own exp, double tree sum), selection scores and top-k of token t's logits s_l, in wave 0
+// (s_y: >= 64 floats of scratch)
+__device__ __forceinline__ void router_select(const RouterArgs & a, int t, int E, const float * s_l, float * s_y,
+                                              const float (&sb)[4], const float (&mk)[4]) {
+    const int lane = threadIdx.x & 63;
     float lg[4], pr[4], sc[4];
     float mx = -__builtin_inff();
 #pragma unroll
@@ -2183,14 +2157,94 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
     }
 }
 
-// one block per token; a single wave per SIMD suffices (16-ish blocks), so the three weight
-// matrices can all be register-resident
+// The router tail for router_dim = 8 * NM (<= 128 outputs per layer): token blockIdx.x (LOOP false:
+// one block per token, decode steps) or tokens blockIdx.x, blockIdx.x + gridDim.x, ... (LOOP: wide
+// passes, the three MLP matrices loaded once per block and kept in registers). Every global load of
+// the block is issued at entry, the first state row first: the norm waits only for it, and the
+// matrices, the biases and the mask arrive while it runs; with LOOP each further token's state row is
+// requested a token ahead.
+template <int NM, bool LOOP>
+__device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
+    const int rd = a.rd, E = a.E;
+    float * s_x = sm_rt;                        // [rd]
+    float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
+    float * s_l = s_y + max(rd, 64);            // [E]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float rh_n[4], nw[4], sb[4], mk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane + 64 * j;
+        rh_n[j] = i < rd ? a.rh[(int64_t) blockIdx.x * rd + i] : 0.0f;
+        nw[j] = i < rd ? a.norm_w[i] : 0.0f;
+    }
+    // the small vectors before the three matrices: loads complete in issue order, so a layer that
+    // needs its bias waits only for the loads issued before it
+    float b0[4], b2[4], blg[4], bmk[4];
+    rt_bias(a.b0, rd, b0);
+    rt_bias(a.b2, rd, b2);
+    rt_bias(a.logit_bias, E, blg);
+    rt_bias(a.mask, E, bmk);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane + 64 * j;
+        sb[j] = i < E ? a.sc_bias[i] : 0.0f;
+        mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
+    }
+    const int ldw = rd + 4;
+    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w0t, ldw, rd, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w2t, ldw, rd, w2);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM>(a.w4t, ldw, E, w4);
+    for (int t = blockIdx.x; t < a.T; t += gridDim.x) {
+        float rh[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rh[j] = rh_n[j];
+        const int tn = t + (int) gridDim.x;
+        if (LOOP && tn < a.T) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = lane + 64 * j;
+                rh_n[j] = i < rd ? a.rh[(int64_t) tn * rd + i] : 0.0f;
+            }
+        }
+        if (LOOP && t != (int) blockIdx.x) lds_sync();  // the previous token's top-k has read s_y
+        // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
+        if (wave == 0) {
+            double part = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
+            const double ss = wave_tree_d(part);
+            const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = lane + 64 * j;
+                if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
+            }
+        }
+        lds_sync();                               // s_x holds the normalised state
+        rt_layer<0, NM>(w0, s_x, rd, s_y, b0, b0, false, false);
+        lds_sync();
+        rt_layer<0, NM>(w2, s_y, rd, s_x, b2, b2, false, false);
+        lds_sync();
+        rt_layer<1, NM>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
+        lds_sync();
+        if (wave == 0) router_select(a, t, E, s_l, s_y, sb, mk);
+        if (!LOOP) break;
+    }
+}
+
+// grid: one block per token (decode steps) or up to one per CU with a token loop (LOOP, wide passes);
+// a single wave per SIMD, so the three weight matrices can all be register-resident
+template <bool LOOP>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
     switch (a.rd) {                                  // router_dim in {32, 64, 128} (host-checked)
-        case 32:  router_tail_body<4>(a, sm_rt); break;
-        case 64:  router_tail_body<8>(a, sm_rt); break;
-        default:  router_tail_body<16>(a, sm_rt); break;
+        case 32:  router_tail_body<4, LOOP>(a, sm_rt); break;
+        case 64:  router_tail_body<8, LOOP>(a, sm_rt); break;
+        default:  router_tail_body<16, LOOP>(a, sm_rt); break;
     }
 }
 
