@@ -1676,7 +1676,7 @@ __global__ void __launch_bounds__(256) k_attn_tile_f32(AttnArgs a, const int4 * 
         // P.V: lane = dim pair, rows in order
 #pragma unroll
         for (int h = 0; h < GRP; ++h) {
-            if (lane >= NP) break;
+            if (lane >= NP) continue;
             float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll 16
             for (int r = 0; r < ATT_CH; ++r) {
