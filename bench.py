@@ -354,9 +354,9 @@ def type_name(t):
 def gateup_kernel_of(bulk):
     from zonos2_amd.configs import TYPE_NAMES
     w = TYPE_NAMES[bulk]
-    if w in ("Q4_K", "Q8_0"):
+    if w in ("Q4_K", "Q8_0", "Q6_K"):
         return f"k_gemv_mfma<{w}, DUAL> grouped expert gate/up + SwiGLU"
-    return f"k_gemv_rows<{w}> grouped expert gate and up"
+    return f"k_gemm_f16<DUAL> grouped expert gate/up + SwiGLU"
 
 
 

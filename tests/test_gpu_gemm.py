@@ -5,7 +5,8 @@ dense FFN block (dense gate/up/down GEMMs) and an MoE block (32 experts top-4, g
 
 Q4_K: every Q4_K matmul folds a row's superblocks in order with the same operations
 (fma(dx, fma(d, isum, -dmin * msum), acc)); F16: every F16 matmul runs on k_gemm_f16 (wide or narrow
-tiles), the same chain of f16 MFMA products per row. So a row's logits and K/V are the same bits in a
+tiles), the same chain of f16 MFMA products per row. Q6_K: the expert matmuls run on the 16-row MFMA
+GEMV (8-route passes) at every width, the dense ones on the 64-row tile GEMV. So a row's logits and K/V are the same bits in a
 96-column step and in 16-column steps, and a prompt prefilled in 200-row chunks equals one prefilled
 in 16-row chunks. The wide step is held to the oracle layer by layer (teacher-forced, full bar)."""
 import dataclasses
@@ -41,7 +42,7 @@ def _ctx(cfg, model, lens, cap):
     return m, ctx, om, okv
 
 
-@pytest.mark.parametrize("bulk", [configs.Q4_K, configs.F16], ids=["q4_k", "f16"])
+@pytest.mark.parametrize("bulk", [configs.Q4_K, configs.F16, configs.Q6_K], ids=["q4_k", "f16", "q6_k"])
 def test_wide_step_gemm_equals_narrow_steps_and_oracle(bulk):
     cfg, model = _cut(bulk, 61)
     rng = np.random.default_rng(62)

@@ -303,9 +303,76 @@ int upload_mat_m16(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mat
     return Z2H_OK;
 }
 
+// Q6_K expert matrices in the 16-row MFMA layout (k_gemv_mfma<WF_Q6_K>): per (16-row group, 256-column
+// unit) 3360 B = two 1 KiB low-nibble chunks and one 1 KiB high-bit chunk (16 bytes per lane,
+// lane-major), then the 16 rows' int8 scales (16 B each) and f16 d (2 B each). Lane l = (k-slice
+// q = l/16, row r = l%16) owns elements 32m + 8q + j (j < 8) of each 32-element chunk m of the
+// superblock, as 6-bit unsigned values v (the GGUF value + 32): low dword m byte j = (v_j & 15) |
+// (v_{4+j} & 15) << 4; high dword m/2 byte j = h(v_j, m) | h(v_{4+j}, m) << 2 | h(v_j, m+1) << 4 |
+// h(v_{4+j}, m+1) << 6 for even m, h = bits 4-5.
+int upload_mat_m16q6(z2h_model * mdl, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+    constexpr int UB = 3360;
+    if (K % 256) return seterr(mdl, Z2H_EINVAL, "K-quant row not a multiple of 256");
+    dm.type = Z2H_Q6_K; dm.m16 = true; dm.rows = (int) rows; dm.K = (int) K; dm.nsb = (int) (K / 256);
+    dm.tiles = (int) ((rows + 15) / 16); dm.n_mats = n_mats;
+    dm.mat_bytes = (int64_t) dm.tiles * dm.nsb * UB;
+    const int64_t rb = z2::row_bytes(Z2H_Q6_K, K);
+    std::vector<uint8_t> out((size_t) dm.mat_bytes * n_mats, 0);
+    auto do_groups = [&](int64_t g0, int64_t g1) {
+        for (int64_t gg = g0; gg < g1; ++gg) {
+            const int e = (int) (gg / dm.tiles), g = (int) (gg % dm.tiles);
+            uint8_t * mat = out.data() + (size_t) e * dm.mat_bytes;
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = (int64_t) g * 16 + r;
+                if (row >= rows) break;
+                const uint8_t * rp = src + ((int64_t) e * rows + row) * rb;
+                for (int sb = 0; sb < dm.nsb; ++sb) {
+                    const uint8_t * blk = rp + 210 * sb;             // ql[128] qh[64] scales[16] d
+                    uint8_t v[256];
+                    for (int n = 0; n < 2; ++n) {
+                        const uint8_t * ql = blk + 64 * n, * qh = blk + 128 + 32 * n;
+                        for (int l = 0; l < 32; ++l) {
+                            v[128 * n + l]      = (uint8_t) ((ql[l] & 15) | ((qh[l] & 3) << 4));
+                            v[128 * n + l + 32] = (uint8_t) ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4));
+                            v[128 * n + l + 64] = (uint8_t) ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4));
+                            v[128 * n + l + 96] = (uint8_t) ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4));
+                        }
+                    }
+                    uint8_t * unit = mat + ((size_t) g * dm.nsb + sb) * UB;
+                    for (int q = 0; q < 4; ++q) {
+                        const int lane = 16 * q + r;
+                        uint32_t lo[8] = {0}, hi[4] = {0};
+                        for (int m = 0; m < 8; ++m)
+                            for (int j = 0; j < 4; ++j) {
+                                const uint32_t e0 = v[32 * m + 8 * q + j], e1 = v[32 * m + 8 * q + 4 + j];
+                                lo[m] |= ((e0 & 15u) | ((e1 & 15u) << 4)) << (8 * j);
+                                hi[m >> 1] |= (((e0 >> 4) & 3u) | (((e1 >> 4) & 3u) << 2)) << (8 * j + 4 * (m & 1));
+                            }
+                        std::memcpy(unit + (size_t) lane * 16, lo, 16);
+                        std::memcpy(unit + (size_t) (64 + lane) * 16, lo + 4, 16);
+                        std::memcpy(unit + (size_t) (128 + lane) * 16, hi, 16);
+                    }
+                    std::memcpy(unit + 3072 + 16 * r, blk + 192, 16);
+                    std::memcpy(unit + 3328 + 2 * r, blk + 208, 2);
+                }
+            }
+        }
+    };
+    const int64_t total = (int64_t) n_mats * dm.tiles;
+    const int nth = (int) std::max<int64_t>(1, std::min<int64_t>(16, total / 64));
+    std::vector<std::thread> th;
+    for (int i = 0; i < nth; ++i) th.emplace_back([&, i] { do_groups(total * i / nth, total * (i + 1) / nth); });
+    for (auto & t : th) t.join();
+    if (int rc = dalloc(mdl, &dm.w, out.size(), mdl->bytes_w)) return rc;
+    HIPM(hipMemcpy(dm.w, out.data(), out.size(), hipMemcpyHostToDevice));
+    return Z2H_OK;
+}
+
 // Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the device layout: the 16-row
-// MFMA layout for Q4_K / Q8_0, the 64-row tiles for Q6_K / F16.
-int upload_mat(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+// MFMA layout for Q4_K / Q8_0 and for Q6_K expert matrices, the 64-row tiles for other Q6_K and F16.
+int upload_mat(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm,
+               bool experts = false) {
+    if (type == Z2H_Q6_K && experts) return upload_mat_m16q6(mdl, K, rows, n_mats, src, dm);
     if (type == Z2H_Q4_K || type == Z2H_Q8_0) {
         if (type == Z2H_Q4_K && K % 256) return seterr(mdl, Z2H_EINVAL, "K-quant row not a multiple of 256");
         if (type == Z2H_Q8_0 && K % 32) return seterr(mdl, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
@@ -593,7 +660,9 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     if (m0.m16) {
         // grouped: ROWS = MT_G routes per pass (an expert serves at most n_tok routes); dense: all
         // MT tokens of a chunk per pass, so each weight tile is read once
-        const int rows = a.grouped && !a.r_perm ? MT_G : MT;   // large (sorted) batches: full 16-route MFMA passes
+        // large (sorted) batches: full 16-route MFMA passes; Q6_K (experts only) always 8-route passes
+        if (m0.type == Z2H_Q6_K && !a.grouped) return seterr(ctx, Z2H_EINVAL, "Q6_K 16-row layout is for expert matrices");
+        const int rows = (a.grouped && !a.r_perm) || m0.type == Z2H_Q6_K ? MT_G : MT;
         const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
         const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
@@ -617,6 +686,8 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         if (m0.type == Z2H_Q4_K) {
             if (rows == MT_G) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
+        } else if (m0.type == Z2H_Q6_K) {
+            if (dual) MM16(WF_Q6_K, true, MT_G); else MM16(WF_Q6_K, false, MT_G);
         } else {
             if (rows == MT_G) { if (dual) MM16(WF_Q8_0, true, MT_G); else MM16(WF_Q8_0, false, MT_G); }
             else { if (dual) MM16(WF_Q8_0, true, MT); else MM16(WF_Q8_0, false, MT); }
@@ -1091,6 +1162,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
+    LDS_ATTR((k_gemv_mfma<WF_Q6_K, false, MT_G, m16fmt<WF_Q6_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q6_K, true, MT_G, m16fmt<WF_Q6_K>::GPF>))
     LDS_ATTR((k_router_down_t<4, false>)) LDS_ATTR((k_router_down_t<8, false>)) LDS_ATTR((k_router_down_t<16, false>))
     LDS_ATTR((k_router_down_t<32, false>)) LDS_ATTR((k_router_down_t<64, false>))
     LDS_ATTR((k_router_down_t<4, true>)) LDS_ATTR((k_router_down_t<8, true>)) LDS_ATTR((k_router_down_t<16, true>))
@@ -1319,9 +1391,9 @@ int z2h_model_upload_tensor(z2h_model * mdl, const char * name_c, int type, cons
         if (rest == "ffn_up.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_up);
         if (rest == "ffn_gate.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_gate);
         if (rest == "ffn_down.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_down);
-        if (rest == "ffn_gate_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps);
-        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps); }
-        if (rest == "ffn_down_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps);
+        if (rest == "ffn_gate_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps, true);
+        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps, true); }
+        if (rest == "ffn_down_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps, true);
         copy_host();
         if (rest == "attn_norm.weight") return upload_f32(mdl, t, &ly.attn_norm, hp.n_embd);
         if (rest == "ffn_norm.weight") return upload_f32(mdl, t, &ly.ffn_norm, hp.n_embd);

@@ -901,19 +901,31 @@ template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constex
                                      static constexpr int GPF = 1; static constexpr int GWPE = 5; };
 template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int WPE = 4;
                                      static constexpr int GPF = 1; static constexpr int GWPE = 4; };
+// Q6_K (expert matrices only, 8-route passes): 3360 B = 2 x 1 KiB low-nibble chunks + 1 KiB of high
+// bits + 16 x 16 B scales + 16 x f16 d; qs[3].x holds the d pair of the lane's row
+template <> struct m16fmt<WF_Q6_K> { static constexpr int QS = 4; static constexpr int BYTES = 3360; static constexpr int WPE = 4;
+                                     static constexpr int GPF = 1; static constexpr int GWPE = 4; };
 constexpr int MT = 16;                  // tokens per MFMA pass
 
 // token rows per pass of the m16 kernels: grouped expert launches stage up to MT_G routes (an
 // expert serves ~2 at 16 requests), dense launches all MT tokens so each weight tile is read once
 constexpr int MT_G = 8;
+constexpr int M16_ZERO = 256;           // Q6_K: zero bytes ahead of the staged rows (the idle halves of the A operand)
 __host__ __device__ inline size_t gemv_mfma_lds_bytes(int wf, int K, int rows) {
     const size_t KP = (size_t) K + 16;
     if (wf == WF_Q4_K) return rows * KP + (size_t) rows * (K / 32) * 4 + (size_t) rows * (K / 256) * 4 + 64;
+    if (wf == WF_Q6_K) return M16_ZERO + rows * KP + (size_t) rows * (K / 16) * 4 + (size_t) rows * (K / 256) * 4 + 64;
     return rows * KP + (size_t) rows * (K / 32) * 4 + 64;
 }
 
 template <int WF>
 __device__ __forceinline__ void m16_load(const uint4 * __restrict__ unit, int lane, uint4 (&qs)[m16fmt<WF>::QS], uint4 & hd) {
+    if constexpr (WF == WF_Q6_K) {
+        qs[0] = unit[lane]; qs[1] = unit[64 + lane]; qs[2] = unit[128 + lane];
+        hd = unit[192 + (lane & 15)];                                    // the row's 16 scales
+        qs[3].x = ((const uint32_t *) (unit + 208))[(lane & 15) >> 1];   // d of rows 2i, 2i + 1
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < m16fmt<WF>::QS; ++c) qs[c] = unit[c * 64 + lane];
     hd = unit[m16fmt<WF>::QS * 64 + (lane & 15)];
@@ -982,6 +994,60 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
             acc[i] = __builtin_fmaf(d, (float) sumi[i], -(dmin * S[i]));
             xd[i] = dx[i];
         }
+    } else if constexpr (WF == WF_Q6_K) {
+        // At most 8 token rows, doubled: A slot s < 8 is token s over k-slots 0-15 of a 32-element
+        // chunk (scale group 2m), slot s >= 8 token s - 8 over k-slots 16-31 (group 2m + 1); a lane
+        // whose k-slice lies in the other half feeds zeros (M16_ZERO bytes ahead of the staged rows).
+        // One MFMA then gives both groups' dots, lanes 0-31 group 2m and lanes 32-63 group 2m + 1
+        // for the same tokens. The weights enter unsigned (0..63); the -32 offset is subtracted as
+        // 32 * sum_g sc_g * bsum_g (bsum = the activation's sum over group g), an fp32 16x16x4
+        // product of integers (|sum| < 2^23: exact). The unit value is the Q6_K row kernels':
+        // x = (d * dx) * (float) sum_g sc_g * (dot_g - 32 bsum_g).
+        const int q = lane >> 4, s = lane & 15, par = lane >> 5;
+        const int8_t * arow = (s < 8) == (q < 2) ? sq + min(s & 7, ntm1) * KP + sb * 256 + 8 * q : sq - M16_ZERO + 8 * q;
+        long A[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) A[m] = *(const long *) (arow + 32 * m);
+        const float * bsf = (const float *) sbs2 + min(s & 7, ntm1) * (K / 16) + sb * 16 + q;   // group 4 kb + q
+        float bs4[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) bs4[kb] = bsf[4 * kb];
+        float dx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dx[i] = sdx[min(4 * (q & 1) + i, ntm1) * nsb + sb];
+        const uint32_t L[8] = {qs[0].x, qs[0].y, qs[0].z, qs[0].w, qs[1].x, qs[1].y, qs[1].z, qs[1].w};
+        const uint32_t H[4] = {qs[2].x, qs[2].y, qs[2].z, qs[2].w};
+        v4i_t C[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const uint32_t hh = H[m >> 1] >> (4 * (m & 1));
+            const uint32_t b0 = (L[m] & 0x0f0f0f0fu) | ((hh << 4) & 0x30303030u);          // elements 0-3
+            const uint32_t b1 = ((L[m] >> 4) & 0x0f0f0f0fu) | ((hh << 2) & 0x30303030u);   // elements 4-7
+            C[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m], (long) (((uint64_t) b1 << 32) | b0), zero, 0, 0, 0);
+        }
+        // bias term: sum_g sc_g * bsum_g over the 16 groups as four k = 4 products
+        const uint32_t scw[4] = {hd.x, hd.y, hd.z, hd.w};
+        v4f_t S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const float scg = (float) __builtin_amdgcn_sbfe(scw[kb], 8 * q, 8);
+            S = __builtin_amdgcn_mfma_f32_16x16x4f32(bs4[kb], scg, S, 0, 0, 0);
+        }
+        int sumi[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int scm = __builtin_amdgcn_sbfe(scw[m >> 1], 16 * (m & 1) + 8 * par, 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scm, C[m][i]);      // |products| < 2^24
+        }
+        const uint32_t dd = qs[3].x >> (16 * (s & 1));
+        const float d = h2f(dd & 0xffffu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tot = sumi[i] + up32_i(sumi[i]) - 32 * (int) S[i];        // lanes 0-31
+            acc[i] = (d * dx[i]) * (float) tot;
+            xd[i] = 1.0f;
+        }
     } else {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -1008,8 +1074,9 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
 // (no index division); every global load of a batch is issued before its first LDS store, and
 // indices past the end re-read the last item, so the loads issue without branches. mid() runs once,
 // after the first batch's loads are issued: the caller's weight loads go there, behind the staging
-// loads, so the stores wait only for the staging data (loads complete in issue order).
-template <int AF, int RB, class TokFn, class MidFn>
+// loads, so the stores wait only for the staging data (loads complete in issue order). BS16 (Q6_K):
+// the Q8_K sums of 16 as floats [rows][K/16] in place of the sums of 32.
+template <int AF, int RB, bool BS16 = false, class TokFn, class MidFn>
 __device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2, float * sdx,
                                           MidFn mid) {
     const int tid = threadIdx.x, KP = K + 16;
@@ -1041,8 +1108,15 @@ __device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok,
                 if (row >= nt) break;
                 if (c < per) *(u32x4 *) (sq + row * KP + c * 16) = v[rr];
                 if (c < ns) {
-                    if constexpr (AF == ACT_Q8_K) sbs2[row * ns + c] = (int) (int16_t) (sv[rr] & 0xffffu) + (int) (int16_t) (sv[rr] >> 16);
-                    else sdx[row * ns + c] = __builtin_bit_cast(float, sv[rr]);
+                    if constexpr (BS16) {
+                        float * f = (float *) sbs2 + row * (K / 16) + 2 * c;
+                        f[0] = (float) (int16_t) (sv[rr] & 0xffffu);
+                        f[1] = (float) (int16_t) (sv[rr] >> 16);
+                    } else if constexpr (AF == ACT_Q8_K) {
+                        sbs2[row * ns + c] = (int) (int16_t) (sv[rr] & 0xffffu) + (int) (int16_t) (sv[rr] >> 16);
+                    } else {
+                        sdx[row * ns + c] = __builtin_bit_cast(float, sv[rr]);
+                    }
                 }
                 if (AF == ACT_Q8_K && c < nd) sdx[row * nd + c] = dv[rr];
             }
@@ -1063,6 +1137,7 @@ template <int WF, bool DUAL, int ROWS, int PF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE,
                                                                           PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE)))
 k_gemv_mfma(GemvArgs a) {
+    static_assert(WF != WF_Q6_K || ROWS <= 8, "Q6_K doubles at most 8 token rows into the 16 MFMA slots");
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1073,10 +1148,12 @@ k_gemv_mfma(GemvArgs a) {
     const int g16 = blockIdx.x * 4 + wave;
     const int nm = DUAL ? 1 : a.n_mats;
     const int m = blockIdx.z % nm, pass = blockIdx.z / nm;
-    int8_t * sq = (int8_t *) smem;                                   // [ROWS][K+16]
-    int * sbs2 = (int *) (smem + ROWS * KP);                         // Q4_K: [ROWS][K/32] sums of 32
-    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32))  // Q4_K: [ROWS][K/256]
+    constexpr int ZB = WF == WF_Q6_K ? M16_ZERO : 0;                  // Q6_K: zero bytes, then the rows
+    int8_t * sq = (int8_t *) smem + ZB;                              // [ROWS][K+16]
+    int * sbs2 = (int *) (smem + ZB + ROWS * KP);                    // Q4_K: [ROWS][K/32] sums of 32; Q6_K: float [ROWS][K/16]
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / (WF == WF_Q6_K ? 16 : 32)))  // [ROWS][K/256]
                                  : (float *) (smem + ROWS * KP);     // Q8_0: [ROWS][K/32]
+    if (WF == WF_Q6_K && tid < M16_ZERO / 16) ((uint4 *) smem)[tid] = make_uint4(0, 0, 0, 0);
     int n_items, c0, e = 0;
     const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
@@ -1104,7 +1181,7 @@ k_gemv_mfma(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF, (PF > 1 ? 4 : 2)>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+    m16_stage<AF, (PF > 1 ? 4 : 2), WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
 #pragma unroll
         for (int j = 0; j < PF; ++j)
             if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
