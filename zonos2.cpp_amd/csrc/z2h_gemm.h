@@ -24,7 +24,9 @@
 namespace z2d {
 
 constexpr int GM_T = 64;                 // token (route) rows per block tile
-constexpr int GM_QP = 256 + 16;          // LDS pitch of a row's int8 superblock (bytes)
+constexpr int GM_QP = 256 + 8;           // LDS pitch of a row's int8 superblock (bytes): 66 dwords, so the
+                                         // 8-byte A reads of 16 rows fall in distinct banks
+constexpr int GM_SP = 10;                // LDS pitch (dwords) of a row's 8 sub-block sum pairs (same reason)
 constexpr int GM_HP = 256 + 8;           // LDS pitch of a row's f16 superblock (halves)
 
 typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
@@ -101,7 +103,7 @@ __device__ __forceinline__ float gemm_epi(const GemmArgs & a, float y, int it) {
 // ------------------------------------------------------------------ Q4_K x Q8_K
 // One superblock of GM_T activation rows in registers (4 x 16 B of values, 2 sub-block sum pairs and
 // the block scale per thread), then in LDS: values [GM_T][GM_QP], sums as f16 pairs (hi, lo) with
-// sum = 64 * hi + lo [GM_T][8], scales [GM_T].
+// sum = 64 * hi + lo [GM_T][GM_SP], scales [GM_T].
 struct GmQ8K { u32x4 v[4]; uint32_t s[2]; float dx; };
 
 __device__ __forceinline__ void gm_load_q8k(GmQ8K & st, const ActBuf & act, int K, int sb, const int * s_row) {
@@ -124,14 +126,16 @@ __device__ __forceinline__ void gm_store_q8k(const GmQ8K & st, int8_t * sq, uint
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = tid + 256 * j, r = i >> 4, c = i & 15;
-        *(u32x4 *) (sq + r * GM_QP + c * 16) = st.v[j];
+        uint2 * dst = (uint2 *) (sq + r * GM_QP + c * 16);            // 8-byte aligned rows
+        dst[0] = make_uint2(st.v[j].x, st.v[j].y);
+        dst[1] = make_uint2(st.v[j].z, st.v[j].w);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int i = tid + 256 * j;
         const int s = (int) (int16_t) (st.s[j] & 0xffffu) + (int) (int16_t) (st.s[j] >> 16);   // |s| <= 32 * 128
         const _Float16 hi = (_Float16) (s >> 6), lo = (_Float16) (s & 63);
-        ss[i] = (uint32_t) __builtin_bit_cast(uint16_t, hi) | ((uint32_t) __builtin_bit_cast(uint16_t, lo) << 16);
+        ss[(i >> 3) * GM_SP + (i & 7)] = (uint32_t) __builtin_bit_cast(uint16_t, hi) | ((uint32_t) __builtin_bit_cast(uint16_t, lo) << 16);
     }
     if (tid < GM_T) sdx[tid] = st.dx;
 }
@@ -175,12 +179,12 @@ __device__ __forceinline__ void gm_prep_q4k(const uint4 & q0, const uint4 & q1, 
 
 // grid: x = row blocks (DUAL: 4 16-row groups of gate and up, each wave one group of both; else 8
 // groups, two per wave), y = tile slots. 256 threads; dynamic LDS gemm_q4k_lds().
-__host__ __device__ inline size_t gemm_q4k_lds() { return 2 * (size_t) (GM_T * GM_QP + GM_T * 8 * 4 + GM_T * 4) + 2 * GM_T * 4; }
+__host__ __device__ inline size_t gemm_q4k_lds() { return 2 * (size_t) (GM_T * GM_QP + GM_T * GM_SP * 4 + GM_T * 4) + 2 * GM_T * 4; }
 
 template <bool DUAL>
 __global__ void __launch_bounds__(256, 2) k_gemm_q4k(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    constexpr int BUF = GM_T * GM_QP + GM_T * 8 * 4 + GM_T * 4;
+    constexpr int BUF = GM_T * GM_QP + GM_T * GM_SP * 4 + GM_T * 4;
     int * s_row = (int *) (smem + 2 * BUF), * s_out = s_row + GM_T;
     int e, c0, nt;
     if (!gemm_tile<GM_T>(a, blockIdx.y, e, c0, nt)) return;
@@ -201,7 +205,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q4k(GemmArgs a) {
     lds_sync();                                                      // s_row
     GmQ8K st;
     gm_load_q8k(st, a.act, K, 0, s_row);
-    gm_store_q8k(st, (int8_t *) smem, (uint32_t *) (smem + GM_T * GM_QP), (float *) (smem + GM_T * GM_QP + GM_T * 32));
+    gm_store_q8k(st, (int8_t *) smem, (uint32_t *) (smem + GM_T * GM_QP), (float *) (smem + GM_T * GM_QP + GM_T * GM_SP * 4));
     lds_sync();
     float acc[2][GM_T / 16][4] = {};
     const v4i_t zi = {0, 0, 0, 0};
@@ -211,7 +215,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q4k(GemmArgs a) {
         char * buf = smem + (sb & 1) * BUF;
         const int8_t * sq = (const int8_t *) buf;
         const uint32_t * ss = (const uint32_t *) (buf + GM_T * GM_QP);
-        const float * sdx = (const float *) (buf + GM_T * GM_QP + GM_T * 32);
+        const float * sdx = (const float *) (buf + GM_T * GM_QP + GM_T * GM_SP * 4);
         const bool more = sb + 1 < a.nsb;
         if (more) gm_load_q8k(st, a.act, K, sb + 1, s_row);
         if (has) {
@@ -229,7 +233,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q4k(GemmArgs a) {
                     const uint2 lo = *(const uint2 *) (ap + 64 * s), hi = *(const uint2 *) (ap + 64 * s + 32);
                     A[s] = (v4i_t) {(int) lo.x, (int) lo.y, (int) hi.x, (int) hi.y};
                 }
-                const v4h_t As = *(const v4h_t *) (ss + r * 8 + 2 * q);
+                const v4h_t As = *(const v4h_t *) (ss + r * GM_SP + 2 * q);
                 const v4f_t dx = *(const v4f_t *) (sdx + ts * 16 + 4 * q);
 #pragma unroll
                 for (int x = 0; x < 2; ++x) {
@@ -251,7 +255,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q4k(GemmArgs a) {
         }
         if (more) {
             char * nb = smem + ((sb + 1) & 1) * BUF;
-            gm_store_q8k(st, (int8_t *) nb, (uint32_t *) (nb + GM_T * GM_QP), (float *) (nb + GM_T * GM_QP + GM_T * 32));
+            gm_store_q8k(st, (int8_t *) nb, (uint32_t *) (nb + GM_T * GM_QP), (float *) (nb + GM_T * GM_QP + GM_T * GM_SP * 4));
         }
         lds_sync();
     }
