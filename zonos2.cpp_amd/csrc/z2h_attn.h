@@ -183,7 +183,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fa(AttnArgs a) {
             const int r = i / (HD / 8), c = i % (HD / 8);
             *(uint4 *) &s_k[r * KP + 8 * c] = k0 + r <= cmax ? kr[j] : make_uint4(0, 0, 0, 0);
         }
-        if (HD < HDP)                                                 // zero dims [HD, HDP) of the K rows
+        if constexpr (HD < HDP)                                       // zero dims [HD, HDP) of the K rows
             for (int i = tid; i < FA_SEG * (HDP - HD) / 8; i += 256) {
                 const int r = i / ((HDP - HD) / 8), c = i % ((HDP - HD) / 8);
                 *(uint4 *) &s_k[r * KP + HD + 8 * c] = make_uint4(0, 0, 0, 0);
