@@ -660,9 +660,12 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     if (m0.m16) {
         // grouped: ROWS = MT_G routes per pass (an expert serves at most n_tok routes); dense: all
         // MT tokens of a chunk per pass, so each weight tile is read once
-        // large (sorted) batches: full 16-route MFMA passes; Q6_K (experts only) always 8-route passes
+        // grouped: 8-route passes for small batches (an expert serves ~2 routes at 16 requests), 16-route
+        // passes from 128 routes (popular experts re-read their weights per pass; Q6_K keeps 8-route
+        // passes there, its second product set costing more than the re-reads) and for the sorted
+        // table; dense: 16-token passes
         if (m0.type == Z2H_Q6_K && !a.grouped) return seterr(ctx, Z2H_EINVAL, "Q6_K 16-row layout is for expert matrices");
-        const int rows = (a.grouped && !a.r_perm) || m0.type == Z2H_Q6_K ? MT_G : MT;
+        const int rows = a.grouped && !a.r_perm && (a.n_tok * a.k < 128 || m0.type == Z2H_Q6_K) ? MT_G : MT;
         const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
         const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
@@ -687,7 +690,8 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
             if (rows == MT_G) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
         } else if (m0.type == Z2H_Q6_K) {
-            if (dual) MM16(WF_Q6_K, true, MT_G); else MM16(WF_Q6_K, false, MT_G);
+            if (rows == MT_G) { if (dual) MM16(WF_Q6_K, true, MT_G); else MM16(WF_Q6_K, false, MT_G); }
+            else { if (dual) MM16(WF_Q6_K, true, MT); else MM16(WF_Q6_K, false, MT); }
         } else {
             if (rows == MT_G) { if (dual) MM16(WF_Q8_0, true, MT_G); else MM16(WF_Q8_0, false, MT_G); }
             else { if (dual) MM16(WF_Q8_0, true, MT); else MM16(WF_Q8_0, false, MT); }
@@ -1163,6 +1167,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q6_K, false, MT_G, m16fmt<WF_Q6_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q6_K, true, MT_G, m16fmt<WF_Q6_K>::GPF>))
+    LDS_ATTR((k_gemv_mfma<WF_Q6_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q6_K, true, MT, 1>))
     LDS_ATTR((k_router_down_t<4, false>)) LDS_ATTR((k_router_down_t<8, false>)) LDS_ATTR((k_router_down_t<16, false>))
     LDS_ATTR((k_router_down_t<32, false>)) LDS_ATTR((k_router_down_t<64, false>))
     LDS_ATTR((k_router_down_t<4, true>)) LDS_ATTR((k_router_down_t<8, true>)) LDS_ATTR((k_router_down_t<16, true>))

@@ -943,7 +943,7 @@ __device__ __forceinline__ void m16_fold(float & acc, float x, float xd) {
     if constexpr (WF == WF_Q4_K) acc = __builtin_fmaf(xd, x, acc);
     else acc = acc + x;
 }
-template <int WF>
+template <int WF, int ROWS = 16>
 __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], const uint4 & hd, int sb, int K, int lane,
                                          const int8_t * sq, const int * sbs2, const float * sdx, int nsb, int ntm1, float (&acc)[4],
                                          float (&xd)[4]) {
@@ -995,56 +995,82 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
             xd[i] = dx[i];
         }
     } else if constexpr (WF == WF_Q6_K) {
-        // At most 8 token rows, doubled: A slot s < 8 is token s over k-slots 0-15 of a 32-element
+        // Token rows doubled, 8 per product: A slot s < 8 is token s over k-slots 0-15 of a 32-element
         // chunk (scale group 2m), slot s >= 8 token s - 8 over k-slots 16-31 (group 2m + 1); a lane
         // whose k-slice lies in the other half feeds zeros (M16_ZERO bytes ahead of the staged rows).
         // One MFMA then gives both groups' dots, lanes 0-31 group 2m and lanes 32-63 group 2m + 1
-        // for the same tokens. The weights enter unsigned (0..63); the -32 offset is subtracted as
-        // 32 * sum_g sc_g * bsum_g (bsum = the activation's sum over group g), an fp32 16x16x4
-        // product of integers (|sum| < 2^23: exact). The unit value is the Q6_K row kernels':
-        // x = (d * dx) * (float) sum_g sc_g * (dot_g - 32 bsum_g).
+        // for the same tokens. ROWS = 16: a second product set (tokens 8-15) on the same weight
+        // operands, its totals in lanes 32-63. The weights enter unsigned (0..63); the -32 offset is
+        // subtracted as 32 * sum_g sc_g * bsum_g (bsum = the activation's sum over group g), an fp32
+        // 16x16x4 product of integers (|sum| < 2^23: exact). The unit value is the Q6_K row
+        // kernels': x = (d * dx) * (float) sum_g sc_g * (dot_g - 32 bsum_g).
+        constexpr int NH = ROWS > 8 ? 2 : 1;
         const int q = lane >> 4, s = lane & 15, par = lane >> 5;
-        const int8_t * arow = (s < 8) == (q < 2) ? sq + min(s & 7, ntm1) * KP + sb * 256 + 8 * q : sq - M16_ZERO + 8 * q;
-        long A[8];
+        const bool on = (s < 8) == (q < 2);
+        long A[NH][8];
+        float bs4[NH][4];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) A[m] = *(const long *) (arow + 32 * m);
-        const float * bsf = (const float *) sbs2 + min(s & 7, ntm1) * (K / 16) + sb * 16 + q;   // group 4 kb + q
-        float bs4[4];
+        for (int hh = 0; hh < NH; ++hh) {
+            const int tok = min(8 * hh + (s & 7), ntm1);
+            const int8_t * arow = on ? sq + tok * KP + sb * 256 + 8 * q : sq - M16_ZERO + 8 * q;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) bs4[kb] = bsf[4 * kb];
+            for (int m = 0; m < 8; ++m) A[hh][m] = *(const long *) (arow + 32 * m);
+            const float * bsf = (const float *) sbs2 + tok * (K / 16) + sb * 16 + q;   // group 4 kb + q
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) bs4[hh][kb] = bsf[4 * kb];
+        }
         float dx[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dx[i] = sdx[min(4 * (q & 1) + i, ntm1) * nsb + sb];
+        for (int i = 0; i < 4; ++i) dx[i] = sdx[min((NH == 2 ? 4 * q : 4 * (q & 1)) + i, ntm1) * nsb + sb];
         const uint32_t L[8] = {qs[0].x, qs[0].y, qs[0].z, qs[0].w, qs[1].x, qs[1].y, qs[1].z, qs[1].w};
         const uint32_t H[4] = {qs[2].x, qs[2].y, qs[2].z, qs[2].w};
-        v4i_t C[8];
+        const uint32_t scw[4] = {hd.x, hd.y, hd.z, hd.w};
+        int sumi[NH][4];
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sumi[hh][i] = 0;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const uint32_t hh = H[m >> 1] >> (4 * (m & 1));
-            const uint32_t b0 = (L[m] & 0x0f0f0f0fu) | ((hh << 4) & 0x30303030u);          // elements 0-3
-            const uint32_t b1 = ((L[m] >> 4) & 0x0f0f0f0fu) | ((hh << 2) & 0x30303030u);   // elements 4-7
-            C[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[m], (long) (((uint64_t) b1 << 32) | b0), zero, 0, 0, 0);
+            const uint32_t hb = H[m >> 1] >> (4 * (m & 1));
+            const uint32_t b0 = (L[m] & 0x0f0f0f0fu) | ((hb << 4) & 0x30303030u);          // elements 0-3
+            const uint32_t b1 = ((L[m] >> 4) & 0x0f0f0f0fu) | ((hb << 2) & 0x30303030u);   // elements 4-7
+            const long B = (long) (((uint64_t) b1 << 32) | b0);
+            const int scm = __builtin_amdgcn_sbfe(scw[m >> 1], 16 * (m & 1) + 8 * par, 8);
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+                const v4i_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[hh][m], B, zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sumi[hh][i] += __mul24(scm, C[i]);   // |products| < 2^24
+            }
         }
         // bias term: sum_g sc_g * bsum_g over the 16 groups as four k = 4 products
-        const uint32_t scw[4] = {hd.x, hd.y, hd.z, hd.w};
-        v4f_t S = {0.0f, 0.0f, 0.0f, 0.0f};
+        v4f_t S[NH];
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) S[hh] = (v4f_t) {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const float scg = (float) __builtin_amdgcn_sbfe(scw[kb], 8 * q, 8);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(bs4[kb], scg, S, 0, 0, 0);
-        }
-        int sumi[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const int scm = __builtin_amdgcn_sbfe(scw[m >> 1], 16 * (m & 1) + 8 * par, 8);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sumi[i] += __mul24(scm, C[m][i]);      // |products| < 2^24
+            for (int hh = 0; hh < NH; ++hh) S[hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(bs4[hh][kb], scg, S[hh], 0, 0, 0);
         }
         const uint32_t dd = qs[3].x >> (16 * (s & 1));
         const float d = h2f(dd & 0xffffu);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int tot = sumi[i] + up32_i(sumi[i]) - 32 * (int) S[i];        // lanes 0-31
+            int tot;
+            float sb32;
+            if constexpr (NH == 1) {
+                tot = sumi[0][i] + up32_i(sumi[0][i]);                           // lanes 0-31
+                sb32 = S[0][i];
+            } else {
+                // lanes 0-31: tokens 0-7 (own even groups + lane + 32's odd ones); lanes 32-63:
+                // tokens 8-15 (own odd groups + lane - 32's even ones), one lane swap for both
+                const auto sw = __builtin_amdgcn_permlane32_swap((unsigned) sumi[0][i], (unsigned) sumi[1][i], false, false);
+                tot = par ? sumi[1][i] + (int) sw[0] : sumi[0][i] + (int) sw[1];
+                sb32 = par ? S[1][i] : S[0][i];
+            }
+            tot -= 32 * (int) sb32;
             acc[i] = (d * dx[i]) * (float) tot;
             xd[i] = 1.0f;
         }
@@ -1137,7 +1163,7 @@ template <int WF, bool DUAL, int ROWS, int PF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE,
                                                                           PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE)))
 k_gemv_mfma(GemvArgs a) {
-    static_assert(WF != WF_Q6_K || ROWS <= 8, "Q6_K doubles at most 8 token rows into the 16 MFMA slots");
+    static_assert(WF != WF_Q6_K || ROWS == 8 || ROWS == 16, "Q6_K: one or two doubled 8-row product sets");
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1196,7 +1222,7 @@ k_gemv_mfma(GemvArgs a) {
             const int u = c + j;
             if (u < U) {
                 float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
-                m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
+                m16_unit<WF, ROWS>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
                 if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
                 if (!DUAL || u < nsb) {
 #pragma unroll
