@@ -303,7 +303,7 @@ int upload_mat_m16(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mat
     return Z2H_OK;
 }
 
-// Q6_K expert matrices in the 16-row MFMA layout (k_gemv_mfma<WF_Q6_K>): per (16-row group, 256-column
+// Q6_K matrices in the 16-row MFMA layout (k_gemv_mfma / k_gemv_split<WF_Q6_K>): per (16-row group, 256-column
 // unit) 3360 B = two 1 KiB low-nibble chunks and one 1 KiB high-bit chunk (16 bytes per lane,
 // lane-major), then the 16 rows' int8 scales (16 B each) and f16 d (2 B each). Lane l = (k-slice
 // q = l/16, row r = l%16) owns elements 32m + 8q + j (j < 8) of each 32-element chunk m of the
@@ -369,10 +369,9 @@ int upload_mat_m16q6(z2h_model * mdl, int64_t K, int64_t rows, int n_mats, const
 }
 
 // Repack n_mats matrices of `rows` x K (GGUF rows, contiguous) into the device layout: the 16-row
-// MFMA layout for Q4_K / Q8_0 and for Q6_K expert matrices, the 64-row tiles for other Q6_K and F16.
-int upload_mat(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm,
-               bool experts = false) {
-    if (type == Z2H_Q6_K && experts) return upload_mat_m16q6(mdl, K, rows, n_mats, src, dm);
+// MFMA layouts for Q4_K / Q8_0 / Q6_K, the 64-row tiles for F16.
+int upload_mat(z2h_model * mdl, int type, int64_t K, int64_t rows, int n_mats, const uint8_t * src, DevMat & dm) {
+    if (type == Z2H_Q6_K) return upload_mat_m16q6(mdl, K, rows, n_mats, src, dm);
     if (type == Z2H_Q4_K || type == Z2H_Q8_0) {
         if (type == Z2H_Q4_K && K % 256) return seterr(mdl, Z2H_EINVAL, "K-quant row not a multiple of 256");
         if (type == Z2H_Q8_0 && K % 32) return seterr(mdl, Z2H_EINVAL, "Q8_0 row not a multiple of 32");
@@ -664,7 +663,6 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         // passes from 128 routes (popular experts re-read their weights per pass; Q6_K keeps 8-route
         // passes there, its second product set costing more than the re-reads) and for the sorted
         // table; dense: 16-token passes
-        if (m0.type == Z2H_Q6_K && !a.grouped) return seterr(ctx, Z2H_EINVAL, "Q6_K 16-row layout is for expert matrices");
         const int rows = a.grouped && !a.r_perm && (a.n_tok * a.k < 128 || m0.type == Z2H_Q6_K) ? MT_G : MT;
         const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
         const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
@@ -678,6 +676,7 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
 #define SPL(W_, D_, R_) KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
 #define SPL_R(W_, D_) do { if (a.grouped) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
             if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
+            else if (m0.type == Z2H_Q6_K) { if (dual) SPL_R(WF_Q6_K, true); else SPL_R(WF_Q6_K, false); }
             else { if (dual) SPL_R(WF_Q8_0, true); else SPL_R(WF_Q8_0, false); }
 #undef SPL_R
 #undef SPL
@@ -1168,6 +1167,8 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q6_K, false, MT_G, m16fmt<WF_Q6_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q6_K, true, MT_G, m16fmt<WF_Q6_K>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q6_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q6_K, true, MT, 1>))
+    LDS_ATTR((k_gemv_split<WF_Q6_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q6_K, true, MT>))
+    LDS_ATTR((k_gemv_split<WF_Q6_K, false, MT_G>)) LDS_ATTR((k_gemv_split<WF_Q6_K, true, MT_G>))
     LDS_ATTR((k_router_down_t<4, false>)) LDS_ATTR((k_router_down_t<8, false>)) LDS_ATTR((k_router_down_t<16, false>))
     LDS_ATTR((k_router_down_t<32, false>)) LDS_ATTR((k_router_down_t<64, false>))
     LDS_ATTR((k_router_down_t<4, true>)) LDS_ATTR((k_router_down_t<8, true>)) LDS_ATTR((k_router_down_t<16, true>))
@@ -1396,9 +1397,9 @@ int z2h_model_upload_tensor(z2h_model * mdl, const char * name_c, int type, cons
         if (rest == "ffn_up.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_up);
         if (rest == "ffn_gate.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_gate);
         if (rest == "ffn_down.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], 1, src, ly.ffn_down);
-        if (rest == "ffn_gate_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps, true);
-        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps, true); }
-        if (rest == "ffn_down_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps, true);
+        if (rest == "ffn_gate_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.gate_exps);
+        if (rest == "ffn_up_exps.weight") { ly.E = (int) t.ne[2]; return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.up_exps); }
+        if (rest == "ffn_down_exps.weight") return upload_mat(mdl, type, t.ne[0], t.ne[1], (int) t.ne[2], src, ly.down_exps);
         copy_host();
         if (rest == "attn_norm.weight") return upload_f32(mdl, t, &ly.attn_norm, hp.n_embd);
         if (rest == "ffn_norm.weight") return upload_f32(mdl, t, &ly.ffn_norm, hp.n_embd);

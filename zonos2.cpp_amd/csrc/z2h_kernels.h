@@ -901,7 +901,7 @@ template <> struct m16fmt<WF_Q4_K> { static constexpr int QS = 2; static constex
                                      static constexpr int GPF = 1; static constexpr int GWPE = 5; };
 template <> struct m16fmt<WF_Q8_0> { static constexpr int QS = 4; static constexpr int BYTES = 4352; static constexpr int WPE = 4;
                                      static constexpr int GPF = 1; static constexpr int GWPE = 4; };
-// Q6_K (expert matrices only, 8-route passes): 3360 B = 2 x 1 KiB low-nibble chunks + 1 KiB of high
+// Q6_K (8 or 16 token rows per pass): 3360 B = 2 x 1 KiB low-nibble chunks + 1 KiB of high
 // bits + 16 x 16 B scales + 16 x f16 d; qs[3].x holds the d pair of the lane's row
 template <> struct m16fmt<WF_Q6_K> { static constexpr int QS = 4; static constexpr int BYTES = 3360; static constexpr int WPE = 4;
                                      static constexpr int GPF = 1; static constexpr int GWPE = 4; };
@@ -1267,11 +1267,14 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     __shared__ int s_wcnt[4];
     __shared__ int s_tok[ROWS];
     __shared__ float s_x[4 * SPLIT_UMAX][4][64];                    // [unit][token of the lane][lane]
+    static_assert(WF != WF_Q6_K || ROWS == 8 || ROWS == 16, "Q6_K: one or two doubled 8-row product sets");
     const int K = a.nsb * 256, KP = K + 16, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g16 = blockIdx.x;
-    int8_t * sq = (int8_t *) smem;
-    int * sbs2 = (int *) (smem + ROWS * KP);
-    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / 32)) : (float *) (smem + ROWS * KP);
+    constexpr int ZB = WF == WF_Q6_K ? M16_ZERO : 0;                  // Q6_K: zero bytes, then the rows
+    int8_t * sq = (int8_t *) smem + ZB;
+    int * sbs2 = (int *) (smem + ZB + ROWS * KP);                    // Q4_K: sums of 32; Q6_K: float sums of 16
+    float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / (WF == WF_Q6_K ? 16 : 32))) : (float *) (smem + ROWS * KP);
+    if (WF == WF_Q6_K && tid < M16_ZERO / 16) ((uint4 *) smem)[tid] = make_uint4(0, 0, 0, 0);
     int e = 0, m = 0, n_items, c0;
     const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
@@ -1301,7 +1304,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF, 4>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+    m16_stage<AF, 4, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
 #pragma unroll
         for (int j = 0; j < SPLIT_UMAX; ++j)
             if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
@@ -1312,7 +1315,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         const int u = wave + 4 * j;
         if (u < U) {
             float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
-            m16_unit<WF>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
+            m16_unit<WF, ROWS>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
 #pragma unroll
             for (int i = 0; i < 4; ++i) s_x[u][i][lane] = t4[i];
         }
