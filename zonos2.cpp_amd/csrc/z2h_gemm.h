@@ -101,20 +101,20 @@ __device__ __forceinline__ float gemm_epi(const GemmArgs & a, float y, int it) {
 }
 
 // ------------------------------------------------------------------ Q4_K x Q8_K
-// One superblock of GM_T activation rows in registers (4 x 16 B of values, 2 sub-block sum pairs and
-// the block scale per thread), then in LDS: values [GM_T][GM_QP], sums as f16 pairs (hi, lo) with
-// sum = 64 * hi + lo [GM_T][GM_SP], scales [GM_T].
-struct GmQ8K { u32x4 v[4]; uint32_t s[2]; float dx; };
+// One superblock of GM_T activation rows in registers (GM_T / 16 x 16 B of values, GM_T / 32 sub-block
+// sum pairs and the block scale per thread), then in LDS: values [GM_T][GM_QP], sums as f16 pairs
+// (hi, lo) with sum = 64 * hi + lo [GM_T][GM_SP], scales [GM_T].
+struct GmQ8K { u32x4 v[GM_T / 16]; uint32_t s[GM_T / 32]; float dx; };
 
 __device__ __forceinline__ void gm_load_q8k(GmQ8K & st, const ActBuf & act, int K, int sb, const int * s_row) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < GM_T / 16; ++j) {
         const int i = tid + 256 * j, r = i >> 4, c = i & 15;
         st.v[j] = *(const u32x4 *) (act.q + (int64_t) s_row[r] * K + sb * 256 + c * 16);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < GM_T / 32; ++j) {
         const int i = tid + 256 * j, r = i >> 3, jj = i & 7;
         st.s[j] = *(const uint32_t *) (act.bs + (int64_t) s_row[r] * (K / 16) + sb * 16 + 2 * jj);
     }
@@ -124,14 +124,14 @@ __device__ __forceinline__ void gm_load_q8k(GmQ8K & st, const ActBuf & act, int 
 __device__ __forceinline__ void gm_store_q8k(const GmQ8K & st, int8_t * sq, uint32_t * ss, float * sdx) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < GM_T / 16; ++j) {
         const int i = tid + 256 * j, r = i >> 4, c = i & 15;
         uint2 * dst = (uint2 *) (sq + r * GM_QP + c * 16);            // 8-byte aligned rows
         dst[0] = make_uint2(st.v[j].x, st.v[j].y);
         dst[1] = make_uint2(st.v[j].z, st.v[j].w);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < GM_T / 32; ++j) {
         const int i = tid + 256 * j;
         const int s = (int) (int16_t) (st.s[j] & 0xffffu) + (int) (int16_t) (st.s[j] >> 16);   // |s| <= 32 * 128
         const _Float16 hi = (_Float16) (s >> 6), lo = (_Float16) (s & 63);
