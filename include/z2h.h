@@ -200,10 +200,13 @@ int z2h_set_logit_bias(z2h_ctx * ctx, int layer, const float * bias);
 /* Frame sampling on the device, for callers that keep the logits in HBM. It follows the reference's
  * per-codebook sampler (src/zonos2-sampler.cpp:16-77, called per slot by zonos2_slot_sample,
  * src/zonos2-graph.cpp:843-870) with the random generator left on the host: column i, codebook cb
- * applies the repetition penalty over hist, temperature, top-k (logit descending, ties to the lower
- * id), softmax (float exp terms over a double sum), top-p, min-p and draws at u * kept mass along the
- * candidates, where u[i][cb] is the canonical double in [0, 1) that the host sampler's
- * std::uniform_real_distribution would take from its mt19937 (std::generate_canonical<double, 53>).
+ * applies the repetition penalty over hist, temperature, top-k (logit descending), softmax (float
+ * exp terms over a double sum), top-p, min-p and draws at u * kept mass along the candidates, with
+ * equal logits and probabilities in the orders that the reference's std::partial_sort / std::sort
+ * (GCC 11 libstdc++) give them. u[i][cb] is the canonical double in [0, 1) that the host sampler's
+ * std::uniform_real_distribution would take from its mt19937 (std::generate_canonical<double, 53>);
+ * it is not used where the kept mass is 0 (for finite logits: min_p > 1), where the host sampler
+ * takes no draw.
  * The exp terms are exp(x) computed in double and rounded to float, so a draw can differ from the
  * host sampler's (glibc expf) only where the two roundings differ by an ulp and u falls between the
  * two cumulative sums.

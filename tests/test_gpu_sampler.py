@@ -3,7 +3,9 @@
 With the same logits, settings, histories and canonical draws u, the device codes equal orc_sample's
 with exp_mode 1 (exp in double rounded to float, the device's arithmetic) on every draw; against
 exp_mode 0 (std::exp on floats, the reference's arithmetic) they agree on all but a rare draw that
-falls between the two roundings' cumulative sums. Logits are distinct random values (no ties)."""
+falls between the two roundings' cumulative sums. Logits are distinct random values, except in the
+tied-logits test (equal keys in the orders of std::partial_sort / std::sort on both sides); min_p > 1
+keeps no mass, so the code is the most probable candidate whatever u is."""
 import numpy as np
 import pytest
 
@@ -20,6 +22,7 @@ SETTINGS = [
     dict(temperature=0.0, top_k=50, top_p=0.0, min_p=0.0, rep_penalty=1.3, rep_codebooks=9, greedy=0),
     dict(temperature=1.0, top_k=0, top_p=0.0, min_p=0.0, rep_penalty=1.2, rep_codebooks=8, greedy=1),
     dict(temperature=1.3, top_k=1025, top_p=0.95, min_p=0.02, rep_penalty=1.1, rep_codebooks=9, greedy=0),
+    dict(temperature=1.0, top_k=40, top_p=0.8, min_p=1.5, rep_penalty=1.2, rep_codebooks=8, greedy=0),   # kept mass 0
 ]
 
 
@@ -61,6 +64,47 @@ def test_device_sampler_matches_oracle(ctx):
         agree0 += int((got == _oracle_codes(lg, sp, u, hist, hlen, 0)).sum())
         total += got.size
     assert agree0 >= total - 2
+
+
+def test_device_sampler_tied_logits_and_zero_mass(ctx):
+    """Equal keys: logits on a coarse grid (runs of equal logits, so equal probabilities, at the top-k
+    cut, at the top and inside the walk) and logits one ulp apart (distinct logits whose exp terms
+    round to equal probabilities). The reference orders such keys as std::partial_sort / std::sort
+    leave them, and so does orc_sample (it calls them): device == oracle on every code. With
+    min_p > 1 (no kept mass) the code is the first id of the probability order for any u."""
+    import torch
+    cfg, wl, c = ctx
+    n, ncb, av = wl.n_slots, cfg.n_codebooks, cfg.audio_vocab
+    rng = np.random.default_rng(13)
+    no_hist = np.zeros((n, ncb, 1), np.int32), np.zeros((n, ncb), np.int32)
+    tied = SETTINGS + [dict(temperature=1.0, top_k=1, top_p=0.0, min_p=0.0, rep_penalty=1.0, rep_codebooks=0, greedy=0),
+                       dict(temperature=1.0, top_k=3, top_p=0.5, min_p=0.0, rep_penalty=1.0, rep_codebooks=0, greedy=0)]
+    for trial in range(12):
+        print(f"tied trial {trial}", flush=True)
+        if trial % 2 == 0:
+            lg = (np.round(rng.standard_normal((n, ncb, av)) * 2.0) * 0.5).astype(np.float32)
+        else:
+            lg = (rng.standard_normal((n, ncb, av)) * 0.3).astype(np.float32)
+            src = rng.integers(0, av, (n, ncb, av // 2))
+            dst = rng.integers(0, av, (n, ncb, av // 2))
+            for i in range(n):
+                for cb in range(ncb):
+                    lg[i, cb, dst[i, cb]] = np.nextafter(lg[i, cb, src[i, cb]], np.float32(np.inf))
+        sp = [tied[(trial + i) % len(tied)] for i in range(n)]
+        u = rng.random((n, ncb))
+        d = torch.from_numpy(lg).cuda()
+        torch.cuda.synchronize()
+        got = c.sample(sp, u, d_logits=d.data_ptr())
+        np.testing.assert_array_equal(got, _oracle_codes(lg, sp, u, *no_hist, 1))
+    zero = SETTINGS[-1]
+    assert zero["min_p"] > 1
+    lg = (rng.standard_normal((n, ncb, av)) * 2.5).astype(np.float32)
+    d = torch.from_numpy(lg).cuda()
+    torch.cuda.synchronize()
+    a = c.sample([zero] * n, rng.random((n, ncb)), d_logits=d.data_ptr())
+    b = c.sample([zero] * n, rng.random((n, ncb)), d_logits=d.data_ptr())
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(a, lg.argmax(axis=2))                 # temperature 1, no history
 
 
 def test_device_sampler_on_step_logits(ctx):

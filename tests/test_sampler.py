@@ -94,6 +94,7 @@ CASES = [
     dict(seed=7, greedy=0, temperature=0.8, top_k=0, top_p=0.9, min_p=0.0, rep_penalty=1.0, rep_window=50, rep_codebooks=8),
     dict(seed=123, greedy=0, temperature=1.0, top_k=20, top_p=0.7, min_p=0.05, rep_penalty=1.5, rep_window=4, rep_codebooks=3),
     dict(seed=5, greedy=1, temperature=1.0, top_k=0, top_p=0.0, min_p=0.0, rep_penalty=1.2, rep_window=50, rep_codebooks=8),
+    dict(seed=9, greedy=0, temperature=1.0, top_k=40, top_p=0.8, min_p=1.5, rep_penalty=1.2, rep_window=50, rep_codebooks=8),
 ]
 
 
@@ -119,3 +120,34 @@ def test_sampler_draws_match_restatement(kat_bin, tmp_path, case):
     assert got == want
     if sp["greedy"]:
         assert want[0] == [int(np.argmax(lg[0, cb])) for cb in range(ncb)]
+
+
+@pytest.mark.parametrize("min_p", [1.0, np.nextafter(np.float32(1.0), np.float32(2.0)), 1.5, 7.0])
+def test_kept_mass_is_zero_exactly_above_min_p_one(min_p):
+    """The sampler takes no draw where the kept mass is 0. For finite logits the most probable
+    candidate survives top-p, and min-p drops it exactly when min_p > 1 (min_p * p_max rounds above
+    p_max for every float above 1): the rule the device sampling glue uses to skip a draw."""
+    rng = np.random.default_rng(3)
+    sp = dict(seed=4, greedy=0, temperature=0.9, top_k=0, top_p=0.6, min_p=float(np.float32(min_p)),
+              rep_penalty=1.0, rep_window=8, rep_codebooks=0)
+    for trial in range(40):
+        ps = PySampler(sp, 1, 257)
+        lg = (rng.standard_normal(257) * (0.01 if trial % 2 else 4.0)).astype(np.float32)
+        before = ps.bg.state["state"]["pos"]
+        code = ps.sample(lg, 0)
+        drew = ps.bg.state["state"]["pos"] != before
+        assert drew == (not np.float32(min_p) > 1), (trial, min_p)
+        if not drew:
+            assert code == int(np.argmax(lg))
+
+
+def test_library_orders_match_std_sorts(tmp_path):
+    """The device sampler's exact orders for equal keys (csrc/z2h_stdorder.h) against this
+    toolchain's std::partial_sort and std::sort, the calls of the reference sampler
+    (src/zonos2-sampler.cpp:40-58): identical permutations on keys with many equal values and on
+    McIlroy-adversary inputs that drive the introsort into its heap-sort fallback."""
+    out = tmp_path / "stdorder_kat"
+    subprocess.run(["g++", "-O2", "-std=c++17", str(ROOT / "tests" / "native" / "stdorder_kat.cpp"), "-o", str(out)],
+                   check=True)
+    r = subprocess.run([str(out), "4000"], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout

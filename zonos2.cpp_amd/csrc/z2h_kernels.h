@@ -32,6 +32,7 @@
 // plane, F16 512 B = 32 chunks.
 #pragma once
 #include "z2h_common.h"
+#include "z2h_stdorder.h"
 
 namespace z2d {
 
@@ -2371,9 +2372,12 @@ __host__ __device__ inline size_t sample_lds_bytes(int av, int np2) { return (si
 // greedy = first maximum of the raw logits; otherwise the repetition penalty (each history occurrence
 // once, in order), temperature, candidates = the top_k ids by logit in descending order (or all ids in
 // id order), p = exp(l - max) over a double sum, top-p along the probability order, min-p against the
-// largest p, and the draw r = u * mass walked along the candidates. The ranking is a bitonic sort of
-// (logit descending, id ascending) over np2 entries in LDS; the order-dependent sums (normaliser, kept
-// mass, the walk) run in one thread in candidate order, as the reference's loops do.
+// largest p, and the draw r = u * mass walked along the candidates (no draw is used where the kept
+// mass is 0: the code is then the first id of the probability order). The ranking is a bitonic sort
+// of (logit descending, id ascending) over np2 entries in LDS; the order-dependent sums (normaliser,
+// kept mass, the walk) run in one thread in candidate order, as the reference's loops do. Where equal
+// logits or probabilities could change the code, the decisions run again on the exact orders of
+// std::partial_sort / std::sort (z2h_order), so the codes are the reference's with ties too.
 __global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
     extern __shared__ __attribute__((aligned(16))) char sm_s[];
     float * s_key = (float *) sm_s;                              // [np2]
@@ -2450,31 +2454,68 @@ __global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
     for (int j = tid; j < n; j += 256) s_p[j] = (float) ((double) s_p[j] / z);
     __syncthreads();
     if (tid != 0) return;
-    auto rank = [&](int r) { return topk ? r : s_idx[r]; };
-    if (sp.top_p > 0.0f && sp.top_p < 1.0f) {
-        double c = 0.0; bool reached = false;
-        for (int r = 0; r < n; ++r) {
-            const int j = rank(r);
-            if (reached) s_keep[j] = 0;
-            c += (double) s_p[j];
-            if (c >= (double) sp.top_p) reached = true;
+    // The decisions run along two orders: the candidate order (the walk) and the probability order
+    // (top-p, the min-p reference, the fallback). Where keys are distinct, the bitonic orders are the
+    // reference's. Where equal keys make the reference's order depend on std::partial_sort /
+    // std::sort, the position each decision lands on holds the same value in both orders, but it
+    // can hold another id. So the first pass flags the cases where an equal-key neighbour could swap
+    // the outcome: a top-p cut inside a run of equal probabilities, a fallback whose top probability
+    // is shared, or a code whose logit is shared (top-k). Those cases run again on the library's
+    // exact orders (z2h_order, one thread).
+    const double top_p = sp.top_p > 0.0f && sp.top_p < 1.0f ? (double) sp.top_p : -1.0;
+    auto decide = [&](auto cand_at, auto rank_at, bool flag_ties, bool & tie) -> int {
+        tie = false;
+        if (top_p > 0.0) {
+            double c = 0.0; bool reached = false;
+            for (int r = 0; r < n; ++r) {
+                const int j = rank_at(r);
+                if (reached) s_keep[j] = 0;
+                c += (double) s_p[j];
+                if (!reached && c >= top_p) {
+                    reached = true;
+                    if (flag_ties && r + 1 < n && s_p[rank_at(r + 1)] == s_p[j]) tie = true;
+                }
+            }
         }
-    }
-    const int j0 = rank(0);
-    if (sp.min_p > 0.0f) {
-        const float floor_p = sp.min_p * s_p[j0];
-        for (int j = 0; j < n; ++j) if (s_p[j] < floor_p) s_keep[j] = 0;
-    }
-    double mass = 0.0;
-    for (int j = 0; j < n; ++j) mass += s_keep[j] ? (double) s_p[j] : 0.0;
-    int code = cand(j0);
-    if (mass > 0.0) {
-        const double r = a.u[(size_t) col * a.ncb + cb] * (mass - 0.0) + 0.0;
-        double acc = 0.0;
-        for (int j = 0; j < n; ++j) {
-            acc += s_keep[j] ? (double) s_p[j] : 0.0;
-            if (acc >= r) { code = cand(j); break; }
+        const int j0 = rank_at(0);
+        if (sp.min_p > 0.0f) {
+            const float floor_p = sp.min_p * s_p[j0];
+            for (int j = 0; j < n; ++j) if (s_p[j] < floor_p) s_keep[j] = 0;
         }
+        double mass = 0.0;
+        for (int j = 0; j < n; ++j) mass += s_keep[j] ? (double) s_p[j] : 0.0;
+        // equal logits around candidate position j (top-k: the candidate order is the logit order)
+        auto shared_logit = [&](int j) {
+            return topk && ((j > 0 && s_key[j - 1] == s_key[j]) || (j + 1 < av && s_key[j + 1] == s_key[j]));
+        };
+        if (mass > 0.0) {
+            const double r = a.u[(size_t) col * a.ncb + cb] * (mass - 0.0) + 0.0;
+            double acc = 0.0;
+            for (int j = 0; j < n; ++j) {
+                acc += s_keep[j] ? (double) s_p[j] : 0.0;
+                if (acc >= r) {
+                    if (flag_ties && shared_logit(j)) tie = true;
+                    return cand_at(j);
+                }
+            }
+        }
+        if (flag_ties && ((n > 1 && s_p[rank_at(1)] == s_p[j0]) || shared_logit(j0))) tie = true;
+        return cand_at(j0);
+    };
+    bool tie = false;
+    int code = decide([&](int j) { return topk ? s_idx[j] : j; }, [&](int r) { return topk ? r : s_idx[r]; }, true, tie);
+    if (tie) {
+        // the library's orders: ids by logit (std::partial_sort over all ids, first top_k kept), then
+        // candidate positions by probability (std::sort); s_key is free now and holds the id arrays
+        int * ord = (int *) s_key;
+        if (topk) {
+            for (int i = 0; i < av; ++i) ord[i] = i;
+            z2h_order::partial_order(ord, n, av, [&](int x, int y) { return s_lg[x] > s_lg[y]; });
+            for (int j = 0; j < n; ++j) s_idx[j] = ord[j];
+        }
+        for (int j = 0; j < n; ++j) { ord[j] = j; s_keep[j] = 1; }
+        z2h_order::sort_order(ord, n, [&](int x, int y) { return s_p[x] > s_p[y]; });
+        code = decide([&](int j) { return topk ? s_idx[j] : j; }, [&](int r) { return ord[r]; }, false, tie);
     }
     *out = code;
 }

@@ -347,8 +347,11 @@ bool zonos2_batch_sample(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *>
             for (const int t : h) hist[((size_t) c * ncb + cb) * cap + j++] = t;
             hlen[(size_t) c * ncb + cb] = j;
             // the host sampler's draw: uniform_real_distribution<double>(0, mass) on its mt19937 is
-            // generate_canonical<double, 53> times the mass, taken once per codebook in order
-            if (!smp.sp.greedy)
+            // generate_canonical<double, 53> times the mass, taken once per codebook in order. It
+            // takes none where the kept mass is 0 (src/zonos2-sampler.cpp:70); with finite logits the
+            // largest probability is > 0 and survives top-p, so that happens exactly when min-p
+            // drops it too, min_p > 1 (min_p * p_max rounds above p_max for any float min_p > 1)
+            if (!smp.sp.greedy && !(smp.sp.min_p > 1.0f))
                 u[(size_t) c * ncb + cb] = std::generate_canonical<double, std::numeric_limits<double>::digits>(smp.rng);
         }
     }
