@@ -5,8 +5,9 @@ dense FFN block (dense gate/up/down GEMMs) and an MoE block (32 experts top-4, g
 
 Q4_K: every Q4_K matmul folds a row's superblocks in order with the same operations
 (fma(dx, fma(d, isum, -dmin * msum), acc)); F16: every F16 matmul runs on k_gemm_f16 (wide or narrow
-tiles), the same chain of f16 MFMA products per row. Q6_K: the expert matmuls run on the 16-row MFMA
-GEMV (8-route passes) at every width, the dense ones on the 64-row tile GEMV. So a row's logits and K/V are the same bits in a
+tiles), the same chain of f16 MFMA products per row. Q6_K: every Q6_K matmul runs on the 16-row MFMA
+GEMV at every width (experts in 8- or 16-route passes, dense projections in 16-token passes), each
+row adding its superblocks' (d * dx) * sum in order. So a row's logits and K/V are the same bits in a
 96-column step and in 16-column steps, and a prompt prefilled in 200-row chunks equals one prefilled
 in 16-row chunks. The wide step is held to the oracle layer by layer (teacher-forced, full bar)."""
 import dataclasses
