@@ -1151,6 +1151,60 @@ __device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok,
     }
 }
 
+// m16_stage for the K-split GEMV, whose blocks stage all ROWS tokens of a chunk: the block's 256
+// threads walk the nt x (K/16) items of the chunk in one flat sequence (thread tid takes items tid,
+// tid + 256, ...; rows are not padded to the block width), MAXJ items per thread in flight, so a
+// 16-token chunk of a 2048-wide row takes one round trip instead of one per row batch. Items past the
+// chunk re-read its last row (every load issues without a branch) and are not stored.
+template <int AF, int MAXJ, bool BS16 = false, class TokFn, class MidFn>
+__device__ __forceinline__ void m16_stage_flat(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2,
+                                               float * sdx, MidFn mid) {
+    const int tid = threadIdx.x, KP = K + 16;
+    const int per = K / 16, ns = K / 32, nd = K / 256;
+    const int dq = 256 / per, dr = 256 - dq * per;                   // item i -> i + 256: rows, columns
+    int row = tid / per, c = tid - row * per;
+    bool first = true;
+    for (int base = 0; base < nt * per; base += 256 * MAXJ) {
+        u32x4 v[MAXJ];
+        uint32_t sv[MAXJ];
+        float dv[MAXJ];
+        int rj[MAXJ], cj[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            rj[j] = row; cj[j] = c;
+            const int tr = tok(min(row, nt - 1)), cs = min(c, ns - 1), cd = min(c, nd - 1);
+            v[j] = *(const u32x4 *) (act.q + (int64_t) tr * K + c * 16);
+            if constexpr (AF == ACT_Q8_K) {
+                sv[j] = *(const uint32_t *) (act.bs + (int64_t) tr * (K / 16) + 2 * cs);
+                dv[j] = act.d256[(int64_t) tr * nd + cd];
+            } else {
+                sv[j] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tr * ns + cs]);
+            }
+            row += dq; c += dr;
+            if (c >= per) { c -= per; ++row; }
+        }
+        if (first) { mid(); first = false; }
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int r = rj[j], cc = cj[j];
+            if (r >= nt) continue;
+            *(u32x4 *) (sq + r * KP + cc * 16) = v[j];
+            if (cc < ns) {
+                if constexpr (BS16) {
+                    float * f = (float *) sbs2 + r * (K / 16) + 2 * cc;
+                    f[0] = (float) (int16_t) (sv[j] & 0xffffu);
+                    f[1] = (float) (int16_t) (sv[j] >> 16);
+                } else if constexpr (AF == ACT_Q8_K) {
+                    sbs2[r * ns + cc] = (int) (int16_t) (sv[j] & 0xffffu) + (int) (int16_t) (sv[j] >> 16);
+                } else {
+                    sdx[r * ns + cc] = __builtin_bit_cast(float, sv[j]);
+                }
+            }
+            if (AF == ACT_Q8_K && cc < nd) sdx[r * nd + cc] = dv[j];
+        }
+    }
+}
+
 // grid: x = 16-row group quads, y = expert (grouped) or token chunk of ROWS (dense), z = matrix +
 // n_mats * route pass (grouped: routes [ROWS*pass, ROWS*pass+ROWS) of the expert, so hot experts
 // spread over blocks). DUAL: each wave computes the same 16 rows of two matrices (w[0] = gate,
@@ -1305,7 +1359,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF, 4, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+    m16_stage_flat<AF, 8, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
 #pragma unroll
         for (int j = 0; j < SPLIT_UMAX; ++j)
             if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
@@ -2135,11 +2189,23 @@ __device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, flo
     }
 }
 
-// bias entries of the lane group's outputs g + 32u (u < 4; rows beyond n_out clamp)
-__device__ __forceinline__ void rt_bias(const float * b, int n_out, float (&bv)[4]) {
+// p[i] for i < n, else 0, with the load taken by every lane at a clamped index: a load under a lane
+// or null-pointer condition becomes a branch, and the join after it waits for every load in flight,
+// which would hold back the matrix loads issued after it
+__device__ __forceinline__ float ld_or0(const float * p, int i, int n) {
+    const float v = p[min(i, n - 1)];
+    return i < n ? v : 0.0f;
+}
+// bias entries of the lane group's outputs g + 32u (u < 4; rows beyond n_out clamp); a null b reads
+// fb (>= n_out entries) and gives zeros
+__device__ __forceinline__ void rt_bias(const float * b, const float * fb, int n_out, float (&bv)[4]) {
     const int g = threadIdx.x >> 3;
+    const float * q = b ? b : fb;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) bv[u] = b ? b[min(g + 32 * u, n_out - 1)] : 0.0f;
+    for (int u = 0; u < 4; ++u) {
+        const float v = q[min(g + 32 * u, n_out - 1)];
+        bv[u] = b ? v : 0.0f;
+    }
 }
 
 // y[o] = post(dot(W[o], x)) for the lane group's outputs (n_out <= 128); MODE 0: gelu(dot + b1[u]);
@@ -2281,21 +2347,24 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = lane + 64 * j;
-        rh_n[j] = i < rd ? a.rh[(int64_t) blockIdx.x * rd + i] : 0.0f;
-        nw[j] = i < rd ? a.norm_w[i] : 0.0f;
+        rh_n[j] = ld_or0(a.rh + (int64_t) blockIdx.x * rd, i, rd);
+        nw[j] = ld_or0(a.norm_w, i, rd);
     }
     // the small vectors before the three matrices: loads complete in issue order, so a layer that
-    // needs its bias waits only for the loads issued before it
+    // needs its bias waits only for the loads issued before it (norm_w and sc_bias, never null,
+    // stand in for absent rd- and E-sized vectors)
     float b0[4], b2[4], blg[4], bmk[4];
-    rt_bias(a.b0, rd, b0);
-    rt_bias(a.b2, rd, b2);
-    rt_bias(a.logit_bias, E, blg);
-    rt_bias(a.mask, E, bmk);
+    rt_bias(a.b0, a.norm_w, rd, b0);
+    rt_bias(a.b2, a.norm_w, rd, b2);
+    rt_bias(a.logit_bias, a.sc_bias, E, blg);
+    rt_bias(a.mask, a.sc_bias, E, bmk);
+    const float * mask_or = a.mask ? a.mask : a.sc_bias;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = lane + 64 * j;
-        sb[j] = i < E ? a.sc_bias[i] : 0.0f;
-        mk[j] = i < E && a.mask ? a.mask[i] : 0.0f;
+        sb[j] = ld_or0(a.sc_bias, i, E);
+        const float m = ld_or0(mask_or, i, E);
+        mk[j] = a.mask ? m : 0.0f;
     }
     const int ldw = rd + 4;
     float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
@@ -2312,10 +2381,7 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
         const int tn = t + (int) gridDim.x;
         if (LOOP && tn < a.T) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = lane + 64 * j;
-                rh_n[j] = i < rd ? a.rh[(int64_t) tn * rd + i] : 0.0f;
-            }
+            for (int j = 0; j < 4; ++j) rh_n[j] = ld_or0(a.rh + (int64_t) tn * rd, lane + 64 * j, rd);
         }
         if (LOOP && t != (int) blockIdx.x) lds_sync();  // the previous token's top-k has read s_y
         // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
