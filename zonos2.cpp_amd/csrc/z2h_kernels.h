@@ -1097,65 +1097,13 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
 
 // Stage the encoded activation rows of nt tokens (LDS row tt = token tok(tt)) for the m16 kernels:
 // int8 values [rows][K+16], Q8_K sums of 32 [rows][K/32] and scales [rows][K/256], or Q8_0 scales
-// [rows][K/32]. Rows go in batches of RB with thread tid on 16-byte column item c0 + tid of each row
-// (no index division); every global load of a batch is issued before its first LDS store, and
-// indices past the end re-read the last item, so the loads issue without branches. mid() runs once,
-// after the first batch's loads are issued: the caller's weight loads go there, behind the staging
-// loads, so the stores wait only for the staging data (loads complete in issue order). BS16 (Q6_K):
-// the Q8_K sums of 16 as floats [rows][K/16] in place of the sums of 32.
-template <int AF, int RB, bool BS16 = false, class TokFn, class MidFn>
-__device__ __forceinline__ void m16_stage(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2, float * sdx,
-                                          MidFn mid) {
-    const int tid = threadIdx.x, KP = K + 16;
-    const int per = K / 16, ns = K / 32, nd = K / 256;
-    bool first = true;
-    for (int r0 = 0; r0 < nt; r0 += RB) {
-        int tr[RB];
-#pragma unroll
-        for (int rr = 0; rr < RB; ++rr) tr[rr] = tok(min(r0 + rr, nt - 1));
-        for (int c0 = 0; c0 < per; c0 += 256) {
-            const int c = c0 + tid, cq = min(c, per - 1), cs = min(c, ns - 1), cd = min(c, nd - 1);
-            u32x4 v[RB];
-            uint32_t sv[RB];
-            float dv[RB];
-#pragma unroll
-            for (int rr = 0; rr < RB; ++rr) {
-                v[rr] = *(const u32x4 *) (act.q + (int64_t) tr[rr] * K + cq * 16);
-                if constexpr (AF == ACT_Q8_K) {
-                    sv[rr] = *(const uint32_t *) (act.bs + (int64_t) tr[rr] * (K / 16) + 2 * cs);
-                    dv[rr] = act.d256[(int64_t) tr[rr] * nd + cd];
-                } else {
-                    sv[rr] = __builtin_bit_cast(uint32_t, act.d32[(int64_t) tr[rr] * ns + cs]);
-                }
-            }
-            if (first) { mid(); first = false; }
-#pragma unroll
-            for (int rr = 0; rr < RB; ++rr) {
-                const int row = r0 + rr;
-                if (row >= nt) break;
-                if (c < per) *(u32x4 *) (sq + row * KP + c * 16) = v[rr];
-                if (c < ns) {
-                    if constexpr (BS16) {
-                        float * f = (float *) sbs2 + row * (K / 16) + 2 * c;
-                        f[0] = (float) (int16_t) (sv[rr] & 0xffffu);
-                        f[1] = (float) (int16_t) (sv[rr] >> 16);
-                    } else if constexpr (AF == ACT_Q8_K) {
-                        sbs2[row * ns + c] = (int) (int16_t) (sv[rr] & 0xffffu) + (int) (int16_t) (sv[rr] >> 16);
-                    } else {
-                        sdx[row * ns + c] = __builtin_bit_cast(float, sv[rr]);
-                    }
-                }
-                if (AF == ACT_Q8_K && c < nd) sdx[row * nd + c] = dv[rr];
-            }
-        }
-    }
-}
-
-// m16_stage for the K-split GEMV, whose blocks stage all ROWS tokens of a chunk: the block's 256
-// threads walk the nt x (K/16) items of the chunk in one flat sequence (thread tid takes items tid,
-// tid + 256, ...; rows are not padded to the block width), MAXJ items per thread in flight, so a
-// 16-token chunk of a 2048-wide row takes one round trip instead of one per row batch. Items past the
-// chunk re-read its last row (every load issues without a branch) and are not stored.
+// [rows][K/32]. The block's 256 threads walk the nt x (K/16) 16-byte items in one flat sequence
+// (thread tid takes items tid, tid + 256, ...; rows are not padded to the block width) with MAXJ
+// items per thread in flight, so a chunk of nt * K/16 <= 256 * MAXJ items takes one round trip. Items
+// past the chunk re-read its last row (every load issues without a branch) and are not stored. mid()
+// runs once, after the first MAXJ items' loads are issued: the caller's weight loads go there, behind
+// the staging loads, so the stores wait only for the staging data (loads complete in issue order).
+// BS16 (Q6_K): the Q8_K sums of 16 as floats [rows][K/16] in place of the sums of 32.
 template <int AF, int MAXJ, bool BS16 = false, class TokFn, class MidFn>
 __device__ __forceinline__ void m16_stage_flat(const ActBuf & act, int nt, TokFn tok, int K, int8_t * sq, int * sbs2,
                                                float * sdx, MidFn mid) {
@@ -1262,7 +1210,7 @@ k_gemv_mfma(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage<AF, (PF > 1 ? 4 : 2), WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+    m16_stage_flat<AF, 2, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
 #pragma unroll
         for (int j = 0; j < PF; ++j)
             if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
