@@ -2124,13 +2124,13 @@ __host__ __device__ inline size_t router_tail_lds(int rd, int E) {
     return (size_t) 4 * (2 * rd + (E <= 64 ? 64 : pad4(E)) + 64);
 }
 
-// the lane's weights of outputs g + 32u (u < 4) of a [n_out][ldw] matrix (rows beyond n_out clamp):
+// the lane's weights of outputs g + 32u (u < U) of a [n_out][ldw] matrix (rows beyond n_out clamp):
 // elements [p*NM, p*NM + NM) of each row
-template <int NM>
+template <int NM, int U>
 __device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, float4 (&wv)[4][NM / 4]) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
         const float4 * wr = (const float4 *) (w + (int64_t) min(g + 32 * u, n_out - 1) * ldw + p * NM);
 #pragma unroll
         for (int m = 0; m < NM / 4; ++m) wv[u][m] = wr[m];
@@ -2144,21 +2144,26 @@ __device__ __forceinline__ float ld_or0(const float * p, int i, int n) {
     const float v = p[min(i, n - 1)];
     return i < n ? v : 0.0f;
 }
-// bias entries of the lane group's outputs g + 32u (u < 4; rows beyond n_out clamp); a null b reads
-// fb (>= n_out entries) and gives zeros
+// bias entries of the lane group's outputs g + 32u (u < U; rows beyond n_out clamp, entries u >= U
+// are 0); a null b reads fb (>= n_out entries) and gives zeros
+template <int U>
 __device__ __forceinline__ void rt_bias(const float * b, const float * fb, int n_out, float (&bv)[4]) {
     const int g = threadIdx.x >> 3;
     const float * q = b ? b : fb;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const float v = q[min(g + 32 * u, n_out - 1)];
-        bv[u] = b ? v : 0.0f;
+        if (u < U) {
+            const float v = q[min(g + 32 * u, n_out - 1)];
+            bv[u] = b ? v : 0.0f;
+        } else {
+            bv[u] = 0.0f;
+        }
     }
 }
 
-// y[o] = post(dot(W[o], x)) for the lane group's outputs (n_out <= 128); MODE 0: gelu(dot + b1[u]);
-// MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
-template <int MODE, int NM>
+// y[o] = post(dot(W[o], x)) for the lane group's outputs g + 32u, u < U (n_out <= 32 U); MODE 0:
+// gelu(dot + b1[u]); MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
+template <int MODE, int NM, int U>
 __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const float * x, int n_out, float * y,
                                          const float (&b1)[4], const float (&b2)[4], bool has1, bool has2) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
@@ -2169,7 +2174,7 @@ __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const fl
 #pragma unroll
     for (int m = 0; m < NM / 4; ++m)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             acc[u] = __builtin_fmaf(wv[u][m].x, xr[m].x, acc[u]);
             acc[u] = __builtin_fmaf(wv[u][m].y, xr[m].y, acc[u]);
             acc[u] = __builtin_fmaf(wv[u][m].z, xr[m].z, acc[u]);
@@ -2178,13 +2183,13 @@ __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const fl
     // lane p = 0 of the group ends with ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), the xor
     // butterfly's (4, 2, 1) sum, from DPP row shifts (lane i reads lane i + n of its 16-lane row)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
         acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 4>(acc[u]);
         acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 2>(acc[u]);
         acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 1>(acc[u]);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int o = g + 32 * u;
         if (o >= n_out) break;
         float v = acc[u];                          // the group's sum (valid in lane p = 0)
@@ -2284,16 +2289,20 @@ __device__ __forceinline__ void router_select(const RouterArgs & a, int t, int E
 // the block is issued at entry, the first state row first: the norm waits only for it, and the
 // matrices, the biases and the mask arrive while it runs; with LOOP each further token's state row is
 // requested a token ahead.
-template <int NM, bool LOOP>
+template <int NM, int UE, bool LOOP>
 __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
+    // per lane: UO outputs of each rd-wide layer and UE of the expert layer (lane group g takes
+    // outputs g + 32u), J state elements (lane + 64j) and JE expert entries; only these are loaded,
+    // which keeps a wave's loads within the 63 the wait counter tracks
+    constexpr int UO = NM / 4, J = (8 * NM + 63) / 64, JE = (32 * UE + 63) / 64;
     const int rd = a.rd, E = a.E;
     float * s_x = sm_rt;                        // [rd]
     float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
     float * s_l = s_y + max(rd, 64);            // [E]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float rh_n[4], nw[4], sb[4], mk[4];
+    float rh_n[J], nw[J], sb[4], mk[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
         const int i = lane + 64 * j;
         rh_n[j] = ld_or0(a.rh + (int64_t) blockIdx.x * rd, i, rd);
         nw[j] = ld_or0(a.norm_w, i, rd);
@@ -2302,55 +2311,59 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
     // needs its bias waits only for the loads issued before it (norm_w and sc_bias, never null,
     // stand in for absent rd- and E-sized vectors)
     float b0[4], b2[4], blg[4], bmk[4];
-    rt_bias(a.b0, a.norm_w, rd, b0);
-    rt_bias(a.b2, a.norm_w, rd, b2);
-    rt_bias(a.logit_bias, a.sc_bias, E, blg);
-    rt_bias(a.mask, a.sc_bias, E, bmk);
+    rt_bias<UO>(a.b0, a.norm_w, rd, b0);
+    rt_bias<UO>(a.b2, a.norm_w, rd, b2);
+    rt_bias<UE>(a.logit_bias, a.sc_bias, E, blg);
+    rt_bias<UE>(a.mask, a.sc_bias, E, bmk);
     const float * mask_or = a.mask ? a.mask : a.sc_bias;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int i = lane + 64 * j;
-        sb[j] = ld_or0(a.sc_bias, i, E);
-        const float m = ld_or0(mask_or, i, E);
-        mk[j] = a.mask ? m : 0.0f;
+        if (j < JE) {
+            const int i = lane + 64 * j;
+            sb[j] = ld_or0(a.sc_bias, i, E);
+            const float m = ld_or0(mask_or, i, E);
+            mk[j] = a.mask ? m : 0.0f;
+        } else {
+            sb[j] = 0.0f; mk[j] = 0.0f;
+        }
     }
     const int ldw = rd + 4;
     float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
     __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w0t, ldw, rd, w0);
+    rt_load<NM, UO>(a.w0t, ldw, rd, w0);
     __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w2t, ldw, rd, w2);
+    rt_load<NM, UO>(a.w2t, ldw, rd, w2);
     __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM>(a.w4t, ldw, E, w4);
+    rt_load<NM, UE>(a.w4t, ldw, E, w4);
     for (int t = blockIdx.x; t < a.T; t += gridDim.x) {
-        float rh[4];
+        float rh[J];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rh[j] = rh_n[j];
+        for (int j = 0; j < J; ++j) rh[j] = rh_n[j];
         const int tn = t + (int) gridDim.x;
         if (LOOP && tn < a.T) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) rh_n[j] = ld_or0(a.rh + (int64_t) tn * rd, lane + 64 * j, rd);
+            for (int j = 0; j < J; ++j) rh_n[j] = ld_or0(a.rh + (int64_t) tn * rd, lane + 64 * j, rd);
         }
         if (LOOP && t != (int) blockIdx.x) lds_sync();  // the previous token's top-k has read s_y
         // router RMS norm: double lane partials (i = lane, lane + 64, ...) + wave tree
         if (wave == 0) {
             double part = 0.0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
+            for (int j = 0; j < J; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
             const double ss = wave_tree_d(part);
             const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < J; ++j) {
                 const int i = lane + 64 * j;
                 if (i < rd) s_x[i] = (rh[j] * scale) * nw[j];
             }
         }
         lds_sync();                               // s_x holds the normalised state
-        rt_layer<0, NM>(w0, s_x, rd, s_y, b0, b0, false, false);
+        rt_layer<0, NM, UO>(w0, s_x, rd, s_y, b0, b0, false, false);
         lds_sync();
-        rt_layer<0, NM>(w2, s_y, rd, s_x, b2, b2, false, false);
+        rt_layer<0, NM, UO>(w2, s_y, rd, s_x, b2, b2, false, false);
         lds_sync();
-        rt_layer<1, NM>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
+        rt_layer<1, NM, UE>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
         lds_sync();
         if (wave == 0) router_select(a, t, E, s_l, s_y, sb, mk);
         if (!LOOP) break;
@@ -2362,11 +2375,16 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
 template <bool LOOP>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
-    switch (a.rd) {                                  // router_dim in {32, 64, 128} (host-checked)
-        case 32:  router_tail_body<4, LOOP>(a, sm_rt); break;
-        case 64:  router_tail_body<8, LOOP>(a, sm_rt); break;
-        default:  router_tail_body<16, LOOP>(a, sm_rt); break;
+    // router_dim in {32, 64, 128}, E <= 128 (host-checked)
+#define RT_E(NM_) do { if (a.E <= 32) router_tail_body<NM_, 1, LOOP>(a, sm_rt); \
+                       else if (a.E <= 64) router_tail_body<NM_, 2, LOOP>(a, sm_rt); \
+                       else router_tail_body<NM_, 4, LOOP>(a, sm_rt); } while (0)
+    switch (a.rd) {
+        case 32:  RT_E(4); break;
+        case 64:  RT_E(8); break;
+        default:  RT_E(16); break;
     }
+#undef RT_E
 }
 
 // ------------------------------------------------------------------ frame sampler
