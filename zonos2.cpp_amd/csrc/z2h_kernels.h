@@ -2114,26 +2114,37 @@ __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) 
 // Router tail: RMS norm, the erf-GELU MLP (rd -> rd -> rd -> E), softmax, selection bias, top-k, one
 // block per token. An MLP output is the dot of its weight row with the layer input as 8 fmaf partial
 // chains over contiguous eighths of the row (partial p sums i = p*rd/8 ... (p+1)*rd/8 - 1 ascending)
-// combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group; the block's 32 groups take
-// outputs g, g+32, g+64, g+96. Each lane's weights (rows padded to rd + 4 floats) go straight from
-// global memory to registers as float4s, all three matrices at entry, so the weight traffic overlaps
-// the state load and the norm. The norm and softmax sums are wave trees; top-k ranks each expert
+// combined by a xor butterfly (4, 2, 1) across the 8 lanes of a lane group; the block's 128 groups
+// take one output each (router_dim and E are at most 128), so a lane's chain is NM fmas and four waves
+// per SIMD cover each other's latency. Each lane's weights (rows padded to rd + 4 floats) go straight
+// from global memory to registers as float4s, all three matrices at entry, so the weight traffic
+// overlaps the state load and the norm. The norm and softmax sums are wave trees; top-k ranks each expert
 // against all others (score descending, ties to the lower index).
 __host__ __device__ inline int pad4(int n) { return (n + 3) & ~3; }
 __host__ __device__ inline size_t router_tail_lds(int rd, int E) {
     return (size_t) 4 * (2 * rd + (E <= 64 ? 64 : pad4(E)) + 64);
 }
 
-// the lane's weights of outputs g + 32u (u < U) of a [n_out][ldw] matrix (rows beyond n_out clamp):
-// elements [p*NM, p*NM + NM) of each row
+// Router tail blocks: RT_THREADS threads = RT_GROUPS lane groups of 8; lane group g takes outputs
+// g + RT_GROUPS u of each MLP layer, lane p of the group the elements [p*NM, p*NM + NM) of each row.
+constexpr int RT_THREADS = 1024, RT_GROUPS = RT_THREADS / 8;
+
+// the lane's weights of outputs g + RT_GROUPS u (u < U) of a [n_out][ldw] matrix (rows beyond n_out
+// clamp); a wave whose 8 groups all lie past n_out loads nothing (a wave-uniform test, no lane branch)
 template <int NM, int U>
-__device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, float4 (&wv)[4][NM / 4]) {
+__device__ __forceinline__ void rt_load(const float * w, int ldw, int n_out, float4 (&wv)[U][NM / 4]) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
+    const int g0 = __builtin_amdgcn_readfirstlane(tid >> 6) * 8;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const float4 * wr = (const float4 *) (w + (int64_t) min(g + 32 * u, n_out - 1) * ldw + p * NM);
+        if (g0 + RT_GROUPS * u < n_out) {
+            const float4 * wr = (const float4 *) (w + (int64_t) min(g + RT_GROUPS * u, n_out - 1) * ldw + p * NM);
 #pragma unroll
-        for (int m = 0; m < NM / 4; ++m) wv[u][m] = wr[m];
+            for (int m = 0; m < NM / 4; ++m) wv[u][m] = wr[m];
+        } else {
+#pragma unroll
+            for (int m = 0; m < NM / 4; ++m) wv[u][m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
 }
 
@@ -2144,33 +2155,31 @@ __device__ __forceinline__ float ld_or0(const float * p, int i, int n) {
     const float v = p[min(i, n - 1)];
     return i < n ? v : 0.0f;
 }
-// bias entries of the lane group's outputs g + 32u (u < U; rows beyond n_out clamp, entries u >= U
-// are 0); a null b reads fb (>= n_out entries) and gives zeros
+// bias entries of the lane group's outputs g + RT_GROUPS u (u < U; rows beyond n_out clamp); a null b
+// reads fb (>= n_out entries) and gives zeros
 template <int U>
-__device__ __forceinline__ void rt_bias(const float * b, const float * fb, int n_out, float (&bv)[4]) {
+__device__ __forceinline__ void rt_bias(const float * b, const float * fb, int n_out, float (&bv)[U]) {
     const int g = threadIdx.x >> 3;
     const float * q = b ? b : fb;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        if (u < U) {
-            const float v = q[min(g + 32 * u, n_out - 1)];
-            bv[u] = b ? v : 0.0f;
-        } else {
-            bv[u] = 0.0f;
-        }
+    for (int u = 0; u < U; ++u) {
+        const float v = q[min(g + RT_GROUPS * u, n_out - 1)];
+        bv[u] = b ? v : 0.0f;
     }
 }
 
-// y[o] = post(dot(W[o], x)) for the lane group's outputs g + 32u, u < U (n_out <= 32 U); MODE 0:
-// gelu(dot + b1[u]); MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
+// y[o] = post(dot(W[o], x)) for the lane group's outputs g + RT_GROUPS u, u < U (n_out <= RT_GROUPS U);
+// MODE 0: gelu(dot + b1[u]); MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
 template <int MODE, int NM, int U>
-__device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const float * x, int n_out, float * y,
-                                         const float (&b1)[4], const float (&b2)[4], bool has1, bool has2) {
+__device__ __forceinline__ void rt_layer(const float4 (&wv)[U][NM / 4], const float * x, int n_out, float * y,
+                                         const float (&b1)[U], const float (&b2)[U], bool has1, bool has2) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
     float4 xr[NM / 4];
 #pragma unroll
     for (int m = 0; m < NM / 4; ++m) xr[m] = *(const float4 *) (x + p * NM + 4 * m);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
 #pragma unroll
     for (int m = 0; m < NM / 4; ++m)
 #pragma unroll
@@ -2190,7 +2199,7 @@ __device__ __forceinline__ void rt_layer(const float4 (&wv)[4][NM / 4], const fl
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int o = g + 32 * u;
+        const int o = g + RT_GROUPS * u;
         if (o >= n_out) break;
         float v = acc[u];                          // the group's sum (valid in lane p = 0)
         if (MODE == 0) v = z_gelu(v + b1[u]);
@@ -2249,16 +2258,20 @@ __device__ __forceinline__ void router_select(const RouterArgs & a, int t, int E
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (E <= 64) {
-        float4 sv[16];
-#pragma unroll
-        for (int f4 = 0; f4 < 16; ++f4) sv[f4] = *(const float4 *) (s_s + 4 * f4);
         const float me = sc[0];
         int rank = 0;
 #pragma unroll
-        for (int f4 = 0; f4 < 16; ++f4) {
-            const float vv[4] = {sv[f4].x, sv[f4].y, sv[f4].z, sv[f4].w};
+        for (int q4 = 0; q4 < 16; q4 += 4) {                         // 4 float4 of scores at a time
+            float4 sv[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) rank += (int) (vv[c] > me) | ((int) (vv[c] == me) & (int) (4 * f4 + c < lane));
+            for (int f = 0; f < 4; ++f) sv[f] = *(const float4 *) (s_s + 4 * (q4 + f));
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                const int f4 = q4 + f;
+                const float vv[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) rank += (int) (vv[c] > me) | ((int) (vv[c] == me) & (int) (4 * f4 + c < lane));
+            }
         }
         if (lane < E && rank < a.k) {
             a.sel[(int64_t) t * a.k + rank] = lane;
@@ -2291,10 +2304,9 @@ __device__ __forceinline__ void router_select(const RouterArgs & a, int t, int E
 // requested a token ahead.
 template <int NM, int UE, bool LOOP>
 __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
-    // per lane: UO outputs of each rd-wide layer and UE of the expert layer (lane group g takes
-    // outputs g + 32u), J state elements (lane + 64j) and JE expert entries; only these are loaded,
-    // which keeps a wave's loads within the 63 the wait counter tracks
-    constexpr int UO = NM / 4, J = (8 * NM + 63) / 64, JE = (32 * UE + 63) / 64;
+    // per lane: one output of each layer (lane group g takes output g), J state elements (lane + 64j)
+    // and JE expert entries (E <= 64 JE) for wave 0's norm and top-k; only these are loaded
+    constexpr int UO = 1, J = (8 * NM + 63) / 64, JE = UE;
     const int rd = a.rd, E = a.E;
     float * s_x = sm_rt;                        // [rd]
     float * s_y = s_x + rd;                     // [rd] (then the top-k scores, >= 64 entries)
@@ -2310,11 +2322,11 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
     // the small vectors before the three matrices: loads complete in issue order, so a layer that
     // needs its bias waits only for the loads issued before it (norm_w and sc_bias, never null,
     // stand in for absent rd- and E-sized vectors)
-    float b0[4], b2[4], blg[4], bmk[4];
+    float b0[UO], b2[UO], blg[UO], bmk[UO];
     rt_bias<UO>(a.b0, a.norm_w, rd, b0);
     rt_bias<UO>(a.b2, a.norm_w, rd, b2);
-    rt_bias<UE>(a.logit_bias, a.sc_bias, E, blg);
-    rt_bias<UE>(a.mask, a.sc_bias, E, bmk);
+    rt_bias<UO>(a.logit_bias, a.sc_bias, E, blg);
+    rt_bias<UO>(a.mask, a.sc_bias, E, bmk);
     const float * mask_or = a.mask ? a.mask : a.sc_bias;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -2328,13 +2340,14 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
         }
     }
     const int ldw = rd + 4;
-    float4 w0[4][NM / 4], w2[4][NM / 4], w4[4][NM / 4];
+    float4 w0[UO][NM / 4], w2[UO][NM / 4], w4[UO][NM / 4];
     __builtin_amdgcn_sched_barrier(0);
     rt_load<NM, UO>(a.w0t, ldw, rd, w0);
     __builtin_amdgcn_sched_barrier(0);
     rt_load<NM, UO>(a.w2t, ldw, rd, w2);
     __builtin_amdgcn_sched_barrier(0);
-    rt_load<NM, UE>(a.w4t, ldw, E, w4);
+    rt_load<NM, UO>(a.w4t, ldw, E, w4);
+#pragma unroll 1
     for (int t = blockIdx.x; t < a.T; t += gridDim.x) {
         float rh[J];
 #pragma unroll
@@ -2363,22 +2376,21 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
         lds_sync();
         rt_layer<0, NM, UO>(w2, s_y, rd, s_x, b2, b2, false, false);
         lds_sync();
-        rt_layer<1, NM, UE>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
+        rt_layer<1, NM, UO>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr);
         lds_sync();
         if (wave == 0) router_select(a, t, E, s_l, s_y, sb, mk);
         if (!LOOP) break;
     }
 }
 
-// grid: one block per token (decode steps) or up to one per CU with a token loop (LOOP, wide passes);
-// a single wave per SIMD, so the three weight matrices can all be register-resident
+// grid: one block of RT_THREADS per token (decode steps) or up to one per CU with a token loop (LOOP,
+// wide passes)
 template <bool LOOP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_router_tail(RouterArgs a) {
+__global__ void __launch_bounds__(RT_THREADS) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
     // router_dim in {32, 64, 128}, E <= 128 (host-checked)
-#define RT_E(NM_) do { if (a.E <= 32) router_tail_body<NM_, 1, LOOP>(a, sm_rt); \
-                       else if (a.E <= 64) router_tail_body<NM_, 2, LOOP>(a, sm_rt); \
-                       else router_tail_body<NM_, 4, LOOP>(a, sm_rt); } while (0)
+#define RT_E(NM_) do { if (a.E <= 64) router_tail_body<NM_, 1, LOOP>(a, sm_rt); \
+                       else router_tail_body<NM_, 2, LOOP>(a, sm_rt); } while (0)
     switch (a.rd) {
         case 32:  RT_E(4); break;
         case 64:  RT_E(8); break;
