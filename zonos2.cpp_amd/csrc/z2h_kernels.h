@@ -1255,7 +1255,7 @@ k_gemv_mfma(GemvArgs a) {
 
 // m16 GEMV with the K units split over the block's 4 waves: one 16-row group per block (grid x), wave
 // w takes units w, w+4, ... (all requested behind the first activation staging loads, so a wave has
-// all its weight bytes in flight at once); every unit's values go to LDS and wave 0 folds them in superblock order (m16_fold), the
+// all its weight bytes in flight at once); every unit's values go to LDS and the 4 waves fold them (one token slot each) in superblock order (m16_fold), the
 // order of every other Q4_K matmul. Dense: grid (groups, token chunks of ROWS, mats);
 // grouped (expert matmuls): grid (groups, experts, passes of ROWS routes), the expert's routes listed
 // first so blocks of untouched experts read no weights. Each 16-row group gives 4x more, shorter
@@ -1324,13 +1324,12 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         }
     }
     lds_sync();
-    if (wave != 0) return;
-    const int q = lane >> 4, row = g16 * 16 + (lane & 15);
+    // wave w folds token slot i = w of the MFMA layout (tokens 4q + w) for the group's 16 rows
+    const int q = lane >> 4, row = g16 * 16 + (lane & 15), i = wave;
     if (row >= a.rows) return;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    {
         const int t = 4 * q + i;
-        if (t >= nt) continue;
+        if (t >= nt) return;
         const int it = a.grouped ? s_list[c0 + t] : c0 + t;
         // the units in superblock order (the block scale of the token's superblock sb: Q8_K only)
         float g = 0.0f, up = 0.0f;
