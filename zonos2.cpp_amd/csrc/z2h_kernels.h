@@ -165,6 +165,31 @@ __device__ __forceinline__ void encode_row_rt(int af, const float * x, int K, co
     else if (af == ACT_F16) encode_row<ACT_F16>(x, K, nullptr, nullptr, nullptr, nullptr, a.h + (int64_t) t * Kp);
 }
 
+// Q8_K of a row that a 256-thread block holds in registers the norm kernels' way (thread tid owns
+// elements 4 (tid + 256 j) .. + 3, so wave w holds 256-blocks w + 4j in q8k lane order): the blocks
+// are encoded in place, in encode_row's pairs (w + 8m, w + 8m + 4), with no LDS round trip.
+// Needs K % 1024 == 0 and K <= 1024 NV.
+template <int NV>
+__device__ __forceinline__ void encode_q8k_regs(const float4 (&xv)[NV], int K, const ActBuf & a, int t) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, Kp = kpad(K), nj = K / 1024;
+    int8_t * q = a.q + (int64_t) t * Kp;
+    float * d256 = a.d256 + (int64_t) t * (Kp / 256);
+    int16_t * bs = a.bs + (int64_t) t * (Kp / 16);
+#pragma unroll
+    for (int j = 0; j < NV; j += 2) {
+        if (j >= nj) break;
+        const int b = wave + 4 * j;
+        const float v0[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        if (j + 1 < nj) {
+            const int b1 = b + 4;
+            const float v1[4] = {xv[j + 1].x, xv[j + 1].y, xv[j + 1].z, xv[j + 1].w};
+            q8k_block_v2(v0, v1, q + 256 * b, q + 256 * b1, d256 + b, d256 + b1, bs + 16 * b, bs + 16 * b1, lane);
+        } else {
+            q8k_block_v(v0, q + 256 * b, d256 + b, bs + 16 * b, lane);
+        }
+    }
+}
+
 // Block-wide copy of n 16-byte items with all loads of a batch issued before its stores (a loop
 // that loads and stores per iteration is not software-pipelined and pays one memory round trip per
 // iteration). src(i) / dst(i) give the item addresses.
@@ -414,7 +439,9 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             xv[j] = make_float4((xv[j].x * scale) * nw[j].x, (xv[j].y * scale) * nw[j].y, (xv[j].z * scale) * nw[j].z, (xv[j].w * scale) * nw[j].w);
         }
     }
-    if (a.act_fmt != ACT_NONE) {
+    if (a.act_fmt == ACT_Q8_K && d % 1024 == 0) {
+        encode_q8k_regs(xv, d, a.act, t);            // each wave holds its blocks already
+    } else if (a.act_fmt != ACT_NONE) {
         // the encoders read the row from LDS (a 256-block spans the elements of 64 threads)
 #pragma unroll
         for (int j = 0; j < RN_NV; ++j) {
@@ -2100,7 +2127,8 @@ __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) 
         if (lane == 0) r.rh[(int64_t) t * r.rd + o] = v;
     }
     if (!lead) return;
-    if (f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
+    if (f.act_fmt == ACT_Q8_K && d % 1024 == 0) encode_q8k_regs(xv, d, f.act, t);
+    else if (f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
 #pragma unroll
     for (int j = 0; j < RN_NV; ++j) {
         const int i0 = 4 * (tid + 256 * j);
