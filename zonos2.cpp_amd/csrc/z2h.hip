@@ -764,7 +764,16 @@ int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
     a.eps = ctx->hp.rms_eps; a.err = ctx->d_err;
     const size_t lds = (size_t) kpad(a.d) * 4;
     switch (a.mode) {
-        case RN_EMBED: KL(k_resnorm<RN_EMBED>, dim3(T), dim3(256), lds, ctx->stream, a); break;
+        case RN_EMBED: {
+            // token ids over tables of one type (F32, F16, Q8_0): the switch-free gather
+            int tt = a.W > 0 ? a.tab_type[0] : -1;
+            for (int k = 1; k < a.W; ++k) if (a.tab_type[k] != tt) tt = -1;
+            if (tt == 8) KL((k_resnorm<RN_EMBED, 8>), dim3(T), dim3(256), lds, ctx->stream, a);
+            else if (tt == 1) KL((k_resnorm<RN_EMBED, 1>), dim3(T), dim3(256), lds, ctx->stream, a);
+            else if (tt == 0) KL((k_resnorm<RN_EMBED, 0>), dim3(T), dim3(256), lds, ctx->stream, a);
+            else KL(k_resnorm<RN_EMBED>, dim3(T), dim3(256), lds, ctx->stream, a);
+            break;
+        }
         case RN_ACCUM: KL(k_resnorm<RN_ACCUM>, dim3(T), dim3(256), lds, ctx->stream, a); break;
         case RN_ADD: KL(k_resnorm<RN_ADD>, dim3(T), dim3(256), lds, ctx->stream, a); break;
         default: KL(k_resnorm<RN_ENCODE>, dim3(T), dim3(256), lds, ctx->stream, a); break;
@@ -1180,7 +1189,7 @@ int set_lds_limits(std::string & err) {
                    LDS_ATTR((k_attn_merge<H_, 1>)) LDS_ATTR((k_attn_merge<H_, 2>)) LDS_ATTR((k_attn_merge<H_, 4>)) LDS_ATTR((k_attn_merge<H_, 8>))
     LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
 #undef LDS_TF
-    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
+    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR((k_resnorm<RN_EMBED, 8>)) LDS_ATTR((k_resnorm<RN_EMBED, 1>)) LDS_ATTR((k_resnorm<RN_EMBED, 0>)) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     return Z2H_OK;
 }

@@ -305,14 +305,33 @@ __device__ __forceinline__ float4 table_elem4(const uint8_t * row, int type, int
     return make_float4(table_elem(row, type, i0), table_elem(row, type, i0 + 1), table_elem(row, type, i0 + 2), table_elem(row, type, i0 + 3));
 }
 
+// table_elem4 for a table type known at compile time (F32 / F16 / Q8_0), with no type switch
+template <int TT>
+__device__ __forceinline__ float4 table_elem4_t(const uint8_t * row, int i0) {
+    if constexpr (TT == 0) {
+        return *(const float4 *) (row + 4 * (int64_t) i0);
+    } else if constexpr (TT == 1) {
+        const uint2 h = *(const uint2 *) (row + 2 * (int64_t) i0);
+        return make_float4(h2f(h.x & 0xffffu), h2f(h.x >> 16), h2f(h.y & 0xffffu), h2f(h.y >> 16));
+    } else {
+        static_assert(TT == 8, "F32, F16 or Q8_0 tables");
+        const uint8_t * b = row + 34 * (i0 >> 5);
+        const float dd = h2f(*(const uint16_t *) b);
+        const uint8_t * qv = b + 2 + (i0 & 31);
+        return make_float4((float) (int8_t) qv[0] * dd, (float) (int8_t) qv[1] * dd, (float) (int8_t) qv[2] * dd, (float) (int8_t) qv[3] * dd);
+    }
+}
+
 // One block per token; thread tid owns elements 4*(tid + 256*j) .. +3 (d % 4 == 0, d <= 4096). Every
 // global read the block needs (norm weight, routes, residual, embedding rows) is issued before the
 // first reduction and before the first store (a store between loads would order them: the
 // compiler cannot tell the residual row from the sources), and every global store comes after the
 // last barrier (a barrier waits for the block's outstanding stores). One instantiation per mode
-// keeps each kernel's code to its own path.
+// keeps each kernel's code to its own path. TT >= 0 (RN_EMBED): every table has GGUF type TT, and the
+// token's table rows are read with no type switch: all tables' loads of an element group go out
+// together (tables past W re-read the last one and are not added), the sum keeps the table order.
 constexpr int RN_NV = 4;
-template <int MODE>
+template <int MODE, int TT = -1>
 __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     extern __shared__ float sm_rn[];
     float * xs = sm_rn;                // [d]
@@ -336,6 +355,37 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             for (int j = 0; j < RN_NV; ++j) {
                 const int i0 = 4 * (tid + 256 * j);
                 if (i0 < d) xv[j] = *(const float4 *) (er + i0);
+            }
+        } else if constexpr (TT >= 0) {
+            const uint8_t * rows[MAX_TABLES];
+            const int64_t rb = table_row_bytes(TT, d);
+            int ids[MAX_TABLES];                                   // every id read before any flag write
+#pragma unroll
+            for (int kk = 0; kk < MAX_TABLES; ++kk) ids[kk] = a.ids[(int64_t) t * a.W + min(kk, a.W - 1)];
+            bool bad = false;
+#pragma unroll
+            for (int kk = 0; kk < MAX_TABLES; ++kk) {
+                const int kc = min(kk, a.W - 1);
+                const bool ok = ids[kk] >= 0 && ids[kk] < a.tab_rows[kc];
+                bad = bad || !ok;
+                rows[kk] = a.tab[kc] + (int64_t) (ok ? ids[kk] : 0) * rb;
+            }
+            if (bad && tid == 0) atomicOr(a.err, 1);
+#pragma unroll
+            for (int j = 0; j < RN_NV; ++j) {
+                if (1024 * j >= d) break;                          // (uniform) groups past the row
+                const int i0 = min(4 * (tid + 256 * j), d - 4);
+                float4 e[MAX_TABLES];
+#pragma unroll
+                for (int kk = 0; kk < MAX_TABLES; ++kk) e[kk] = table_elem4_t<TT>(rows[kk], i0);
+                __builtin_amdgcn_sched_barrier(0);                 // every load of the group issues first
+                float4 x = e[0];
+#pragma unroll
+                for (int kk = 1; kk < MAX_TABLES; ++kk) {
+                    const float4 y = add4(x, e[kk]);
+                    x = kk < a.W ? y : x;
+                }
+                xv[j] = x;
             }
         } else {
             // sum of the W tables' rows in column order (kk = 0, 1, ...), each row gathered whole
