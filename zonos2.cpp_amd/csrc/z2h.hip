@@ -670,11 +670,15 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         const bool dual = a.mode == MM_SWIGLU;
         if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
         if (!a.grouped && (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX) {
-            // K split over the 4 waves of a block, one 16-row group per block
-            const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, a.grouped ? MT_G : MT);
-            dim3 grid(m0.tiles, a.grouped ? a.E : grid_y, a.grouped ? passes : (dual ? 1 : a.n_mats)), block(256);
+            // K split over the 4 waves of a block, one 16-row group per block; chunks of 8 tokens
+            // where that still gives at most one block per compute unit (a weight tile is then read
+            // by two blocks, which halves each block's staging and products)
+            const bool half = (int64_t) m0.tiles * ((a.n_tok + MT_G - 1) / MT_G) <= ctx->n_cu;
+            const int srows = half ? MT_G : MT;
+            const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, srows);
+            dim3 grid(m0.tiles, (a.n_tok + srows - 1) / srows, dual ? 1 : a.n_mats), block(256);
 #define SPL(W_, D_, R_) KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
-#define SPL_R(W_, D_) do { if (a.grouped) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
+#define SPL_R(W_, D_) do { if (half) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
             if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
             else if (m0.type == Z2H_Q6_K) { if (dual) SPL_R(WF_Q6_K, true); else SPL_R(WF_Q6_K, false); }
             else { if (dual) SPL_R(WF_Q8_0, true); else SPL_R(WF_Q8_0, false); }
