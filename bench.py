@@ -163,6 +163,17 @@ def main() -> int:
     got = d_logits.cpu().numpy()
     assert np.array_equal(got, logits_gpu), "device-resident step differs from the host-API step"
 
+    # the host-buffer boundary (z2h_step: slot ids, n_past and token ids uploaded, logits copied back
+    # and waited for), wall clock per call; reported beside `value`, never as it
+    host_ms = []
+    for i in range(args.warmup + args.steps):
+        t0 = time.perf_counter()
+        ctx.step(inp.slot_idx, inp.n_past, ids=inp.ids)
+        if i >= args.warmup:
+            host_ms.append((time.perf_counter() - t0) * 1000.0)
+    host_med = float(np.median(host_ms))
+    log(f"host-API step (PCIe both ways, synchronous): {host_med:.3f} ms median over {args.steps} calls")
+
     # per-kernel HIP-event window (separate pass over the same steps, eager launches): every launch
     # carries a start / stop event pair timestamped at the kernel's own start and end
     ctx.profile_begin()
@@ -273,6 +284,8 @@ def main() -> int:
                                f"(KV {min(wl.kv_lens)}..{max(wl.kv_lens)}), d_model {cfg.n_embd}, "
                                f"{cfg.n_expert} experts top-{cfg.top_k}",
                    "requests": T, "kv_lens": wl.kv_lens, "parallelism": "single GPU"},
+        "host_api": {"ms_per_step": round(host_med, 4), "tok_per_s": round(T / (host_med / 1000.0), 1),
+                     "note": "z2h_step with host buffers: inputs uploaded, logits read back, synchronous"},
         "step_hbm": {"bytes": B, "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": {"kernel": gateup_kernel_of(cfg.bulk), "bound": "hbm",

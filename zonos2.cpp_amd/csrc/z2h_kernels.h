@@ -538,56 +538,94 @@ struct GemvArgs {
 };
 
 // The grouping of mul_mat_id's routes by expert, as a stable counting sort of the flat top-k ids
-// (route r = token * k + j): counts per expert (LDS atomics), exclusive offsets, then every route's
-// position = offset of its expert + routes of that expert before it. One 1024-thread block; routes
-// are placed 1024 at a time in order, each wave ranking its 64 routes per distinct expert with
-// ballots and the waves' counts prefix-summed in wave order, so the order within an expert is the
-// flat route order. E <= SORT_EMAX.
+// (route r = token * k + j): position of a route = offset of its expert + routes of that expert
+// before it. One 1024-thread block; wave w owns the contiguous routes [w seg, (w + 1) seg) (whole
+// 64-route rounds, the waves in flat order) and loads up to SORT_RPW rounds at once:
+//   1. per wave and expert counts (LDS atomics);
+//   2. expert offsets (a scan over the experts) and each wave's first position per expert;
+//   3. each wave places its rounds in order with no block barrier: a lane's mask of the round's
+//      lanes with the same expert comes from one ballot per bit of the expert id, its rank within
+//      the expert from that mask, and the expert's lowest lane advances the wave's next position of
+//      the expert (LDS; every lane reads it before that lane writes it).
+// E <= SORT_EMAX.
 constexpr int SORT_EMAX = 256;
+constexpr int SORT_RPW = 16;
 constexpr int LIST_MAX = 1024;   // routes a grouped matmul block lists in LDS itself (without k_route_sort)
 __global__ void __launch_bounds__(1024) k_route_sort(const int32_t * sel, int n_routes, int E, int32_t * off, int32_t * perm,
                                                      int32_t * cap_counts, int32_t * cap_off, int32_t * cap_perm) {
-    __shared__ int s_cnt[SORT_EMAX], s_off[SORT_EMAX + 1], s_run[SORT_EMAX];
-    __shared__ int s_wc[16][SORT_EMAX];
+    __shared__ int s_wc[16][SORT_EMAX];              // per wave and expert: routes, then the wave's first position
+    __shared__ int s_cnt[SORT_EMAX], s_off[SORT_EMAX + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += 1024) { s_cnt[e] = 0; s_run[e] = 0; }
+    const int seg = (n_routes + 1023) / 1024 * 64;
+    const int lo = min(n_routes, wave * seg), hi = min(n_routes, lo + seg);
+    // the wave's rounds b, b + 64, ... (up to SORT_RPW of them): route b + 64 j + lane in v[j]
+    auto load_rounds = [&](int b, int (&v)[SORT_RPW]) {
+#pragma unroll
+        for (int j = 0; j < SORT_RPW; ++j) v[j] = sel[min(b + 64 * j + lane, hi - 1)];
+    };
+    for (int e = lane; e < E; e += 64) s_wc[wave][e] = 0;
     __syncthreads();
-    for (int r = tid; r < n_routes; r += 1024) atomicAdd(&s_cnt[sel[r]], 1);
-    __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; ++e) { s_off[e] = acc; acc += s_cnt[e]; }
-        s_off[E] = acc;
+    for (int b = lo; b < hi; b += 64 * SORT_RPW) {
+        int v[SORT_RPW];
+        load_rounds(b, v);
+#pragma unroll
+        for (int j = 0; j < SORT_RPW; ++j)
+            if (b + 64 * j + lane < hi) atomicAdd(&s_wc[wave][v[j]], 1);
     }
     __syncthreads();
+    for (int e = tid; e < E; e += 1024) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += s_wc[w][e];
+        s_cnt[e] = t;
+    }
+    __syncthreads();
+    if (wave == 0) {                                 // exclusive offsets, experts 4 l .. 4 l + 3 in lane l
+        int c[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { const int e = 4 * lane + i; c[i] = e < E ? s_cnt[e] : 0; sum += c[i]; }
+        int incl = sum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) { const int u = __shfl_up(incl, d, 64); if (lane >= d) incl += u; }
+        int acc = incl - sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { const int e = 4 * lane + i; if (e < E) s_off[e] = acc; acc += c[i]; }
+        if (lane == 63) s_off[E] = incl;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 1024) {
+        int c[16];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) c[w] = s_wc[w][e];
+        int acc = s_off[e];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) { s_wc[w][e] = acc; acc += c[w]; }
+    }
+    __syncthreads();
+    const int nbits = 32 - __builtin_clz(max(E - 1, 1));
     const uint64_t lt = (1ull << lane) - 1ull;
-    for (int base = 0; base < n_routes; base += 1024) {
-        const int r = base + tid;
-        const bool valid = r < n_routes;
-        const int me = valid ? sel[r] : -1;
-        for (int e = lane; e < E; e += 64) s_wc[wave][e] = 0;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        int rank = 0;
-        uint64_t todo = __ballot(valid);
-        while (todo) {
-            const int leader = __ffsll((unsigned long long) todo) - 1;
-            const int e0 = __shfl(me, leader, 64);
-            const uint64_t m = __ballot(valid && me == e0);
-            if (me == e0) rank = __popcll(m & lt);
-            if (lane == 0) s_wc[wave][e0] = __popcll(m);
-            todo &= ~m;
+    for (int b = lo; b < hi; b += 64 * SORT_RPW) {
+        int v[SORT_RPW];
+        load_rounds(b, v);
+#pragma unroll
+        for (int j = 0; j < SORT_RPW; ++j) {
+            const int r = b + 64 * j + lane;
+            if (b + 64 * j >= hi) break;                 // wave-uniform
+            const bool valid = r < hi;
+            const int me = valid ? v[j] : 0;
+            uint64_t same = __ballot(valid);
+            for (int bit = 0; bit < nbits; ++bit) {
+                const bool on = (me >> bit) & 1;
+                const uint64_t bb = __ballot(on);
+                same &= on ? bb : ~bb;
+            }
+            const int rank = __popcll(same & lt);
+            const int first = s_wc[wave][me];
+            if (valid) {
+                perm[first + rank] = r;
+                if (rank == 0) s_wc[wave][me] = first + __popcll(same);
+            }
         }
-        __syncthreads();
-        for (int e = tid; e < E; e += 1024) {            // per expert: routes before each wave
-            int acc = s_run[e];
-            for (int w = 0; w < 16; ++w) { const int c = s_wc[w][e]; s_wc[w][e] = acc; acc += c; }
-            s_run[e] = acc;
-        }
-        __syncthreads();
-        if (valid) perm[s_off[me] + s_wc[wave][me] + rank] = r;
-        __syncthreads();
     }
     for (int e = tid; e <= E; e += 1024) off[e] = s_off[e];
     if (cap_counts) {
