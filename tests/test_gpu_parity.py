@@ -371,3 +371,32 @@ def test_route_lists_in_lds_match_the_sorted_table():
     b = ctx.step(slots, npast, emb=emb)
     np.testing.assert_array_equal(a, b)
     ctx.close()
+
+
+@pytest.mark.parametrize("E,k,T", [(64, 8, 2100), (48, 3, 300)])
+def test_route_table_over_many_routes_and_experts(E, k, T):
+    """The route grouping (mul_mat_id, src/zonos2-graph.cpp:222-231) of a wide MoE pass: 2100 tokens x
+    top-8 of 64 experts is 16800 routes, more than one 1024 x 16-route chunk of the sort kernel; 48
+    experts (not a power of two) x top-3. Router outputs and the counts, offsets and permutation are
+    bit-exact against the oracle, the layer output within the bar."""
+    cfg = configs.ModelConfig("wide-route-sort", n_layer=1, n_embd=256, n_head=8, n_head_kv=2, head_dim=32,
+                              n_expert=E, top_k=k, n_ff=256, bulk=configs.Q8_0, router_bias_std=1e-4)
+    model = synth.generate_model(cfg, 46)
+    ctx = Context(cfg.hparams(), T, 4)
+    ctx.upload(model)
+    om = O.OracleModel(cfg.hparams(), model)
+    x = synth.gen_normal_f32((T, cfg.n_embd), 47, "inputs.moe")
+    ctx.set_capture(True)
+    got = ctx.moe_forward(0, x)
+    ref = O.router(om, 0, x, None)
+    sel = ctx.read_capture(0, "sel", T).reshape(T, ctx.kmax)[:, :k]
+    assert np.array_equal(sel, ref["sel"])
+    assert np.array_equal(ctx.read_capture(0, "probs", T).reshape(ref["probs"].shape).view(np.uint32),
+                          ref["probs"].view(np.uint32))
+    counts, offsets, perm = O.group(ref["sel"], E)
+    assert np.array_equal(ctx.read_capture(0, "counts", T), counts)
+    assert np.array_equal(ctx.read_capture(0, "offsets", T), offsets)
+    assert np.array_equal(ctx.read_capture(0, "perm", T)[:T * k], perm)
+    eo, out = O.experts(om, 0, x, ref["sel"], ref["w"])
+    assert_close("moe out", got, out)
+    ctx.close()
