@@ -373,12 +373,15 @@ def test_route_lists_in_lds_match_the_sorted_table():
     ctx.close()
 
 
-@pytest.mark.parametrize("E,k,T", [(64, 8, 2100), (48, 3, 300)])
+@pytest.mark.parametrize("E,k,T", [(64, 8, 2100), (48, 3, 300), (128, 4, 200), (128, 6, 40)])
 def test_route_table_over_many_routes_and_experts(E, k, T):
     """The route grouping (mul_mat_id, src/zonos2-graph.cpp:222-231) of a wide MoE pass: 2100 tokens x
     top-8 of 64 experts is 16800 routes, more than one 1024 x 16-route chunk of the sort kernel; 48
-    experts (not a power of two) x top-3. Router outputs and the counts, offsets and permutation are
-    bit-exact against the oracle, the layer output within the bar."""
+    experts (not a power of two) x top-3; 128 experts (the most a model may have: two expert entries
+    per lane in the router's top-k) through the wide (200 tokens) and the per-token (40) router. Router
+    outputs and the counts, offsets and permutation are bit-exact against the oracle, the layer output
+    within the bar, and the same pass without captures (experts listing their routes in LDS up to
+    1024 routes) gives the same bits."""
     cfg = configs.ModelConfig("wide-route-sort", n_layer=1, n_embd=256, n_head=8, n_head_kv=2, head_dim=32,
                               n_expert=E, top_k=k, n_ff=256, bulk=configs.Q8_0, router_bias_std=1e-4)
     model = synth.generate_model(cfg, 46)
@@ -399,4 +402,6 @@ def test_route_table_over_many_routes_and_experts(E, k, T):
     assert np.array_equal(ctx.read_capture(0, "perm", T)[:T * k], perm)
     eo, out = O.experts(om, 0, x, ref["sel"], ref["w"])
     assert_close("moe out", got, out)
+    ctx.set_capture(False)
+    np.testing.assert_array_equal(ctx.moe_forward(0, x), got)
     ctx.close()
