@@ -883,7 +883,7 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         prof_scope ps(ctx, Z2H_KF_ROUTER_TAIL);
         // wide passes: up to one block per compute unit, each looping over its tokens with the MLP
         // matrices loaded once
-        if (T >= GEMM_MIN_ROWS) KL(k_router_tail<true>, dim3(std::min(T, ctx->n_cu)), dim3(RT_THREADS), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
+        if (T >= GEMM_MIN_ROWS) KL(k_router_tail<true>, dim3(std::min((T + RT_NTOK - 1) / RT_NTOK, ctx->n_cu)), dim3(RT_THREADS), router_tail_wide_lds(ctx->rd, ly.E), ctx->stream, r);
         else KL(k_router_tail<false>, dim3(T), dim3(RT_THREADS), router_tail_lds(ctx->rd, ly.E), ctx->stream, r);
         HIPX(hipGetLastError());
     }

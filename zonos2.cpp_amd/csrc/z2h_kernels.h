@@ -2285,44 +2285,53 @@ __device__ __forceinline__ void rt_bias(const float * b, const float * fb, int n
 
 // y[o] = post(dot(W[o], x)) for the lane group's outputs g + RT_GROUPS u, u < U (n_out <= RT_GROUPS U);
 // MODE 0: gelu(dot + b1[u]); MODE 1: dot (+ b1[u] when has1: logit bias) (+ b2[u] when has2: mask)
-template <int MODE, int NM, int U>
+// NT > 1: the same for NT token vectors x + n xs -> y + n ys on the same weight registers (each
+// token's chain and sums as with NT = 1)
+template <int MODE, int NM, int U, int NT = 1>
 __device__ __forceinline__ void rt_layer(const float4 (&wv)[U][NM / 4], const float * x, int n_out, float * y,
-                                         const float (&b1)[U], const float (&b2)[U], bool has1, bool has2) {
+                                         const float (&b1)[U], const float (&b2)[U], bool has1, bool has2,
+                                         int xs = 0, int ys = 0) {
     const int tid = threadIdx.x, g = tid >> 3, p = tid & 7;
-    float4 xr[NM / 4];
+    float acc[NT][U];
 #pragma unroll
-    for (int m = 0; m < NM / 4; ++m) xr[m] = *(const float4 *) (x + p * NM + 4 * m);
-    float acc[U];
+    for (int n = 0; n < NT; ++n) {                 // one token's inputs in registers at a time
+        float4 xr[NM / 4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+        for (int m = 0; m < NM / 4; ++m) xr[m] = *(const float4 *) (x + n * xs + p * NM + 4 * m);
 #pragma unroll
-    for (int m = 0; m < NM / 4; ++m)
+        for (int u = 0; u < U; ++u) acc[n][u] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < NM / 4; ++m)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                acc[n][u] = __builtin_fmaf(wv[u][m].x, xr[m].x, acc[n][u]);
+                acc[n][u] = __builtin_fmaf(wv[u][m].y, xr[m].y, acc[n][u]);
+                acc[n][u] = __builtin_fmaf(wv[u][m].z, xr[m].z, acc[n][u]);
+                acc[n][u] = __builtin_fmaf(wv[u][m].w, xr[m].w, acc[n][u]);
+            }
+        // lane p = 0 of the group ends with ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), the xor
+        // butterfly's (4, 2, 1) sum, from DPP row shifts (lane i reads lane i + n of its 16-lane row)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            acc[u] = __builtin_fmaf(wv[u][m].x, xr[m].x, acc[u]);
-            acc[u] = __builtin_fmaf(wv[u][m].y, xr[m].y, acc[u]);
-            acc[u] = __builtin_fmaf(wv[u][m].z, xr[m].z, acc[u]);
-            acc[u] = __builtin_fmaf(wv[u][m].w, xr[m].w, acc[u]);
+            acc[n][u] = acc[n][u] + dpp_f<DPP_ROW_SHL + 4>(acc[n][u]);
+            acc[n][u] = acc[n][u] + dpp_f<DPP_ROW_SHL + 2>(acc[n][u]);
+            acc[n][u] = acc[n][u] + dpp_f<DPP_ROW_SHL + 1>(acc[n][u]);
         }
-    // lane p = 0 of the group ends with ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)), the xor
-    // butterfly's (4, 2, 1) sum, from DPP row shifts (lane i reads lane i + n of its 16-lane row)
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 4>(acc[u]);
-        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 2>(acc[u]);
-        acc[u] = acc[u] + dpp_f<DPP_ROW_SHL + 1>(acc[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int o = g + RT_GROUPS * u;
         if (o >= n_out) break;
-        float v = acc[u];                          // the group's sum (valid in lane p = 0)
-        if (MODE == 0) v = z_gelu(v + b1[u]);
-        else {
-            if (has1) v = v + b1[u];
-            if (has2) v = v + b2[u];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            float v = acc[n][u];                   // the group's sum (valid in lane p = 0)
+            if (MODE == 0) v = z_gelu(v + b1[u]);
+            else {
+                if (has1) v = v + b1[u];
+                if (has2) v = v + b2[u];
+            }
+            if (p == 0) y[n * ys + o] = v;
         }
-        if (p == 0) y[o] = v;
     }
 }
 
@@ -2412,11 +2421,11 @@ __device__ __forceinline__ void router_select(const RouterArgs & a, int t, int E
 }
 
 // The router tail for router_dim = 8 * NM (<= 128 outputs per layer): token blockIdx.x (LOOP false:
-// one block per token, decode steps) or tokens blockIdx.x, blockIdx.x + gridDim.x, ... (LOOP: wide
-// passes, the three MLP matrices loaded once per block and kept in registers). Every global load of
-// the block is issued at entry, the first state row first: the norm waits only for it, and the
-// matrices, the biases and the mask arrive while it runs; with LOOP each further token's state row is
-// requested a token ahead.
+// one block per token, decode steps; wide passes take router_tail_wide) or tokens blockIdx.x,
+// blockIdx.x + gridDim.x, ... (LOOP: the three MLP matrices loaded once per block and kept in
+// registers). Every global load of the block is issued at entry, the first state row first: the norm
+// waits only for it, and the matrices, the biases and the mask arrive while it runs; with LOOP each
+// further token's state row is requested a token ahead.
 template <int NM, int UE, bool LOOP>
 __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * sm_rt) {
     // per lane: one output of each layer (lane group g takes output g), J state elements (lane + 64j)
@@ -2500,12 +2509,101 @@ __device__ __forceinline__ void router_tail_body(const RouterArgs & a, float * s
 
 // grid: one block of RT_THREADS per token (decode steps) or up to one per CU with a token loop (LOOP,
 // wide passes)
+// The router tail for wide passes: tokens t + G n (n < RT_NTOK; G = gridDim.x, t = blockIdx.x +
+// RT_NTOK G i) RT_NTOK at a time, the three MLP matrices loaded once per block and kept in registers.
+// Each MLP layer forms every token's outputs on the same weight registers (rt_layer<..., RT_NTOK>);
+// wave n normalises and selects token n. Every token's arithmetic is router_tail_body's. Dynamic LDS
+// router_tail_wide_lds(rd, E).
+constexpr int RT_NTOK = 4;
+__host__ __device__ inline int rt_el(int E) { return E <= 64 ? 64 : pad4(E); }
+__host__ __device__ inline size_t router_tail_wide_lds(int rd, int E) {
+    const int sy = rd > rt_el(E) ? rd : rt_el(E);
+    return (size_t) 4 * RT_NTOK * (rd + sy + rt_el(E));
+}
+template <int NM, int UE>
+__device__ __forceinline__ void router_tail_wide(const RouterArgs & a, float * sm_rt) {
+    constexpr int UO = 1, J = (8 * NM + 63) / 64, JE = UE, NT = RT_NTOK;
+    const int rd = a.rd, E = a.E, G = gridDim.x, el = rt_el(E), sy = max(rd, el);
+    float * s_x = sm_rt;                        // [NT][rd]
+    float * s_y = s_x + NT * rd;                // [NT][sy] (then the top-k scores, el entries)
+    float * s_l = s_y + NT * sy;                // [NT][el]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t0 = blockIdx.x;
+    // the state row of the wave's token (waves n < NT: token t + G n; tokens past T read row T - 1)
+    const int wn = min(wave, NT - 1);
+    float rn[J], nw[J], sb[4], mk[4];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = lane + 64 * j;
+        rn[j] = ld_or0(a.rh + (int64_t) min(t0 + G * wn, a.T - 1) * rd, i, rd);
+        nw[j] = ld_or0(a.norm_w, i, rd);
+    }
+    float b0[UO], b2[UO], blg[UO], bmk[UO];
+    rt_bias<UO>(a.b0, a.norm_w, rd, b0);
+    rt_bias<UO>(a.b2, a.norm_w, rd, b2);
+    rt_bias<UO>(a.logit_bias, a.sc_bias, E, blg);
+    rt_bias<UO>(a.mask, a.sc_bias, E, bmk);
+    const float * mask_or = a.mask ? a.mask : a.sc_bias;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < JE) {
+            const int i = lane + 64 * j;
+            sb[j] = ld_or0(a.sc_bias, i, E);
+            const float m = ld_or0(mask_or, i, E);
+            mk[j] = a.mask ? m : 0.0f;
+        } else {
+            sb[j] = 0.0f; mk[j] = 0.0f;
+        }
+    }
+    const int ldw = rd + 4;
+    float4 w0[UO][NM / 4], w2[UO][NM / 4], w4[UO][NM / 4];
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM, UO>(a.w0t, ldw, rd, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM, UO>(a.w2t, ldw, rd, w2);
+    __builtin_amdgcn_sched_barrier(0);
+    rt_load<NM, UO>(a.w4t, ldw, E, w4);
+#pragma unroll 1
+    for (int t = t0; t < a.T; t += NT * G) {
+        float rh[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) rh[j] = rn[j];
+        const int tn = t + NT * G;              // the next group's row of the wave's token
+        if (tn < a.T) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) rn[j] = ld_or0(a.rh + (int64_t) min(tn + G * wn, a.T - 1) * rd, lane + 64 * j, rd);
+        }
+        if (t != t0) lds_sync();                // the previous group's top-k has read s_y / s_l
+        // router RMS norm of the wave's token: double lane partials + wave tree
+        if (wave < NT) {
+            double part = 0.0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) if (lane + 64 * j < rd) part += (double) (rh[j] * rh[j]);
+            const double ss = wave_tree_d(part);
+            const float scale = 1.0f / sqrtf((float) (ss / (double) rd) + a.eps);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int i = lane + 64 * j;
+                if (i < rd) s_x[wave * rd + i] = (rh[j] * scale) * nw[j];
+            }
+        }
+        lds_sync();
+        rt_layer<0, NM, UO, NT>(w0, s_x, rd, s_y, b0, b0, false, false, rd, sy);
+        lds_sync();
+        rt_layer<0, NM, UO, NT>(w2, s_y, rd, s_x, b2, b2, false, false, sy, rd);
+        lds_sync();
+        rt_layer<1, NM, UO, NT>(w4, s_x, E, s_l, blg, bmk, a.logit_bias != nullptr, a.mask != nullptr, rd, el);
+        lds_sync();
+        const int tw = t + G * wave;            // (tokens past T: computed, not stored)
+        if (wave < NT && tw < a.T) router_select(a, tw, E, s_l + wave * el, s_y + wave * sy, sb, mk);
+    }
+}
+
 template <bool LOOP>
 __global__ void __launch_bounds__(RT_THREADS) k_router_tail(RouterArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sm_rt[];
     // router_dim in {32, 64, 128}, E <= 128 (host-checked)
-#define RT_E(NM_) do { if (a.E <= 64) router_tail_body<NM_, 1, LOOP>(a, sm_rt); \
-                       else router_tail_body<NM_, 2, LOOP>(a, sm_rt); } while (0)
+#define RT_E(NM_) do { if (LOOP) { if (a.E <= 64) router_tail_wide<NM_, 1>(a, sm_rt); else router_tail_wide<NM_, 2>(a, sm_rt); } \
+                       else { if (a.E <= 64) router_tail_body<NM_, 1, false>(a, sm_rt); else router_tail_body<NM_, 2, false>(a, sm_rt); } } while (0)
     switch (a.rd) {
         case 32:  RT_E(4); break;
         case 64:  RT_E(8); break;
