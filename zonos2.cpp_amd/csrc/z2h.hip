@@ -772,10 +772,15 @@ int launch_resnorm(z2h_ctx * ctx, int T, ResNormArgs a) {
             // token ids over tables of one type (F32, F16, Q8_0): the switch-free gather
             int tt = a.W > 0 ? a.tab_type[0] : -1;
             for (int k = 1; k < a.W; ++k) if (a.tab_type[k] != tt) tt = -1;
-            if (tt == 8) KL((k_resnorm<RN_EMBED, 8>), dim3(T), dim3(256), lds, ctx->stream, a);
-            else if (tt == 1) KL((k_resnorm<RN_EMBED, 1>), dim3(T), dim3(256), lds, ctx->stream, a);
-            else if (tt == 0) KL((k_resnorm<RN_EMBED, 0>), dim3(T), dim3(256), lds, ctx->stream, a);
+            // (10 table slots cover the 9 codebooks + text of Zonos2 models with 10/16 of the loads)
+            const bool w10 = a.W <= 10;
+#define RNE(T_) do { if (w10) KL((k_resnorm<RN_EMBED, T_, 10>), dim3(T), dim3(256), lds, ctx->stream, a); \
+                     else KL((k_resnorm<RN_EMBED, T_, MAX_TABLES>), dim3(T), dim3(256), lds, ctx->stream, a); } while (0)
+            if (tt == 8) RNE(8);
+            else if (tt == 1) RNE(1);
+            else if (tt == 0) RNE(0);
             else KL(k_resnorm<RN_EMBED>, dim3(T), dim3(256), lds, ctx->stream, a);
+#undef RNE
             break;
         }
         case RN_ACCUM: KL(k_resnorm<RN_ACCUM>, dim3(T), dim3(256), lds, ctx->stream, a); break;
@@ -1193,7 +1198,7 @@ int set_lds_limits(std::string & err) {
                    LDS_ATTR((k_attn_merge<H_, 1>)) LDS_ATTR((k_attn_merge<H_, 2>)) LDS_ATTR((k_attn_merge<H_, 4>)) LDS_ATTR((k_attn_merge<H_, 8>))
     LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
 #undef LDS_TF
-    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR((k_resnorm<RN_EMBED, 8>)) LDS_ATTR((k_resnorm<RN_EMBED, 1>)) LDS_ATTR((k_resnorm<RN_EMBED, 0>)) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
+    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR((k_resnorm<RN_EMBED, 8>)) LDS_ATTR((k_resnorm<RN_EMBED, 1>)) LDS_ATTR((k_resnorm<RN_EMBED, 0>)) LDS_ATTR((k_resnorm<RN_EMBED, 8, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 1, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 0, 10>)) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     return Z2H_OK;
 }

@@ -329,9 +329,10 @@ __device__ __forceinline__ float4 table_elem4_t(const uint8_t * row, int i0) {
 // last barrier (a barrier waits for the block's outstanding stores). One instantiation per mode
 // keeps each kernel's code to its own path. TT >= 0 (RN_EMBED): every table has GGUF type TT, and the
 // token's table rows are read with no type switch: all tables' loads of an element group go out
-// together (tables past W re-read the last one and are not added), the sum keeps the table order.
+// together (TW table slots, W <= TW; slots past W re-read the last table and are not added), the sum
+// keeps the table order.
 constexpr int RN_NV = 4;
-template <int MODE, int TT = -1>
+template <int MODE, int TT = -1, int TW = MAX_TABLES>
 __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     extern __shared__ float sm_rn[];
     float * xs = sm_rn;                // [d]
@@ -357,14 +358,14 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
                 if (i0 < d) xv[j] = *(const float4 *) (er + i0);
             }
         } else if constexpr (TT >= 0) {
-            const uint8_t * rows[MAX_TABLES];
+            const uint8_t * rows[TW];
             const int64_t rb = table_row_bytes(TT, d);
-            int ids[MAX_TABLES];                                   // every id read before any flag write
+            int ids[TW];                                           // every id read before any flag write
 #pragma unroll
-            for (int kk = 0; kk < MAX_TABLES; ++kk) ids[kk] = a.ids[(int64_t) t * a.W + min(kk, a.W - 1)];
+            for (int kk = 0; kk < TW; ++kk) ids[kk] = a.ids[(int64_t) t * a.W + min(kk, a.W - 1)];
             bool bad = false;
 #pragma unroll
-            for (int kk = 0; kk < MAX_TABLES; ++kk) {
+            for (int kk = 0; kk < TW; ++kk) {
                 const int kc = min(kk, a.W - 1);
                 const bool ok = ids[kk] >= 0 && ids[kk] < a.tab_rows[kc];
                 bad = bad || !ok;
@@ -375,13 +376,13 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
             for (int j = 0; j < RN_NV; ++j) {
                 if (1024 * j >= d) break;                          // (uniform) groups past the row
                 const int i0 = min(4 * (tid + 256 * j), d - 4);
-                float4 e[MAX_TABLES];
+                float4 e[TW];
 #pragma unroll
-                for (int kk = 0; kk < MAX_TABLES; ++kk) e[kk] = table_elem4_t<TT>(rows[kk], i0);
+                for (int kk = 0; kk < TW; ++kk) e[kk] = table_elem4_t<TT>(rows[kk], i0);
                 __builtin_amdgcn_sched_barrier(0);                 // every load of the group issues first
                 float4 x = e[0];
 #pragma unroll
-                for (int kk = 1; kk < MAX_TABLES; ++kk) {
+                for (int kk = 1; kk < TW; ++kk) {
                     const float4 y = add4(x, e[kk]);
                     x = kk < a.W ? y : x;
                 }
