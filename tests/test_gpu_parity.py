@@ -89,6 +89,35 @@ def test_c1_step_with_token_ids():
     assert_close("logits(ids)", got, want)
 
 
+def test_device_resident_step_equals_host_step():
+    """z2h_step_device (inputs and logits in device memory, enqueued on the caller's stream; the
+    entry the decode benchmark times) against z2h_step (host buffers): the same logits bit for bit,
+    with token ids and with injected embeddings. A step writes its K/V row at n_past, so repeating
+    it with the same inputs rewrites the same values."""
+    import torch
+    cfg, wl = configs.C1()
+    model, ctx, om, okv = _build(cfg, wl, seed=47)
+    inp = synth.step_inputs(cfg, wl)
+    T = len(wl.kv_lens)
+    dev = torch.device("cuda:0")
+    d_slot = torch.from_numpy(inp.slot_idx).to(dev)
+    d_npast = torch.from_numpy(inp.n_past).to(dev)
+    d_ids = torch.from_numpy(inp.ids).to(dev)
+    d_emb = torch.from_numpy(inp.emb).to(dev)
+    d_out = torch.empty((T, cfg.n_codebooks * cfg.audio_vocab), dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    for kind in ("ids", "emb"):
+        want = ctx.step(inp.slot_idx, inp.n_past, **({"ids": inp.ids} if kind == "ids" else {"emb": inp.emb}))
+        d_out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        ctx.step_device(T, d_slot.data_ptr(), d_npast.data_ptr(), inp.n_past,
+                        d_ids.data_ptr() if kind == "ids" else 0, d_emb.data_ptr() if kind == "emb" else 0,
+                        d_out.data_ptr(), stream=stream.cuda_stream)
+        stream.synchronize()
+        np.testing.assert_array_equal(d_out.cpu().numpy(), want, err_msg=kind)
+    ctx.close()
+
+
 def test_c1_batch_invariance():
     """A column's result does not depend on the other columns (reference --batch-test F.1/F.2)."""
     cfg, wl = configs.C1()
