@@ -671,9 +671,9 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
         if (!a.grouped && (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX) {
             // K split over the 4 waves of a block, one 16-row group per block; chunks of 8 tokens
-            // where that still gives at most one block per compute unit (a weight tile is then read
+            // where that still gives at most two blocks per compute unit (a weight tile is then read
             // by two blocks, which halves each block's staging and products)
-            const bool half = (int64_t) m0.tiles * ((a.n_tok + MT_G - 1) / MT_G) <= ctx->n_cu;
+            const bool half = (int64_t) m0.tiles * ((a.n_tok + MT_G - 1) / MT_G) <= 2 * ctx->n_cu;
             const int srows = half ? MT_G : MT;
             const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, srows);
             dim3 grid(m0.tiles, (a.n_tok + srows - 1) / srows, dual ? 1 : a.n_mats), block(256);
