@@ -7,8 +7,13 @@
 //  * Quantized matmuls follow ggml's CPU scheme: the fp32 activation row is first encoded in the
 //    weight type's dot type (Q8_K per 256 for Q4_K/Q6_K, Q8_0 per 32 for Q8_0, f16 for F16), the
 //    block dot is exact integer arithmetic, and each block's value is combined in fp32 as written
-//    in dot_block(). The order in which block values are summed is NOT pinned (ggml's SIMD order
-//    is unknown here): oracle and device may differ there, within the tolerance.
+//    in dot_block() / dot_row(). ggml's own SIMD summation order is not known here, so the order is
+//    fixed to the device matmuls' (dot_row), which makes every Q4_K / Q6_K / Q8_0 matmul output
+//    bit-identical on the CPU and the device for identical inputs. F16 matmuls run on the device's
+//    matrix cores, whose internal order is the hardware's: those agree within the tolerance only.
+//  * The rest of a decode step is specified the same way (rms_norm, qk_norm, z_sincos for RoPE,
+//    attention_fwd's 64-row chunks and their merge, z_softcap), so that a whole decode step of a
+//    Q4_K / Q6_K / Q8_0 model gives bit-identical hidden states, routing and logits.
 //  * The router (src/zonos2-graph.cpp:199-220) is specified exactly, including reduction order
 //    and the exp/erf implementations, so that identical router inputs give bit-identical logits,
 //    probabilities, top-k indices and weights on the CPU and on the device:
@@ -123,6 +128,61 @@ float z_erff(float x) {                                       // Abramowitz & St
 float z_gelu(float x) { return (0.5f * x) * (1.0f + z_erff(x * 0.70710678118654752f)); }
 float z_silu(float x) { return x / (1.0f + z_expf(-x)); }
 float z_sigmoid(float x) { return 1.0f / (1.0f + z_expf(-x)); }
+
+// exp in double: x = n ln2 + r (ln2 in two parts, Cody-Waite), exp(r) by the degree-13 Taylor
+// polynomial in Horner form with fma, times 2^n.
+double exp_d(double x) {
+    if (x < -745.0) return 0.0;
+    const double n = std::rint(x * 0x1.71547652b82fep+0);
+    double r = std::fma(-n, 0x1.62e42fee00000p-1, x);
+    r = std::fma(-n, 0x1.a39ef35793c76p-33, r);
+    static const double c[14] = {0x1.6124613a86d09p-33, 0x1.1eed8eff8d898p-29, 0x1.ae64567f544e4p-26, 0x1.27e4fb7789f5cp-22,
+                                 0x1.71de3a556c734p-19, 0x1.a01a01a01a01ap-16, 0x1.a01a01a01a01ap-13, 0x1.6c16c16c16c17p-10,
+                                 0x1.1111111111111p-7, 0x1.5555555555555p-5, 0x1.5555555555555p-3, 0.5, 1.0, 1.0};
+    double p = c[0];
+    for (int i = 1; i < 14; ++i) p = std::fma(p, r, c[i]);
+    return std::ldexp(p, (int) n);
+}
+
+// Logit softcap cap * tanh(x / cap) (graph.cpp:359-362). y = x * (1/cap) in fp32; tanh(|y|) in
+// double: below 2^-10 its Taylor series to y^5 (next term < 2^-60 relative), above it
+// 1 - 2 / (exp(2|y|) + 1); rounded to fp32, the sign restored, times cap.
+float z_softcap(float x, float cap) {
+    const float y = x * (1.0f / cap);
+    const double a = std::fabs((double) y);
+    double t;
+    if (a < 0x1p-10) {
+        const double a2 = a * a;
+        t = a + (a * a2) * (-1.0 / 3.0 + a2 * (2.0 / 15.0));
+    } else {
+        t = 1.0 - 2.0 / (exp_d(2.0 * a) + 1.0);
+    }
+    return std::copysign((float) t, y) * cap;
+}
+
+// sin and cos of a RoPE angle (0 <= x < 2^24): reduced modulo 2 pi in double, then by quadrant to
+// [-pi/4, pi/4] (rounded to fp32 there), degree-9 / degree-8 Taylor polynomials in fp32 with fma.
+void z_sincos(float x, float & s, float & c) {
+    const double xd = (double) x;
+    const double k2 = std::rint(xd * 0.15915494309189533577);
+    const double rd = std::fma(-k2, 6.28318530717958647692, xd);
+    const double q = std::rint(rd * 0.63661977236758134308);
+    const float r = (float) std::fma(-q, 1.57079632679489661923, rd);
+    const float r2 = r * r;
+    float sp = 2.75573192e-6f;
+    sp = std::fma(sp, r2, -1.98412698e-4f);
+    sp = std::fma(sp, r2, 8.33333333e-3f);
+    sp = std::fma(sp, r2, -1.66666667e-1f);
+    const float sr = std::fma(sp * r2, r, r);
+    float cp = 2.48015873e-5f;
+    cp = std::fma(cp, r2, -1.38888889e-3f);
+    cp = std::fma(cp, r2, 4.16666667e-2f);
+    cp = std::fma(cp, r2, -0.5f);
+    const float cr = std::fma(cp, r2, 1.0f);
+    const int qi = ((int) q) & 3;
+    s = qi == 0 ? sr : qi == 1 ? cr : qi == 2 ? -sr : -cr;
+    c = qi == 0 ? cr : qi == 1 ? -sr : qi == 2 ? -cr : sr;
+}
 
 // ------------------------------------------------------------------ tensors
 struct tensor {
@@ -284,8 +344,10 @@ float dot_block(int type, const uint8_t * blk, const qact & a, int64_t b) {
                 sumi += s * isum;
                 summ += m * (a.bsum[16 * b + 2 * j] + a.bsum[16 * b + 2 * j + 1]);
             }
-            const float d = from_f16(rd16(blk)), dmin = from_f16(rd16(blk + 2)), dx = a.d[b];
-            return (d * dx) * (float) sumi - (dmin * dx) * (float) summ;
+            // the superblock's value before the activation scale: d * sumi - dmin * summ with one
+            // rounding of the product sum (dot_row folds it with the activation scale)
+            const float d = from_f16(rd16(blk)), dmin = from_f16(rd16(blk + 2));
+            return std::fma(d, (float) sumi, -(dmin * (float) summ));
         }
         case 14: {
             const int8_t * sc = (const int8_t *) (blk + 192);
@@ -324,7 +386,11 @@ float dot_block(int type, const uint8_t * blk, const qact & a, int64_t b) {
     return NAN;
 }
 
-// one output element: sum of block values in ascending block order
+// One output element. The summation order of the block values is the device matmuls' (every
+// quantized matmul, any batch width): Q4_K folds each superblock value x (dot_block) with the
+// activation's superblock scale dx as s = fma(dx, x, s) in superblock order; Q8_0 adds the block
+// products of each 256-column unit (8 blocks) in order from zero, then adds the unit sums in order;
+// Q6_K adds the superblock values in order; F16 / F32 add 256-column chunk values in order.
 float dot_row(int type, const uint8_t * row, const qact & a) {
     const int64_t n = a.n;
     if (type == 0 || type == 1) {
@@ -336,9 +402,19 @@ float dot_row(int type, const uint8_t * row, const qact & a) {
             s += type == 0 ? ((const float *) row)[j] * a.f[j] : from_f16(rd16(row + 2 * j)) * from_f16(a.h[j]);
         return s;
     }
-    const int64_t be = blk_elems(type), bb = blk_bytes(type);
+    const int64_t be = blk_elems(type), bb = blk_bytes(type), nb = n / be;
     float s = 0.0f;
-    for (int64_t b = 0; b < n / be; ++b) s += dot_block(type, row + bb * b, a, b);
+    if (type == 12) {
+        for (int64_t b = 0; b < nb; ++b) s = std::fma(a.d[b], dot_block(type, row + bb * b, a, b), s);
+    } else if (type == 8) {
+        for (int64_t g = 0; g < nb; g += 8) {
+            float u = 0.0f;
+            for (int64_t b = g; b < std::min(nb, g + 8); ++b) u += dot_block(type, row + bb * b, a, b);
+            s = s + u;
+        }
+    } else {
+        for (int64_t b = 0; b < nb; ++b) s += dot_block(type, row + bb * b, a, b);
+    }
     return s;
 }
 
@@ -356,13 +432,50 @@ void matmul(const tensor & w, int64_t expert, int T, const float * x, float * y)
     });
 }
 
-// ggml rms_norm (double sum of fp32 squares, sequential) followed by the optional weight mul
+// ggml rms_norm: x / sqrt(mean(x^2) + eps), then the optional weight mul (graph.cpp:92-95). The sum of
+// squares is in double (as ggml's CPU sums it); its order is the device norm kernels': a 256-thread
+// block in which thread tid owns the 4-element groups i0 = 4 (tid + 256 j), j = 0, 1, ... (i0 < n) and
+// adds (((x0^2 + x1^2) + x2^2) + x3^2) per group in j order (squares rounded to fp32, sums in double);
+// each wave's 64 partials go through the xor butterfly and the four wave sums add left to right.
+double tree64d(double * p);
+double block_sumsq(const float * x, int64_t n) {
+    double ws[4];
+    for (int wv = 0; wv < 4; ++wv) {
+        double p[64];
+        for (int l = 0; l < 64; ++l) {
+            const int64_t tid = 64 * wv + l;
+            double ss = 0.0;
+            for (int64_t i0 = 4 * tid; i0 < n; i0 += 1024) {
+                double g = (double) (x[i0] * x[i0]);
+                for (int e = 1; e < 4; ++e) g = g + (i0 + e < n ? (double) (x[i0 + e] * x[i0 + e]) : 0.0);
+                ss += g;
+            }
+            p[l] = ss;
+        }
+        ws[wv] = tree64d(p);
+    }
+    return ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
 void rms_norm(const float * x, const float * w, int64_t n, float eps, float * y) {
-    double s = 0.0;
-    for (int64_t i = 0; i < n; ++i) s += (double) (x[i] * x[i]);
+    const double s = block_sumsq(x, n);
     const float mean = (float) (s / (double) n);
     const float scale = 1.0f / std::sqrt(mean + eps);
     for (int64_t i = 0; i < n; ++i) y[i] = w ? (x[i] * scale) * w[i] : x[i] * scale;
+}
+
+// Per-head QK RMSNorm (graph.cpp:113-116) times mul (|temp| for queries, 1 for keys), in the device's
+// order: lane l of one wave holds the dim pair (x[2l], x[2l+1]) (lanes past hd/2 hold zeros) and adds
+// its two squares in double; the 64 lanes go through the xor butterfly.
+void qk_norm(float * x, int hd, float eps, float mul) {
+    double p[64];
+    for (int l = 0; l < 64; ++l)
+        p[l] = 2 * l + 1 < hd ? (double) (x[2 * l] * x[2 * l]) + (double) (x[2 * l + 1] * x[2 * l + 1]) : 0.0;
+    const double ss = tree64d(p);
+    const float sc = 1.0f / std::sqrt((float) (ss / (double) hd) + eps);
+    for (int i = 0; i < hd; ++i) {
+        const float z = x[i] * sc;
+        x[i] = mul != 1.0f ? z * mul : z;
+    }
 }
 
 // ------------------------------------------------------------------ exact router primitives
@@ -423,12 +536,13 @@ void router_rms(const float * x, const float * w, int64_t n, float eps, float * 
 }
 
 // ------------------------------------------------------------------ RoPE (ggml NORMAL mode)
-// theta_i = pos * base^(-2i/hd), generated by repeated multiplication by base^(-2/hd) in fp32
+// theta_i = pos * base^(-2i/hd), generated by repeated multiplication by base^(-2/hd) in fp32; sin
+// and cos by z_sincos (the library's sin / cos are not part of the contract)
 void rope_inplace(float * x, int n_heads, int hd, int pos, float base) {
     const float theta_scale = std::pow(base, -2.0f / (float) hd);
     std::vector<float> c(hd / 2), s(hd / 2);
     float theta = (float) pos;
-    for (int i = 0; i < hd / 2; ++i) { c[i] = std::cos(theta); s[i] = std::sin(theta); theta *= theta_scale; }
+    for (int i = 0; i < hd / 2; ++i) { z_sincos(theta, s[i], c[i]); theta *= theta_scale; }
     for (int h = 0; h < n_heads; ++h) {
         float * v = x + (int64_t) h * hd;
         for (int i = 0; i < hd / 2; ++i) {
@@ -587,8 +701,12 @@ void dense_fwd(const orc_layer & ly, int T, const float * x, float * out) {
 }
 
 // Decode attention for T columns: QKV + gate projections, QK-norm, |temp|, RoPE, KV append (f16),
-// flash_attn_ext over the slot's band [0, n_past] (graph.cpp:107-175). Query rounded to f16 as
-// ggml's CPU flash attention does for an F16 cache; scores/softmax/PV accumulate in fp32/fp64.
+// flash_attn_ext over the slot's band [0, n_past] (graph.cpp:107-175). The query is rounded to f16 as
+// ggml's CPU flash attention does for an F16 cache. ggml's accumulation order inside flash_attn_ext
+// is not known here; the order is fixed to the device decode kernels' split softmax: chunks of
+// ATT_ROWS cache rows, each with its own max / exp sum / unnormalised P.V in fp32, merged with
+// weights exp(m_c - M) as written below.
+constexpr int ATT_ROWS = 64;
 void attention_fwd(const orc_model & m, orc_kv & kv, int L, int T, const int32_t * slot_idx, const int32_t * n_past,
                    const float * cur, float * q_cap, float * k_cap, float * v_cap, float * g_cap,
                    float * attn_o, float * attn_out) {
@@ -605,12 +723,11 @@ void attention_fwd(const orc_model & m, orc_kv & kv, int L, int T, const int32_t
     for (int t = 0; t < T; ++t) {
         for (int h = 0; h < nh; ++h) {
             float * qh = &q[((int64_t) t * nh + h) * hd];
-            rms_norm(qh, nullptr, hd, m.hp.qk_norm_eps, qh);
-            for (int i = 0; i < hd; ++i) qh[i] = qh[i] * temp[h];
+            qk_norm(qh, hd, m.hp.qk_norm_eps, temp[h]);
         }
         for (int h = 0; h < nkv; ++h) {
             float * kh = &k[((int64_t) t * nkv + h) * hd];
-            rms_norm(kh, nullptr, hd, m.hp.qk_norm_eps, kh);
+            qk_norm(kh, hd, m.hp.qk_norm_eps, 1.0f);
         }
         rope_inplace(&q[(int64_t) t * nh * hd], nh, hd, n_past[t], m.hp.rope_freq_base);
         rope_inplace(&k[(int64_t) t * nkv * hd], nkv, hd, n_past[t], m.hp.rope_freq_base);
@@ -624,31 +741,60 @@ void attention_fwd(const orc_model & m, orc_kv & kv, int L, int T, const int32_t
     if (g_cap) std::memcpy(g_cap, g.data(), g.size() * 4);
     const float scale = 1.0f / std::sqrt((float) hd);
     const int grp = nh / nkv;
+    // parts of the chunk merge's weighted sum: 8 / hpb, hpb = the smallest power of two <= 8 that
+    // divides the group and whose heads span whole 256-element blocks (else 1)
+    int hpb = 0;
+    for (int hb = 1; hb <= 8 && !hpb; hb *= 2)
+        if (grp % hb == 0 && (hb * hd) % 256 == 0) hpb = hb;
+    const int parts = 8 / (hpb ? hpb : 1);
     std::vector<float> o((size_t) T * nh * hd);
     parallel_for((int64_t) T * nh, [&](int64_t it) {
         const int t = (int) (it / nh), h = (int) (it % nh), gk = h / grp;
-        const int n = n_past[t] + 1;
+        const int n = n_past[t] + 1, nc = (n_past[t] + ATT_ROWS) / ATT_ROWS;
         const uint16_t * kb = kv.k[L].data() + (int64_t) slot_idx[t] * S * nkv * hd;
         const uint16_t * vb = kv.v[L].data() + (int64_t) slot_idx[t] * S * nkv * hd;
-        std::vector<float> qh(hd), s(n);
+        std::vector<float> qh(hd), mc(nc), lc(nc), oc((size_t) nc * hd, 0.0f);
         for (int i = 0; i < hd; ++i) qh[i] = from_f16(to_f16(q[((int64_t) t * nh + h) * hd + i]));
-        float mx = -INFINITY;
-        for (int p = 0; p < n; ++p) {
-            const uint16_t * kr = kb + ((int64_t) p * nkv + gk) * hd;
-            float acc = 0.0f;
-            for (int i = 0; i < hd; ++i) acc += qh[i] * from_f16(kr[i]);
-            s[p] = acc * scale;
-            mx = std::max(mx, s[p]);
+        // per chunk of ATT_ROWS rows: scores (fma chain over the head dims), chunk max, exp, sum
+        // (xor butterfly, lane = row), unnormalised P.V (fma chain over the rows)
+        for (int c = 0; c < nc; ++c) {
+            const int r0 = c * ATT_ROWS, nr = std::min(ATT_ROWS, n - r0);
+            float sc[ATT_ROWS], pe[64];
+            float mx = -INFINITY;
+            for (int r = 0; r < nr; ++r) {
+                const uint16_t * kr = kb + ((int64_t) (r0 + r) * nkv + gk) * hd;
+                float acc = 0.0f;
+                for (int i = 0; i < hd; ++i) acc = std::fma(qh[i], from_f16(kr[i]), acc);
+                sc[r] = acc * scale;
+                mx = std::max(mx, sc[r]);
+            }
+            for (int l = 0; l < 64; ++l) pe[l] = l < nr ? z_expf(sc[l] - mx) : 0.0f;
+            float * ov = &oc[(size_t) c * hd];
+            for (int r = 0; r < nr; ++r) {
+                const uint16_t * vr = vb + ((int64_t) (r0 + r) * nkv + gk) * hd;
+                for (int i = 0; i < hd; ++i) ov[i] = std::fma(pe[r], from_f16(vr[i]), ov[i]);
+            }
+            mc[c] = mx;
+            lc[c] = tree64(pe);
         }
-        double sum = 0.0;
-        std::vector<double> acc(hd, 0.0);
-        for (int p = 0; p < n; ++p) {
-            const float e = z_expf(s[p] - mx);
-            sum += e;
-            const uint16_t * vr = vb + ((int64_t) p * nkv + gk) * hd;
-            for (int i = 0; i < hd; ++i) acc[i] += (double) e * from_f16(vr[i]);
+        // merge: weights e_c = exp(m_c - M); denominator: lane l folds chunks l, l + 64, ... with fma,
+        // then the xor butterfly; numerator: part p folds chunks p, p + parts, ... with fma, and the
+        // parts add in order; out = num * (gate / den)
+        float M = -INFINITY;
+        for (int c = 0; c < nc; ++c) M = std::max(M, mc[c]);
+        std::vector<float> e(nc);
+        float dl[64];
+        for (int l = 0; l < 64; ++l) dl[l] = 0.0f;
+        for (int c = 0; c < nc; ++c) { e[c] = z_expf(mc[c] - M); dl[c % 64] = std::fma(e[c], lc[c], dl[c % 64]); }
+        const float den = tree64(dl);
+        const float gd = g[(int64_t) t * nh + h] / den;
+        for (int i = 0; i < hd; ++i) {
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int c = 0; c < nc; ++c) acc[c % parts] = std::fma(e[c], oc[(size_t) c * hd + i], acc[c % parts]);
+            float num = 0.0f;
+            for (int p = 0; p < parts; ++p) num += acc[p];
+            o[((int64_t) t * nh + h) * hd + i] = num * gd;
         }
-        for (int i = 0; i < hd; ++i) o[((int64_t) t * nh + h) * hd + i] = (float) (acc[i] / sum) * g[(int64_t) t * nh + h];
     });
     if (attn_o) std::memcpy(attn_o, o.data(), o.size() * 4);
     matmul(ly.wo, 0, T, o.data(), attn_out);
@@ -898,7 +1044,7 @@ static int step_impl(orc_model * m, orc_kv * kv, int T, const int32_t * slot_idx
     matmul(m->output, 0, T, cur.data(), logits);
     const float c = hp.logit_softcap;
     if (c > 0.0f)                                               // graph.cpp:359-362
-        for (int64_t i = 0; i < (int64_t) T * nout; ++i) logits[i] = std::tanh(logits[i] * (1.0f / c)) * c;
+        for (int64_t i = 0; i < (int64_t) T * nout; ++i) logits[i] = z_softcap(logits[i], c);
     return 0;
 }
 
@@ -969,10 +1115,9 @@ int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n
         for (int t = 0; t < n; ++t) {
             for (int h = 0; h < nh; ++h) {
                 float * qh = &q[((int64_t) t * nh + h) * hd];
-                rms_norm(qh, nullptr, hd, hp.qk_norm_eps, qh);
-                for (int i = 0; i < hd; ++i) qh[i] = qh[i] * temp[h];
+                qk_norm(qh, hd, hp.qk_norm_eps, temp[h]);
             }
-            for (int h = 0; h < nkv; ++h) { float * kh = &k[((int64_t) t * nkv + h) * hd]; rms_norm(kh, nullptr, hd, hp.qk_norm_eps, kh); }
+            for (int h = 0; h < nkv; ++h) { float * kh = &k[((int64_t) t * nkv + h) * hd]; qk_norm(kh, hd, hp.qk_norm_eps, 1.0f); }
             rope_inplace(&q[(int64_t) t * nh * hd], nh, hd, t, hp.rope_freq_base);
             rope_inplace(&k[(int64_t) t * nkv * hd], nkv, hd, t, hp.rope_freq_base);
             uint16_t * kc = kv->k[L].data() + ((int64_t) slot * S + t) * nkv * hd;
@@ -1019,7 +1164,7 @@ int orc_prefill(orc_model * m, orc_kv * kv, int slot, const int32_t * ids, int n
     rms_norm(&res[(int64_t) (n - 1) * d], f32p(m->output_norm), d, hp.rms_eps, hl.data());
     matmul(m->output, 0, 1, hl.data(), last_logits);
     const float c = hp.logit_softcap;
-    if (c > 0.0f) for (int64_t i = 0; i < nout; ++i) last_logits[i] = std::tanh(last_logits[i] * (1.0f / c)) * c;
+    if (c > 0.0f) for (int64_t i = 0; i < nout; ++i) last_logits[i] = z_softcap(last_logits[i], c);
     return 0;
 }
 
@@ -1099,6 +1244,8 @@ int orc_quant_act(int act, const float * x, int64_t n, int8_t * q, float * d, in
 }
 
 float orc_expf(float x) { return z_expf(x); }
+void orc_sincos(float x, float * s, float * c) { z_sincos(x, *s, *c); }
+float orc_softcap(float x, float cap) { return z_softcap(x, cap); }
 float orc_erff(float x) { return z_erff(x); }
 float orc_gelu_erf(float x) { return z_gelu(x); }
 float orc_silu(float x) { return z_silu(x); }

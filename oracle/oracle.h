@@ -117,6 +117,8 @@ int   orc_dequant(int type, const void * src, float * dst, int64_t n);
 int   orc_matmul(int type, const void * w, int64_t n_in, int64_t n_out, int T, const float * x, float * y);
 int   orc_quant_act(int act, const float * x, int64_t n, int8_t * q, float * d, int16_t * bsum, uint16_t * h);
 float orc_expf(float x);
+void  orc_sincos(float x, float * s, float * c);   // RoPE angle sin / cos (z_sincos)
+float orc_softcap(float x, float cap);             // cap * tanh(x / cap) (z_softcap)
 float orc_erff(float x);
 float orc_gelu_erf(float x);
 float orc_silu(float x);

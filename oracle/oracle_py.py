@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         "orc_quant_act": (i32, [i32, vp, i64, vp, vp, vp, vp]),
         "orc_expf": (f32, [f32]), "orc_erff": (f32, [f32]), "orc_gelu_erf": (f32, [f32]),
         "orc_silu": (f32, [f32]),
+        "orc_sincos": (None, [f32, C.POINTER(f32), C.POINTER(f32)]),
+        "orc_softcap": (f32, [f32, f32]),
         "orc_rope": (i32, [vp, i32, i32, i32, f32]),
         "orc_f32_to_f16": (C.c_uint16, [f32]), "orc_f16_to_f32": (f32, [C.c_uint16]),
         "orc_sample": (i32, [vp, i32, f32, i32, f32, f32, f32, i32, i32, i32, vp, i32, C.c_double, i32]),

@@ -3,13 +3,14 @@
 Every layer is checked with the device's own layer inputs (teacher forcing), so the bar holds per
 layer rather than after 24 layers of drift: attention from attn_in, the router from ffn_in
 (bit-exact), the experts from ffn_in with the device's routing, the residual folds exactly, and the
-head from the device's out_norm. End-to-end logits get a sanity bound only (routing feedback).
+head from the device's out_norm. End to end (the oracle's own step from the same ids and cache),
+every stage, the routing and the logits are bit-identical.
 """
 import numpy as np
 import pytest
 
 import oracle_py as O
-from helpers import assert_close, cos, explain_topk_flips, fill_kv, oracle_pair
+from helpers import assert_close, end_to_end_stages, fill_kv, oracle_pair, report_stages
 from zonos2_amd import configs, synth
 from zonos2_amd.z2h import Context
 
@@ -77,17 +78,31 @@ def test_c3_layers_teacher_forced(c3):
     mout = O.matmul(hw.type, hw.data, hw.ne[0], hw.ne[1], hn).astype(np.float64)
     cap_ = cfg.logit_softcap
     assert_close("head + softcap", got, cap_ * np.tanh(mout / cap_))
-    # end to end, routing decisions feed back through 24 layers: a top-k near-tie that rounds the
-    # other way in one layer changes every later layer's input. Every layer where the two runs route
-    # a token differently must be a near-tie: the oracle's margin between the swapped experts below
-    # the score movement the measured hidden-state difference causes there.
+    print(f"worst per-layer cos {worst:.7f}")
+
+
+def test_c3_end_to_end_bit_identical(c3):
+    """The whole 24-layer step, not teacher-forced: the oracle runs its own step from the same token
+    ids and KV cache. Every quantized matmul, norm, RoPE, attention split and merge, router and head
+    follows one fixed operation order on both sides, so every stage of every layer, the routing and
+    the logits are the same bits. The captured step's logits equal the uncaptured step's."""
+    cfg, wl, model, ctx, om, okv = c3
+    T = len(wl.kv_lens)
+    # (the oracle's step rewrites row n_past of every slot in each layer before that layer's
+    # attention, so rows appended by other tests do not leak in)
+    inp = synth.step_inputs(cfg, wl)
+    ctx.set_capture(False)
+    plain = ctx.step(inp.slot_idx, inp.n_past, ids=inp.ids)
+    ctx.set_capture(True)
+    got = ctx.step(inp.slot_idx, inp.n_past, ids=inp.ids)
+    assert np.array_equal(plain.view(np.uint32), got.view(np.uint32)), "capture changed the step"
     want, ocap = O.step(om, okv, inp.slot_idx, inp.n_past, ids=inp.ids, capture=True)
-    gcap = {L: {"ffn_in": rd(L, "ffn_in").reshape(T, d), "sel": rd(L, "sel").reshape(T, k)} for L in range(cfg.n_layer)}
-    orc = {L: {"ffn_in": ocap["ffn_in"][L]} for L in range(cfg.n_layer)}
-    flips = explain_topk_flips(om, model, cfg, T, gcap, orc, "C3")
-    print(f"worst per-layer cos {worst:.7f}; end-to-end logits cos {cos(got, want):.7f} maxabs {np.abs(got - want).max():.3e}; "
-          f"{len(flips)} layers with a top-k near-tie flip")
-    assert cos(got, want) >= 0.99
+    rows = end_to_end_stages(ctx, ocap, cfg, T)
+    report_stages("C3", rows, got, want)
+    for L in range(cfg.n_layer):
+        assert np.array_equal(ctx.read_capture(L, "sel", T).reshape(T, -1), ocap["sel"][L]), f"L{L}: routing differs"
+    assert not rows, f"first differing stage: L{rows[0][0]} {rows[0][1]}"
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "logits differ"
 
 
 def test_c3_step_deterministic_and_slot_independent(c3):

@@ -5,6 +5,7 @@ checked against the correctly rounded double-precision functions. RoPE is checke
 defining properties (norm preservation, identity at position 0, relative-position invariance of
 q.k) and attention through a float64 softmax restatement on tiny cases plus invariants.
 """
+import ctypes as C
 import math
 
 import numpy as np
@@ -40,6 +41,42 @@ def test_erf_abs_error():
     # |erf| = 1 adds up to ~2 ulp(1) = 2.4e-7
     assert err <= 4e-7
     assert L.orc_erff(0.0) == 0.0 and L.orc_erff(-1.0) == -L.orc_erff(1.0)
+
+
+def _sincos(x):
+    s, c = C.c_float(), C.c_float()
+    L.orc_sincos(float(x), C.byref(s), C.byref(c))
+    return s.value, c.value
+
+
+def test_rope_sincos_against_double():
+    # RoPE angles pos * base^(-2i/hd): every quadrant, multiples of pi/2 (the reduction's edges) and
+    # large positions; the reduction is in double, the polynomials in fp32 (< 4e-9), so the error is
+    # the fp32 rounding of the reduced angle and of the result: < 1.5e-7
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([rng.uniform(0, 8192, 20000), np.arange(0, 40) * (math.pi / 4), [0.0, 1e-30, 2 ** 23]])
+    worst = 0.0
+    for x in xs.astype(np.float32):
+        s, c = _sincos(x)
+        worst = max(worst, abs(s - math.sin(float(x))), abs(c - math.cos(float(x))))
+    assert worst < 1.5e-7, worst
+    assert _sincos(0.0) == (0.0, 1.0)
+
+
+def test_softcap_against_double_tanh():
+    # cap * tanh(x / cap) for cap 15: within 2 fp32 ulps of the result over the logit range, odd,
+    # exact at 0, saturating at +-cap; the small-|y| Taylor branch and the exp branch meet at 2^-10
+    cap = 15.0
+    xs = np.concatenate([np.linspace(-200, 200, 40001), 15 * 2.0 ** -10 * np.linspace(0.9, 1.1, 2001),
+                         [1e-30, 1e-8, 3e-4]]).astype(np.float32)
+    worst = 0
+    for x in xs:
+        got = L.orc_softcap(float(x), cap)
+        want = np.float32(cap * math.tanh(float(np.float32(float(x) * np.float32(1.0 / cap)))))
+        worst = max(worst, ulp_dist(got, want))
+        assert L.orc_softcap(-float(x), cap) == -got
+    assert worst <= 2, worst
+    assert L.orc_softcap(0.0, cap) == 0.0 and L.orc_softcap(1e6, cap) == cap
 
 
 def test_gelu_silu():

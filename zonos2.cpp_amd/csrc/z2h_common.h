@@ -60,6 +60,23 @@ __device__ __forceinline__ double z_exp_d(double x) {
 }
 __device__ __forceinline__ float z_expf_cr(float x) { return (float) z_exp_d((double) x); }
 
+// Logit softcap cap * tanh(x / cap): y = x * (1/cap) in fp32; tanh(|y|) in double, below 2^-10 by
+// its Taylor series to y^5 (next term < 2^-60 relative), above it as 1 - 2 / (exp(2|y|) + 1); rounded
+// to fp32, the sign restored, times cap. Every operation is IEEE double / fp32 as written, so the
+// CPU oracle reproduces it bit for bit.
+__device__ __forceinline__ float z_softcap(float x, float cap) {
+    const float y = x * (1.0f / cap);
+    const double a = fabs((double) y);
+    double t;
+    if (a < 0x1p-10) {
+        const double a2 = a * a;
+        t = a + (a * a2) * (-1.0 / 3.0 + a2 * (2.0 / 15.0));
+    } else {
+        t = 1.0 - 2.0 / (z_exp_d(2.0 * a) + 1.0);
+    }
+    return copysignf((float) t, y) * cap;
+}
+
 // erf: Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7).
 __device__ __forceinline__ float z_erff(float x) {
     const float ax = fabsf(x);

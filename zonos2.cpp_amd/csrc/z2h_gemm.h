@@ -95,7 +95,7 @@ __device__ __forceinline__ void gemm_rows(const GemmArgs & a, int e, int c0, int
 }
 
 __device__ __forceinline__ float gemm_epi(const GemmArgs & a, float y, int it) {
-    if (a.epi == EPI_SOFTCAP) return tanhf(y * (1.0f / a.cap)) * a.cap;
+    if (a.epi == EPI_SOFTCAP) return z_softcap(y, a.cap);
     if (a.epi == EPI_ROUTE_W) return y * a.route_w[it];
     return y;
 }

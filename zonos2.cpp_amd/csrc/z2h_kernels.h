@@ -909,7 +909,7 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
             if (row >= a.rows) continue;
             const int it = a.grouped ? s_list[c0 + tt] : item0 + c0 + tt;
             float y = v;
-            if (a.epi == EPI_SOFTCAP) y = tanhf(v * (1.0f / a.cap)) * a.cap;
+            if (a.epi == EPI_SOFTCAP) y = z_softcap(v, a.cap);
             else if (a.epi == EPI_ROUTE_W) y = v * a.route_w[it];
             a.out[m][(int64_t) it * a.out_ld + row] = y;
         }
@@ -1362,7 +1362,7 @@ k_gemv_mfma(GemvArgs a) {
             const int it = a.grouped ? s_list[c0 + t] : c0 + t;
             float y = acc0[i];
             if (DUAL) y = acc1[i] * z_silu(acc0[i]);
-            else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+            else if (a.epi == EPI_SOFTCAP) y = z_softcap(y, a.cap);
             else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
             a.out[m][(int64_t) it * a.out_ld + row] = y;
         }
@@ -1456,7 +1456,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         }
         float y = g;
         if (DUAL) y = up * z_silu(g);
-        else if (a.epi == EPI_SOFTCAP) y = tanhf(y * (1.0f / a.cap)) * a.cap;
+        else if (a.epi == EPI_SOFTCAP) y = z_softcap(y, a.cap);
         else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
         a.out[m][(int64_t) it * a.out_ld + row] = y;
     }
@@ -1632,7 +1632,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     constexpr int KST = HD + 8;                    // LDS row stride of K (halfs): breaks bank aliasing
     __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
-    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];     // f16 pairs
+    __shared__ __attribute__((aligned(16))) float s_q[GRP][HD];        // f16-rounded queries
     __shared__ float s_p[ATT_CH][GRP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
     int n_items, t, np, slot, c, g;
@@ -1692,7 +1692,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
                 float y0, y1;
                 norm_rope<HD>(xq[j][0], xq[j][1], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
                 if (lane < NP) {
-                    s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
+                    *(float2 *) &s_q[h][2 * lane] = make_float2(h2f(f2h(y0)), h2f(f2h(y1)));
                     if (a.cap_q && c == 0) {
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
@@ -1731,16 +1731,19 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             *(uint32_t *) &s_v[(nr - 1) * HD + 2 * lane] = nv;
         }
         lds_sync();
-        // ---- scores: one (row, head) per thread
+        // ---- scores: one (row, head) per thread, an fp32 fma chain over the head dims in order (the
+        // f16 x f16 products are exact in fp32, so each step rounds once)
         for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
             const int r = sidx / GRP, h = sidx % GRP;
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < RW; ++j) {
                 const uint4 kk = *(const uint4 *) &s_k[r * KST + 8 * j];
-                const uint4 qq = *(const uint4 *) &s_q[h][4 * j];
-                acc = fdot2(kk.x, qq.x, acc); acc = fdot2(kk.y, qq.y, acc);
-                acc = fdot2(kk.z, qq.z, acc); acc = fdot2(kk.w, qq.w, acc);
+                const float4 qa = *(const float4 *) &s_q[h][8 * j], qb = *(const float4 *) &s_q[h][8 * j + 4];
+                acc = __builtin_fmaf(qa.x, h2f(kk.x & 0xffffu), acc); acc = __builtin_fmaf(qa.y, h2f(kk.x >> 16), acc);
+                acc = __builtin_fmaf(qa.z, h2f(kk.y & 0xffffu), acc); acc = __builtin_fmaf(qa.w, h2f(kk.y >> 16), acc);
+                acc = __builtin_fmaf(qb.x, h2f(kk.z & 0xffffu), acc); acc = __builtin_fmaf(qb.y, h2f(kk.z >> 16), acc);
+                acc = __builtin_fmaf(qb.z, h2f(kk.w & 0xffffu), acc); acc = __builtin_fmaf(qb.w, h2f(kk.w >> 16), acc);
             }
             s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
         }
