@@ -381,27 +381,11 @@ def mixed_pass(np, Context, synth, cfg, mdl):
     2088 rows through every layer in one z2h_step_mixed call (host API: ids up, 40 logit rows down).
     Median of 3 after one warm-up; algorithmic FLOPs count the expert, projection and attention-score
     products (2 per multiply-add)."""
-    rng = np.random.default_rng(55)
-    n_pre, n_dec, chunk = 8, 32, 256
-    plen = rng.integers(300, 1201, n_pre)
-    r0 = [int(rng.integers(0, (int(p) - chunk) // 256 + 1)) * 256 for p in plen]
-    dlen = [int(x) for x in rng.integers(32, 1201, n_dec)]
-    cap = max(max(r + chunk + 1 for r in r0), max(dlen) + 1)
-    slots, npast, emap, groups = [], [], [], []
-    for i, r in enumerate(r0):
-        g = []
-        for j in range(chunk + 1):                 # the speaker row, then the chunk's prompt rows
-            slots.append(i); npast.append(r + j); emap.append(i if j == 0 else -1); g.append(len(slots) - 1)
-        groups.append(g)
-    for i, n in enumerate(dlen):
-        slots.append(n_pre + i); npast.append(n); emap.append(-1); groups.append([len(slots) - 1])
-    R = len(slots)
-    W = cfg.n_codebooks + 1
-    ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (R, cfg.n_codebooks)),
-                          rng.integers(0, cfg.text_vocab + 1, (R, 1))], axis=1).astype(np.int32)
-    assert ids.shape[1] == W
-    spk = rng.standard_normal((n_pre, cfg.spk_dim)).astype(np.float32)   # speaker vectors, projected per pass
-    out_rows = np.array([g[-1] for g in groups], np.int32)
+    from zonos2_amd.configs import mixed_layout
+    lay = mixed_layout(cfg)                        # seed 55: 8 x (256 + 1) + 32 = 2088 rows
+    n_pre, n_dec, chunk = len(lay.r0), len(lay.dlen), 256
+    r0, dlen, cap, spk = lay.r0, lay.dlen, lay.cap, lay.spk
+    R = len(lay.slots)
     mctx = Context(None, n_pre + n_dec, cap, model=mdl, max_rows=R)
     for L in range(cfg.n_layer):
         for i, r in enumerate(r0):
@@ -411,8 +395,9 @@ def mixed_pass(np, Context, synth, cfg, mdl):
         for i, n in enumerate(dlen):
             k, v = synth.kv_rows(cfg, L, n_pre + i, n, 11)
             mctx.kv_write(L, n_pre + i, 0, k, v)
-    args = (np.array(slots, np.int32), np.array(npast, np.int32), ids, out_rows)
-    emap_a = np.array(emap, np.int32)
+    args = (lay.slots, lay.npast, lay.ids, lay.out_rows)
+    emap_a = lay.emap
+    npast = lay.npast
 
     def one_pass():
         emb = mctx.speaker_embed(spk)                  # spk_lda -> spk_proj on the device (graph.cpp:262-297)

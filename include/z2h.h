@@ -182,7 +182,7 @@ int z2h_moe_forward_device(z2h_ctx * ctx, int layer, int n_tokens, const float *
  * null stream) without synchronizing. d_x [n_tokens][n_embd] (the layer's ffn_in), d_state_in
  * ([n_tokens][router_dim] or NULL), d_state_out (NULL, or [n_tokens][router_dim] receiving this
  * layer's router state), d_out [n_tokens][n_embd]. Results are bit-identical to z2h_moe_forward_device.
- * Errors: z2h_model_last_error. */
+ * The caller's current HIP device is the same on return. Errors: z2h_model_last_error. */
 int z2h_model_moe_forward_noalloc(z2h_model * m, int layer, int n_tokens, const float * d_x, const float * d_state_in,
                                   float * d_state_out, float * d_out, void * stream);
 

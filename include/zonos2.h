@@ -23,6 +23,7 @@
 //   zonos2_batch_step           src/zonos2.h:291-294, src/zonos2-graph.cpp:762-837
 //   zonos2_batch_slot_logits    src/zonos2.h:296-298, src/zonos2-graph.cpp:839-841
 //   zonos2_slot_sample          src/zonos2.h:300-306, src/zonos2-graph.cpp:843-870
+//   zonos2_generate             src/zonos2.h:308-325, src/zonos2-graph.cpp:515-605 (recompute), 877-981 (KV)
 #pragma once
 
 #include "z2h.h"
@@ -224,3 +225,21 @@ bool zonos2_batch_sample(zonos2_batch_ctx & bc, const std::vector<zonos2_slot *>
 bool zonos2_slot_sample(const zonos2_model & model, zonos2_slot & slot, zonos2_sampler & smp,
                         const float * logits, std::vector<int32_t> & out_codes,
                         int max_frames, const zonos2_frame_cb & on_frame);
+
+// Autoregressive generation of one sequence. use_kv = true: one prefill, then one decode step per
+// frame against the KV cache (the batch runtime at one slot; with spk, spk_emotion_delta and
+// sp.emotion_cfg_scale != 1 a second slot is prefilled without the delta and every frame is drawn
+// from uncond + scale * (cond - uncond)). use_kv = false: every frame recomputes a full prefill of
+// the prompt and the frames so far (O(n^2)). prompt_ids: row-major [n0][n_codebooks + 1] floats.
+// Appends the codes to out_codes ([n_frames][n_codebooks]), sets eos_frame (-1 if none), returns
+// the frame count (0 on a failed start). spk ([spk_dim]) replaces row spk_pos's embedding during the
+// prefill by spk_proj(spk_lda(spk)) (+ spk_emotion_delta [n_embd]). out_full_ids (optional) receives
+// the consumed sequence [n0 + n_frames][n_codebooks + 1]: the prompt rows, then each frame's codes and
+// the text pad. on_frame streams frames; returning false stops.
+int zonos2_generate(const zonos2_model & model, const float * prompt_ids, int n0,
+                    int max_frames, const zonos2_sampling & sp,
+                    std::vector<int32_t> & out_codes, int & eos_frame, bool use_kv = true,
+                    const float * spk = nullptr, int spk_pos = 0,
+                    std::vector<int32_t> * out_full_ids = nullptr,
+                    const zonos2_frame_cb & on_frame = {},
+                    const float * spk_emotion_delta = nullptr);

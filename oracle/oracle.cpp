@@ -86,7 +86,7 @@ uint16_t to_f16(float f) {
     return (uint16_t) (s | r);
 }
 
-float from_f16(uint16_t h) {
+float from_f16_calc(uint16_t h) {
     const uint32_t s = (uint32_t) (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
     float f;
     if (e == 0) f = std::ldexp((float) m, -24);
@@ -94,6 +94,14 @@ float from_f16(uint16_t h) {
     else f = std::ldexp((float) (m | 0x400u), (int) e - 25);
     return s ? -f : f;
 }
+
+// every f16 value's float, computed once (the F16 matmuls convert two values per product)
+struct f16_table {
+    float v[65536];
+    f16_table() { for (uint32_t h = 0; h < 65536; ++h) v[h] = from_f16_calc((uint16_t) h); }
+};
+const f16_table g_f16;
+inline float from_f16(uint16_t h) { return g_f16.v[h]; }
 
 // ------------------------------------------------------------------ exact elementwise functions
 float z_expf(float x) {

@@ -77,6 +77,9 @@ def end_to_end_stages(ctx, ocap, cfg, T):
             o = np.asarray(ocap[st][L])
             if st in ("sel", "weights"):                      # device [T][k_L], oracle [T][K]
                 g, o = g.ravel()[:T * k].reshape(T, k), o.reshape(T, K)[:, :k]
+            elif st in ("router_logits", "probs"):           # device [T][E_L], oracle [T][E]
+                E = cfg.n_exp(L)
+                g, o = g.ravel()[:T * E].reshape(T, E), o.reshape(T, -1)[:, :E]
             g, o = g.reshape(T, -1), o.reshape(T, -1)
             if g.dtype == np.float32:
                 neq = g.view(np.uint32) != o.view(np.uint32)

@@ -126,3 +126,28 @@ def test_batch_api_refuses_a_step_past_slot_capacity(root):
              "--dup", "--max-frames", "64", "--prompt-len", "250", "--slot-cap", "256")
     assert r.returncode == 3, r.stdout + r.stderr
     assert "batch-test: step refused: slot" in r.stdout and "at n_past 256 (slot capacity 256)" in r.stdout
+
+
+def test_generate_matches_batch_api_loops(root):
+    """zonos2_generate (src/zonos2.h:308-325) on the reference's fixture: the KV path equals a
+    one-slot batch loop, the emotion-guided KV path a two-slot loop mixing uncond + scale *
+    (cond - uncond), the recompute path a prefill of the growing sequence per frame; greedy and
+    sampled, with out_full_ids and on_frame's early stop (tests/native/generate_kat.cpp)."""
+    kat = BUILD / "generate_kat"
+    assert kat.exists(), "generate_kat not built (python __graft_entry__.py)"
+    r = subprocess.run([str(kat), str(root / FIXTURE)], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0 and "generate KAT: OK" in r.stdout, r.stdout + r.stderr
+
+
+def test_generate_cli_reports_frames(root):
+    r = _cli("--model", str(root / FIXTURE), "--generate", "--greedy", "--max-frames", "16", "--prompt-len", "10")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "generate: prompt [10, " in r.stdout and "kv-cache" in r.stdout
+    assert "generate: " in r.stdout and "frames, eos_frame=" in r.stdout and "  frame0:" in r.stdout
+    r2 = _cli("--model", str(root / FIXTURE), "--generate", "--greedy", "--max-frames", "16", "--prompt-len", "10", "--no-kv")
+    assert r2.returncode == 0 and "recompute" in r2.stdout, r2.stdout + r2.stderr
+    # the first frame comes from the prompt's prefill on both paths
+    f0 = [l for l in r.stdout.splitlines() if l.startswith("  frame0:")]
+    f0r = [l for l in r2.stdout.splitlines() if l.startswith("  frame0:")]
+    assert f0 == f0r

@@ -153,12 +153,14 @@ def test_c2_moe_layer_vs_oracle():
     assert_close("moe out", got, out)
 
 
-def test_router_ties_go_to_the_lower_expert_index():
+@pytest.mark.parametrize("T", [4, 100], ids=["per-token-router", "wide-router"])
+def test_router_ties_go_to_the_lower_expert_index(T):
     """Exact ties in the selection scores through the device router: with router_mlp4 zero every
     router logit is 0, so the softmax gives exactly 1/E (1/7 under a one-expert mask) to every kept
     expert, and router_bias decides the order with tied values. north_star's contract: scores
     descending, ties to the lower expert index. The device's top-k ids, weights and grouping must be
-    the oracle's, and the ids the closed-form answer."""
+    the oracle's, and the ids the closed-form answer. 4 tokens take the per-token router tail
+    (k_router_tail<false>), 100 the wide passes' (k_router_down_t + k_router_tail<true>, from 65 rows)."""
     cfg, wl = configs.C1()
     model = synth.generate_model(cfg, 45)
     E, k, d = cfg.n_expert, cfg.top_k, cfg.n_embd
@@ -168,10 +170,9 @@ def test_router_ties_go_to_the_lower_expert_index():
             continue
         model[f"blk.{L}.router_mlp4.weight"].data[...] = 0
         model[f"blk.{L}.router_bias"].data[...] = bias.view(model[f"blk.{L}.router_bias"].data.dtype)
-    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx = Context(cfg.hparams(), max(T, wl.n_slots), wl.slot_cap, max_rows=T)
     ctx.upload(model)
     om = O.OracleModel(cfg.hparams(), model)
-    T = wl.n_slots
     x = synth.gen_normal_f32((T, d), 3, "inputs.ties")
     L = next(L for L in range(cfg.n_layer) if cfg.expert_used[L])
     ctx.set_capture(True)

@@ -2,8 +2,9 @@
 the library's static device scratch, no allocation) against the existing entry point that takes its
 buffers from a context (z2h_moe_forward_device, through z2h_moe_forward): bit-identical outputs and
 router state on two calls in a row, the second with fewer tokens (the scratch keeps the first call's
-contents), for Q4_K experts (fused gate/up + SwiGLU kernels) and Q6_K experts (separate gate and up,
-SwiGLU pass); a call whose buffers exceed the scratch is refused before any launch."""
+contents), for Q4_K experts (fused gate/up + SwiGLU GEMVs, and from 65 tokens the sorted route table
+and the int8 MFMA GEMMs), Q6_K and Q8_0 experts (the m16 GEMVs) and F16 experts (the fp16 MFMA GEMMs);
+a call whose buffers exceed the scratch is refused before any launch."""
 import dataclasses
 
 import numpy as np
@@ -20,16 +21,20 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
 
 
-@pytest.mark.parametrize("bulk", [configs.Q4_K, configs.Q6_K], ids=["q4_k", "q6_k"])
-def test_noalloc_moe_layer_matches_the_context_entry_point(bulk):
+# tokens per call: Q4_K adds a 96-token call (from 65 rows the wide path: k_router_down_t,
+# k_router_tail<true>, k_route_sort and the k_gemm_q4k expert GEMMs, their tables in the scratch)
+@pytest.mark.parametrize("bulk,calls", [(configs.Q4_K, (96, 40, 7)), (configs.Q6_K, (40, 7)), (configs.Q8_0, (40, 7)),
+                                        (configs.F16, (24, 7))], ids=["q4_k", "q6_k", "q8_0", "f16"])
+def test_noalloc_moe_layer_matches_the_context_entry_point(bulk, calls):
     cfg, wl = configs.C2()
     cfg = dataclasses.replace(cfg, bulk=bulk)
     model = synth.generate_model(cfg, 42)
     m = Model(cfg.hparams(), model)
-    ctx = Context(None, 64, 256, model=m)
+    ctx = Context(None, 128, 256, model=m, max_rows=128)
     ctx.set_capture(True)
     rd = cfg.router_dim
-    for T in (40, 7):                                  # second call: fewer tokens, scratch holds the first call's data
+    dev0 = torch.cuda.current_device()
+    for T in calls:                                    # later calls: fewer tokens, scratch holds the earlier data
         print(f"{cfg.name} T={T}", flush=True)
         x = synth.gen_normal_f32((T, cfg.n_embd), 11 + T, "inputs.noalloc")
         st = synth.gen_normal_f32((T, rd), 12 + T, "state.noalloc")
@@ -43,6 +48,7 @@ def test_noalloc_moe_layer_matches_the_context_entry_point(bulk):
         got = dout.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"T={T}: outputs differ"
         assert np.array_equal(dso.cpu().numpy().view(np.uint32), want_state.view(np.uint32)), f"T={T}: router state differs"
+        assert torch.cuda.current_device() == dev0
     # state kept in the scratch (d_state_out NULL): same outputs
     dout2 = torch.empty((7, cfg.n_embd), dtype=torch.float32, device="cuda:0")
     m.moe_forward_noalloc(0, 7, dx.data_ptr(), ds.data_ptr(), 0, dout2.data_ptr())

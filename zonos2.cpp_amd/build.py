@@ -70,7 +70,7 @@ def build_api(force: bool = True) -> tuple[Path, Path]:
     lib = BUILD / "libzonos2.so"
     cli = BUILD / "zonos2-batch"
     host = PKG / "host"
-    srcs = [host / "zonos2_batch.cpp", host / "gguf.cpp", host / "zonos2_sampler.cpp"]
+    srcs = [host / "zonos2_batch.cpp", host / "gguf.cpp", host / "zonos2_sampler.cpp", host / "zonos2_generate.cpp"]
     deps = srcs + [ROOT / "include" / "zonos2.h", ROOT / "include" / "zonos2-sampler.h", ROOT / "include" / "z2h.h", host / "gguf.h"]
     inc = [f"-I{ROOT / 'include'}", f"-I{host}"]
     rpath = "-Wl,-rpath,$ORIGIN"
@@ -81,6 +81,11 @@ def build_api(force: bool = True) -> tuple[Path, Path]:
     if force or _stale(cli, [cli_src, lib]):
         _run(["g++", *HOST_FLAGS, *inc, str(cli_src), "-o", str(cli), f"-L{BUILD}", "-lzonos2",
               "-lzonos2_hip", "-lzonos2_host", rpath])
+    # the generation known-answer program the GPU tests run (tests/native/generate_kat.cpp)
+    kat_src = ROOT / "tests" / "native" / "generate_kat.cpp"
+    kat = BUILD / "generate_kat"
+    if kat_src.exists() and (force or _stale(kat, [kat_src, lib])):
+        _run(["g++", *HOST_FLAGS, *inc, str(kat_src), "-o", str(kat), f"-L{BUILD}", "-lzonos2", "-lzonos2_hip", rpath])
     return lib, cli
 
 

@@ -1338,9 +1338,11 @@ namespace {
 constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 void * g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+int g_scratch_cus[NOALLOC_MAX_DEVICES] = {};
 
-// the device address of `scratch` on `device` (looked up on the first call for that device)
-int scratch_address(int device, void ** out, std::string & err) {
+// the device address of `scratch` on `device` and the device's compute-unit count (both looked up on
+// the first call for that device, with that device current; the caller's current device is kept)
+int scratch_address(int device, void ** out, int * n_cu, std::string & err) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (device < 0 || device >= NOALLOC_MAX_DEVICES) { err = "device index out of range"; return Z2H_EINVAL; }
     if (!g_scratch_ptr[device]) {
@@ -1349,13 +1351,29 @@ int scratch_address(int device, void ** out, std::string & err) {
         if (hipSetDevice(device) != hipSuccess) { err = "hipSetDevice failed"; return Z2H_EDEVICE; }
         void * p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        int cus = 0;
+        const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
         (void) hipSetDevice(keep);
         if (e != hipSuccess || !p) { err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e); return Z2H_EDEVICE; }
+        if (e2 != hipSuccess || cus <= 0) { err = "compute-unit count query failed"; return Z2H_EDEVICE; }
         g_scratch_ptr[device] = p;
+        g_scratch_cus[device] = cus;
     }
     *out = g_scratch_ptr[device];
+    *n_cu = g_scratch_cus[device];
     return Z2H_OK;
 }
+
+// makes `device` current for a scope and restores the caller's current device on every exit path
+struct DeviceScope {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceScope(int device) {
+        if (hipGetDevice(&prev) != hipSuccess) return;
+        ok = prev == device || hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceScope() { if (ok && prev >= 0) (void) hipSetDevice(prev); }
+};
 } // namespace
 
 // ====================================================================== C ABI
@@ -1924,13 +1942,15 @@ int z2h_model_moe_forward_noalloc(z2h_model * mdl, int layer, int T, const float
         return seterr(mdl, Z2H_EINVAL, "z2h_model_moe_forward_noalloc: " + std::to_string(T) + " tokens need " + std::to_string(total) +
                                        " bytes of scratch; the static scratch holds " + std::to_string(NOALLOC_SCRATCH_BYTES));
     void * base = nullptr;
+    int n_cu = 0;
     std::string err;
-    if (int rc = scratch_address(mdl->device, &base, err)) return seterr(mdl, rc, err);
-    if (hipSetDevice(mdl->device) != hipSuccess) return seterr(mdl, Z2H_EDEVICE, "hipSetDevice failed");
+    if (int rc = scratch_address(mdl->device, &base, &n_cu, err)) return seterr(mdl, rc, err);
+    DeviceScope on(mdl->device);                      // the caller's current device comes back on return
+    if (!on.ok) return seterr(mdl, Z2H_EDEVICE, "hipSetDevice failed");
     size_t off = 0;
     for (const Piece & pc : plan) { *pc.at = (uint8_t *) base + off; off += (pc.bytes + 255) & ~(size_t) 255; }
     if (d_state_out) c.state_one = d_state_out;
-    c.m = mdl; c.hp = hp; c.device = mdl->device; c.stream = (hipStream_t) stream;
+    c.m = mdl; c.hp = hp; c.device = mdl->device; c.stream = (hipStream_t) stream; c.n_cu = n_cu;
     c.W = mdl->W; c.rd = mdl->rd; c.kmax = mdl->kmax; c.Tmax = c.Tstep = T; c.finalized = true;
     c.cur = const_cast<float *>(d_x);                 // read only: the router input and the encoder's source
     // the kernels of z2h_moe_forward_device: encode, router + grouped experts, k-sum (no memset, no copy)

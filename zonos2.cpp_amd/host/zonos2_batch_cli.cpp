@@ -9,6 +9,9 @@
 //                    its batch runtime at one slot) and inside one shared batch with idle slots; the
 //                    codes are compared per frame. F.1 (one slot, greedy) must be exact; F.2 (identical
 //                    prompts in two slots) must match.
+//   --generate       zonos2_generate on one prompt (src/main.cpp:545-578): KV path, or --no-kv for the
+//                    recompute path; --cfg S adds a seeded speaker vector and emotion delta with
+//                    emotion_cfg_scale S; prints the reference's "generate:" report lines
 // Prompts are seeded random id rows of --prompt-len frames (the text prompt builder is not part of
 // this library); --requests R gives R prompts, request i reusing prompt i % 2 when --dup is set.
 // --gpu-sample samples the batched run's frames on the GPU from the step's logits
@@ -36,15 +39,18 @@ struct Args {
     bool info = false, bench = false, test = false, greedy = false, dup = false;
     bool gpu_sample = false;          // sample on the GPU from the step's logits (zonos2_batch_sample)
     bool sampled = false;             // decode-bench: default sampling settings instead of greedy
+    bool generate = false, no_kv = false;
+    float cfg = 1.0f;                 // generate: emotion_cfg_scale (with a seeded speaker + delta when != 1)
     int slots = 0, steps = 64, max_frames = 48, prompt_len = 32, requests = 3;
     int slot_cap = 0;                 // batch-test: slot capacity of the shared context (0: fits every request)
     uint32_t seed = 1;
 };
 
 int usage() {
-    fprintf(stderr, "usage: zonos2-batch --model F.gguf (--info | --decode-bench | --batch-test)\n"
+    fprintf(stderr, "usage: zonos2-batch --model F.gguf (--info | --decode-bench | --batch-test | --generate)\n"
                     "       [--slots N] [--steps K] [--max-frames M] [--prompt-len N0] [--requests R]\n"
-                    "       [--greedy] [--dup] [--seed S] [--gpu-sample] [--sampled] [--slot-cap N]\n");
+                    "       [--greedy] [--dup] [--seed S] [--gpu-sample] [--sampled] [--slot-cap N]\n"
+                    "       [--no-kv] [--cfg S]\n");
     return 2;
 }
 
@@ -265,6 +271,35 @@ int run_batch_test(zonos2_model & m, const Args & a) {
     return fails ? 1 : 0;
 }
 
+// generate: one request through zonos2_generate, with the reference CLI's report lines
+int run_generate(zonos2_model & m, const Args & a) {
+    const int ncb = (int) m.hp.n_codebooks, n0 = a.prompt_len;
+    zonos2_sampling sp; sp.greedy = a.greedy; sp.seed = a.seed; sp.emotion_cfg_scale = a.cfg;
+    const std::vector<float> ids = make_prompt(m, n0, a.seed);
+    std::vector<float> spk, delta;
+    if (a.cfg != 1.0f) {                                  // a seeded speaker vector and emotion delta
+        std::mt19937 rng(a.seed + 1);
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        spk.resize(m.hp.spk_dim); delta.resize(m.hp.n_embd);
+        for (float & x : spk) x = nd(rng);
+        for (float & x : delta) x = 0.5f * nd(rng);
+    }
+    printf("generate: prompt [%d, %d], max=%d, %s, seed=%u, %s\n", n0, ncb + 1, a.max_frames,
+           sp.greedy ? "greedy" : "sampling", sp.seed, a.no_kv ? "recompute" : "kv-cache");
+    std::vector<int32_t> codes;
+    int eos_frame = -1;
+    const int n = zonos2_generate(m, ids.data(), n0, a.max_frames, sp, codes, eos_frame, !a.no_kv,
+                                  spk.empty() ? nullptr : spk.data(), 0, nullptr, {},
+                                  delta.empty() ? nullptr : delta.data());
+    printf("generate: %d frames, eos_frame=%d\n", n, eos_frame);
+    if (n > 0) {
+        printf("  frame0:");
+        for (int cb = 0; cb < ncb; ++cb) printf(" %d", codes[cb]);
+        printf("\n");
+    }
+    return n > 0 ? 0 : 1;
+}
+
 } // namespace
 
 int main(int argc, char ** argv) {
@@ -288,13 +323,16 @@ int main(int argc, char ** argv) {
         else if (s == "--requests" && (v = next())) a.requests = std::atoi(v);
         else if (s == "--seed" && (v = next())) a.seed = (uint32_t) std::strtoul(v, nullptr, 10);
         else if (s == "--slot-cap" && (v = next())) a.slot_cap = std::atoi(v);
+        else if (s == "--generate") a.generate = true;
+        else if (s == "--no-kv") a.no_kv = true;
+        else if (s == "--cfg" && (v = next())) a.cfg = (float) std::atof(v);
         else return usage();
     }
-    if (a.model.empty() || (a.info + a.bench + a.test) != 1) return usage();
+    if (a.model.empty() || (a.info + a.bench + a.test + a.generate) != 1) return usage();
     if (a.info) return run_info(a);
     zonos2_model m;
     if (!zonos2_model_load(m, a.model.c_str(), true)) return 1;
-    const int rc = a.bench ? run_decode_bench(m, a) : run_batch_test(m, a);
+    const int rc = a.bench ? run_decode_bench(m, a) : a.generate ? run_generate(m, a) : run_batch_test(m, a);
     zonos2_model_free(m);
     return rc;
 }

@@ -56,10 +56,15 @@ class ModelConfig:
     router_bias_std: float = 0.0
     router_mlp_std: float = 0.02               # router MLP matrices mlp0 / mlp2 N(0, std)
     router_out_std: float = 0.02               # router output matrix mlp4 N(0, std)
+    layer_experts: dict | None = None          # pruned layers: {layer: expert count} (ne[2] of the stacks)
 
     def __post_init__(self):
         if self.expert_used is None:
             self.expert_used = [self.top_k] * self.n_layer
+
+    def n_exp(self, layer: int) -> int:
+        """Experts of an MoE layer: the stacks' ne[2], fewer than n_expert in a pruned layer."""
+        return (self.layer_experts or {}).get(layer, self.n_expert)
 
     @property
     def codebook_size(self) -> int:
@@ -118,7 +123,7 @@ class ModelConfig:
                     (b + "ffn_down.weight", bt, (ff, d), W),
                 ]
                 continue
-            E = self.n_expert
+            E = self.n_exp(L)
             out += [
                 (b + "ffn_gate_exps.weight", bt, (d, ff, E), W),
                 (b + "ffn_up_exps.weight", bt, (d, ff, E), W),
@@ -194,6 +199,21 @@ def C4(bulk: int) -> tuple[ModelConfig, Workload]:
                                       extra={"balance": True})
 
 
+def shipped(bulk: int = Q4_K) -> tuple[ModelConfig, Workload]:
+    """The released model's topology (docs/INTERNALS.md:252-259): 28 layers, dense SwiGLU FFN on layers
+    0, 1, 2 and 27, MoE on 3-26 with 16 experts top-1 (top-2 on layer 26), router_dim 128, 9 x 1026
+    logits (eoa 1024, pad 1025). Layers 9 and 20 are pruned to 12 and 14 experts, the per-layer counts
+    a pruned GGUF carries in the stacks' ne[2] (src/zonos2-graph.cpp:194-197). The FFN hidden size
+    1536 stands in for the checkpoint's. Workload: C3's 16 ragged requests."""
+    eu = [0, 0, 0] + [1] * 23 + [2] + [0]
+    m = ModelConfig(f"zonos2-shipped-{TYPE_NAMES[bulk].lower()}", n_layer=28, n_embd=2048, n_head=16, n_head_kv=4,
+                    head_dim=128, n_expert=16, top_k=1, n_ff=1536, bulk=bulk, audio_vocab=1026, spk_dim=2048,
+                    spk_lda_dim=1024, router_mlp_std=128 ** -0.5, router_out_std=0.3, expert_used=eu,
+                    layer_experts={9: 12, 20: 14})
+    _, w3 = C3()
+    return m, Workload("shipped-16req-ragged", n_slots=16, kv_lens=w3.kv_lens, slot_cap=2049, extra={"balance": True})
+
+
 def zipf_bias(n_expert: int, s: float, layer: int, seed: int = 99):
     """Additive log-popularity bias log(p_e) for p_e ~ 1/rank^s, rank permuted per layer."""
     import numpy as np
@@ -202,3 +222,43 @@ def zipf_bias(n_expert: int, s: float, layer: int, seed: int = 99):
     p = 1.0 / ranks.astype(np.float64) ** s
     p /= p.sum()
     return np.log(p).astype(np.float32)
+
+
+@dataclass
+class MixedLayout:
+    """Rows of one mixed pass: prefill chunks of several prompts (each after a speaker row) and decode
+    columns, in pass order."""
+    slots: "np.ndarray"      # int32 [R] slot of each row
+    npast: "np.ndarray"      # int32 [R] position (row of the slot's band) of each row
+    emap: "np.ndarray"       # int32 [R] -1: the row sums its ids; e >= 0: the row takes speaker row e
+    ids: "np.ndarray"        # int32 [R][n_codebooks + 1]
+    spk: "np.ndarray"        # float32 [n_pre][spk_dim] speaker vectors (through spk_lda -> spk_proj)
+    r0: list                 # chunk start inside each prompt (256-aligned; earlier rows pre-filled)
+    dlen: list               # KV length of each decode column
+    out_rows: "np.ndarray"   # int32 rows whose logits are read: each chunk's last row, every decode row
+    cap: int                 # slot capacity the layout needs
+
+
+def mixed_layout(cfg: ModelConfig, seed: int = 55, n_pre: int = 8, n_dec: int = 32, chunk: int = 256) -> MixedLayout:
+    """The mixed chunked-prefill + decode batch of the C5 workload: n_pre chunks of `chunk` prompt rows,
+    each after a speaker row, at a 256-aligned offset inside a prompt of U[300, 1200] rows, plus n_dec
+    decode columns with KV lengths U[32, 1200]. With the defaults: 8 x (256 + 1) + 32 = 2088 rows."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    plen = rng.integers(300, 1201, n_pre)
+    r0 = [int(rng.integers(0, (int(p) - chunk) // 256 + 1)) * 256 for p in plen]
+    dlen = [int(x) for x in rng.integers(32, 1201, n_dec)]
+    cap = max(max(r + chunk + 1 for r in r0), max(dlen) + 1)
+    slots, npast, emap, last = [], [], [], []
+    for i, r in enumerate(r0):
+        for j in range(chunk + 1):                 # the speaker row, then the chunk's prompt rows
+            slots.append(i); npast.append(r + j); emap.append(i if j == 0 else -1)
+        last.append(len(slots) - 1)
+    for i, n in enumerate(dlen):
+        slots.append(n_pre + i); npast.append(n); emap.append(-1); last.append(len(slots) - 1)
+    R = len(slots)
+    ids = np.concatenate([rng.integers(0, cfg.audio_vocab, (R, cfg.n_codebooks)),
+                          rng.integers(0, cfg.text_vocab + 1, (R, 1))], axis=1).astype(np.int32)
+    spk = rng.standard_normal((n_pre, cfg.spk_dim)).astype(np.float32)
+    return MixedLayout(np.array(slots, np.int32), np.array(npast, np.int32), np.array(emap, np.int32), ids, spk,
+                       r0, dlen, np.array(last, np.int32), cap)

@@ -111,9 +111,8 @@ def router_biases(ctx, cfg: ModelConfig, wl: Workload) -> dict | None:
     if not wl.extra.get("balance") and not wl.zipf:
         return None
     T = len(wl.kv_lens)
-    E = cfg.n_expert
     moe = [L for L in range(cfg.n_layer) if cfg.expert_used[L] > 0]
-    bias = {L: np.zeros(E, np.float32) for L in moe}
+    bias = {L: np.zeros(cfg.n_exp(L), np.float32) for L in moe}
     if wl.extra.get("balance"):
         inp = step_inputs(cfg, wl)
         rng = np.random.default_rng(wl.seed + 17)
@@ -124,13 +123,14 @@ def router_biases(ctx, cfg: ModelConfig, wl: Workload) -> dict | None:
         ctx.set_capture(True)
         ctx.step(inp.slot_idx, inp.n_past, ids=ids)
         for L in moe:
-            lg = ctx.read_capture(L, "router_logits", T).reshape(T, E)
+            E = cfg.n_exp(L)                                 # the capture holds [T][E] of the layer
+            lg = ctx.read_capture(L, "router_logits", T)[:T * E].reshape(T, E)
             bias[L] = (-lg.astype(np.float64).mean(0)).astype(np.float32)
         ctx.set_capture(False)
     if wl.zipf:
         from .configs import zipf_bias
         for L in moe:
-            bias[L] = (bias[L] + zipf_bias(E, wl.zipf, L)).astype(np.float32)
+            bias[L] = (bias[L] + zipf_bias(cfg.n_exp(L), wl.zipf, L)).astype(np.float32)
     for L in moe:
         ctx.set_logit_bias(L, bias[L])
     return bias
