@@ -414,7 +414,7 @@ def mixed_pass(np, Context, synth, cfg, mdl):
     d, ff, k = cfg.n_embd, cfg.n_ff, cfg.top_k
     R_qkvg = (cfg.n_head + 2 * cfg.n_head_kv) * cfg.head_dim + cfg.n_head
     per_row = 2 * (k * 3 * ff * d + R_qkvg * d + d * cfg.n_head * cfg.head_dim)
-    ctx_rows = sum(n + 1 for n in npast)
+    ctx_rows = int(sum(int(n) + 1 for n in npast))
     flops = cfg.n_layer * (R * per_row + 2 * 2 * ctx_rows * cfg.n_head * cfg.head_dim)
     tops = flops / (ms / 1000.0) / 1e12
     f16 = cfg.bulk == configs_f16()

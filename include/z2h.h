@@ -155,7 +155,8 @@ int z2h_speaker_embed(z2h_ctx * ctx, int n, const float * spk, const float * del
 int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const int32_t * n_past, const int32_t * ids,
                    const int32_t * emb_map, const float * emb, int n_emb, int n_out, const int32_t * out_rows, float * out_logits);
 
-/* Rows per prefill chunk (1 .. Z2H_PREFILL_CHUNK_MAX; default the maximum).
+/* Rows per prefill chunk (1 .. the context's row capacity, max(n_slots, Z2H_PREFILL_CHUNK_MAX, max_rows);
+ * default the capacity, so a prompt that fits is one pass and streams each layer's weights once).
  * A chunk's rows go through each layer together (the projections and expert matmuls see them as one
  * batch; every row appends its K/V before the chunk's attention), so a prompt of n0 rows takes
  * ceil(n0 / rows) passes instead of n0 single-row steps. Any chunk size gives the same results. No

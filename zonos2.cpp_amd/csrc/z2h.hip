@@ -481,14 +481,14 @@ size_t samp_stage_bytes(int T, int ncb) {
 
 int alloc_scratch(z2h_ctx * ctx) {
     const auto & hp = ctx->hp;
-    // rows: a step's columns, or a prefill chunk of up to Z2H_PREFILL_CHUNK_MAX prompt rows (capped so a
-    // chunk's routes fit the grouped GEMVs' route lists)
+    // rows: a step's columns, or a pass of up to max(Z2H_PREFILL_CHUNK_MAX, max_rows) rows (a prefill
+    // chunk or a mixed pass); a prompt is prefilled in passes of the whole row capacity by default
     const int pmax = Z2H_PREFILL_CHUNK_MAX;
     const int T = std::max({ctx->n_slots, pmax, ctx->max_rows}), d = hp.n_embd, nh = hp.n_head, nkv = hp.n_head_kv, hd = hp.head_dim;
     const int ff = hp.n_ff, K = ctx->kmax, E = std::max(1, hp.n_expert), rd = std::max(1, ctx->rd);
     ctx->Tmax = T;
     ctx->Tstep = ctx->n_slots;
-    ctx->pch = pmax;
+    ctx->pch = T;
     ctx->Kmax = std::max({kpad(d), kpad(nh * hd), kpad(ff), kpad(std::max(1, hp.spk_dim)), kpad(std::max(1, hp.spk_lda_dim))});
     const int R = (nh + 2 * nkv) * hd + nh;
     const int grp = nh / nkv;
@@ -663,7 +663,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         // passes from 128 routes (popular experts re-read their weights per pass; Q6_K keeps 8-route
         // passes there, its second product set costing more than the re-reads) and for the sorted
         // table; dense: 16-token passes
-        const int rows = a.grouped && !a.r_perm && (a.n_tok * a.k < 128 || m0.type == Z2H_Q6_K) ? MT_G : MT;
+        // one pass of 16 routes covers every expert of a batch of at most 16 tokens (a token routes to an
+        // expert once): those launches request each wave's first weight unit at entry (EARLY)
+        const bool early = a.grouped && !a.r_perm && a.n_tok <= MT && m0.type == Z2H_Q4_K;
+        const int rows = early ? MT : a.grouped && !a.r_perm && (a.n_tok * a.k < 128 || m0.type == Z2H_Q6_K) ? MT_G : MT;
         const size_t lds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, rows);
         const int passes = a.grouped ? (a.n_tok + rows - 1) / rows : 1;
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
@@ -689,7 +692,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         }
         dim3 grid((m0.tiles + 3) / 4, grid_y, (dual ? 1 : a.n_mats) * passes), block(256);
 #define MM16(W_, D_, R_) KL((k_gemv_mfma<W_, D_, R_, R_ == MT_G ? m16fmt<W_>::GPF : 1>), grid, block, lds, ctx->stream, a)
-        if (m0.type == Z2H_Q4_K) {
+        if (early) {
+            if (dual) KL((k_gemv_mfma<WF_Q4_K, true, MT, 1, true>), grid, block, lds, ctx->stream, a);
+            else KL((k_gemv_mfma<WF_Q4_K, false, MT, 1, true>), grid, block, lds, ctx->stream, a);
+        } else if (m0.type == Z2H_Q4_K) {
             if (rows == MT_G) { if (dual) MM16(WF_Q4_K, true, MT_G); else MM16(WF_Q4_K, false, MT_G); }
             else { if (dual) MM16(WF_Q4_K, true, MT); else MM16(WF_Q4_K, false, MT); }
         } else if (m0.type == Z2H_Q6_K) {
@@ -1180,6 +1186,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_gemv_split<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT>))
     LDS_ATTR((k_gemv_split<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT, 1>))
+    LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1, true>)) LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1, true>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT_G, m16fmt<WF_Q8_0>::GPF>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT_G, m16fmt<WF_Q4_K>::GPF>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT_G, m16fmt<WF_Q8_0>::GPF>))
@@ -1871,7 +1878,7 @@ int z2h_step_mixed(z2h_ctx * ctx, int n_rows, const int32_t * slot_idx, const in
 int z2h_set_prefill_chunk(z2h_ctx * ctx, int rows) {
     if (!ctx) return Z2H_EINVAL;
     if (!ctx->finalized) return seterr(ctx, Z2H_ESTATE, "z2h_finalize not called");
-    if (rows <= 0 || rows > Z2H_PREFILL_CHUNK_MAX) return seterr(ctx, Z2H_EINVAL, "prefill chunk out of range");
+    if (rows <= 0 || rows > ctx->Tmax) return seterr(ctx, Z2H_EINVAL, "prefill chunk out of range (1 .. the context's row capacity)");
     ctx->pch = rows;
     return Z2H_OK;
 }

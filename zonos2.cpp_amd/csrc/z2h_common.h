@@ -216,6 +216,13 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(ha, hb, c, false);
 }
 
+// acc + a.lo * b.lo, then + a.hi * b.hi, for two f16 pairs: fp32 fmas in that order (the f16 x f16
+// products are exact in fp32, so each adds with one rounding; each compiles to one v_fma_mix_f32)
+__device__ __forceinline__ float fma_f16x2(uint32_t a, uint32_t b, float acc) {
+    acc = __builtin_fmaf(h2f(b & 0xffffu), h2f(a & 0xffffu), acc);
+    return __builtin_fmaf(h2f(b >> 16), h2f(a >> 16), acc);
+}
+
 // Q4_K 6-bit scale / min of sub-block j from the 12 packed bytes (GGUF K-quant layout).
 __device__ __forceinline__ void q4k_sm(const uint8_t * sc, int j, int & s, int & m) {
     if (j < 4) { s = sc[j] & 63; m = sc[j + 4] & 63; }

@@ -1278,7 +1278,11 @@ __device__ __forceinline__ void m16_stage_flat(const ActBuf & act, int nt, TokFn
 // SIMD; deeper rings (fewer waves per SIMD) keep more bytes in flight per wave where few blocks are
 // resident (the expert matmuls: the touched experts x row-group quads come to under three blocks per
 // CU).
-template <int WF, bool DUAL, int ROWS, int PF>
+// EARLY (a launch whose grid has one pass: every block's rows exist unless its expert is untouched):
+// the wave's first PF weight units are requested unconditionally at entry, before the route listing,
+// so the weight stream starts under it (an untouched expert's blocks, ~1 in 6 at 16 requests, read
+// them for nothing). A conditional entry load would make the compiler wait for it at the branch's join.
+template <int WF, bool DUAL, int ROWS, int PF, bool EARLY = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE,
                                                                           PF > 1 ? m16fmt<WF>::GWPE : m16fmt<WF>::WPE)))
 k_gemv_mfma(GemvArgs a) {
@@ -1299,10 +1303,20 @@ k_gemv_mfma(GemvArgs a) {
     float * sdx = AF == ACT_Q8_K ? (float *) (sbs2 + ROWS * (K / (WF == WF_Q6_K ? 16 : 32)))  // [ROWS][K/256]
                                  : (float *) (smem + ROWS * KP);     // Q8_0: [ROWS][K/32]
     if (WF == WF_Q6_K && tid < M16_ZERO / 16) ((uint4 *) smem)[tid] = make_uint4(0, 0, 0, 0);
-    int n_items, c0, e = 0;
+    const int e = a.grouped ? (int) blockIdx.y : 0;
+    const bool has = g16 < a.tiles;
+    const int nsb = a.nsb, U = (DUAL ? 2 : 1) * nsb;
+    const uint4 * ub0 = (const uint4 *) (a.w[DUAL ? 0 : m] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB);
+    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB) : ub0;
+    auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
+    uint4 pq[PF][QS], ph[PF];
+    if constexpr (EARLY) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
+    }
+    int n_items, c0;
     const int32_t * s_list = nullptr;                                // grouped: the expert's routes
     if (a.grouped) {
-        e = blockIdx.y;
         s_list = expert_routes(a, e, s_lds, s_wcnt, n_items);
         c0 = pass * ROWS;
     } else {
@@ -1311,12 +1325,6 @@ k_gemv_mfma(GemvArgs a) {
     }
     if (c0 >= n_items) return;
     const int nt = min(ROWS, n_items - c0);
-    const bool has = g16 < a.tiles;
-    const int nsb = a.nsb, U = (DUAL ? 2 : 1) * nsb;
-    const uint4 * ub0 = (const uint4 *) (a.w[DUAL ? 0 : m] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB);
-    const uint4 * ub1 = DUAL ? (const uint4 *) (a.w[1] + (int64_t) e * a.mat_bytes + (size_t) (has ? g16 : 0) * nsb * UB) : ub0;
-    auto unit_ptr = [&](int u) { return u < nsb ? ub0 + (size_t) u * (UB / 16) : ub1 + (size_t) (u - nsb) * (UB / 16); };
-    uint4 pq[PF][QS], ph[PF];
     if (tid < ROWS) {
         int tok = 0;
         if (tid < nt) {
@@ -1329,7 +1337,7 @@ k_gemv_mfma(GemvArgs a) {
     m16_stage_flat<AF, 2, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
 #pragma unroll
         for (int j = 0; j < PF; ++j)
-            if (has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
+            if (!EARLY && has && j < U) m16_load<WF>(unit_ptr(j), lane, pq[j], ph[j]);
     });
     lds_sync();
     if (!has) return;
@@ -1632,7 +1640,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     constexpr int KST = HD + 8;                    // LDS row stride of K (halfs): breaks bank aliasing
     __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
-    __shared__ __attribute__((aligned(16))) float s_q[GRP][HD];        // f16-rounded queries
+    __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];     // f16 pairs
     __shared__ float s_p[ATT_CH][GRP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
     int n_items, t, np, slot, c, g;
@@ -1692,7 +1700,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
                 float y0, y1;
                 norm_rope<HD>(xq[j][0], xq[j][1], a.temp[qh], a.qk_eps, cs, sn, y0, y1);
                 if (lane < NP) {
-                    *(float2 *) &s_q[h][2 * lane] = make_float2(h2f(f2h(y0)), h2f(f2h(y1)));
+                    s_q[h][lane] = (uint32_t) f2h(y0) | ((uint32_t) f2h(y1) << 16);
                     if (a.cap_q && c == 0) {
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane] = y0;
                         a.cap_q[((int64_t) t * a.nh + qh) * HD + 2 * lane + 1] = y1;
@@ -1732,18 +1740,16 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         }
         lds_sync();
         // ---- scores: one (row, head) per thread, an fp32 fma chain over the head dims in order (the
-        // f16 x f16 products are exact in fp32, so each step rounds once)
+        // f16 x f16 products are exact in fp32, so each step rounds once: one v_fma_mix_f32 each)
         for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
             const int r = sidx / GRP, h = sidx % GRP;
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < RW; ++j) {
                 const uint4 kk = *(const uint4 *) &s_k[r * KST + 8 * j];
-                const float4 qa = *(const float4 *) &s_q[h][8 * j], qb = *(const float4 *) &s_q[h][8 * j + 4];
-                acc = __builtin_fmaf(qa.x, h2f(kk.x & 0xffffu), acc); acc = __builtin_fmaf(qa.y, h2f(kk.x >> 16), acc);
-                acc = __builtin_fmaf(qa.z, h2f(kk.y & 0xffffu), acc); acc = __builtin_fmaf(qa.w, h2f(kk.y >> 16), acc);
-                acc = __builtin_fmaf(qb.x, h2f(kk.z & 0xffffu), acc); acc = __builtin_fmaf(qb.y, h2f(kk.z >> 16), acc);
-                acc = __builtin_fmaf(qb.z, h2f(kk.w & 0xffffu), acc); acc = __builtin_fmaf(qb.w, h2f(kk.w >> 16), acc);
+                const uint4 qq = *(const uint4 *) &s_q[h][4 * j];
+                acc = fma_f16x2(kk.x, qq.x, acc); acc = fma_f16x2(kk.y, qq.y, acc);
+                acc = fma_f16x2(kk.z, qq.z, acc); acc = fma_f16x2(kk.w, qq.w, acc);
             }
             s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
         }
