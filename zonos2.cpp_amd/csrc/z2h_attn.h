@@ -15,8 +15,10 @@
 // two operands); V is transposed on its way into LDS.
 // A row whose band fits one segment is finished in the block (normalised, gated, encoded for W_o);
 // the others leave one partial (max, sum, O) per segment, which k_attn_merge folds in order. A row's
-// arithmetic does not depend on the tile it is in, so a decode step and a wide pass give the same
-// bits.
+// arithmetic does not depend on the tile it is in, so a row gives the same bits in any wide pass. A
+// decode step attends through k_attn_chunk / k_attn_combine instead (64-row chunks, VALU arithmetic),
+// so a row's attention output differs in its last bits between a decode step and a wide pass; the K/V
+// rows it appends are the same bits either way.
 #pragma once
 #include "z2h_gemm.h"
 
