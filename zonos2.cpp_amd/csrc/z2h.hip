@@ -1035,7 +1035,21 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     // per-slot prefill (f32_prompt): tiles of up to ATT_TILE rows of one slot at consecutive positions
     // share each 64-row chunk of the prompt's fp32 K/V (k_attn_tile_f32, then k_attn_combine)
     int n_tiles = 0;
-    if (kv_pre && f32_prompt && h_slot && h_npast) {
+    // head_dim 128 and at most 4 query heads per KV head: one block per (tile, KV head) walks the whole
+    // band with an online softmax (k_attn_flash32: no partials, no merge pass)
+    const bool flash32 = kv_pre && f32_prompt && hd == 128 && nh / nkv <= 4;
+    if (flash32 && h_slot && h_npast) {
+        for (int t = 0; t < T;) {
+            int m = 1;
+            while (t + m < T && m < ATT_TILE && h_slot[t + m] == h_slot[t] && h_npast[t + m] == h_npast[t] + m) ++m;
+            for (int g = 0; g < nkv; ++g) {
+                if (n_tiles >= ctx->items_max) return seterr(ctx, Z2H_EINVAL, "attention tile table overflow");
+                ctx->h_tiles[n_tiles++] = make_int4(t, m | (g << 16), 0, 0);
+            }
+            t += m;
+        }
+        HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) n_tiles * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
+    } else if (kv_pre && f32_prompt && h_slot && h_npast) {
         int before = 0;
         for (int t = 0; t < T;) {
             int m = 1;
@@ -1072,11 +1086,25 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         if (f32_prompt) {
             a.kf = ctx->pf_kv + (size_t) (2 * L) * nkv * ctx->S * hd;
             a.vf = a.kf + (size_t) nkv * ctx->S * hd;
+            a.kf_split = flash32;                                    // k_attn_flash32 reads f16 hi / lo planes
         }
         a.act = ctx->act;
         const int wo_act = act_of(ly.wo.type);
         bool in_block;
-        if (!kv_pre || f32_prompt) {
+        if (flash32) {
+            in_block = (grp * hd) % 256 == 0;
+            a.act_fmt = in_block ? wo_act : ACT_NONE;
+            a.tiles = (const int4 *) ctx->d_tiles;
+            prof_scope ps(ctx, Z2H_KF_ATTN);
+            if ((rc = launch_kv_append(ctx, a, T))) return rc;
+            const size_t lds = attn_flash32_lds();
+            switch (grp) {
+                case 1: KL(k_attn_flash32<1>, dim3(n_tiles), dim3(512), lds, ctx->stream, a); break;
+                case 2: KL(k_attn_flash32<2>, dim3(n_tiles), dim3(512), lds, ctx->stream, a); break;
+                default: KL(k_attn_flash32<4>, dim3(n_tiles), dim3(512), lds, ctx->stream, a); break;
+            }
+            HIPX(hipGetLastError());
+        } else if (!kv_pre || f32_prompt) {
             // heads per combine block: the fewest (1, 2, 4 or 8, dividing the group) whose outputs
             // cover whole encoding blocks, so the block encodes its slice for W_o; else a separate
             // encode pass
@@ -1199,6 +1227,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_router_down_t<4, true>)) LDS_ATTR((k_router_down_t<8, true>)) LDS_ATTR((k_router_down_t<16, true>))
     LDS_ATTR((k_router_down_t<32, true>)) LDS_ATTR((k_router_down_t<64, true>))
     LDS_ATTR(k_gemm_q4k<true>) LDS_ATTR(k_gemm_q4k<false>)
+    LDS_ATTR(k_attn_flash32<1>) LDS_ATTR(k_attn_flash32<2>) LDS_ATTR(k_attn_flash32<4>)
     LDS_ATTR((k_gemm_f16<true, 4, 4>)) LDS_ATTR((k_gemm_f16<false, 4, 4>)) LDS_ATTR((k_gemm_f16<true, 2, 1>)) LDS_ATTR((k_gemm_f16<false, 1, 1>))
 #define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>)) \
                    LDS_ATTR((k_attn_fa<H_, 1>)) LDS_ATTR((k_attn_fa<H_, 2>)) LDS_ATTR((k_attn_fa<H_, 4>)) LDS_ATTR((k_attn_fa<H_, 8>)) \

@@ -421,4 +421,252 @@ __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
     fa_store_rows<HD, GRP>(a, s_out, t, 1, g);
 }
 
+// ------------------------------------------------------------------ per-slot prefill, fp32 K/V
+// The prompt's rows attend to the prompt's own fp32 K/V (src/zonos2-graph.cpp:155-169, the reference's
+// manual fp32 attention): one block per (tile of up to 16 rows of one slot at consecutive positions,
+// KV head g) walks every 64-key segment of the band [0, last row] with an online softmax, so no
+// partials leave the block. Every fp32 operand x is carried as two f16 parts, hi = f16(x) and
+// lo = f16(x - hi) (x = hi + lo to about 2^-22 relative; k_kv_append stores the K / V rows split so),
+// and each product a.b takes three v_mfma_f32_16x16x32_f16 (a_hi b_hi + a_lo b_hi + a_hi b_lo; the
+// dropped a_lo b_lo is below 2^-22):
+//   S^T = K Q^T   (M = 16 keys, N = 16 row-heads, k = 32 dims per step)
+//   O^T = V^T P^T (M = 16 dims, N = 16 row-heads, k = 32 keys: slot j of the lane with k-slot group q
+//                  is key 16 (j / 4) + 4 q + j % 4 of the 32, the S^T lanes' own values, so P stays put;
+//                  V is transposed into LDS so the A operand reads those keys as two 8-byte loads)
+// 8 waves: wave w takes row-heads [16 (w % 4), + 16) (rh = row * GRP + head) and keys [32 (w / 4), + 32)
+// of every segment, with its own running max m, sum l and O per row-head (lane = row-head, replicated
+// over the 4 k-slot lanes): m' = max(m, segment max), O = O exp(m - m') + V^T P^T,
+// l = l exp(m - m') + sum P, P = exp(S - m'). At the end the two key halves merge (M = max(m0, m1),
+// O = O0 exp(m0 - M) + O1 exp(m1 - M), likewise l), then O / l times the head's sigmoid gate is
+// stored and encoded for W_o (fa_store_rows). The next segment's rows are requested into registers
+// while the current one is multiplied. A row's arithmetic does not depend on the tile it is in
+// (segments past its position multiply O and l by exactly 1 and add exact zeros), so any prefill
+// chunking gives the same bits.
+// a.tiles[item] = (first row t0, rows m | g << 16, -, -); the rows' positions are n_past[t0 ..].
+constexpr int FL_SEG = 64;                                           // keys per segment
+constexpr int FL_KP = 128 + 8;                                       // K plane row pitch (halves)
+constexpr int FL_VP = FL_SEG + 4;                                    // V^T plane row pitch (halves, 34 dwords)
+__host__ __device__ inline size_t attn_flash32_lds() { return (size_t) 2 * (2 * FL_SEG * FL_KP + 2 * 128 * FL_VP); }
+
+template <int GRP>
+__global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
+    constexpr int HD = 128, NP = HD / 2, DT = HD / 16, KS = HD / 32, RW = HD / 8;   // RW: 16-byte chunks per plane row
+    static_assert(GRP <= 4, "at most 64 row-heads per tile");
+    extern __shared__ __attribute__((aligned(16))) char sm_fl[];
+    uint16_t * s_kh = (uint16_t *) sm_fl;                            // [FL_SEG][FL_KP] K hi
+    uint16_t * s_kl = s_kh + FL_SEG * FL_KP;                         // K lo
+    uint16_t * s_vh = s_kl + FL_SEG * FL_KP;                         // [HD][FL_VP] V^T hi
+    uint16_t * s_vl = s_vh + HD * FL_VP;                             // V^T lo
+    float * s_q = (float *) sm_fl;                                   // [64][HD + 4] queries (before the loop)
+    float2 * s_cs = (float2 *) (sm_fl + 64 * (HD + 4) * 4);          // [16][NP] RoPE (cos, sin)
+    float * s_th = (float *) (sm_fl + 64 * (HD + 4) * 4 + 16 * NP * 8);   // [16][NP] RoPE angles
+    float * s_mrg = (float *) sm_fl;                                 // [4][34][64] key-half partials (after)
+    float * s_out = (float *) (sm_fl + 4 * 34 * 64 * 4);             // [16][GRP * HD] output rows (after)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
+    const int wq = wave & 3, kh = wave >> 2;
+    const int nkv = a.nkv;
+    const int4 e = a.tiles[blockIdx.x];
+    const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16;
+    const int p0 = a.n_past[t0], plast = p0 + m - 1, nseg = plast / FL_SEG + 1;
+    const int P = m * GRP;
+    // rows of 2 RW chunks (hi, then lo): 512 bytes, the fp32 row's
+    const uint4 * ksrc = (const uint4 *) (a.kf + (int64_t) g * a.S * HD), * vsrc = (const uint4 *) (a.vf + (int64_t) g * a.S * HD);
+    // segment s into registers (rows past plast re-read plast; they are masked). K: item i = tid + 512 J
+    // is row i / 32, chunk i % 32 (coalesced rows). V: items (key pair p, chunk c) with p = lane % 16 +
+    // 16 J, c = lane / 16 + 4 wave, both keys' chunk. Named registers: the compiler keeps an array
+    // carried across the segment loop in scratch memory.
+    uint4 ka0, ka1, ka2, ka3, vx0, vy0, vx1, vy1;
+#define FL_LDK(J_, S_)                                                                                      \
+    {                                                                                                       \
+        const int i_ = tid + 512 * (J_), r_ = min(FL_SEG * (S_) + (i_ >> 5), plast);                        \
+        ka##J_ = ksrc[(int64_t) r_ * (2 * RW) + (i_ & 31)];                                                 \
+    }
+#define FL_LDV(J_, S_)                                                                                      \
+    {                                                                                                       \
+        const int p_ = (lane & 15) + 16 * (J_), c_ = (lane >> 4) + 4 * wave;                                \
+        const int r0_ = min(FL_SEG * (S_) + 2 * p_, plast), r1_ = min(FL_SEG * (S_) + 2 * p_ + 1, plast);   \
+        vx##J_ = vsrc[(int64_t) r0_ * (2 * RW) + c_];                                                       \
+        vy##J_ = vsrc[(int64_t) r1_ * (2 * RW) + c_];                                                       \
+    }
+#define FL_LOAD(S_) FL_LDK(0, S_) FL_LDK(1, S_) FL_LDK(2, S_) FL_LDK(3, S_) FL_LDV(0, S_) FL_LDV(1, S_)
+    // K rows into the hi / lo planes; V transposed: the key pair's two halves of dim d form one dword of
+    // plane row d (a wave's 64 lanes write 64 distinct banks)
+#define FL_STK(J_)                                                                                          \
+    {                                                                                                       \
+        const int i_ = tid + 512 * (J_), r_ = i_ >> 5, c_ = i_ & 31;                                        \
+        *(uint4 *) ((c_ < RW ? s_kh : s_kl) + r_ * FL_KP + 8 * (c_ & (RW - 1))) = ka##J_;                   \
+    }
+#define FL_STV(J_)                                                                                          \
+    {                                                                                                       \
+        const int p_ = (lane & 15) + 16 * (J_), c_ = (lane >> 4) + 4 * wave;                                \
+        uint16_t * pl_ = (c_ < RW ? s_vh : s_vl) + 8 * (c_ & (RW - 1)) * FL_VP + 2 * p_;                    \
+        const uint32_t x_[4] = {vx##J_.x, vx##J_.y, vx##J_.z, vx##J_.w}, y_[4] = {vy##J_.x, vy##J_.y, vy##J_.z, vy##J_.w}; \
+        _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                                                  \
+            *(uint32_t *) (pl_ + (2 * u_) * FL_VP) = (x_[u_] & 0xffffu) | (y_[u_] << 16);                   \
+            *(uint32_t *) (pl_ + (2 * u_ + 1) * FL_VP) = (x_[u_] >> 16) | (y_[u_] & 0xffff0000u);           \
+        }                                                                                                   \
+    }
+    FL_LOAD(0)
+    // ---- RoPE: each row's angle chain theta_j = pos * theta_scale^j by repeated fp32 multiplication
+    // (one thread per row), then (cos, sin) of every (row, dim pair)
+    if (tid < m) {
+        float th = (float) (p0 + tid);
+        for (int j = 0; j < NP; ++j) {
+            s_th[tid * NP + j] = th;
+            th = th * a.theta_scale;
+        }
+    }
+    lds_sync();
+    for (int i = tid; i < m * NP; i += 512) {
+        float sn, cs;
+        z_sincos(s_th[i], sn, cs);
+        s_cs[i] = make_float2(cs, sn);
+    }
+    lds_sync();
+    // ---- queries: wave w forms row-heads w, w + 8, ... (lane = dim pair): per-head RMSNorm, |temp|,
+    // RoPE; every input load of the wave is issued before the arithmetic
+    {
+        constexpr int QW = 8;                                        // row-heads per wave at most
+        float2 xq[QW];
+#pragma unroll
+        for (int k = 0; k < QW; ++k) {
+            const int rq = min(wave + 8 * k, P - 1), i = rq / GRP, qh = g * GRP + rq % GRP;
+            xq[k] = *(const float2 *) (a.qkvg + (int64_t) (t0 + i) * a.R + (int64_t) qh * HD + 2 * lane);
+        }
+#pragma unroll
+        for (int k = 0; k < QW; ++k) {
+            const int rq = wave + 8 * k;
+            if (rq < P) {                                            // (wave-uniform)
+                const int i = rq / GRP, qh = g * GRP + rq % GRP;
+                const float2 c = s_cs[i * NP + lane];
+                float y0, y1;
+                norm_rope<HD>(xq[k].x, xq[k].y, a.temp[qh], a.qk_eps, c.x, c.y, y0, y1);
+                *(float2 *) &s_q[rq * (HD + 4) + 2 * lane] = make_float2(y0, y1);
+            }
+        }
+    }
+    lds_sync();
+    const int rh = 16 * wq + c16;                                    // the lane's row-head (B columns)
+    const bool rh_ok = rh < P;
+    const int row = rh_ok ? rh / GRP : 0, pos = p0 + row;
+    v8h_t qh[KS], ql[KS];                                            // Q[rh][32 ks + 8 q4 .. + 7] hi / lo
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        uint32_t hh[4], ll[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float2 x = rh_ok ? *(const float2 *) &s_q[rh * (HD + 4) + 32 * ks + 8 * q4 + 2 * u] : make_float2(0.0f, 0.0f);
+            hh[u] = f16_split2(x.x, x.y, ll[u]);
+        }
+        qh[ks] = __builtin_bit_cast(v8h_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+        ql[ks] = __builtin_bit_cast(v8h_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+    }
+    const bool active = 16 * wq < P;                                 // the wave has row-heads
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    v4f_t o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = (v4f_t) {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < nseg; ++s) {
+        lds_sync();                                                  // the previous segment (or the queries) is done with LDS
+        FL_STK(0) FL_STK(1) FL_STK(2) FL_STK(3) FL_STV(0) FL_STV(1)
+        lds_sync();
+        if (s + 1 < nseg) { FL_LOAD(s + 1) }                         // in flight under this segment's products
+        if (!active) continue;
+        // S^T for the wave's 16 row-heads and its 32 keys of the segment, scaled and masked
+        float sc[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int kr = (32 * kh + 16 * mt + c16) * FL_KP + 8 * q4;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const v8h_t kh_ = *(const v8h_t *) &s_kh[kr + 32 * ks];
+                const v8h_t kl_ = *(const v8h_t *) &s_kl[kr + 32 * ks];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, qh[ks], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl_, qh[ks], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, ql[ks], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = FL_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
+                sc[mt][i] = rh_ok && key <= pos ? acc[i] * a.scale : -__builtin_inff();
+            }
+        }
+        // online softmax over the row-head's 32 keys (8 in each of its 4 k-slot lanes)
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mt][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;    // (all keys so far masked: weights 0)
+        const float alpha = exp_nonpos(m_run - mref);
+        float ps = 0.0f;
+        v8h_t ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = exp_nonpos(sc[j >> 2][j & 3] - mref);
+            ps = ps + p;
+            const _Float16 hi = (_Float16) p;
+            ph[j] = hi;
+            pl[j] = (_Float16) (p - (float) hi);
+        }
+        ps = ps + __shfl_xor(ps, 16);
+        ps = ps + __shfl_xor(ps, 32);
+        l_run = __builtin_fmaf(l_run, alpha, ps);
+        m_run = m_new;
+        // O^T += V^T P^T for the wave's row-heads, every dim tile
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            v4f_t acc = o[d] * alpha;
+            const int off = (16 * d + c16) * FL_VP + 32 * kh + 4 * q4;
+            const uint2 h0 = *(const uint2 *) &s_vh[off], h1 = *(const uint2 *) &s_vh[off + 16];
+            const uint2 l0 = *(const uint2 *) &s_vl[off], l1 = *(const uint2 *) &s_vl[off + 16];
+            const v8h_t vh = __builtin_bit_cast(v8h_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+            const v8h_t vl = __builtin_bit_cast(v8h_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc, 0, 0, 0);
+            o[d] = acc;
+        }
+    }
+    lds_sync();                                                      // LDS free for the partials
+    float * mg = s_mrg + wq * (34 * 64);
+    if (active && kh == 1) {
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mg[(4 * d + i) * 64 + lane] = o[d][i];
+        mg[32 * 64 + lane] = m_run;
+        mg[33 * 64 + lane] = l_run;
+    }
+    lds_sync();
+    if (active && kh == 0 && rh_ok) {
+        const float m1 = mg[32 * 64 + lane], l1 = mg[33 * 64 + lane];
+        const float M = fmaxf(m_run, m1);                            // finite: key 0 is in every band
+        const float a0 = exp_nonpos(m_run - M), a1 = exp_nonpos(m1 - M);
+        const float l = __builtin_fmaf(l_run, a0, l1 * a1);
+        const int h = rh % GRP, qhd = g * GRP + h, t = t0 + row;
+        const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qhd]);
+        const float f = gsig / l;
+        if (a.cap_gate && q4 == 0) a.cap_gate[(int64_t) t * a.nh + qhd] = gsig;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[i] = __builtin_fmaf(o[d][i], a0, mg[(4 * d + i) * 64 + lane] * a1) * f;
+            *(float4 *) (s_out + row * (GRP * HD) + h * HD + 16 * d + 4 * q4) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+    }
+    lds_sync();
+    if (wave < 4) fa_store_rows<HD, GRP>(a, s_out, t0, m, g);        // (a 256-thread helper)
+#undef FL_LOAD
+#undef FL_LDK
+#undef FL_LDV
+#undef FL_STK
+#undef FL_STV
+}
+
 } // namespace z2d

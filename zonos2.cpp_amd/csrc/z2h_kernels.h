@@ -1544,6 +1544,7 @@ struct AttnArgs {
     float * o_out;           // [T][nh*hd] (combine: gated output, fp32)
     ActBuf act; int act_fmt; // encoding of o_out for W_o
     float * kf, * vf;        // per-slot prefill: this layer's fp32 prompt K/V [nkv][S][hd] (null: f16 cache only)
+    int kf_split;            // kf / vf rows hold f16 hi / lo planes ([hd] hi halves, then [hd] lo halves)
     const int4 * tiles;      // k_attn_fa: wide-pass work items (null: decode items located from n_past)
 };
 
@@ -1818,9 +1819,19 @@ __global__ void __launch_bounds__(64) k_kv_append(AttnArgs a) {
         *(uint32_t *) (a.kc + at) = (uint32_t) f2h(k0) | ((uint32_t) f2h(k1) << 16);
         *(uint32_t *) (a.vc + at) = (uint32_t) f2h(v0) | ((uint32_t) f2h(v1) << 16);
         if (a.kf) {                                                  // the prompt's fp32 rows
-            const int64_t af = ((int64_t) g * a.S + np) * HD + 2 * lane;
-            *(float2 *) (a.kf + af) = make_float2(k0, k1);
-            *(float2 *) (a.vf + af) = make_float2(v0, v1);
+            const int64_t af = ((int64_t) g * a.S + np) * HD;
+            if (a.kf_split) {                                        // as f16 hi / lo planes in the row's bytes
+                uint16_t * kr = (uint16_t *) (a.kf + af), * vr = (uint16_t *) (a.vf + af);
+                uint32_t kl, vl;
+                const uint32_t kh = f16_split2(k0, k1, kl), vh = f16_split2(v0, v1, vl);
+                *(uint32_t *) (kr + 2 * lane) = kh;
+                *(uint32_t *) (kr + HD + 2 * lane) = kl;
+                *(uint32_t *) (vr + 2 * lane) = vh;
+                *(uint32_t *) (vr + HD + 2 * lane) = vl;
+            } else {
+                *(float2 *) (a.kf + af + 2 * lane) = make_float2(k0, k1);
+                *(float2 *) (a.vf + af + 2 * lane) = make_float2(v0, v1);
+            }
         }
     }
 }
