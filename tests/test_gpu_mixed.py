@@ -3,6 +3,8 @@ against the oracle's mixed step (orc_step_mixed: every row's K/V appended before
 slot's rows causal within the pass) at the full bar (cos >= 0.9999, max-abs <= 1e-2 per requested row),
 and bit for bit against the same rows run as separate passes (each row's arithmetic depends only on
 its own inputs and its slot's cache rows)."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -47,13 +49,22 @@ def _batch(cfg, rng, chunks, decodes):
             np.stack(emb) if emb else np.zeros((1, cfg.n_embd), np.float32), groups)
 
 
-@pytest.mark.parametrize("big", [False, True])
-def test_mixed_batch_vs_oracle_and_separate_passes(big):
-    cfg, wl = configs.C1()
+@pytest.mark.parametrize("shape,big", [("c1", False), ("c1", True), ("hd128", False)])
+def test_mixed_batch_vs_oracle_and_separate_passes(shape, big):
+    if shape == "hd128":
+        # head_dim 128, 4 query heads per KV head: the one-block-per-tile flash attention over the f16
+        # cache (bands up to 301 keys: several 64-key segments per tile)
+        cfg = dataclasses.replace(configs.zonos2_24l(configs.Q4_K), n_layer=2, expert_used=[4, 4])
+    else:
+        cfg, wl = configs.C1()
     model = synth.generate_model(cfg, 49)
     m = Model(cfg.hparams(), model)
     rng = np.random.default_rng(60 + big)
-    if big:      # > 1024 routes: the grouped matmuls read the device route sort, 16 routes per pass
+    if shape == "hd128":
+        cap, max_rows = 400, 0
+        chunks, decodes = [(0, 0, 40, True), (1, 150, 36, False)], [(2, 130), (3, 300)]
+        pre = {1: 150, 2: 130, 3: 300}
+    elif big:    # > 1024 routes: the grouped matmuls read the device route sort, 16 routes per pass
         cap, max_rows = 700, 700
         chunks, decodes = [(0, 0, 300, True), (1, 256, 300, False)], [(2, 17), (3, 300)]
         pre = {1: 256, 2: 17, 3: 300}

@@ -1013,7 +1013,21 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
     // wide passes (host copies of the rows' slots and positions at hand): work items (tile, KV head,
     // segment), a tile being up to FA_ROWS rows of one slot at consecutive positions (k_attn_fa)
     int n_fa = 0;
-    if (kv_pre && !f32_prompt && h_slot && h_npast) {
+    // head_dim 128 and at most 4 query heads per KV head: one block per (tile, KV head) walks the whole
+    // band with an online softmax (k_attn_flash16: no partials, no merge pass)
+    const bool flash16 = kv_pre && !f32_prompt && hd == 128 && grp <= 4;
+    if (flash16 && h_slot && h_npast) {
+        for (int t = 0; t < T;) {
+            int m = 1;
+            while (t + m < T && m < FA_ROWS && h_slot[t + m] == h_slot[t] && h_npast[t + m] == h_npast[t] + m) ++m;
+            for (int g = 0; g < nkv; ++g) {
+                if (n_fa >= ctx->items_max) return seterr(ctx, Z2H_EINVAL, "attention tile table overflow");
+                ctx->h_tiles[n_fa++] = make_int4(t, m | (g << 16), 0, 0);
+            }
+            t += m;
+        }
+        HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) n_fa * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
+    } else if (kv_pre && !f32_prompt && h_slot && h_npast) {
         const int rows_max = std::max(1, std::min(FA_ROWS, 64 / grp));
         int segs = 0;
         for (int t = 0; t < T;) {
@@ -1135,7 +1149,15 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
             prof_scope ps(ctx, Z2H_KF_ATTN);
             if ((rc = launch_kv_append(ctx, a, T))) return rc;
             a.tiles = (const int4 *) ctx->d_tiles;
-            if (n_fa > 0 && (rc = launch_attn_fa(ctx, a, n_fa))) return rc;
+            if (flash16 && n_fa > 0) {
+                const size_t lds = attn_flash16_lds();
+                switch (grp) {
+                    case 1: KL(k_attn_flash16<1>, dim3(n_fa), dim3(512), lds, ctx->stream, a); break;
+                    case 2: KL(k_attn_flash16<2>, dim3(n_fa), dim3(512), lds, ctx->stream, a); break;
+                    default: KL(k_attn_flash16<4>, dim3(n_fa), dim3(512), lds, ctx->stream, a); break;
+                }
+                HIPX(hipGetLastError());
+            } else if (n_fa > 0 && (rc = launch_attn_fa(ctx, a, n_fa))) return rc;
         }
         if (!in_block) {
             ResNormArgs en{};
@@ -1228,6 +1250,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR((k_router_down_t<32, true>)) LDS_ATTR((k_router_down_t<64, true>))
     LDS_ATTR(k_gemm_q4k<true>) LDS_ATTR(k_gemm_q4k<false>)
     LDS_ATTR(k_attn_flash32<1>) LDS_ATTR(k_attn_flash32<2>) LDS_ATTR(k_attn_flash32<4>)
+    LDS_ATTR(k_attn_flash16<1>) LDS_ATTR(k_attn_flash16<2>) LDS_ATTR(k_attn_flash16<4>)
     LDS_ATTR((k_gemm_f16<true, 4, 4>)) LDS_ATTR((k_gemm_f16<false, 4, 4>)) LDS_ATTR((k_gemm_f16<true, 2, 1>)) LDS_ATTR((k_gemm_f16<false, 1, 1>))
 #define LDS_TF(H_) LDS_ATTR((k_attn_tile_f32<H_, 1>)) LDS_ATTR((k_attn_tile_f32<H_, 2>)) LDS_ATTR((k_attn_tile_f32<H_, 4>)) LDS_ATTR((k_attn_tile_f32<H_, 8>)) \
                    LDS_ATTR((k_attn_fa<H_, 1>)) LDS_ATTR((k_attn_fa<H_, 2>)) LDS_ATTR((k_attn_fa<H_, 4>)) LDS_ATTR((k_attn_fa<H_, 8>)) \

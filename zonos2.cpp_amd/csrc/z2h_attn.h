@@ -421,6 +421,226 @@ __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
     fa_store_rows<HD, GRP>(a, s_out, t, 1, g);
 }
 
+// ------------------------------------------------------------------ wide passes, one flash pass per tile
+// For head_dim 128 and at most 4 query heads per KV head, a wide pass's tiles (up to 16 rows of one slot
+// at consecutive positions) take one block of 8 waves each instead of one item per segment: the block
+// walks every 64-key segment of the band [0, last row] of the slot's f16 cache (the rows k_kv_append
+// put there) with an online softmax, so no partials and no k_attn_merge:
+//   S^T = K Q^T   one v_mfma_f32_16x16x32_f16 per 32 dims (f16 queries, as above)
+//   O^T = V^T P^T P split in two f16 parts (p = hi + lo), two MFMAs per 32 keys
+// Wave w takes row-heads [16 (w % 4), + 16) and keys [32 (w / 4), + 32) of every segment with its own
+// running max m, sum l and O (m' = max(m, segment max), O = O exp(m - m') + V^T P^T, l = l exp(m - m') +
+// sum P); at the end the two key halves merge (M = max(m0, m1), O = O0 exp(m0 - M) + O1 exp(m1 - M),
+// likewise l) and O / l times the head's sigmoid gate is stored and encoded for W_o. The K / V segments
+// are double-buffered in LDS: a segment's rows are stored while the one before is multiplied, with one
+// barrier per segment. A row's arithmetic does not depend on the tile or the pass it is in (segments
+// past its position multiply O and l by exactly 1 and add exact zeros).
+// a.tiles[item] = (first row t0, rows m | g << 16, -, -); slot and positions from slot_idx / n_past.
+constexpr int FH_SEG = 64;                                           // keys per segment
+constexpr int FH_KP = 128 + 8;                                       // K row pitch (halves)
+constexpr int FH_VP = FH_SEG + 4;                                    // V^T row pitch (halves, 34 dwords)
+constexpr int FH_BUF = (FH_SEG * FH_KP + 128 * FH_VP) * 2;           // one buffer: K rows, then V^T (bytes)
+__host__ __device__ inline size_t attn_flash16_lds() { return (size_t) 2 * FH_BUF; }
+
+template <int GRP>
+__global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
+    constexpr int HD = 128, NP = HD / 2, DT = HD / 16, KS = HD / 32, RW = HD / 8;   // RW: uint4 per row
+    static_assert(GRP <= 4, "at most 64 row-heads per tile");
+    extern __shared__ __attribute__((aligned(16))) char sm_fh[];
+    float * s_q = (float *) sm_fh;                                   // [64][HD + 4] queries (before the loop)
+    float2 * s_cs = (float2 *) (sm_fh + 64 * (HD + 4) * 4);          // [16][NP] RoPE (cos, sin)
+    float * s_th = (float *) (sm_fh + 64 * (HD + 4) * 4 + 16 * NP * 8);   // [16][NP] RoPE angles
+    float * s_mrg = (float *) sm_fh;                                 // [4][34][64] key-half partials (after)
+    float * s_out = (float *) (sm_fh + 4 * 34 * 64 * 4);             // [16][GRP * HD] output rows (after)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
+    const int wq = wave & 3, kh = wave >> 2;
+    const int nkv = a.nkv;
+    const int4 e = a.tiles[blockIdx.x];
+    const int t0 = e.x, m = e.y & 0xffff, g = e.y >> 16;
+    const int p0 = a.n_past[t0], slot = a.slot_idx[t0], plast = p0 + m - 1, nseg = plast / FH_SEG + 1;
+    const int P = m * GRP;
+    const int64_t band = ((int64_t) slot * nkv + g) * a.S * HD;
+    const uint4 * ksrc = (const uint4 *) (a.kc + band), * vsrc = (const uint4 *) (a.vc + band);
+    // segment s into registers (rows past plast re-read plast; they are masked). K: item i = tid + 512 J
+    // is row i / 16, 16-byte chunk i % 16 (coalesced rows). V: the key pair p = lane % 16 + 16 (wave / 4)
+    // at chunk c = lane / 16 + 4 (wave % 4), both keys' chunk (named registers, not an array).
+    uint4 ka0, ka1, vx, vy;
+#define FH_LOAD(S_)                                                                                         \
+    {                                                                                                       \
+        const int r0_ = min(FH_SEG * (S_) + (tid >> 4), plast), r1_ = min(FH_SEG * (S_) + ((tid + 512) >> 4), plast); \
+        ka0 = ksrc[(int64_t) r0_ * RW + (tid & 15)];                                                        \
+        ka1 = ksrc[(int64_t) r1_ * RW + (tid & 15)];                                                        \
+        const int p_ = (lane & 15) + 16 * (wave >> 2), c_ = (lane >> 4) + 4 * (wave & 3);                   \
+        const int v0_ = min(FH_SEG * (S_) + 2 * p_, plast), v1_ = min(FH_SEG * (S_) + 2 * p_ + 1, plast);   \
+        vx = vsrc[(int64_t) v0_ * RW + c_];                                                                 \
+        vy = vsrc[(int64_t) v1_ * RW + c_];                                                                 \
+    }
+    // into buffer B_: K rows; V transposed (the key pair's two halves of dim d form one dword of row d;
+    // a wave's 64 lanes write 64 distinct banks)
+#define FH_STORE(B_)                                                                                        \
+    {                                                                                                       \
+        uint16_t * bk_ = (uint16_t *) (sm_fh + (B_) * FH_BUF), * bv_ = bk_ + FH_SEG * FH_KP;                \
+        *(uint4 *) (bk_ + (tid >> 4) * FH_KP + 8 * (tid & 15)) = ka0;                                        \
+        *(uint4 *) (bk_ + ((tid + 512) >> 4) * FH_KP + 8 * (tid & 15)) = ka1;                                \
+        const int p_ = (lane & 15) + 16 * (wave >> 2), c_ = (lane >> 4) + 4 * (wave & 3);                   \
+        uint16_t * pl_ = bv_ + 8 * c_ * FH_VP + 2 * p_;                                                     \
+        const uint32_t x_[4] = {vx.x, vx.y, vx.z, vx.w}, y_[4] = {vy.x, vy.y, vy.z, vy.w};                 \
+        _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                                                  \
+            *(uint32_t *) (pl_ + (2 * u_) * FH_VP) = (x_[u_] & 0xffffu) | (y_[u_] << 16);                   \
+            *(uint32_t *) (pl_ + (2 * u_ + 1) * FH_VP) = (x_[u_] >> 16) | (y_[u_] & 0xffff0000u);           \
+        }                                                                                                   \
+    }
+    FH_LOAD(0)
+    // ---- RoPE angle chains (one thread per row), (cos, sin) per (row, dim pair), then the queries
+    // (wave w: row-heads w, w + 8, ...; per-head RMSNorm, |temp|, RoPE; f16 for the products)
+    if (tid < m) {
+        float th = (float) (p0 + tid);
+        for (int j = 0; j < NP; ++j) {
+            s_th[tid * NP + j] = th;
+            th = th * a.theta_scale;
+        }
+    }
+    lds_sync();
+    for (int i = tid; i < m * NP; i += 512) {
+        float sn, cs;
+        z_sincos(s_th[i], sn, cs);
+        s_cs[i] = make_float2(cs, sn);
+    }
+    lds_sync();
+    {
+        constexpr int QW = 8;
+        float2 xq[QW];
+#pragma unroll
+        for (int k = 0; k < QW; ++k) {
+            const int rq = min(wave + 8 * k, P - 1), i = rq / GRP, qh = g * GRP + rq % GRP;
+            xq[k] = *(const float2 *) (a.qkvg + (int64_t) (t0 + i) * a.R + (int64_t) qh * HD + 2 * lane);
+        }
+#pragma unroll
+        for (int k = 0; k < QW; ++k) {
+            const int rq = wave + 8 * k;
+            if (rq < P) {                                            // (wave-uniform)
+                const int i = rq / GRP, qh = g * GRP + rq % GRP;
+                const float2 c = s_cs[i * NP + lane];
+                float y0, y1;
+                norm_rope<HD>(xq[k].x, xq[k].y, a.temp[qh], a.qk_eps, c.x, c.y, y0, y1);
+                *(float2 *) &s_q[rq * (HD + 4) + 2 * lane] = make_float2(y0, y1);
+                if (a.cap_q) *(float2 *) (a.cap_q + ((int64_t) (t0 + i) * a.nh + qh) * HD + 2 * lane) = make_float2(y0, y1);
+            }
+        }
+    }
+    lds_sync();
+    const int rh = 16 * wq + c16;                                    // the lane's row-head (B columns)
+    const bool rh_ok = rh < P;
+    const int row = rh_ok ? rh / GRP : 0, pos = p0 + row;
+    v8h_t qv[KS];                                                    // f16(Q[rh][32 ks + 8 q4 .. + 7])
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qv[ks][j] = rh_ok ? (_Float16) s_q[rh * (HD + 4) + 32 * ks + 8 * q4 + j] : (_Float16) 0.0f;
+    }
+    lds_sync();                                                      // queries read: LDS free for the K / V buffers
+    FH_STORE(0)
+    if (nseg > 1) { FH_LOAD(1) }
+    lds_sync();
+    const bool active = 16 * wq < P;                                 // the wave has row-heads
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    v4f_t o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = (v4f_t) {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < nseg; ++s) {
+        if (s + 1 < nseg) {                                          // the next segment into the other buffer
+            FH_STORE((s + 1) & 1)
+            if (s + 2 < nseg) { FH_LOAD(s + 2) }
+        }
+        if (active) {
+            const uint16_t * bk = (const uint16_t *) (sm_fh + (s & 1) * FH_BUF), * bv = bk + FH_SEG * FH_KP;
+            // S^T for the wave's 16 row-heads and its 32 keys of the segment, scaled and masked
+            float sc[2][4];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                const int kr = (32 * kh + 16 * mt + c16) * FH_KP + 8 * q4;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const v8h_t *) &bk[kr + 32 * ks], qv[ks], acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = FH_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
+                    sc[mt][i] = rh_ok && key <= pos ? acc[i] * a.scale : -__builtin_inff();
+                }
+            }
+            // online softmax over the row-head's 32 keys (8 in each of its 4 k-slot lanes)
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mt][i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m_run, mx);
+            const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;    // (all keys so far masked: weights 0)
+            const float alpha = exp_nonpos(m_run - mref);
+            float ps = 0.0f;
+            v8h_t ph, pl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = exp_nonpos(sc[j >> 2][j & 3] - mref);
+                ps = ps + p;
+                const _Float16 hi = (_Float16) p;
+                ph[j] = hi;
+                pl[j] = (_Float16) (p - (float) hi);
+            }
+            ps = ps + __shfl_xor(ps, 16);
+            ps = ps + __shfl_xor(ps, 32);
+            l_run = __builtin_fmaf(l_run, alpha, ps);
+            m_run = m_new;
+            // O^T += V^T P^T for the wave's row-heads, every dim tile
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const int off = (16 * d + c16) * FH_VP + 32 * kh + 4 * q4;
+                const uint2 h0 = *(const uint2 *) &bv[off], h1 = *(const uint2 *) &bv[off + 16];
+                const v8h_t vv = __builtin_bit_cast(v8h_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                v4f_t acc = o[d] * alpha;
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl, acc, 0, 0, 0);
+                o[d] = acc;
+            }
+        }
+        lds_sync();                                                  // segment s read, segment s + 1 stored
+    }
+    float * mg = s_mrg + wq * (34 * 64);
+    if (active && kh == 1) {
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mg[(4 * d + i) * 64 + lane] = o[d][i];
+        mg[32 * 64 + lane] = m_run;
+        mg[33 * 64 + lane] = l_run;
+    }
+    lds_sync();
+    if (active && kh == 0 && rh_ok) {
+        const float m1 = mg[32 * 64 + lane], l1 = mg[33 * 64 + lane];
+        const float M = fmaxf(m_run, m1);                            // finite: key 0 is in every band
+        const float a0 = exp_nonpos(m_run - M), a1 = exp_nonpos(m1 - M);
+        const float l = __builtin_fmaf(l_run, a0, l1 * a1);
+        const int h = rh % GRP, qhd = g * GRP + h, t = t0 + row;
+        const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qhd]);
+        const float f = gsig / l;
+        if (a.cap_gate && q4 == 0) a.cap_gate[(int64_t) t * a.nh + qhd] = gsig;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[i] = __builtin_fmaf(o[d][i], a0, mg[(4 * d + i) * 64 + lane] * a1) * f;
+            *(float4 *) (s_out + row * (GRP * HD) + h * HD + 16 * d + 4 * q4) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+    }
+    lds_sync();
+    if (wave < 4) fa_store_rows<HD, GRP>(a, s_out, t0, m, g);        // (a 256-thread helper)
+#undef FH_LOAD
+#undef FH_STORE
+}
+
 // ------------------------------------------------------------------ per-slot prefill, fp32 K/V
 // The prompt's rows attend to the prompt's own fp32 K/V (src/zonos2-graph.cpp:155-169, the reference's
 // manual fp32 attention): one block per (tile of up to 16 rows of one slot at consecutive positions,
