@@ -82,7 +82,8 @@ def test_c5_mixed_pass_layers_teacher_forced(bulk, layout):
         O.check(O.lib().orc_attention(om.m, okv.kv, L, T, O.ptr(slots), O.ptr(npast), O.ptr(attn_in), O.ptr(ao), O.ptr(oo)))
         c, _ = assert_close(f"L{L} attn_out", attn_out, oo)
         worst = min(worst, c)
-        assert_close(f"L{L} attn_o", rd(L, "attn_o").reshape(T, -1), ao)
+        c_o, m_o = assert_close(f"L{L} attn_o", rd(L, "attn_o").reshape(T, -1), ao)
+        print(f"L{L}: attention output vs the oracle: cos {c_o:.8f} max |d| {m_o:.3e}", flush=True)
         for s_, n_ in list(enumerate(lay.r0)) + [(n_pre + i, n) for i, n in enumerate(lay.dlen)]:
             rows = CHUNK + 1 if s_ < n_pre else 1
             gk, gv = ctx.kv_read(L, s_, n_, rows)

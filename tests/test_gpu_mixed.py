@@ -82,14 +82,20 @@ def test_mixed_batch_vs_oracle_and_separate_passes(shape, big):
         _fill(cfg, [ctx.kv_write, okv.write], s, n, 70 + s)
     got = ctx.step_mixed(slots, npast, ids, out_rows, emb_map=emap, emb=emb)
     want = O.step_mixed(om, okv, slots, npast, ids, emb_map=emap, emb=emb)[out_rows]
+    # the 2048-wide Q4_K model end to end: the Q8_K encoding before every projection turns a last-bit
+    # difference of an attention output into a step of one quantization level now and then, so its rows
+    # (logits and the second layer's K / V rows) are held to cos >= 0.9999 and max |d| <= 5e-2 here (the
+    # per-layer bar holds teacher-forced in test_gpu_c5.py, where the attention output agrees with the
+    # oracle's to ~1e-6)
+    tol = {"maxabs": 5e-2} if shape == "hd128" else {}
     for i, r in enumerate(out_rows):
-        assert_close(f"mixed row {r}", got[i], want[i])
+        assert_close(f"mixed row {r}", got[i], want[i], **tol)
     for s, r0, n, _ in chunks:
         for L in range(cfg.n_layer):
             gk, gv = ctx.kv_read(L, s, r0, n)
             ok, ov = okv.read(L, s, r0, n)
-            assert_close(f"K rows slot {s} L{L}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32))
-            assert_close(f"V rows slot {s} L{L}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32))
+            assert_close(f"K rows slot {s} L{L}", gk.view(np.float16).astype(np.float32), ok.view(np.float16).astype(np.float32), **tol)
+            assert_close(f"V rows slot {s} L{L}", gv.view(np.float16).astype(np.float32), ov.view(np.float16).astype(np.float32), **tol)
     # the same rows as separate passes (one per chunk / decode column) on a second context
     ctx2 = Context(None, 4, cap, model=m, max_rows=max_rows)
     for s, n in pre.items():

@@ -442,6 +442,37 @@ constexpr int FH_VP = FH_SEG + 4;                                    // V^T row 
 constexpr int FH_BUF = (FH_SEG * FH_KP + 128 * FH_VP) * 2;           // one buffer: K rows, then V^T (bytes)
 __host__ __device__ inline size_t attn_flash16_lds() { return (size_t) 2 * FH_BUF; }
 
+// max / sum of a value over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one MFMA column's k-slot lanes):
+// v_permlane16_swap / v_permlane32_swap with both operands v hand each lane its partner's value and
+// its own; every lane ends with the same bits (the lower row's value is the first operand). The two
+// results are copied to scalars before the bit cast: __builtin_bit_cast of an element of the returned
+// vector reads element 0 with this compiler.
+__device__ __forceinline__ void fl_swap16(float v, float & lo, float & hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    lo = __builtin_bit_cast(float, r0);
+    hi = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void fl_swap32(float v, float & lo, float & hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    lo = __builtin_bit_cast(float, r0);
+    hi = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float fl_max4(float v) {
+    float a, b;
+    fl_swap16(v, a, b);
+    fl_swap32(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float fl_sum4(float v) {
+    float a, b;
+    fl_swap16(v, a, b);
+    fl_swap32(a + b, a, b);
+    return a + b;
+}
+constexpr float FL_TAU = 8.0f;                                       // lazy rescale: P <= 2^8
+
 template <int GRP>
 __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
     constexpr int HD = 128, NP = HD / 2, DT = HD / 16, KS = HD / 32, RW = HD / 8;   // RW: uint4 per row
@@ -532,7 +563,10 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
     const int rh = 16 * wq + c16;                                    // the lane's row-head (B columns)
     const bool rh_ok = rh < P;
     const int row = rh_ok ? rh / GRP : 0, pos = p0 + row;
-    v8h_t qv[KS];                                                    // f16(Q[rh][32 ks + 8 q4 .. + 7])
+    // f16(Q[rh][32 ks + 8 q4 .. + 7]) (the f16 query of the K / V products); the scores are taken to
+    // log2 units in fp32 (times scale * log2(e)), so P = exp2(S - m)
+    const float qscale = a.scale * 1.44269504088896341f;
+    v8h_t qv[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
@@ -543,7 +577,9 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
     if (nseg > 1) { FH_LOAD(1) }
     lds_sync();
     const bool active = 16 * wq < P;                                 // the wave has row-heads
-    float m_run = -__builtin_inff(), l_run = 0.0f;
+    // m_run: the row-head's reference max (log2 units), raised only when a segment's max exceeds it by
+    // more than FL_TAU, so P <= 2^FL_TAU; l_part: this lane's share of the row-head's sum
+    float m_run = -__builtin_inff(), l_part = 0.0f;
     v4f_t o[DT];
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[d] = (v4f_t) {0.0f, 0.0f, 0.0f, 0.0f};
@@ -554,7 +590,9 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
         }
         if (active) {
             const uint16_t * bk = (const uint16_t *) (sm_fh + (s & 1) * FH_BUF), * bv = bk + FH_SEG * FH_KP;
-            // S^T for the wave's 16 row-heads and its 32 keys of the segment, scaled and masked
+            // S^T for the wave's 16 row-heads and its 32 keys of the segment; the causal mask only in
+            // segments reaching past the tile's first row (block-uniform)
+            const bool masked = FH_SEG * s + FH_SEG - 1 > p0;
             float sc[2][4];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
@@ -564,50 +602,49 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
                 for (int ks = 0; ks < KS; ++ks)
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const v8h_t *) &bk[kr + 32 * ks], qv[ks], acc, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = FH_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
-                    sc[mt][i] = rh_ok && key <= pos ? acc[i] * a.scale : -__builtin_inff();
+                for (int i = 0; i < 4; ++i) sc[mt][i] = acc[i] * qscale;
+                if (masked) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int key = FH_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
+                        if (!(rh_ok && key <= pos)) sc[mt][i] = -__builtin_inff();
+                    }
                 }
             }
-            // online softmax over the row-head's 32 keys (8 in each of its 4 k-slot lanes)
-            float mx = -__builtin_inff();
+            float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])), fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+            mx = fl_max4(mx);
+            const bool need = mx > m_run + FL_TAU;                   // (the first keys: m_run = -inf)
+            if (__any(need)) {
+                const float m_new = need ? mx : m_run;
+                const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;   // (0 from -inf)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mt][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;    // (all keys so far masked: weights 0)
-            const float alpha = exp_nonpos(m_run - mref);
-            float ps = 0.0f;
+                for (int d = 0; d < DT; ++d) o[d] = o[d] * alpha;
+                l_part = l_part * alpha;
+                m_run = m_new;
+            }
+            const float mref = m_run == -__builtin_inff() ? 0.0f : m_run;    // (all keys so far masked: weights 0)
             v8h_t ph, pl;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p = exp_nonpos(sc[j >> 2][j & 3] - mref);
-                ps = ps + p;
+                const float p = __builtin_amdgcn_exp2f(sc[j >> 2][j & 3] - mref);
+                l_part = l_part + p;
                 const _Float16 hi = (_Float16) p;
                 ph[j] = hi;
                 pl[j] = (_Float16) (p - (float) hi);
             }
-            ps = ps + __shfl_xor(ps, 16);
-            ps = ps + __shfl_xor(ps, 32);
-            l_run = __builtin_fmaf(l_run, alpha, ps);
-            m_run = m_new;
             // O^T += V^T P^T for the wave's row-heads, every dim tile
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
                 const int off = (16 * d + c16) * FH_VP + 32 * kh + 4 * q4;
                 const uint2 h0 = *(const uint2 *) &bv[off], h1 = *(const uint2 *) &bv[off + 16];
                 const v8h_t vv = __builtin_bit_cast(v8h_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                v4f_t acc = o[d] * alpha;
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl, acc, 0, 0, 0);
-                o[d] = acc;
+                v4f_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl, acc, 0, 0, 0);
             }
         }
         lds_sync();                                                  // segment s read, segment s + 1 stored
     }
+    const float l_run = fl_sum4(l_part);
     float * mg = s_mrg + wq * (34 * 64);
     if (active && kh == 1) {
 #pragma unroll
@@ -621,7 +658,7 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
     if (active && kh == 0 && rh_ok) {
         const float m1 = mg[32 * 64 + lane], l1 = mg[33 * 64 + lane];
         const float M = fmaxf(m_run, m1);                            // finite: key 0 is in every band
-        const float a0 = exp_nonpos(m_run - M), a1 = exp_nonpos(m1 - M);
+        const float a0 = __builtin_amdgcn_exp2f(m_run - M), a1 = __builtin_amdgcn_exp2f(m1 - M);
         const float l = __builtin_fmaf(l_run, a0, l1 * a1);
         const int h = rh % GRP, qhd = g * GRP + h, t = t0 + row;
         const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qhd]);
