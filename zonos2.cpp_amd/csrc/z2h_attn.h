@@ -686,34 +686,30 @@ __global__ void __launch_bounds__(512) k_attn_flash16(AttnArgs a) {
 // lo = f16(x - hi) (x = hi + lo to about 2^-22 relative; k_kv_append stores the K / V rows split so),
 // and each product a.b takes three v_mfma_f32_16x16x32_f16 (a_hi b_hi + a_lo b_hi + a_hi b_lo; the
 // dropped a_lo b_lo is below 2^-22):
-//   S^T = K Q^T   (M = 16 keys, N = 16 row-heads, k = 32 dims per step)
+//   S^T = K Q^T   (M = 16 keys, N = 16 row-heads, k = 32 dims per step), then times scale * log2(e)
 //   O^T = V^T P^T (M = 16 dims, N = 16 row-heads, k = 32 keys: slot j of the lane with k-slot group q
 //                  is key 16 (j / 4) + 4 q + j % 4 of the 32, the S^T lanes' own values, so P stays put;
 //                  V is transposed into LDS so the A operand reads those keys as two 8-byte loads)
 // 8 waves: wave w takes row-heads [16 (w % 4), + 16) (rh = row * GRP + head) and keys [32 (w / 4), + 32)
-// of every segment, with its own running max m, sum l and O per row-head (lane = row-head, replicated
-// over the 4 k-slot lanes): m' = max(m, segment max), O = O exp(m - m') + V^T P^T,
-// l = l exp(m - m') + sum P, P = exp(S - m'). At the end the two key halves merge (M = max(m0, m1),
-// O = O0 exp(m0 - M) + O1 exp(m1 - M), likewise l), then O / l times the head's sigmoid gate is
-// stored and encoded for W_o (fa_store_rows). The next segment's rows are requested into registers
-// while the current one is multiplied. A row's arithmetic does not depend on the tile it is in
-// (segments past its position multiply O and l by exactly 1 and add exact zeros), so any prefill
-// chunking gives the same bits.
+// of every segment with its own reference max m (log2 units, raised only when a segment's max exceeds
+// it by more than FL_TAU, so P = exp2(S - m) <= 2^FL_TAU), O and per-lane sums; at the end the two key
+// halves merge (M = max(m0, m1), O = O0 2^(m0 - M) + O1 2^(m1 - M), likewise l), then O / l times the
+// head's sigmoid gate is stored and encoded for W_o (fa_store_rows). The K / V segments are
+// double-buffered in LDS: a segment's rows are stored while the one before is multiplied, one barrier
+// per segment. A row's arithmetic does not depend on the tile it is in (segments past its position
+// add exact zeros and rescale by exactly 1), so any prefill chunking gives the same bits.
 // a.tiles[item] = (first row t0, rows m | g << 16, -, -); the rows' positions are n_past[t0 ..].
 constexpr int FL_SEG = 64;                                           // keys per segment
 constexpr int FL_KP = 128 + 8;                                       // K plane row pitch (halves)
 constexpr int FL_VP = FL_SEG + 4;                                    // V^T plane row pitch (halves, 34 dwords)
-__host__ __device__ inline size_t attn_flash32_lds() { return (size_t) 2 * (2 * FL_SEG * FL_KP + 2 * 128 * FL_VP); }
+constexpr int FL_BUF = 2 * (2 * FL_SEG * FL_KP + 2 * 128 * FL_VP);   // one buffer: K hi, K lo, V^T hi, V^T lo (bytes)
+__host__ __device__ inline size_t attn_flash32_lds() { return (size_t) 2 * FL_BUF; }
 
 template <int GRP>
 __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
     constexpr int HD = 128, NP = HD / 2, DT = HD / 16, KS = HD / 32, RW = HD / 8;   // RW: 16-byte chunks per plane row
     static_assert(GRP <= 4, "at most 64 row-heads per tile");
     extern __shared__ __attribute__((aligned(16))) char sm_fl[];
-    uint16_t * s_kh = (uint16_t *) sm_fl;                            // [FL_SEG][FL_KP] K hi
-    uint16_t * s_kl = s_kh + FL_SEG * FL_KP;                         // K lo
-    uint16_t * s_vh = s_kl + FL_SEG * FL_KP;                         // [HD][FL_VP] V^T hi
-    uint16_t * s_vl = s_vh + HD * FL_VP;                             // V^T lo
     float * s_q = (float *) sm_fl;                                   // [64][HD + 4] queries (before the loop)
     float2 * s_cs = (float2 *) (sm_fl + 64 * (HD + 4) * 4);          // [16][NP] RoPE (cos, sin)
     float * s_th = (float *) (sm_fl + 64 * (HD + 4) * 4 + 16 * NP * 8);   // [16][NP] RoPE angles
@@ -746,23 +742,26 @@ __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
         vy##J_ = vsrc[(int64_t) r1_ * (2 * RW) + c_];                                                       \
     }
 #define FL_LOAD(S_) FL_LDK(0, S_) FL_LDK(1, S_) FL_LDK(2, S_) FL_LDK(3, S_) FL_LDV(0, S_) FL_LDV(1, S_)
-    // K rows into the hi / lo planes; V transposed: the key pair's two halves of dim d form one dword of
-    // plane row d (a wave's 64 lanes write 64 distinct banks)
-#define FL_STK(J_)                                                                                          \
+    // into buffer B_: K rows into the hi / lo planes; V transposed (the key pair's two halves of dim d
+    // form one dword of plane row d; a wave's 64 lanes write 64 distinct banks)
+#define FL_STK(B_, J_)                                                                                      \
     {                                                                                                       \
+        uint16_t * kh_ = (uint16_t *) (sm_fl + (B_) * FL_BUF), * kl_ = kh_ + FL_SEG * FL_KP;                \
         const int i_ = tid + 512 * (J_), r_ = i_ >> 5, c_ = i_ & 31;                                        \
-        *(uint4 *) ((c_ < RW ? s_kh : s_kl) + r_ * FL_KP + 8 * (c_ & (RW - 1))) = ka##J_;                   \
+        *(uint4 *) ((c_ < RW ? kh_ : kl_) + r_ * FL_KP + 8 * (c_ & (RW - 1))) = ka##J_;                     \
     }
-#define FL_STV(J_)                                                                                          \
+#define FL_STV(B_, J_)                                                                                      \
     {                                                                                                       \
+        uint16_t * vh_ = (uint16_t *) (sm_fl + (B_) * FL_BUF) + 2 * FL_SEG * FL_KP, * vl_ = vh_ + HD * FL_VP; \
         const int p_ = (lane & 15) + 16 * (J_), c_ = (lane >> 4) + 4 * wave;                                \
-        uint16_t * pl_ = (c_ < RW ? s_vh : s_vl) + 8 * (c_ & (RW - 1)) * FL_VP + 2 * p_;                    \
+        uint16_t * pl_ = (c_ < RW ? vh_ : vl_) + 8 * (c_ & (RW - 1)) * FL_VP + 2 * p_;                      \
         const uint32_t x_[4] = {vx##J_.x, vx##J_.y, vx##J_.z, vx##J_.w}, y_[4] = {vy##J_.x, vy##J_.y, vy##J_.z, vy##J_.w}; \
         _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                                                  \
             *(uint32_t *) (pl_ + (2 * u_) * FL_VP) = (x_[u_] & 0xffffu) | (y_[u_] << 16);                   \
             *(uint32_t *) (pl_ + (2 * u_ + 1) * FL_VP) = (x_[u_] >> 16) | (y_[u_] & 0xffff0000u);           \
         }                                                                                                   \
     }
+#define FL_STORE(B_) FL_STK(B_, 0) FL_STK(B_, 1) FL_STK(B_, 2) FL_STK(B_, 3) FL_STV(B_, 0) FL_STV(B_, 1)
     FL_LOAD(0)
     // ---- RoPE: each row's angle chain theta_j = pos * theta_scale^j by repeated fp32 multiplication
     // (one thread per row), then (cos, sin) of every (row, dim pair)
@@ -806,6 +805,7 @@ __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
     const int rh = 16 * wq + c16;                                    // the lane's row-head (B columns)
     const bool rh_ok = rh < P;
     const int row = rh_ok ? rh / GRP : 0, pos = p0 + row;
+    const float qscale = a.scale * 1.44269504088896341f;             // scores to log2 units
     v8h_t qh[KS], ql[KS];                                            // Q[rh][32 ks + 8 q4 .. + 7] hi / lo
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -818,78 +818,86 @@ __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
         qh[ks] = __builtin_bit_cast(v8h_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
         ql[ks] = __builtin_bit_cast(v8h_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
     }
+    lds_sync();                                                      // queries read: LDS free for the K / V buffers
+    FL_STORE(0)
+    if (nseg > 1) { FL_LOAD(1) }
+    lds_sync();
     const bool active = 16 * wq < P;                                 // the wave has row-heads
-    float m_run = -__builtin_inff(), l_run = 0.0f;
+    float m_run = -__builtin_inff(), l_part = 0.0f;
     v4f_t o[DT];
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[d] = (v4f_t) {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = 0; s < nseg; ++s) {
-        lds_sync();                                                  // the previous segment (or the queries) is done with LDS
-        FL_STK(0) FL_STK(1) FL_STK(2) FL_STK(3) FL_STV(0) FL_STV(1)
-        lds_sync();
-        if (s + 1 < nseg) { FL_LOAD(s + 1) }                         // in flight under this segment's products
-        if (!active) continue;
-        // S^T for the wave's 16 row-heads and its 32 keys of the segment, scaled and masked
-        float sc[2][4];
+        if (s + 1 < nseg) {                                          // the next segment into the other buffer
+            FL_STORE((s + 1) & 1)
+            if (s + 2 < nseg) { FL_LOAD(s + 2) }
+        }
+        if (active) {
+            const uint16_t * bkh = (const uint16_t *) (sm_fl + (s & 1) * FL_BUF), * bkl = bkh + FL_SEG * FL_KP;
+            const uint16_t * bvh = bkh + 2 * FL_SEG * FL_KP, * bvl = bvh + HD * FL_VP;
+            // S^T for the wave's 16 row-heads and its 32 keys of the segment, in log2 units; the causal
+            // mask only in segments reaching past the tile's first row (block-uniform)
+            const bool masked = FL_SEG * s + FL_SEG - 1 > p0;
+            float sc[2][4];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            const int kr = (32 * kh + 16 * mt + c16) * FL_KP + 8 * q4;
+            for (int mt = 0; mt < 2; ++mt) {
+                v4f_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                const int kr = (32 * kh + 16 * mt + c16) * FL_KP + 8 * q4;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const v8h_t kh_ = *(const v8h_t *) &s_kh[kr + 32 * ks];
-                const v8h_t kl_ = *(const v8h_t *) &s_kl[kr + 32 * ks];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, qh[ks], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl_, qh[ks], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, ql[ks], acc, 0, 0, 0);
+                for (int ks = 0; ks < KS; ++ks) {
+                    const v8h_t kh_ = *(const v8h_t *) &bkh[kr + 32 * ks];
+                    const v8h_t kl_ = *(const v8h_t *) &bkl[kr + 32 * ks];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, qh[ks], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl_, qh[ks], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh_, ql[ks], acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[mt][i] = acc[i] * qscale;
+                if (masked) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int key = FL_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
+                        if (!(rh_ok && key <= pos)) sc[mt][i] = -__builtin_inff();
+                    }
+                }
             }
+            float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])), fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+            mx = fl_max4(mx);
+            const bool need = mx > m_run + FL_TAU;                   // (the first keys: m_run = -inf)
+            if (__any(need)) {
+                const float m_new = need ? mx : m_run;
+                const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;   // (0 from -inf)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = FL_SEG * s + 32 * kh + 16 * mt + 4 * q4 + i;
-                sc[mt][i] = rh_ok && key <= pos ? acc[i] * a.scale : -__builtin_inff();
+                for (int d = 0; d < DT; ++d) o[d] = o[d] * alpha;
+                l_part = l_part * alpha;
+                m_run = m_new;
+            }
+            const float mref = m_run == -__builtin_inff() ? 0.0f : m_run;    // (all keys so far masked: weights 0)
+            v8h_t ph, pl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = __builtin_amdgcn_exp2f(sc[j >> 2][j & 3] - mref);
+                l_part = l_part + p;
+                const _Float16 hi = (_Float16) p;
+                ph[j] = hi;
+                pl[j] = (_Float16) (p - (float) hi);
+            }
+            // O^T += V^T P^T for the wave's row-heads, every dim tile
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const int off = (16 * d + c16) * FL_VP + 32 * kh + 4 * q4;
+                const uint2 h0 = *(const uint2 *) &bvh[off], h1 = *(const uint2 *) &bvh[off + 16];
+                const uint2 l0 = *(const uint2 *) &bvl[off], l1 = *(const uint2 *) &bvl[off + 16];
+                const v8h_t vh = __builtin_bit_cast(v8h_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                const v8h_t vl = __builtin_bit_cast(v8h_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                v4f_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, o[d], 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc, 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc, 0, 0, 0);
             }
         }
-        // online softmax over the row-head's 32 keys (8 in each of its 4 k-slot lanes)
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[mt][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;    // (all keys so far masked: weights 0)
-        const float alpha = exp_nonpos(m_run - mref);
-        float ps = 0.0f;
-        v8h_t ph, pl;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float p = exp_nonpos(sc[j >> 2][j & 3] - mref);
-            ps = ps + p;
-            const _Float16 hi = (_Float16) p;
-            ph[j] = hi;
-            pl[j] = (_Float16) (p - (float) hi);
-        }
-        ps = ps + __shfl_xor(ps, 16);
-        ps = ps + __shfl_xor(ps, 32);
-        l_run = __builtin_fmaf(l_run, alpha, ps);
-        m_run = m_new;
-        // O^T += V^T P^T for the wave's row-heads, every dim tile
-#pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            v4f_t acc = o[d] * alpha;
-            const int off = (16 * d + c16) * FL_VP + 32 * kh + 4 * q4;
-            const uint2 h0 = *(const uint2 *) &s_vh[off], h1 = *(const uint2 *) &s_vh[off + 16];
-            const uint2 l0 = *(const uint2 *) &s_vl[off], l1 = *(const uint2 *) &s_vl[off + 16];
-            const v8h_t vh = __builtin_bit_cast(v8h_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
-            const v8h_t vl = __builtin_bit_cast(v8h_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc, 0, 0, 0);
-            o[d] = acc;
-        }
+        lds_sync();                                                  // segment s read, segment s + 1 stored
     }
-    lds_sync();                                                      // LDS free for the partials
+    const float l_run = fl_sum4(l_part);
     float * mg = s_mrg + wq * (34 * 64);
     if (active && kh == 1) {
 #pragma unroll
@@ -903,7 +911,7 @@ __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
     if (active && kh == 0 && rh_ok) {
         const float m1 = mg[32 * 64 + lane], l1 = mg[33 * 64 + lane];
         const float M = fmaxf(m_run, m1);                            // finite: key 0 is in every band
-        const float a0 = exp_nonpos(m_run - M), a1 = exp_nonpos(m1 - M);
+        const float a0 = __builtin_amdgcn_exp2f(m_run - M), a1 = __builtin_amdgcn_exp2f(m1 - M);
         const float l = __builtin_fmaf(l_run, a0, l1 * a1);
         const int h = rh % GRP, qhd = g * GRP + h, t = t0 + row;
         const float gsig = z_sigmoid(a.qkvg[(int64_t) t * a.R + (int64_t) (a.nh + 2 * nkv) * HD + qhd]);
@@ -922,6 +930,7 @@ __global__ void __launch_bounds__(512) k_attn_flash32(AttnArgs a) {
 #undef FL_LOAD
 #undef FL_LDK
 #undef FL_LDV
+#undef FL_STORE
 #undef FL_STK
 #undef FL_STV
 }
