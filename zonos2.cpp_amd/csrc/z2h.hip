@@ -1026,6 +1026,11 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
             }
             t += m;
         }
+        // longest bands first: blocks start in grid order, so a grid larger than the chip's resident
+        // blocks ends with short tiles instead of a late long one (each tile's arithmetic is its own)
+        std::stable_sort(ctx->h_tiles, ctx->h_tiles + n_fa, [&](const int4 & x, const int4 & y) {
+            return h_npast[x.x] + (x.y & 0xffff) > h_npast[y.x] + (y.y & 0xffff);
+        });
         HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) n_fa * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
     } else if (kv_pre && !f32_prompt && h_slot && h_npast) {
         const int rows_max = std::max(1, std::min(FA_ROWS, 64 / grp));
@@ -1062,6 +1067,9 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
             }
             t += m;
         }
+        std::stable_sort(ctx->h_tiles, ctx->h_tiles + n_tiles, [&](const int4 & x, const int4 & y) {   // longest bands first
+            return h_npast[x.x] + (x.y & 0xffff) > h_npast[y.x] + (y.y & 0xffff);
+        });
         HIPX(hipMemcpyAsync(ctx->d_tiles, ctx->h_tiles, (size_t) n_tiles * sizeof(int4), hipMemcpyHostToDevice, ctx->stream));
     } else if (kv_pre && f32_prompt && h_slot && h_npast) {
         int before = 0;
