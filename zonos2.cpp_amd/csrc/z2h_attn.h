@@ -1,8 +1,13 @@
-// z2h_attn.h — ragged GQA attention on MFMA for decode steps and wide passes (prefill chunks, mixed
-// batches): src/zonos2-graph.cpp:113-175 (QK-norm, |temp|, interleaved RoPE, f16 KV append,
-// softmax(K^T q / sqrt(hd)) V over the slot's band [0, n_past], sigmoid gate).
+// z2h_attn.h — ragged GQA attention on MFMA for wide passes (prefill chunks, mixed batches) and the
+// per-slot prefill: src/zonos2-graph.cpp:113-175 (QK-norm, |temp|, interleaved RoPE, f16 KV append,
+// softmax(K^T q / sqrt(hd)) V over the slot's band [0, n_past], sigmoid gate). Three kernels:
+//   k_attn_flash16  wide passes with head_dim 128 and at most 4 query heads per KV head (the model
+//                   family's shape): one block per tile walks the whole band over the f16 cache.
+//   k_attn_flash32  the per-slot prefill's in-prompt attention over the prompt's fp32 K/V (same shapes).
+//   k_attn_fa       every other shape, with k_attn_merge; described here first.
+// (Decode steps attend through k_attn_chunk / k_attn_combine in z2h_kernels.h.)
 //
-// Work item = (tile, KV head g, segment s): a tile is one row (decode) or a run of up to FA_ROWS rows
+// k_attn_fa: work item = (tile, KV head g, segment s): a tile is one row (decode) or a run of up to FA_ROWS rows
 // of one slot at consecutive positions (wide passes); segment s is keys [128 s, 128 s + 128) of the
 // band. The block loads the segment's K rows and V columns once for all rows of the tile, forms the
 // rows' queries (one wave per row: per-head RMSNorm, |temp|, RoPE, f16) and computes, per row-head
