@@ -33,24 +33,6 @@ __device__ __forceinline__ float z_expf(float x) {
     return ldexpf(p, (int) n);
 }
 
-// exp(x) for x <= 0 (softmax weights): z_expf's reduction and polynomial on max(x, -103.97208),
-// 0 below that, so no branches; the same bits as z_expf wherever x lies in [-103.97208, 0].
-__device__ __forceinline__ float exp_nonpos(float x) {
-    const float xc = fmaxf(x, -103.97208f);
-    const float n = rintf(xc * 1.44269504088896341f);
-    float r = __builtin_fmaf(n, -0.693145751953125f, xc);
-    r = __builtin_fmaf(n, -1.428606765330187e-06f, r);
-    float p = 1.98412698e-4f;
-    p = __builtin_fmaf(p, r, 1.38888889e-3f);
-    p = __builtin_fmaf(p, r, 8.33333333e-3f);
-    p = __builtin_fmaf(p, r, 4.16666667e-2f);
-    p = __builtin_fmaf(p, r, 1.66666667e-1f);
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    return x < -103.97208f ? 0.0f : ldexpf(p, (int) n);
-}
-
 // fp32 pair -> f16 hi / lo pairs: hi = f16(x), lo = f16(x - hi) (x - hi is exact in fp32), so
 // hi + lo carries x to about 2^-22 relative; low half = the first value.
 __device__ __forceinline__ uint32_t f16_split2(float x0, float x1, uint32_t & lo) {
