@@ -3,11 +3,13 @@ FFNs on layers 0, 1, 2 and 27 between 24 MoE layers of 16 experts, top-1 routing
 26, router_dim 128, 9 x 1026 logits, and two layers pruned to 12 and 14 experts (the per-layer counts of
 a pruned GGUF, src/zonos2-graph.cpp:194-197), stepped for 16 ragged requests. End to end against the
 oracle's own step: every stage of every layer, the routing and the logits bit-identical."""
+import dataclasses
+
 import numpy as np
 import pytest
 
 import oracle_py as O
-from helpers import end_to_end_stages, fill_kv, oracle_pair, report_stages
+from helpers import assert_close, end_to_end_stages, fill_kv, oracle_pair, report_stages
 from zonos2_amd import configs, synth
 from zonos2_amd.z2h import Context
 
@@ -52,4 +54,44 @@ def test_shipped_topology_end_to_end_bit_identical():
     ctx.set_capture(False)
     part = ctx.step(inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub])
     assert np.array_equal(part, got[sub])
+    ctx.close()
+
+
+@pytest.mark.parametrize("bulk", [configs.Q8_0, configs.Q6_K, configs.Q4_K])
+def test_one_and_two_request_steps_bit_identical(bulk):
+    """Steps of one and two requests on a 4-layer cut of the released topology (dense, top-1 MoE,
+    top-2 MoE pruned to 12 experts, dense) at d 2048: the expert matmuls of so few routes take the
+    K-split GEMV (one block per 16-row group and route), every stage and the logits bit-identical to
+    the oracle's step (the logits behind the Q8_0 model's F16 head at the full bar), and each request's
+    logits the same bits alone and in the pair."""
+    base, _ = configs.shipped(bulk)
+    cfg = dataclasses.replace(base, name=f"{base.name}-cut4", n_layer=4, expert_used=[0, 1, 2, 0],
+                              layer_experts={2: 12})
+    wl = configs.Workload("two-requests", n_slots=2, kv_lens=[300, 77], slot_cap=512)
+    model = synth.generate_model(cfg, 31)
+    ctx = Context(cfg.hparams(), wl.n_slots, wl.slot_cap)
+    ctx.upload(model)
+    om, okv = oracle_pair(cfg, model, wl)
+    fill_kv(cfg, wl, [ctx.kv_write, okv.write])
+    inp = synth.step_inputs(cfg, wl)
+    ctx.set_capture(True)
+    alone = {}
+    for sub in ([0], [1], [1, 0]):
+        T = len(sub)
+        print(f"{cfg.name}: step of requests {sub}", flush=True)
+        got = ctx.step(inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub])
+        want, ocap = O.step(om, okv, inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub], capture=True)
+        rows = end_to_end_stages(ctx, ocap, cfg, T)
+        report_stages(f"{cfg.name} requests {sub}", rows, got, want)
+        assert not rows, f"first differing stage: L{rows[0][0]} {rows[0][1]}"
+        if model["output.weight"].type == configs.F16:
+            # the Q8_0 model's F16 head runs on the matrix cores (their internal summation order)
+            assert_close("logits", got, want)
+        else:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "logits differ"
+        if T == 1:
+            alone[sub[0]] = got[0]
+        else:
+            for i, s in enumerate(sub):
+                assert np.array_equal(got[i].view(np.uint32), alone[s].view(np.uint32))
     ctx.close()

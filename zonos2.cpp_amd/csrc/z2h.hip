@@ -672,14 +672,22 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         if (!a.grouped) grid_y = (a.n_tok + rows - 1) / rows;
         const bool dual = a.mode == MM_SWIGLU;
         if (dual && (!m1 || m1->type != m0.type || m1->nsb != m0.nsb || m1->tiles != m0.tiles)) return seterr(ctx, Z2H_EINVAL, "gate/up layouts differ");
-        if (!a.grouped && (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX) {
+        // grouped launches whose routes, one block per (16-row group, route), stay within two blocks
+        // per compute unit (one or two requests) take the K split too: a touched expert's weights
+        // are then requested by four times as many waves as the row-group quads give it, each wave
+        // with all of its units in flight
+        const bool split_fits = (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX && (dual || a.n_mats == 1 || !a.grouped);
+        const bool gsplit = a.grouped && (int64_t) a.n_tok * a.k * m0.tiles <= 2 * ctx->n_cu;
+        if (split_fits && (!a.grouped || gsplit)) {
             // K split over the 4 waves of a block, one 16-row group per block; chunks of 8 tokens
             // where that still gives at most two blocks per compute unit (a weight tile is then read
-            // by two blocks, which halves each block's staging and products)
-            const bool half = (int64_t) m0.tiles * ((a.n_tok + MT_G - 1) / MT_G) <= 2 * ctx->n_cu;
+            // by two blocks, which halves each block's staging and products). Grouped: grid (groups,
+            // experts, passes of 8 routes)
+            const bool half = a.grouped || (int64_t) m0.tiles * ((a.n_tok + MT_G - 1) / MT_G) <= 2 * ctx->n_cu;
             const int srows = half ? MT_G : MT;
             const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, srows);
-            dim3 grid(m0.tiles, (a.n_tok + srows - 1) / srows, dual ? 1 : a.n_mats), block(256);
+            const int chunks = (a.n_tok + srows - 1) / srows;
+            dim3 grid(m0.tiles, a.grouped ? grid_y : chunks, a.grouped ? chunks : dual ? 1 : a.n_mats), block(256);
 #define SPL(W_, D_, R_) KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
 #define SPL_R(W_, D_) do { if (half) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
             if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
