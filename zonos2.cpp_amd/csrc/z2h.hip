@@ -113,6 +113,7 @@ struct z2h_ctx {
     float * spk_io = nullptr;         // speaker projection: spk | lda out | proj out | delta
     float * res = nullptr, * res2 = nullptr, * cur = nullptr, * qkvg = nullptr, * wo_out = nullptr;
     float * part_o = nullptr, * part_ml = nullptr;
+    float2 * rope = nullptr;          // [S][hd/2] RoPE (cos, sin) per position and dim pair
     float * pf_kv = nullptr;          // z2h_prefill: the prompt's fp32 K/V rows [L][2][nkv][S][hd] (one slot at a time)
     ActBuf act{}, act_y{};
     float * attn_o = nullptr;         // [T][nh*hd] gated attention output
@@ -534,6 +535,16 @@ int alloc_scratch(z2h_ctx * ctx) {
         return rc;
     (void) E;
     if ((rc = dalloc(ctx, &ctx->d_tiles, (size_t) 2 * ctx->items_max * sizeof(int4), b))) return rc;
+    // RoPE (cos, sin) of every (position < S, dim pair), formed once by rope_cs's own arithmetic
+    {
+        const int np2 = hd / 2;
+        if ((rc = dalloc(ctx, &ctx->rope, (size_t) ctx->S * np2 * sizeof(float2), b))) return rc;
+        const int64_t n = (int64_t) ctx->S * np2;
+        KL(k_rope_table, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, ctx->stream, ctx->rope, ctx->S, np2,
+           std::pow(hp.rope_freq_base, -2.0f / (float) hd));
+        HIPX(hipGetLastError());
+        HIPX(hipStreamSynchronize(ctx->stream));
+    }
     if (hipHostMalloc((void **) &ctx->h_tiles, (size_t) 2 * ctx->items_max * sizeof(int4), hipHostMallocDefault) != hipSuccess)
         return seterr(ctx, Z2H_ENOMEM, "hipHostMalloc failed");
     ctx->h_pin_bytes = (size_t) T * (4 + W) * 4;
@@ -1104,7 +1115,7 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
         if ((rc = launch_gemv(ctx, ly.qkvg, nullptr, gemv_dense(ctx, T, ctx->qkvg, R, EPI_STORE), 1, Z2H_KF_GEMV_QKV))) return rc;
         AttnArgs a{};
         a.qkvg = ctx->qkvg; a.R = R; a.nh = nh; a.nkv = nkv; a.hd = hd; a.temp = ly.attn_temp;
-        a.qk_eps = hp.qk_norm_eps; a.theta_scale = std::pow(hp.rope_freq_base, -2.0f / (float) hd);
+        a.qk_eps = hp.qk_norm_eps; a.theta_scale = std::pow(hp.rope_freq_base, -2.0f / (float) hd); a.rope = ctx->rope;
         a.scale = 1.0f / std::sqrt((float) hd);
         a.slot_idx = d_slot; a.n_past = d_npast; a.T = T; a.S = ctx->S;
         const size_t lsz = (size_t) ctx->n_slots * nkv * ctx->S * hd;

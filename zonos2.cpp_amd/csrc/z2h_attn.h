@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fa(AttnArgs a) {
                 const int rh = i * GRP + h;
                 if (rh >= 16 * RT) continue;
                 // one RoPE angle per row: the first row-head slot of each row (every slot with one row)
-                if (i < m && (m == 1 ? k == 0 : h == 0)) rope_cs(p0 + i, min(lane, NP - 1), a.theta_scale, cs, sn);
+                if (i < m && (m == 1 ? k == 0 : h == 0)) rope_at(a, p0 + i, min(lane, NP - 1), cs, sn);
                 uint32_t qv = 0;
                 if (i < m) {
                     const int qh = g * GRP + h;
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fa(AttnArgs a) {
         }
         if (mk && wave == 3) {
             float cs, sn, k0f, k1f;
-            rope_cs(p0, min(lane, NP - 1), a.theta_scale, cs, sn);
+            rope_at(a, p0, min(lane, NP - 1), cs, sn);
             norm_rope<HD>(nx[0], nx[1], 1.0f, a.qk_eps, cs, sn, k0f, k1f);
             if (lane < NP) {
                 nk = (uint32_t) f2h(k0f) | ((uint32_t) f2h(k1f) << 16);

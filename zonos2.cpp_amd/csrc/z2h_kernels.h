@@ -1546,6 +1546,7 @@ struct AttnArgs {
     float * kf, * vf;        // per-slot prefill: this layer's fp32 prompt K/V [nkv][S][hd] (null: f16 cache only)
     int kf_split;            // kf / vf rows hold f16 hi / lo planes ([hd] hi halves, then [hd] lo halves)
     const int4 * tiles;      // k_attn_fa: wide-pass work items (null: decode items located from n_past)
+    const float2 * rope;     // [S][hd/2] RoPE (cos, sin) by position and dim pair (k_rope_table)
 };
 
 // Wave-parallel item bookkeeping: lane u of each 64-token group loads n_past[u] (and slot_idx[u]) and
@@ -1614,6 +1615,21 @@ __device__ __forceinline__ void rope_cs(int pos, int pl, float theta_scale, floa
     for (int j = 0; j < pl; ++j) th = th * theta_scale;
     z_sincos(th, sn, cs);
 }
+// The table of rope_cs for every position < S and dim pair < np2 ([S][np2] (cos, sin)), formed once per
+// context: the attention kernels read a lane's pair instead of walking its angle chain (up to np2 - 1
+// dependent multiplies) per item.
+__global__ void __launch_bounds__(256) k_rope_table(float2 * out, int S, int np2, float theta_scale) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t) S * np2) return;
+    float cs, sn;
+    rope_cs((int) (i / np2), (int) (i % np2), theta_scale, cs, sn);
+    out[i] = make_float2(cs, sn);
+}
+// (cos, sin) of dim pair pl at position pos from the table (positions clamped into [0, S))
+__device__ __forceinline__ void rope_at(const AttnArgs & a, int pos, int pl, float & cs, float & sn) {
+    const float2 v = a.rope[(int64_t) min(max(pos, 0), a.S - 1) * (a.hd / 2) + pl];
+    cs = v.x; sn = v.y;
+}
 // Per-head RMSNorm (one wave, lane = dim pair (x0, x1); lanes past the head hold zeros) times mul,
 // then RoPE with the lane's (cs, sn).
 template <int HD>
@@ -1629,7 +1645,8 @@ __device__ __forceinline__ void norm_rope(float x0, float x1, float mul, float e
 // Decode attention with a block of 4 waves per item = (token, ATT_CH-row chunk of its band [0, n_past],
 // KV head g). The block requests the chunk's K and V rows with coalesced 16-byte loads and, while
 // they are in flight, forms the group's queries from the fused projection output (per-head RMSNorm,
-// |temp|, interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, f16);
+// |temp|, interleaved RoPE with theta = pos * theta_scale^i by repeated fp32 multiplication, read from
+// the context's per-position table and requested ahead of the chunk, f16);
 // the chunk that holds the new row also forms k and v, puts them in the LDS copy and, with the
 // partials after the last barrier (a barrier waits for earlier stores), in the f16 cache. Then every thread scores one (row, head) pair (f16 dot products, fp32 accumulation), one
 // wave per head reduces the chunk's softmax partial (max, sum of exp; lane = row), and every thread accumulates
@@ -1672,6 +1689,8 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             xq[HPW + 1][0] = mk && lane < NP ? vsrc[2 * lane] : 0.0f;
             xq[HPW + 1][1] = mk && lane < NP ? vsrc[2 * lane + 1] : 0.0f;
         }
+        float cs, sn;                                                // the lane's RoPE pair at np
+        rope_at(a, np, min(lane, NP - 1), cs, sn);
         // ---- K and V rows of the chunk, requested now and written to LDS after the query
         // arithmetic (rows past the chunk re-read its last row; the new row, still absent from the
         // cache, is overwritten below)
@@ -1691,8 +1710,6 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         // ---- queries of the group (one wave per head), and the new k / v row (wave 3)
         uint32_t nk = 0, nv = 0;
         {
-            float cs, sn;
-            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
 #pragma unroll
             for (int j = 0; j < HPW; ++j) {
                 const int h = wave + 4 * j;
@@ -1811,7 +1828,7 @@ __global__ void __launch_bounds__(64) k_kv_append(AttnArgs a) {
     const float x0 = lane < NP ? ksrc[2 * lane] : 0.0f, x1 = lane < NP ? ksrc[2 * lane + 1] : 0.0f;
     const float v0 = lane < NP ? vsrc[2 * lane] : 0.0f, v1 = lane < NP ? vsrc[2 * lane + 1] : 0.0f;
     float cs, sn;
-    rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
+    rope_at(a, np, min(lane, NP - 1), cs, sn);
     float k0, k1;
     norm_rope<HD>(x0, x1, 1.0f, a.qk_eps, cs, sn, k0, k1);
     if (lane < NP) {
@@ -1888,7 +1905,7 @@ __global__ void __launch_bounds__(256) k_attn_tile_f32(AttnArgs a, const int4 * 
         {
             const float * row = a.qkvg + (int64_t) t * a.R;
             float cs, sn;
-            rope_cs(np, min(lane, NP - 1), a.theta_scale, cs, sn);
+            rope_at(a, np, min(lane, NP - 1), cs, sn);
 #pragma unroll
             for (int h = 0; h < GRP; ++h) {
                 const int qh = g * GRP + h;
