@@ -1659,7 +1659,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
     __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];     // f16 pairs
-    __shared__ float s_p[ATT_CH][GRP];
+    __shared__ __attribute__((aligned(16))) float s_p[GRP][ATT_CH];     // scores, then weights, by head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
     int n_items, t, np, slot, c, g;
     bool ok = attn_locate(a.n_past, a.slot_idx, a.T, nkv, blockIdx.x, n_items, t, np, slot, c, g);
@@ -1769,7 +1769,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
                 acc = fma_f16x2(kk.x, qq.x, acc); acc = fma_f16x2(kk.y, qq.y, acc);
                 acc = fma_f16x2(kk.z, qq.z, acc); acc = fma_f16x2(kk.w, qq.w, acc);
             }
-            s_p[r][h] = r < nr ? acc * a.scale : -__builtin_inff();
+            s_p[h][r] = r < nr ? acc * a.scale : -__builtin_inff();
         }
         lds_sync();
         // ---- per-head chunk softmax partial (lane = row); (max, sum) stored with the outputs
@@ -1778,23 +1778,28 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
         for (int i = 0; i < (GRP + 3) / 4; ++i) {
             const int h = wave + 4 * i;
             if (h >= GRP) break;
-            const float sv = lane < ATT_CH ? s_p[min(lane, ATT_CH - 1)][h] : -__builtin_inff();
+            const float sv = lane < ATT_CH ? s_p[h][min(lane, ATT_CH - 1)] : -__builtin_inff();
             const float mx = wave_max_f(sv);
             const float pe = lane < nr ? z_expf(sv - mx) : 0.0f;
             ml[i] = make_float2(mx, wave_tree_f(pe));
-            if (lane < ATT_CH) s_p[lane][h] = pe;
+            if (lane < ATT_CH) s_p[h][lane] = pe;
         }
         lds_sync();
-        // ---- P.V: one (head, dim pair) per thread, rows in order
+        // ---- P.V: one (head, dim pair) per thread, rows in order (the weights of 4 rows per LDS read)
+        static_assert(ATT_CH % 4 == 0, "weights read 4 rows at a time");
         for (int o = tid; o < GRP * NP; o += 256) {
             const int h = o / NP, dp = o % NP;
             float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 16
-            for (int r = 0; r < ATT_CH; ++r) {
-                const uint32_t vv = *(const uint32_t *) &s_v[r * HD + 2 * dp];
-                const float pp = s_p[r][h];
-                o0 = __builtin_fmaf(pp, h2f(vv & 0xffffu), o0);
-                o1 = __builtin_fmaf(pp, h2f(vv >> 16), o1);
+#pragma unroll 4
+            for (int r4 = 0; r4 < ATT_CH; r4 += 4) {
+                const float4 p4 = *(const float4 *) &s_p[h][r4];
+                const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t vv = *(const uint32_t *) &s_v[(r4 + j) * HD + 2 * dp];
+                    o0 = __builtin_fmaf(pv[j], h2f(vv & 0xffffu), o0);
+                    o1 = __builtin_fmaf(pv[j], h2f(vv >> 16), o1);
+                }
             }
             *(float2 *) (a.part_o + ((int64_t) item * GRP + h) * HD + 2 * dp) = make_float2(o0, o1);
         }
