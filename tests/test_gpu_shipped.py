@@ -74,12 +74,17 @@ def test_one_and_two_request_steps_bit_identical(bulk):
     om, okv = oracle_pair(cfg, model, wl)
     fill_kv(cfg, wl, [ctx.kv_write, okv.write])
     inp = synth.step_inputs(cfg, wl)
-    ctx.set_capture(True)
     alone = {}
     for sub in ([0], [1], [1, 0]):
         T = len(sub)
         print(f"{cfg.name}: step of requests {sub}", flush=True)
+        # uncaptured steps take the launches of the graph-replayed path (for Q8_0 experts the down
+        # matmul encodes its fp32 rows itself); captured ones the sorted route table
+        ctx.set_capture(False)
+        plain = ctx.step(inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub])
+        ctx.set_capture(True)
         got = ctx.step(inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub])
+        assert np.array_equal(plain.view(np.uint32), got.view(np.uint32)), "capture changed the step"
         want, ocap = O.step(om, okv, inp.slot_idx[sub], inp.n_past[sub], ids=inp.ids[sub], capture=True)
         rows = end_to_end_stages(ctx, ocap, cfg, T)
         report_stages(f"{cfg.name} requests {sub}", rows, got, want)

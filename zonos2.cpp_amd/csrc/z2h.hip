@@ -649,6 +649,14 @@ int launch_gemm(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
     return Z2H_OK;
 }
 
+// A down matmul whose fp32 input rows k_gemv_split encodes itself (no k_encode_rows launch): Q8_0
+// weights in the m16 layout, one K-split block per 16-row group, at most XF_ITEMS float4 of rows per
+// thread (one or two rows of the model's FFN width), grouped launches within the K-split's route limit.
+bool xf_split_ok(const z2h_ctx * ctx, const DevMat & m, int rows, bool grouped) {
+    return m.m16 && m.type == Z2H_Q8_0 && m.nsb <= 4 * SPLIT_UMAX && rows >= 1 &&
+           (int64_t) rows * (m.nsb * 256 / 4) <= 256 * XF_ITEMS && (!grouped || (int64_t) rows * m.tiles <= 2 * ctx->n_cu);
+}
+
 int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvArgs & base, int grid_y, int fam) {
     if (use_gemm(m0, base.n_tok) && (!m1 || gemm_dual_ok(m0, *m1)) && (!base.grouped || (base.r_off && base.r_perm)))
         return launch_gemm(ctx, m0, m1, base, fam);
@@ -689,6 +697,17 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
         // with all of its units in flight
         const bool split_fits = (dual ? 2 : 1) * m0.nsb <= 4 * SPLIT_UMAX && (dual || a.n_mats == 1 || !a.grouped);
         const bool gsplit = a.grouped && (int64_t) a.n_tok * a.k * m0.tiles <= 2 * ctx->n_cu;
+        if (a.xf) {
+            // fp32 activation rows encoded in the staging (down matmuls of one or two tokens / routes)
+            if (!xf_split_ok(ctx, m0, a.grouped ? a.n_tok * a.k : a.n_tok, a.grouped) || dual)
+                return seterr(ctx, Z2H_EINVAL, "fp32-staged matmul outside its shapes");
+            const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, MT_G);
+            const int chunks = (a.n_tok + MT_G - 1) / MT_G;
+            dim3 grid(m0.tiles, a.grouped ? grid_y : chunks, a.grouped ? chunks : 1), block(256);
+            KL((k_gemv_split<WF_Q8_0, false, MT_G, true>), grid, block, slds, ctx->stream, a);
+            HIPX(hipGetLastError());
+            return Z2H_OK;
+        }
         if (split_fits && (!a.grouped || gsplit)) {
             // K split over the 4 waves of a block, one 16-row group per block; chunks of 8 tokens
             // where that still gives at most two blocks per compute unit (a weight tile is then read
@@ -938,10 +957,13 @@ int expert_block(z2h_ctx * ctx, Layer & ly, int L, int T, const float * state_in
         g.out[0] = ctx->gu_g; g.out[1] = ctx->gu_g; g.out_ld = hp.n_ff; g.epi = EPI_STORE;
         g.r_off = sorted ? ctx->r_off : nullptr; g.r_perm = sorted ? ctx->r_perm : nullptr;
         if ((rc = launch_gemv(ctx, ly.gate_exps, &ly.up_exps, g, ly.E, Z2H_KF_GEMV_GATEUP))) return rc;
-        if ((rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T * ly.k, act_of(ly.down_exps.type), ctx->act_y))) return rc;
+        // one or two routes over Q8_0 experts: the down matmul encodes the fp32 rows itself
+        const bool xf = !sorted && xf_split_ok(ctx, ly.down_exps, T * ly.k, true);
+        if (!xf && (rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T * ly.k, act_of(ly.down_exps.type), ctx->act_y))) return rc;
         GemvArgs dn{};
         dn.grouped = 1; dn.n_tok = T; dn.sel = ctx->sel; dn.k = ly.k; dn.E = ly.E;
         dn.act = ctx->act_y; dn.act_by_route = 1;
+        if (xf) { dn.xf = ctx->gu_g; dn.xf_ld = hp.n_ff; }
 
         dn.out[0] = ctx->eo; dn.out[1] = ctx->eo; dn.out_ld = hp.n_embd; dn.epi = EPI_ROUTE_W; dn.route_w = ctx->wsel;
         dn.r_off = sorted ? ctx->r_off : nullptr; dn.r_perm = sorted ? ctx->r_perm : nullptr;
@@ -974,9 +996,11 @@ int dense_block(z2h_ctx * ctx, Layer & ly, int T) {
         GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);
         g.mode = MM_SWIGLU;
         if ((rc = launch_gemv(ctx, ly.ffn_gate, &ly.ffn_up, g, 1, Z2H_KF_GEMV_DENSE))) return rc;
-        if ((rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T, act_of(ly.ffn_down.type), ctx->act_y))) return rc;
+        const bool xf = xf_split_ok(ctx, ly.ffn_down, T, false) && !use_gemm(ly.ffn_down, T);
+        if (!xf && (rc = launch_encode(ctx, ctx->gu_g, hp.n_ff, hp.n_ff, T, act_of(ly.ffn_down.type), ctx->act_y))) return rc;
         GemvArgs dn = gemv_dense(ctx, T, ctx->eo, hp.n_embd, EPI_STORE);
         dn.act = ctx->act_y;
+        if (xf) { dn.xf = ctx->gu_g; dn.xf_ld = hp.n_ff; }
         return launch_gemv(ctx, ly.ffn_down, nullptr, dn, 1, Z2H_KF_GEMV_DENSE);
     }
     GemvArgs g = gemv_dense(ctx, T, ctx->gu_g, hp.n_ff, EPI_STORE);

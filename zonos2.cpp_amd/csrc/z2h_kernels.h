@@ -536,6 +536,8 @@ struct GemvArgs {
     int E;
     const int32_t * r_off;             // grouped: [E+1] route offsets by expert (k_route_sort)
     const int32_t * r_perm;            // grouped: [n_tok*k] flat route ids in expert order
+    const float * xf; int xf_ld;       // k_gemv_split<..., XF>: fp32 source rows (stride xf_ld), encoded
+                                       // to Q8_0 in the block's staging instead of act
 };
 
 // The grouping of mul_mat_id's routes by expert, as a stable counting sort of the flat top-k ids
@@ -1377,6 +1379,40 @@ k_gemv_mfma(GemvArgs a) {
     }
 }
 
+// Stage nt fp32 rows (LDS row tt = source row tok(tt) of x, stride ld) encoded to Q8_0 in the m16
+// staging layout (int8 values [rows][K+16], block scales [rows][K/32]) with k_encode_rows' arithmetic:
+// 8 lanes per 32-element block (4 values each), amax by xor lane swaps, d = amax / 127, q = rint(v *
+// (127 / amax)), the scale stored as f16(d). At most XF_ITEMS float4 per thread (nt * K / 4 <= 256 *
+// XF_ITEMS, host-checked); items past the rows re-read the last one and are not stored. mid() runs
+// after the loads are issued.
+constexpr int XF_ITEMS = 3;
+template <class TokFn, class MidFn>
+__device__ __forceinline__ void m16_stage_xf(const float * x, int ld, int nt, TokFn tok, int K, int8_t * sq, float * sdx, MidFn mid) {
+    const int tid = threadIdx.x, KP = K + 16, per4 = K / 4, n = nt * per4;
+    float4 v[XF_ITEMS];
+#pragma unroll
+    for (int j = 0; j < XF_ITEMS; ++j) {
+        const int i = min(tid + 256 * j, n - 1), r = i / per4, c4 = i - r * per4;
+        v[j] = *(const float4 *) (x + (int64_t) tok(r) * ld + 4 * c4);
+    }
+    mid();
+#pragma unroll
+    for (int j = 0; j < XF_ITEMS; ++j) {
+        const int i = tid + 256 * j, ic = min(i, n - 1), r = ic / per4, c4 = ic - r * per4;
+        float amax = fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+        const float dd = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        const int q0 = (int) rintf(v[j].x * id), q1 = (int) rintf(v[j].y * id), q2 = (int) rintf(v[j].z * id), q3 = (int) rintf(v[j].w * id);
+        if (i < n) {
+            *(uint32_t *) (sq + r * KP + 4 * c4) = (uint32_t) (q0 & 255) | ((uint32_t) (q1 & 255) << 8) |
+                                                   ((uint32_t) (q2 & 255) << 16) | ((uint32_t) (q3 & 255) << 24);
+            if ((c4 & 7) == 0) sdx[r * (K / 32) + (c4 >> 3)] = h2f(f2h(dd));
+        }
+    }
+}
+
 // m16 GEMV with the K units split over the block's 4 waves: one 16-row group per block (grid x), wave
 // w takes units w, w+4, ... (all requested behind the first activation staging loads, so a wave has
 // all its weight bytes in flight at once); every unit's values go to LDS and the 4 waves fold them (one token slot each) in superblock order (m16_fold), the
@@ -1385,7 +1421,9 @@ k_gemv_mfma(GemvArgs a) {
 // first so blocks of untouched experts read no weights. Each 16-row group gives 4x more, shorter
 // waves than a wave streaming the whole K, which keeps enough bytes in flight to cover HBM latency.
 constexpr int SPLIT_UMAX = 4;          // units per wave (U <= 16)
-template <int WF, bool DUAL, int ROWS>
+// XF (Q8_0 weights, at most 256 * XF_ITEMS / (K / 4) rows): the activation rows are a.xf's fp32 rows,
+// encoded in the staging (m16_stage_xf) rather than read from a.act.
+template <int WF, bool DUAL, int ROWS, bool XF = false>
 __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
@@ -1431,11 +1469,17 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         s_tok[tid] = tok;
     }
     lds_sync();
-    m16_stage_flat<AF, 8, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, [&]() {
+    auto loads = [&]() {
 #pragma unroll
         for (int j = 0; j < SPLIT_UMAX; ++j)
             if (wave + 4 * j < U) m16_load<WF>(unit_ptr(wave + 4 * j), lane, pq[j], ph[j]);
-    });
+    };
+    if constexpr (XF) {
+        static_assert(WF == WF_Q8_0, "fp32 rows encoded to Q8_0");
+        m16_stage_xf(a.xf, a.xf_ld, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sdx, loads);
+    } else {
+        m16_stage_flat<AF, 8, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, loads);
+    }
     lds_sync();
 #pragma unroll
     for (int j = 0; j < SPLIT_UMAX; ++j) {
