@@ -1635,6 +1635,34 @@ __device__ __forceinline__ bool attn_locate(const int32_t * n_past, const int32_
     n_items = base * nkv;
     return found;
 }
+// At most 64 tokens: lane u's token row (n_past, slot, chunk prefix) read once per block, and a
+// persistent block's further items located from those registers (attn_locate's answer, no loads).
+struct AttnTok { int npu, su, incl, excl, total; };
+__device__ __forceinline__ AttnTok attn_tokens(const int32_t * n_past, const int32_t * slot_idx, int T) {
+    const int lane = threadIdx.x & 63;
+    AttnTok k;
+    k.npu = lane < T ? n_past[lane] : 0;
+    k.su = lane < T ? slot_idx[lane] : 0;
+    const int nc = lane < T ? (k.npu + ATT_CH) / ATT_CH : 0;
+    k.incl = wave_scan_incl(nc, lane);
+    k.excl = k.incl - nc;
+    k.total = lane_i(k.incl, 63);
+    return k;
+}
+__device__ __forceinline__ bool attn_locate_t(const AttnTok & k, int nkv, int item, int & n_items, int & t, int & np,
+                                              int & slot, int & c, int & g) {
+    const int want = item / nkv;
+    g = item % nkv;
+    n_items = k.total * nkv;
+    const uint64_t hit = __ballot(want >= k.excl && want < k.incl);
+    if (!hit) return false;
+    const int l = __ffsll((unsigned long long) hit) - 1;
+    t = l;
+    np = lane_i(k.npu, l);
+    slot = lane_i(k.su, l);
+    c = want - lane_i(k.excl, l);
+    return true;
+}
 // chunks before token t (exclusive prefix) and token t's own chunk count
 __device__ __forceinline__ void attn_chunks_of(const int32_t * n_past, int T, int t, int & before, int & nc_t) {
     const int lane = threadIdx.x & 63;
@@ -1706,9 +1734,15 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float s_p[GRP][ATT_CH];     // scores, then weights, by head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
     int n_items, t, np, slot, c, g;
-    bool ok = attn_locate(a.n_past, a.slot_idx, a.T, nkv, blockIdx.x, n_items, t, np, slot, c, g);
+    const bool regs = a.T <= 64;                                     // (uniform) items from the token registers
+    AttnTok tk{};
+    if (regs) tk = attn_tokens(a.n_past, a.slot_idx, a.T);
+    bool ok = regs ? attn_locate_t(tk, nkv, blockIdx.x, n_items, t, np, slot, c, g)
+                   : attn_locate(a.n_past, a.slot_idx, a.T, nkv, blockIdx.x, n_items, t, np, slot, c, g);
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        if (item != (int) blockIdx.x) ok = attn_locate(a.n_past, a.slot_idx, a.T, nkv, item, n_items, t, np, slot, c, g);
+        if (item != (int) blockIdx.x)
+            ok = regs ? attn_locate_t(tk, nkv, item, n_items, t, np, slot, c, g)
+                      : attn_locate(a.n_past, a.slot_idx, a.T, nkv, item, n_items, t, np, slot, c, g);
         if (!ok) break;
         const int L = np + 1, r0 = c * ATT_CH, nr = min(ATT_CH, L - r0);
         const bool last = r0 + nr == L;                              // the chunk holds the new row
