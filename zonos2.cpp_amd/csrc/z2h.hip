@@ -1190,7 +1190,10 @@ int run_step(z2h_ctx * ctx, int T, const int32_t * h_npast, const int32_t * d_sl
             }
             prof_scope ps(ctx, Z2H_KF_ATTN_COMBINE);
             const int nc_max = (ctx->S + ATT_CH - 1) / ATT_CH;
-            KL(k_attn_combine, dim3(nh / hpb, T), dim3(512), attn_combine_lds(hpb, hd, nc_max), ctx->stream, a, hpb, nc_max);
+            if (hd == 128 && hpb == 2 && grp == 4)
+                KL((k_attn_combine<128, 2, 4>), dim3(nh / hpb, T), dim3(512), attn_combine_lds(hpb, hd, nc_max), ctx->stream, a, hpb, nc_max);
+            else
+                KL(k_attn_combine<>, dim3(nh / hpb, T), dim3(512), attn_combine_lds(hpb, hd, nc_max), ctx->stream, a, hpb, nc_max);
             HIPX(hipGetLastError());
         } else {
             // wide passes: k_attn_fa / k_attn_merge finish (and encode) a KV group's heads of a row in
@@ -1308,7 +1311,7 @@ int set_lds_limits(std::string & err) {
                    LDS_ATTR((k_attn_merge<H_, 1>)) LDS_ATTR((k_attn_merge<H_, 2>)) LDS_ATTR((k_attn_merge<H_, 4>)) LDS_ATTR((k_attn_merge<H_, 8>))
     LDS_TF(16) LDS_TF(32) LDS_TF(64) LDS_TF(128)
 #undef LDS_TF
-    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR((k_resnorm<RN_EMBED, 8>)) LDS_ATTR((k_resnorm<RN_EMBED, 1>)) LDS_ATTR((k_resnorm<RN_EMBED, 0>)) LDS_ATTR((k_resnorm<RN_EMBED, 8, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 1, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 0, 10>)) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
+    LDS_ATTR(k_router_tail<false>) LDS_ATTR(k_router_tail<true>) LDS_ATTR(k_attn_combine<>) LDS_ATTR((k_attn_combine<128, 2, 4>)) LDS_ATTR(k_resnorm<RN_EMBED>) LDS_ATTR((k_resnorm<RN_EMBED, 8>)) LDS_ATTR((k_resnorm<RN_EMBED, 1>)) LDS_ATTR((k_resnorm<RN_EMBED, 0>)) LDS_ATTR((k_resnorm<RN_EMBED, 8, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 1, 10>)) LDS_ATTR((k_resnorm<RN_EMBED, 0, 10>)) LDS_ATTR(k_resnorm<RN_ACCUM>) LDS_ATTR(k_resnorm<RN_ADD>) LDS_ATTR(k_resnorm<RN_ENCODE>) LDS_ATTR(k_swiglu_encode)
 #undef LDS_ATTR
     return Z2H_OK;
 }

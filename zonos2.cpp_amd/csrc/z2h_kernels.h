@@ -2046,9 +2046,12 @@ __host__ __device__ inline size_t attn_tile_f32_lds(int hd, int grp) {
 // blocks the block encodes them for W_o here, otherwise a separate encode pass follows
 // (a.act_fmt == ACT_NONE).
 constexpr int AM_B = 16;          // partial loads in flight per wave
-__global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb, int ncs) {
+// HD_ / HPB_ / GRP_: the head size, heads per block and group size known at compile time (0: the
+// launch's values), so the index arithmetic of the model family's shape needs no integer divisions.
+template <int HD_ = 0, int HPB_ = 0, int GRP_ = 0>
+__global__ void __launch_bounds__(512) k_attn_combine(AttnArgs a, int hpb_rt, int ncs) {
     extern __shared__ float sm_ac[];
-    const int hd = a.hd, nh = a.nh, nkv = a.nkv, grp = nh / nkv, t = blockIdx.y;
+    const int hd = HD_ ? HD_ : a.hd, hpb = HPB_ ? HPB_ : hpb_rt, nh = a.nh, nkv = a.nkv, grp = GRP_ ? GRP_ : nh / nkv, t = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wph = 8 / hpb, hl = wave / wph, part = wave % wph;
     const int h0 = blockIdx.x * hpb, h = h0 + hl, g = h / grp, hh = h % grp;
