@@ -33,6 +33,7 @@
 #pragma once
 #include "z2h_common.h"
 #include "z2h_stdorder.h"
+#include <type_traits>
 
 namespace z2d {
 
@@ -1213,6 +1214,65 @@ __device__ __forceinline__ void m16_unit(const uint4 (&qs)[m16fmt<WF>::QS], cons
     }
 }
 
+// Q4_K unit for blocks of at most 2 NP token rows. The A rows of token pair p are (token 2p + t,
+// sub-block j) at row 8t + j (lane & 15): MFMA j takes a lane's A row only if the row's sub-block is
+// j (zeros otherwise), so one accumulation chain over the unit's 8 sub-blocks leaves D[8t + j][row] =
+// the sub-block j dot of token 2p + t with weight row `row` (lane & 15), with no products or scaling
+// spent on idle token slots. Lane l (q = l >> 4) holds token 2p + (q >> 1)'s dots of sub-blocks
+// 4 (q & 1) + v for the weight row whose scales it loaded; it forms sum_j sc_j dot_j and
+// sum_j m_j bsum_j over them (integers) and the lane 16 above adds its half (up16_i): lanes with
+// q = 0 and 2 end with the unit value of tokens 2p and 2p + 1 from the same integer sums and final
+// operations as m16_unit (x = fma(d, isum, -(dmin * msum))), so the fold gives the same bits.
+template <int NP>
+__device__ __forceinline__ void m16_unit_q4k_pairs(const uint4 (&qs)[2], const uint4 & hd, int sb, int K, int lane,
+                                                   const int8_t * sq, const int * sbs2, const float * sdx, int nsb,
+                                                   int ntm1, float (&x)[NP], float (&xd)[NP]) {
+    const int c = lane & 15, q = lane >> 4, h = q & 1, ja = c & 7, KP = K + 16;
+    const v4i_t zero = {0, 0, 0, 0};
+    long av[NP];
+    int4 bq[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int ta = min(2 * p + (c >> 3), ntm1), to = min(2 * p + (q >> 1), ntm1);
+        av[p] = *(const long *) (sq + ta * KP + sb * 256 + 32 * ja + 8 * q);
+        bq[p] = *(const int4 *) (sbs2 + to * (K / 32) + sb * 8 + 4 * h);     // sums of 32, sub-blocks 4h..4h+3
+        xd[p] = sdx[to * nsb + sb];
+    }
+    const uint32_t w[8] = {qs[0].x, qs[0].y, qs[0].z, qs[0].w, qs[1].x, qs[1].y, qs[1].z, qs[1].w};
+    v4i_t C[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) C[p] = zero;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int pr = j >> 1;
+        const uint32_t b0 = (j & 1) ? (w[2 * pr] >> 4) & 0x0f0f0f0fu : w[2 * pr] & 0x0f0f0f0fu;
+        const uint32_t b1 = (j & 1) ? (w[2 * pr + 1] >> 4) & 0x0f0f0f0fu : w[2 * pr + 1] & 0x0f0f0f0fu;
+        const long B = (long) (((uint64_t) b1 << 32) | b0);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) C[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ja == j ? av[p] : 0L, B, C[p], 0, 0, 0);
+    }
+    // the 6-bit scales and mins of sub-blocks 4h .. 4h + 3 of the lane's weight row (GGUF K-quant
+    // packing: sub-blocks 0-3 in the low 6 bits of bytes y / z, 4-7 from nibbles of w and the top 2
+    // bits of y / z), selected by bit masks rather than a lane-divergent branch
+    const uint32_t hm = 0u - (uint32_t) h, sh = 2 * h;
+    const uint32_t sc = ((hd.y ^ ((hd.y ^ hd.w) & hm)) & 0x0f0f0f0fu) | ((hd.y >> sh) & 0x30303030u);
+    const uint32_t mn = ((hd.z ^ ((hd.z ^ (hd.w >> 4)) & hm)) & 0x0f0f0f0fu) | ((hd.z >> sh) & 0x30303030u);
+    const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int bs[4] = {bq[p].x, bq[p].y, bq[p].z, bq[p].w};
+        int is = 0, ms = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            is += __mul24((int) ((sc >> (8 * v)) & 0xffu), C[p][v]);      // |products| < 2^22
+            ms += __mul24((int) ((mn >> (8 * v)) & 0xffu), bs[v]);        // < 2^18
+        }
+        is += up16_i(is);
+        ms += up16_i(ms);
+        x[p] = __builtin_fmaf(d, (float) is, -(dmin * (float) ms));       // |ms| < 2^21: exact in fp32
+    }
+}
+
 // Stage the encoded activation rows of nt tokens (LDS row tt = token tok(tt)) for the m16 kernels:
 // int8 values [rows][K+16], Q8_K sums of 32 [rows][K/32] and scales [rows][K/256], or Q8_0 scales
 // [rows][K/32]. The block's 256 threads walk the nt x (K/16) 16-byte items in one flat sequence
@@ -1343,6 +1403,46 @@ k_gemv_mfma(GemvArgs a) {
     });
     lds_sync();
     if (!has) return;
+    const int q = lane >> 4, row = g16 * 16 + (lane & 15);
+    auto store = [&](int t, float v0, float v1) {
+        if (t >= nt) return;
+        const int it = a.grouped ? s_list[c0 + t] : c0 + t;
+        float y = v0;
+        if (DUAL) y = v1 * z_silu(v0);
+        else if (a.epi == EPI_SOFTCAP) y = z_softcap(y, a.cap);
+        else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
+        a.out[m][(int64_t) it * a.out_ld + row] = y;
+    };
+    if constexpr (WF == WF_Q4_K) {
+        // at most two token rows (most expert blocks of a decode step): one token pair per product
+        auto pairs = [&](auto np) {
+            constexpr int NP = decltype(np)::value;
+            float p0[NP], p1[NP];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) p0[p] = p1[p] = 0.0f;
+            for (int c = 0; c < U; c += PF) {
+#pragma unroll
+                for (int j = 0; j < PF; ++j) {
+                    const int u = c + j;
+                    if (u < U) {
+                        float xv[NP], xd[NP];
+                        m16_unit_q4k_pairs<NP>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, xv, xd);
+                        if (u + PF < U) m16_load<WF>(unit_ptr(u + PF), lane, pq[j], ph[j]);
+#pragma unroll
+                        for (int p = 0; p < NP; ++p) {
+                            if (!DUAL || u < nsb) m16_fold<WF>(p0[p], xv[p], xd[p]);
+                            else m16_fold<WF>(p1[p], xv[p], xd[p]);
+                        }
+                    }
+                }
+            }
+            if (row < a.rows && (q & 1) == 0) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p) store(2 * p + (q >> 1), p0[p], p1[p]);
+            }
+        };
+        if (nt <= 2) { pairs(std::integral_constant<int, 1>{}); return; }
+    }
     float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // unit u (the gate matrix's units, then the up matrix's for DUAL) sits in ring slot u % PF
     for (int c = 0; c < U; c += PF) {
@@ -1363,19 +1463,9 @@ k_gemv_mfma(GemvArgs a) {
             }
         }
     }
-    const int q = lane >> 4, row = g16 * 16 + (lane & 15);
     if (row < a.rows) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 4 * q + i;
-            if (t >= nt) continue;
-            const int it = a.grouped ? s_list[c0 + t] : c0 + t;
-            float y = acc0[i];
-            if (DUAL) y = acc1[i] * z_silu(acc0[i]);
-            else if (a.epi == EPI_SOFTCAP) y = z_softcap(y, a.cap);
-            else if (a.epi == EPI_ROUTE_W) y = y * a.route_w[it];
-            a.out[m][(int64_t) it * a.out_ld + row] = y;
-        }
+        for (int i = 0; i < 4; ++i) store(4 * q + i, acc0[i], acc1[i]);
     }
 }
 
