@@ -170,6 +170,7 @@ __device__ __forceinline__ double up16_d(double v) {
 }
 constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;   // lane i of each 8-lane half-row reads lane 7 - i
 __device__ __forceinline__ float lane0_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)); }
 __device__ __forceinline__ double lane0_d(double v) {
     const uint64_t u = __builtin_bit_cast(uint64_t, v);

@@ -191,6 +191,33 @@ __device__ __forceinline__ void encode_q8k_regs(const float4 (&xv)[NV], int K, c
     }
 }
 
+// Q8_0 of a row held in registers the norm kernels' way (thread tid owns elements 4 (tid + 256 j) ..
+// + 3, so a 32-element block is 8 consecutive lanes): the block's largest |x| over those lanes by DPP
+// (xor 1, xor 2 within quads, then the mirrored quad), then encode_row<ACT_Q8_0>'s arithmetic
+// (d = amax / 127, q = rint(x * (127 / amax)), the scale stored as f16(d)). Needs K % 1024 == 0 and
+// K <= 1024 NV.
+template <int NV>
+__device__ __forceinline__ void encode_q80_regs(const float4 (&xv)[NV], int K, const ActBuf & a, int t) {
+    const int tid = threadIdx.x, Kp = kpad(K), nj = K / 1024;
+    int8_t * q = a.q + (int64_t) t * Kp;
+    float * d32 = a.d32 + (int64_t) t * (Kp / 32);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (j >= nj) break;
+        const float4 v = xv[j];
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        m = fmaxf(m, dpp_f<DPP_QUAD_XOR1>(m));
+        m = fmaxf(m, dpp_f<DPP_QUAD_XOR2>(m));
+        m = fmaxf(m, dpp_f<DPP_ROW_HALF_MIRROR>(m));
+        const float dd = m / 127.0f, id = m != 0.0f ? 127.0f / m : 0.0f;
+        const int e = tid + 256 * j;                                  // the thread's 4-element group
+        const int q0 = (int) rintf(v.x * id), q1 = (int) rintf(v.y * id), q2 = (int) rintf(v.z * id), q3 = (int) rintf(v.w * id);
+        *(uint32_t *) (q + 4 * e) = (uint32_t) (q0 & 255) | ((uint32_t) (q1 & 255) << 8) | ((uint32_t) (q2 & 255) << 16) |
+                                    ((uint32_t) (q3 & 255) << 24);
+        if ((tid & 7) == 0) d32[e >> 3] = h2f(f2h(dd));
+    }
+}
+
 // Block-wide copy of n 16-byte items with all loads of a batch issued before its stores (a loop
 // that loads and stores per iteration is not software-pipelined and pays one memory round trip per
 // iteration). src(i) / dst(i) give the item addresses.
@@ -493,6 +520,8 @@ __global__ void __launch_bounds__(256) k_resnorm(ResNormArgs a) {
     }
     if (a.act_fmt == ACT_Q8_K && d % 1024 == 0) {
         encode_q8k_regs(xv, d, a.act, t);            // each wave holds its blocks already
+    } else if (a.act_fmt == ACT_Q8_0 && d % 1024 == 0) {
+        encode_q80_regs(xv, d, a.act, t);            // each 8-lane group holds its block
     } else if (a.act_fmt != ACT_NONE) {
         // the encoders read the row from LDS (a 256-block spans the elements of 64 threads)
 #pragma unroll
@@ -2430,6 +2459,7 @@ __global__ void __launch_bounds__(256) k_ffn_entry(ResNormArgs f, RouterArgs r) 
     }
     if (!lead) return;
     if (f.act_fmt == ACT_Q8_K && d % 1024 == 0) encode_q8k_regs(xv, d, f.act, t);
+    else if (f.act_fmt == ACT_Q8_0 && d % 1024 == 0) encode_q80_regs(xv, d, f.act, t);
     else if (f.act_fmt != ACT_NONE) encode_row_rt(f.act_fmt, xs, d, f.act, t);
 #pragma unroll
     for (int j = 0; j < RN_NV; ++j) {
