@@ -171,6 +171,22 @@ __device__ __forceinline__ double up16_d(double v) {
 constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;   // lane i of each 8-lane half-row reads lane 7 - i
+constexpr int DPP_ROW_MIRROR = 0x140;        // lane i of each 16-lane row reads lane 15 - i
+// Largest value over each aligned group of 8 lanes (xor 1 and xor 2 within quads, then the mirrored
+// quad), or of 32 lanes (then the mirrored half-row, and the row 16 lanes away by a lane swap):
+// every lane of the group ends with it. A maximum does not depend on the order it is taken in.
+__device__ __forceinline__ float max8_f(float m) {
+    m = fmaxf(m, dpp_f<DPP_QUAD_XOR1>(m));
+    m = fmaxf(m, dpp_f<DPP_QUAD_XOR2>(m));
+    return fmaxf(m, dpp_f<DPP_ROW_HALF_MIRROR>(m));
+}
+__device__ __forceinline__ float max32_f(float m) {
+    m = max8_f(m);
+    m = fmaxf(m, dpp_f<DPP_ROW_MIRROR>(m));
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
 __device__ __forceinline__ float lane0_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)); }
 __device__ __forceinline__ double lane0_d(double v) {
     const uint64_t u = __builtin_bit_cast(uint64_t, v);

@@ -144,9 +144,7 @@ __device__ __forceinline__ void encode_row(const float * x, int K, int8_t * q, f
     } else if constexpr (AF == ACT_Q8_0) {
         for (int i = tid; i < Kp; i += 256) {         // 64 lanes = two 32-blocks
             const float v = i < K ? x[i] : 0.0f;
-            float amax = fabsf(v);
-#pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, WAVE));
+            const float amax = max32_f(fabsf(v));
             const float dd = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
             q[i] = (int8_t) (int) rintf(v * id);
             if ((i & 31) == 0) d32[i >> 5] = h2f(f2h(dd));
@@ -205,10 +203,7 @@ __device__ __forceinline__ void encode_q80_regs(const float4 (&xv)[NV], int K, c
     for (int j = 0; j < NV; ++j) {
         if (j >= nj) break;
         const float4 v = xv[j];
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        m = fmaxf(m, dpp_f<DPP_QUAD_XOR1>(m));
-        m = fmaxf(m, dpp_f<DPP_QUAD_XOR2>(m));
-        m = fmaxf(m, dpp_f<DPP_ROW_HALF_MIRROR>(m));
+        const float m = max8_f(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         const float dd = m / 127.0f, id = m != 0.0f ? 127.0f / m : 0.0f;
         const int e = tid + 256 * j;                                  // the thread's 4-element group
         const int q0 = (int) rintf(v.x * id), q1 = (int) rintf(v.y * id), q2 = (int) rintf(v.z * id), q3 = (int) rintf(v.w * id);
@@ -1518,10 +1513,7 @@ __device__ __forceinline__ void m16_stage_xf(const float * x, int ld, int nt, To
 #pragma unroll
     for (int j = 0; j < XF_ITEMS; ++j) {
         const int i = tid + 256 * j, ic = min(i, n - 1), r = ic / per4, c4 = ic - r * per4;
-        float amax = fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+        const float amax = max8_f(fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
         const float dd = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
         const int q0 = (int) rintf(v[j].x * id), q1 = (int) rintf(v[j].y * id), q2 = (int) rintf(v[j].z * id), q3 = (int) rintf(v[j].w * id);
         if (i < n) {
@@ -1672,10 +1664,7 @@ __global__ void __launch_bounds__(256) k_encode_rows(EncodeArgs a) {
     if (a.act_fmt == ACT_Q8_K) {
         q8k_block_v(v, a.act.q + (int64_t) r * Kp + b * 256, a.act.d256 + (int64_t) r * nb + b, a.act.bs + (int64_t) r * (Kp / 16) + b * 16, lane);
     } else if (a.act_fmt == ACT_Q8_0) {
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+        const float amax = max8_f(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
         const float dd = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
         int qi[4];
 #pragma unroll
