@@ -345,9 +345,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c3", "c4-q6_k", "c4-q8_0"],
                     help="the configuration of the main line (value, roofline)")
-    ap.add_argument("--legs", default="all", choices=["all", "main"],
+    ap.add_argument("--legs", default="all", choices=["all", "main", "single"],
                     help="all: also the C4 Q6_K / Q8_0 legs, the single-stream leg and the C1 / C2 CPU baselines "
-                         "beside the C3 line; main: the main configuration only")
+                         "beside the C3 line; main: the main configuration only; single: the single-stream leg "
+                         "alone (its JSON on one line, for profiling)")
     ap.add_argument("--cpu-steps", type=int, default=5, help="timed oracle steps for the CPU baselines after 2 warm-ups (0: skip)")
     ap.add_argument("--no-mixed-f16", dest="mixed_f16", action="store_false",
                     help="skip the mixed pass on the F16-weight model")
@@ -364,6 +365,9 @@ def main() -> int:
     from zonos2_amd import configs, synth
     from zonos2_amd.z2h import Context, Model
 
+    if args.legs == "single":
+        print(json.dumps({"single_stream": single_stream(np, torch, args.steps * 5, args.warmup)}), flush=True)
+        return 0
     if args.config == "c3":
         cfg, wl = configs.C3()
     elif args.config == "c4-q6_k":
