@@ -1831,13 +1831,16 @@ __device__ __forceinline__ void norm_rope(float x0, float x1, float mul, float e
 // partials after the last barrier (a barrier waits for earlier stores), in the f16 cache. Then every thread scores one (row, head) pair (f16 dot products, fp32 accumulation), one
 // wave per head reduces the chunk's softmax partial (max, sum of exp; lane = row), and every thread accumulates
 // one (head, dim pair) of the unnormalised P.V over the chunk's rows. k_attn_combine merges chunks.
+// head_dim 128 in groups of 4 (the model family's shape) is held to five waves per SIMD (96 VGPRs):
+// with K and V sharing the LDS tile (19 KB) that gives five resident blocks per compute unit.
 template <int HD, int GRP>
 __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
     constexpr int NP = HD / 2;                     // dim pairs (<= 64)
     constexpr int RW = HD / 8;                     // uint4 per K / V row
     constexpr int KST = HD + 8;                    // LDS row stride of K (halfs): breaks bank aliasing
+    // the chunk's K rows, then (after the scores) its V rows in the same LDS: V waits in registers
     __shared__ __attribute__((aligned(16))) uint16_t s_k[ATT_CH * KST];
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[ATT_CH * HD];
+    uint16_t * const s_v = s_k;
     __shared__ __attribute__((aligned(16))) uint32_t s_q[GRP][NP];     // f16 pairs
     __shared__ __attribute__((aligned(16))) float s_p[GRP][ATT_CH];     // scores, then weights, by head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nkv = a.nkv;
@@ -1925,24 +1928,16 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
                 }
             }
         }
-        if (tid < N4) {
-            *(uint4 *) &s_k[(tid / RW) * KST + 8 * (tid % RW)] = k0;
-            *(uint4 *) &s_v[(tid / RW) * HD + 8 * (tid % RW)] = v0;
-        }
-        auto kv_put = [&](int i, const uint4 & kk, const uint4 & vv) {
-            if (i < N4) {
-                *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = kk;
-                *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = vv;
-            }
-        };
-        if constexpr (N4 > 256) kv_put(tid + 256, k1, v1);
-        if constexpr (N4 > 512) { kv_put(tid + 512, k2, v2); kv_put(tid + 768, k3, v3); }
-        lds_sync();                                             // the chunk copy is in LDS
-        if (mk && lane < NP) {                                       // replace the stale new row
-            *(uint32_t *) &s_k[(nr - 1) * KST + 2 * lane] = nk;
-            *(uint32_t *) &s_v[(nr - 1) * HD + 2 * lane] = nv;
-        }
-        lds_sync();
+        // the chunk's rows into LDS; where the chunk holds the new row, its slot is written from nk
+        // (nv) by wave 3 instead of the stale cache copy
+        const int skip = last ? nr - 1 : -1;
+        auto k_put = [&](int i, const uint4 & kk) { if (i < N4 && i / RW != skip) *(uint4 *) &s_k[(i / RW) * KST + 8 * (i % RW)] = kk; };
+        auto v_put = [&](int i, const uint4 & vv) { if (i < N4 && i / RW != skip) *(uint4 *) &s_v[(i / RW) * HD + 8 * (i % RW)] = vv; };
+        k_put(tid, k0);
+        if constexpr (N4 > 256) k_put(tid + 256, k1);
+        if constexpr (N4 > 512) { k_put(tid + 512, k2); k_put(tid + 768, k3); }
+        if (mk && lane < NP) *(uint32_t *) &s_k[(nr - 1) * KST + 2 * lane] = nk;
+        lds_sync();                                             // the chunk's K rows are in LDS
         // ---- scores: one (row, head) per thread, an fp32 fma chain over the head dims in order (the
         // f16 x f16 products are exact in fp32, so each step rounds once: one v_fma_mix_f32 each)
         for (int sidx = tid; sidx < ATT_CH * GRP; sidx += 256) {
@@ -1970,6 +1965,11 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
             ml[i] = make_float2(mx, wave_tree_f(pe));
             if (lane < ATT_CH) s_p[h][lane] = pe;
         }
+        // ---- the chunk's V rows over its K rows (every wave has finished the scores)
+        v_put(tid, v0);
+        if constexpr (N4 > 256) v_put(tid + 256, v1);
+        if constexpr (N4 > 512) { v_put(tid + 512, v2); v_put(tid + 768, v3); }
+        if (mk && lane < NP) *(uint32_t *) &s_v[(nr - 1) * HD + 2 * lane] = nv;
         lds_sync();
         // ---- P.V: one (head, dim pair) per thread, rows in order (the weights of 4 rows per LDS read)
         static_assert(ATT_CH % 4 == 0, "weights read 4 rows at a time");
