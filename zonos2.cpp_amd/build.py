@@ -56,7 +56,7 @@ def build_hip(force: bool = True) -> Path:
     BUILD.mkdir(exist_ok=True)
     out = BUILD / "libzonos2_hip.so"
     csrc = PKG / "csrc"
-    srcs = [csrc / "z2h.hip"]
+    srcs = [csrc / "z2h.hip", csrc / "z2h_tp.hip"]
     deps = srcs + sorted(csrc.glob("*.h")) + [ROOT / "include" / "z2h.h", PKG / "host" / "z2_formats.h"]
     if force or _stale(out, deps):
         _run([HIPCC, *HIP_FLAGS, "-shared", f"-I{ROOT / 'include'}", f"-I{PKG / 'host'}",

@@ -28,6 +28,15 @@
 
 using namespace z2d;
 
+// the token-pair K-split kernels, instantiated in z2h_tp.hip
+namespace z2d {
+extern template __global__ void k_gemv_split<WF_Q8_0, true, MT_G, false, true>(GemvArgs);
+extern template __global__ void k_gemv_split<WF_Q8_0, false, MT_G, false, true>(GemvArgs);
+extern template __global__ void k_gemv_split<WF_Q8_0, true, MT, false, true>(GemvArgs);
+extern template __global__ void k_gemv_split<WF_Q8_0, false, MT, false, true>(GemvArgs);
+extern template __global__ void k_gemv_split<WF_Q8_0, false, MT_G, true, true>(GemvArgs);
+} // namespace z2d
+
 namespace {
 
 struct DevMat {
@@ -704,7 +713,8 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
             const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, MT_G);
             const int chunks = (a.n_tok + MT_G - 1) / MT_G;
             dim3 grid(m0.tiles, a.grouped ? grid_y : chunks, a.grouped ? chunks : 1), block(256);
-            KL((k_gemv_split<WF_Q8_0, false, MT_G, true>), grid, block, slds, ctx->stream, a);
+            if (a.n_tok <= 2) KL((k_gemv_split<WF_Q8_0, false, MT_G, true, true>), grid, block, slds, ctx->stream, a);
+            else KL((k_gemv_split<WF_Q8_0, false, MT_G, true>), grid, block, slds, ctx->stream, a);
             HIPX(hipGetLastError());
             return Z2H_OK;
         }
@@ -718,7 +728,10 @@ int launch_gemv(z2h_ctx * ctx, const DevMat & m0, const DevMat * m1, const GemvA
             const size_t slds = gemv_mfma_lds_bytes(m0.type, m0.nsb * 256, srows);
             const int chunks = (a.n_tok + srows - 1) / srows;
             dim3 grid(m0.tiles, a.grouped ? grid_y : chunks, a.grouped ? chunks : dual ? 1 : a.n_mats), block(256);
-#define SPL(W_, D_, R_) KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a)
+            // at most two tokens (so at most two rows per block): Q8_0 takes the token-pair units
+            const bool tp = a.n_tok <= 2;
+#define SPL(W_, D_, R_) do { if (tp && W_ == WF_Q8_0) KL((k_gemv_split<W_, D_, R_, false, W_ == WF_Q8_0>), grid, block, slds, ctx->stream, a); \
+                             else KL((k_gemv_split<W_, D_, R_>), grid, block, slds, ctx->stream, a); } while (0)
 #define SPL_R(W_, D_) do { if (half) SPL(W_, D_, MT_G); else SPL(W_, D_, MT); } while (0)
             if (m0.type == Z2H_Q4_K) { if (dual) SPL_R(WF_Q4_K, true); else SPL_R(WF_Q4_K, false); }
             else if (m0.type == Z2H_Q6_K) { if (dual) SPL_R(WF_Q6_K, true); else SPL_R(WF_Q6_K, false); }
@@ -1289,6 +1302,7 @@ int set_lds_limits(std::string & err) {
     LDS_ATTR(k_gemv_rows<WF_Q4_K>) LDS_ATTR(k_gemv_rows<WF_Q6_K>) LDS_ATTR(k_gemv_rows<WF_Q8_0>) LDS_ATTR(k_gemv_rows<WF_F16>)
     LDS_ATTR((k_gemv_split<WF_Q4_K, false, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT>))
     LDS_ATTR((k_gemv_split<WF_Q4_K, true, MT>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT>))
+    LDS_ATTR((k_gemv_split<WF_Q8_0, false, MT, false, true>)) LDS_ATTR((k_gemv_split<WF_Q8_0, true, MT, false, true>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, false, MT, 1>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, false, MT, 1, true>)) LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1, true>))
     LDS_ATTR((k_gemv_mfma<WF_Q4_K, true, MT, 1>)) LDS_ATTR((k_gemv_mfma<WF_Q8_0, true, MT, 1>))

@@ -35,6 +35,9 @@
 #include "z2h_stdorder.h"
 #include <type_traits>
 
+// Z2H_TEMPLATES_ONLY (defined by a second translation unit that only instantiates kernel templates):
+// the non-template kernels below are left out there, so the library defines each of them once.
+
 namespace z2d {
 
 enum { WF_F16 = 1, WF_Q8_0 = 8, WF_Q4_K = 12, WF_Q6_K = 14 };
@@ -244,6 +247,7 @@ __device__ __forceinline__ double block_sum_d(double v, double * red) {
 }
 
 // y[i] = y[i] + b[i] (+ c[i]): the bias adds after the speaker projections (graph.cpp:272-278)
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_bias_add(float * y, const float * b, const float * c, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
@@ -251,6 +255,7 @@ __global__ void __launch_bounds__(256) k_bias_add(float * y, const float * b, co
     if (c) v = v + c[i];
     y[i] = v;
 }
+#endif
 
 // ------------------------------------------------------------------ dequantised table rows
 __device__ __forceinline__ float table_elem(const uint8_t * row, int type, int i) {
@@ -579,6 +584,7 @@ struct GemvArgs {
 constexpr int SORT_EMAX = 256;
 constexpr int SORT_RPW = 16;
 constexpr int LIST_MAX = 1024;   // routes a grouped matmul block lists in LDS itself (without k_route_sort)
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(1024) k_route_sort(const int32_t * sel, int n_routes, int E, int32_t * off, int32_t * perm,
                                                      int32_t * cap_counts, int32_t * cap_off, int32_t * cap_perm) {
     __shared__ int s_wc[16][SORT_EMAX];              // per wave and expert: routes, then the wave's first position
@@ -663,6 +669,7 @@ __global__ void __launch_bounds__(1024) k_route_sort(const int32_t * sel, int n_
         for (int r = tid; r < n_routes; r += 1024) cap_perm[r] = perm[r];
     }
 }
+#endif
 
 // Routes of expert e in ascending flat order (the stable counting sort of mul_mat_id's grouping).
 __device__ __forceinline__ int build_route_list(const int32_t * sel, int n_routes, int e, int * list, int * wcount) {
@@ -1297,6 +1304,36 @@ __device__ __forceinline__ void m16_unit_q4k_pairs(const uint4 (&qs)[2], const u
     }
 }
 
+// Q8_0 unit for blocks of at most two token rows, in m16_unit_q4k_pairs' (token, sub-block) row layout:
+// lane l (q = l >> 4) holds token q >> 1's dots of sub-blocks 4 (q & 1) + v with weight row l & 15.
+// Each sub-block's value is m16_unit's x_b = (dw_b * dx_b) * dot_b; lanes with q = 0 and 2 take the
+// other four from the lane 16 above and add the eight to 0 in sub-block order, m16_unit's order, so
+// the unit value is the same bits.
+__device__ __forceinline__ float m16_unit_q80_pairs(const uint4 (&qs)[4], const uint4 & hd, int sb, int K, int lane,
+                                                    const int8_t * sq, const float * sdx, int ntm1) {
+    const int c = lane & 15, q = lane >> 4, h = q & 1, ja = c & 7, KP = K + 16;
+    const int ta = min(c >> 3, ntm1), to = min(q >> 1, ntm1);
+    const long av = *(const long *) (sq + ta * KP + sb * 256 + 32 * ja + 8 * q);
+    const float4 dx = *(const float4 *) (sdx + to * (K / 32) + sb * 8 + 4 * h);   // sub-blocks 4h .. 4h + 3
+    v4i_t C = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint4 v = qs[j >> 1];
+        const uint32_t lo = (j & 1) ? v.z : v.x, hi = (j & 1) ? v.w : v.y;
+        C = __builtin_amdgcn_mfma_i32_16x16x32_i8(ja == j ? av : 0L, (long) (((uint64_t) hi << 32) | lo), C, 0, 0, 0);
+    }
+    // the row's f16 scales of sub-blocks 4h .. 4h + 3: two per dword of hd (selected by a bit mask; a
+    // lane-dependent choice between the header's dwords would index a private copy of it)
+    const uint32_t hm = 0u - (uint32_t) h;
+    const uint32_t w0 = hd.x ^ ((hd.x ^ hd.z) & hm), w1 = hd.y ^ ((hd.y ^ hd.w) & hm);
+    const float x0 = (h2f(w0 & 0xffffu) * dx.x) * (float) C[0], x1 = (h2f(w0 >> 16) * dx.y) * (float) C[1];
+    const float x2 = (h2f(w1 & 0xffffu) * dx.z) * (float) C[2], x3 = (h2f(w1 >> 16) * dx.w) * (float) C[3];
+    float t = 0.0f;
+    t = t + x0; t = t + x1; t = t + x2; t = t + x3;
+    t = t + up16_f(x0); t = t + up16_f(x1); t = t + up16_f(x2); t = t + up16_f(x3);
+    return t;
+}
+
 // Stage the encoded activation rows of nt tokens (LDS row tt = token tok(tt)) for the m16 kernels:
 // int8 values [rows][K+16], Q8_K sums of 32 [rows][K/32] and scales [rows][K/256], or Q8_0 scales
 // [rows][K/32]. The block's 256 threads walk the nt x (K/16) 16-byte items in one flat sequence
@@ -1534,8 +1571,11 @@ __device__ __forceinline__ void m16_stage_xf(const float * x, int ld, int nt, To
 constexpr int SPLIT_UMAX = 4;          // units per wave (U <= 16)
 // XF (Q8_0 weights, at most 256 * XF_ITEMS / (K / 4) rows): the activation rows are a.xf's fp32 rows,
 // encoded in the staging (m16_stage_xf) rather than read from a.act.
-template <int WF, bool DUAL, int ROWS, bool XF = false>
+// TP (Q4_K / Q8_0; the launch guarantees at most two token rows per block: at most two tokens): the
+// token-pair units (m16_unit_q4k_pairs / m16_unit_q80_pairs) in place of the 16-slot unit.
+template <int WF, bool DUAL, int ROWS, bool XF = false, bool TP = false>
 __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
+    static_assert(!TP || WF == WF_Q4_K || WF == WF_Q8_0, "token-pair units: Q4_K and Q8_0");
     constexpr int QS = m16fmt<WF>::QS, UB = m16fmt<WF>::BYTES;
     constexpr int AF = wfmt<WF>::ACT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1592,14 +1632,29 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
         m16_stage_flat<AF, 8, WF == WF_Q6_K>(a.act, nt, [&](int tt) { return s_tok[tt]; }, K, sq, sbs2, sdx, loads);
     }
     lds_sync();
+    // token pairs: the unit values (lanes with q = 0 and 2) go where the 16-slot unit leaves tokens 0
+    // and 1 (slot i = t of lanes 0-15)
+    if constexpr (TP) {
 #pragma unroll
-    for (int j = 0; j < SPLIT_UMAX; ++j) {
-        const int u = wave + 4 * j;
-        if (u < U) {
-            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
-            m16_unit<WF, ROWS>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
+        for (int j = 0; j < SPLIT_UMAX; ++j) {
+            const int u = wave + 4 * j;
+            if (u < U) {
+                float xv[1], xd[1];
+                if constexpr (WF == WF_Q4_K) m16_unit_q4k_pairs<1>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, xv, xd);
+                else if constexpr (WF == WF_Q8_0) xv[0] = m16_unit_q80_pairs(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sdx, nt - 1);
+                if (((lane >> 4) & 1) == 0) s_x[u][lane >> 5][lane & 15] = xv[0];
+            }
+        }
+    } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s_x[u][i][lane] = t4[i];
+        for (int j = 0; j < SPLIT_UMAX; ++j) {
+            const int u = wave + 4 * j;
+            if (u < U) {
+                float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xd[4];
+                m16_unit<WF, ROWS>(pq[j], ph[j], u < nsb ? u : u - nsb, K, lane, sq, sbs2, sdx, nsb, nt - 1, t4, xd);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s_x[u][i][lane] = t4[i];
+            }
         }
     }
     lds_sync();
@@ -1627,6 +1682,7 @@ __global__ void __launch_bounds__(256) k_gemv_split(GemvArgs a) {
 
 // Row rows[i] of an encoded activation buffer (row stride Kp) copied to row i of dst: the rows of a
 // pass that get logits, gathered for the output head. One block per row.
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_gather_act(ActBuf src, ActBuf dst, int Kp, int af, const int32_t * rows) {
     const int i = blockIdx.x, tid = threadIdx.x;
     const int64_t r = rows[i];
@@ -1642,10 +1698,12 @@ __global__ void __launch_bounds__(256) k_gather_act(ActBuf src, ActBuf dst, int 
         for (int j = tid; j < Kp / 16; j += 256) dst.bs[(int64_t) i * (Kp / 16) + j] = src.bs[r * (Kp / 16) + j];
     }
 }
+#endif
 
 // Encode fp32 rows x[r][K] (row stride ld) in an activation type: one wave per (row, 256-block),
 // same arithmetic as encode_row. Grid: ceil(n_rows * ceil(K/256) / 4) blocks of 256 threads.
 struct EncodeArgs { const float * x; int ld, K, n_rows, act_fmt; ActBuf act; };
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_encode_rows(EncodeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int Kp = kpad(a.K), nb = Kp / 256;
@@ -1679,6 +1737,7 @@ __global__ void __launch_bounds__(256) k_encode_rows(EncodeArgs a) {
         for (int e = 0; e < 4; ++e) h[e] = f2h(v[e]);
     }
 }
+#endif
 
 // ------------------------------------------------------------------ attention
 struct AttnArgs {
@@ -1798,6 +1857,7 @@ __device__ __forceinline__ void rope_cs(int pos, int pl, float theta_scale, floa
 // The table of rope_cs for every position < S and dim pair < np2 ([S][np2] (cos, sin)), formed once per
 // context: the attention kernels read a lane's pair instead of walking its angle chain (up to np2 - 1
 // dependent multiplies) per item.
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_rope_table(float2 * out, int S, int np2, float theta_scale) {
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t) S * np2) return;
@@ -1805,6 +1865,7 @@ __global__ void __launch_bounds__(256) k_rope_table(float2 * out, int S, int np2
     rope_cs((int) (i / np2), (int) (i % np2), theta_scale, cs, sn);
     out[i] = make_float2(cs, sn);
 }
+#endif
 // (cos, sin) of dim pair pl at position pos from the table (positions clamped into [0, S))
 __device__ __forceinline__ void rope_at(const AttnArgs & a, int pos, int pl, float & cs, float & sn) {
     const float2 v = a.rope[(int64_t) min(max(pos, 0), a.S - 1) * (a.hd / 2) + pl];
@@ -2868,6 +2929,7 @@ __host__ __device__ inline size_t sample_lds_bytes(int av, int np2) { return (si
 // kept mass, the walk) run in one thread in candidate order, as the reference's loops do. Where equal
 // logits or probabilities could change the code, the decisions run again on the exact orders of
 // std::partial_sort / std::sort (z2h_order), so the codes are the reference's with ties too.
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
     extern __shared__ __attribute__((aligned(16))) char sm_s[];
     float * s_key = (float *) sm_s;                              // [np2]
@@ -3009,17 +3071,21 @@ __global__ void __launch_bounds__(256) k_sample(SampleArgs a) {
     }
     *out = code;
 }
+#endif
 
 // Device-resident step tables for the next step: column i's input frame = its sampled codes + the
 // text pad id, and its row n_past + 1 (the slot indices stay).
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(64) k_feed(const int32_t * codes, int ncb, int W, int text_pad, int32_t * ids, int32_t * n_past) {
     const int i = blockIdx.x, l = threadIdx.x;
     if (l < W) ids[(int64_t) i * W + l] = l < ncb ? codes[(int64_t) i * ncb + l] : text_pad;
     if (l == 0) n_past[i] = n_past[i] + 1;
 }
+#endif
 
 // KV rows between the host layout [n][nkv][hd] (staged in device memory) and the cache layout
 // [slot][kvh][S][hd]: dir 0 writes the cache, dir 1 reads it into the staging buffer.
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_kv_move(uint4 * stage, uint16_t * cache, int n, int nkv, int hd, int S,
                                                  int row0, int slot, int dir) {
     const int cpr = hd / 8;                                        // 16-byte chunks per head row
@@ -3031,6 +3097,7 @@ __global__ void __launch_bounds__(256) k_kv_move(uint4 * stage, uint16_t * cache
         else stage[i] = *cp;
     }
 }
+#endif
 
 // y = up * silu(gate) of one route (or dense token) row, encoded for the down matmul.
 struct SwigluArgs {
@@ -3038,6 +3105,7 @@ struct SwigluArgs {
     ActBuf act; int act_fmt;
 };
 
+#ifndef Z2H_TEMPLATES_ONLY
 __global__ void __launch_bounds__(256) k_swiglu_encode(SwigluArgs a) {
     extern __shared__ float sm_sw[];
     const int r = blockIdx.x, tid = threadIdx.x, Kp = kpad(a.ff);
@@ -3047,5 +3115,6 @@ __global__ void __launch_bounds__(256) k_swiglu_encode(SwigluArgs a) {
     __syncthreads();
     encode_row_rt(a.act_fmt, sm_sw, a.ff, a.act, r);
 }
+#endif
 
 } // namespace z2d
